@@ -1,0 +1,184 @@
+// extern "C" entry points of libepure_hip.so (declared in include/epure_hip.h).
+//
+// Validation, kernel selection and error reporting live here; kernels live
+// in gemv.hip (small M), mfma.hip (large M), backward.hip and tile.hip.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "epure_hip.h"
+#include "ep_internal.h"
+
+namespace ep {
+
+static thread_local char g_err[512];
+
+int set_error(int code, const char *fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+static bool valid_dtype(int dt) { return dt == EP_F32 || dt == EP_F16 || dt == EP_BF16; }
+
+static int check_weight(const PackedDesc &w)
+{
+    if (w.levels < 1 || w.levels > 256)
+        return set_error(EP_DECLINE_LEVELS, "levels=%d outside 1..256", w.levels);
+    if (!valid_dtype(w.scale_dtype) || !valid_dtype(w.cb_dtype))
+        return set_error(EP_DECLINE_DTYPE, "scale/cb dtype not served (scale %d, cb %d)",
+                         w.scale_dtype, w.cb_dtype);
+    if (w.group < 1)
+        return set_error(EP_ERR_ARG, "group=%d must be >= 1", w.group);
+    if (w.N < 0 || w.K < 0)
+        return set_error(EP_ERR_ARG, "negative shape N=%lld K=%lld", (long long)w.N,
+                         (long long)w.K);
+    const int64_t G = (w.K + w.group - 1) / w.group;
+    if (w.K > 0 && w.ld_scale < G)
+        return set_error(EP_ERR_ARG, "ld_scale=%lld < ceil(K/group)=%lld", (long long)w.ld_scale,
+                         (long long)G);
+    if (w.N > 0 && w.K > 0 && (!w.packed || !w.scale || !w.cb))
+        return set_error(EP_ERR_ARG, "null weight pointer");
+    return EP_OK;
+}
+
+}  // namespace ep
+
+using namespace ep;
+
+extern "C" {
+
+int ep_abi_version(void) { return EP_ABI_VERSION; }
+
+const char *ep_last_error(void) { return g_err; }
+
+int ep_hip_available(void)
+{
+    static int cached = -1;
+    if (cached >= 0)
+        return cached;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        cached = 0;
+        return cached;
+    }
+    int found = 0;
+    for (int d = 0; d < n && !found; ++d) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, d) == hipSuccess &&
+            strncmp(prop.gcnArchName, "gfx950", 6) == 0)
+            found = 1;
+    }
+    cached = found;
+    return cached;
+}
+
+size_t ep_dequant_matmul_workspace(int64_t M, int64_t N, int64_t K, int levels, int group)
+{
+    (void)N;
+    (void)K;
+    (void)levels;
+    (void)group;
+    // Any M may land on the MFMA path (shapes the GEMV does not serve), so
+    // the per-row exponent buffer is always requested.
+    return mfma_workspace(M);
+}
+
+int ep_dequant_matmul(const void *x, int x_dtype, int64_t ldx, const uint8_t *packed,
+                      const void *scale, int scale_dtype, int64_t ld_scale, const void *cb,
+                      int cb_dtype, int levels, int group, int64_t M, int64_t N, int64_t K,
+                      void *y, int y_dtype, int64_t ldy, int flags, void *workspace,
+                      size_t workspace_bytes, void *stream)
+{
+    g_err[0] = 0;
+    PackedDesc w{packed, scale, scale_dtype, ld_scale, cb, cb_dtype, levels, group, N, K};
+    int rc = check_weight(w);
+    if (rc != EP_OK)
+        return rc;
+    if (!valid_dtype(x_dtype) || !valid_dtype(y_dtype))
+        return set_error(EP_DECLINE_DTYPE, "x/y dtype not served (x %d, y %d)", x_dtype, y_dtype);
+    if (M < 0)
+        return set_error(EP_ERR_ARG, "negative M");
+    if (M == 0 || N == 0)
+        return EP_OK;
+    if (!x || !y)
+        return set_error(EP_ERR_ARG, "null x or y");
+    if ((M > 1 && ldx < K) || (M > 1 && ldy < N))
+        return set_error(EP_ERR_ARG, "ldx/ldy smaller than the row length");
+    ActDesc xa{x, x_dtype, M > 1 ? ldx : K};
+    OutDesc ya{y, y_dtype, M > 1 ? ldy : N, (flags & EP_FLAG_ACCUMULATE) ? 1 : 0};
+    hipStream_t s = (hipStream_t)stream;
+    if (gemv_serves(w, xa, M))
+        return launch_gemv(w, xa, M, ya, s);
+    if (mfma_serves(w, xa, M))
+        return launch_mfma(w, xa, M, ya, workspace, workspace_bytes, s);
+    if (M <= 64)
+        return launch_gemv_generic(w, xa, M, ya, s);
+    return set_error(EP_DECLINE_SHAPE,
+                     "no kernel serves M=%lld N=%lld K=%lld group=%d levels=%d with these strides",
+                     (long long)M, (long long)N, (long long)K, group, levels);
+}
+
+size_t ep_dequant_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int levels, int group)
+{
+    return backward_workspace(M, N, K, levels, group);
+}
+
+int ep_dequant_matmul_bwd(const void *gy, int gy_dtype, int64_t ldgy, const void *x, int x_dtype,
+                          int64_t ldx, const uint8_t *packed, const void *scale, int scale_dtype,
+                          int64_t ld_scale, const void *cb, int cb_dtype, int levels, int group,
+                          int64_t M, int64_t N, int64_t K, void *grad_x, int gx_dtype,
+                          int64_t ldgx, float *grad_cb, float *grad_scale, int64_t ld_gscale,
+                          void *workspace, size_t workspace_bytes, void *stream)
+{
+    g_err[0] = 0;
+    PackedDesc w{packed, scale, scale_dtype, ld_scale, cb, cb_dtype, levels, group, N, K};
+    int rc = check_weight(w);
+    if (rc != EP_OK)
+        return rc;
+    if (!valid_dtype(gy_dtype) || !valid_dtype(x_dtype) || (grad_x && !valid_dtype(gx_dtype)))
+        return set_error(EP_DECLINE_DTYPE, "gy/x/grad_x dtype not served");
+    if (M < 0)
+        return set_error(EP_ERR_ARG, "negative M");
+    if (ldgy < N || ldx < K || (grad_x && ldgx < K) ||
+        (grad_scale && ld_gscale < (K + group - 1) / group))
+        return set_error(EP_ERR_ARG, "leading dimension smaller than the row length");
+    ActDesc gya{gy, gy_dtype, ldgy};
+    ActDesc xa{x, x_dtype, ldx};
+    OutDesc gxa{grad_x, gx_dtype, ldgx, 0};
+    return launch_backward(w, gya, xa, M, gxa, grad_cb, grad_scale, ld_gscale, workspace,
+                           workspace_bytes, (hipStream_t)stream);
+}
+
+int ep_unpack_indices(const uint8_t *packed, int64_t n, int levels, uint8_t *idx, void *stream)
+{
+    g_err[0] = 0;
+    if (levels < 1 || levels > 256)
+        return set_error(EP_DECLINE_LEVELS, "levels=%d outside 1..256", levels);
+    if (n < 0 || (n > 0 && (!packed || !idx)))
+        return set_error(EP_ERR_ARG, "bad unpack arguments");
+    return launch_unpack(packed, n, levels, idx, (hipStream_t)stream);
+}
+
+int ep_dequant_tile(const uint8_t *packed, const void *scale, int scale_dtype, int64_t ld_scale,
+                    const void *cb, int cb_dtype, int levels, int group, int64_t N, int64_t K,
+                    void *out, int out_dtype, int64_t ldo, void *stream)
+{
+    g_err[0] = 0;
+    PackedDesc w{packed, scale, scale_dtype, ld_scale, cb, cb_dtype, levels, group, N, K};
+    int rc = check_weight(w);
+    if (rc != EP_OK)
+        return rc;
+    if (!valid_dtype(out_dtype))
+        return set_error(EP_DECLINE_DTYPE, "out dtype %d not served", out_dtype);
+    if (N > 0 && K > 0 && (!out || ldo < K))
+        return set_error(EP_ERR_ARG, "bad output buffer");
+    return launch_dequant_tile(w, out, out_dtype, ldo, (hipStream_t)stream);
+}
+
+}  // extern "C"

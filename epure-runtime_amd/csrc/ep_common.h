@@ -1,0 +1,89 @@
+// Shared device helpers for the gfx950 kernels: element conversions, the
+// per-row power-of-two activation rescale, and wave reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "epure_hip.h"
+
+typedef _Float16 f16_t;
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+#define EP_DEV __device__ __forceinline__
+
+EP_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// float -> bfloat16, round to nearest even (NaN stays NaN).
+EP_DEV uint16_t f32_to_bf16(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u)
+        return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+EP_DEV uint16_t f16_bits(f16_t h) { return __builtin_bit_cast(uint16_t, h); }
+EP_DEV f16_t f16_from_bits(uint16_t b) { return __builtin_bit_cast(f16_t, b); }
+
+// Load element i of a buffer of element type `dt` as float.
+EP_DEV float load_as_f32(const void *p, int dt, int64_t i)
+{
+    if (dt == EP_F32)
+        return ((const float *)p)[i];
+    if (dt == EP_F16)
+        return (float)((const f16_t *)p)[i];
+    return bf16_to_f32(((const uint16_t *)p)[i]);
+}
+
+EP_DEV void store_from_f32(void *p, int dt, int64_t i, float v)
+{
+    if (dt == EP_F32)
+        ((float *)p)[i] = v;
+    else if (dt == EP_F16)
+        ((f16_t *)p)[i] = (f16_t)v;
+    else
+        ((uint16_t *)p)[i] = f32_to_bf16(v);
+}
+
+// Exponent e such that |x| * 2^-e <= 2^14 for the largest |x| of a row
+// (amax), so every element converts to fp16 without overflow; e is also
+// chosen >= -24 so tiny rows are lifted into the normal fp16 range.  2^-e
+// and 2^e are exact, so rescaling changes no bf16 value and the result is
+// multiplied back by 2^e exactly.  Returns 0 for amax == 0 or non-finite.
+EP_DEV int row_exponent(float amax)
+{
+    if (!(amax > 0.0f) || amax > 3.0e38f)
+        return 0;
+    int e;
+    frexpf(amax, &e);      // amax = f * 2^e, f in [0.5, 1)  ->  amax < 2^e
+    int s = e - 14;        // amax * 2^-s < 2^14
+    if (s < -24)
+        s = -24;
+    if (s > 100)
+        s = 100;
+    return s;
+}
+
+// Sum over the 64 lanes of a wave (result valid in every lane).
+EP_DEV float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+EP_DEV float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}

@@ -1,0 +1,114 @@
+// Index unpack and dequantized-tile kernels.
+//
+// unpack:  the flat nibble stream -> one uint8 per index
+//          (epure/runtime.py:48-54 _unpack4; identity copy above 16 levels).
+// dequant: W[n, k] = cb[idx] * scale[n, k / group] with the rounding of
+//          epure/runtime.py:78-89 materialize(dtype):
+//            f32:       f32(cb) * f32(scale)      (container.py:70-88)
+//            f16/bf16:  dtype(dtype(cb) * dtype(scale))
+//          The exact product of two fp16 (or two bf16) values fits in fp32,
+//          so computing it in fp32 and rounding once is the torch result.
+// Both read indices through the same flat-stream addressing as the GEMV
+// fallback, so odd K with 4-bit packing is covered.
+#include "ep_common.h"
+#include "ep_internal.h"
+
+namespace ep {
+namespace {
+
+__global__ void __launch_bounds__(256) unpack_kernel(const uint8_t *__restrict__ packed, int64_t n,
+                                                     int four, uint8_t *__restrict__ idx)
+{
+    // Each thread expands 8 indices (4 packed bytes for 4-bit).
+    const int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (base >= n)
+        return;
+    uint8_t out[8];
+    if (four) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t p = base + 2 * i;
+            const uint8_t b = p < n ? packed[p >> 1] : 0;
+            out[2 * i] = b & 0x0f;
+            out[2 * i + 1] = b >> 4;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            out[i] = base + i < n ? packed[base + i] : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if (base + i < n)
+            idx[base + i] = out[i];
+}
+
+__device__ __forceinline__ float round_to(int dt, float v)
+{
+    if (dt == EP_F16)
+        return (float)(f16_t)v;
+    if (dt == EP_BF16)
+        return bf16_to_f32(f32_to_bf16(v));
+    return v;
+}
+
+struct TileArgs {
+    const uint8_t *packed;
+    const void *scale;
+    int scale_dtype;
+    int64_t lds;
+    const void *cb;
+    int cb_dtype;
+    int levels;
+    int group;
+    int64_t N, K;
+    void *out;
+    int out_dtype;
+    int64_t ldo;
+};
+
+__global__ void __launch_bounds__(256) dequant_tile_kernel(TileArgs a)
+{
+    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= a.K)
+        return;
+    const bool four = a.levels <= 16;
+    for (int64_t n = blockIdx.y; n < a.N; n += gridDim.y) {
+        const int64_t p = n * a.K + k;
+        const uint8_t byte = a.packed[four ? (p >> 1) : p];
+        const int idx = four ? ((p & 1) ? (byte >> 4) : (byte & 15)) : byte;
+        const float c = idx < a.levels ? load_as_f32(a.cb, a.cb_dtype, idx) : 0.0f;
+        const float s = load_as_f32(a.scale, a.scale_dtype, n * a.lds + k / a.group);
+        const float w = round_to(a.out_dtype, c) * round_to(a.out_dtype, s);
+        store_from_f32(a.out, a.out_dtype, n * a.ldo + k, w);
+    }
+}
+
+}  // namespace
+
+int launch_unpack(const uint8_t *packed, int64_t n, int levels, uint8_t *idx, hipStream_t stream)
+{
+    if (n <= 0)
+        return EP_OK;
+    const int64_t threads = (n + 7) / 8;
+    const int64_t grid = (threads + 255) / 256;
+    hipLaunchKernelGGL(unpack_kernel, dim3((unsigned)grid), dim3(256), 0, stream, packed, n,
+                       levels <= 16 ? 1 : 0, idx);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+int launch_dequant_tile(const PackedDesc &w, void *out, int out_dtype, int64_t ldo,
+                        hipStream_t stream)
+{
+    if (w.N <= 0 || w.K <= 0)
+        return EP_OK;
+    TileArgs a{w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
+               w.group, w.N, w.K, out, out_dtype, ldo};
+    dim3 grid((unsigned)((w.K + 255) / 256), (unsigned)(w.N < 65535 ? w.N : 65535));
+    hipLaunchKernelGGL(dequant_tile_kernel, grid, dim3(256), 0, stream, a);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+}  // namespace ep

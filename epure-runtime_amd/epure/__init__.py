@@ -1,0 +1,25 @@
+"""epure (MI355X build) -- the fused codebook dequant-matmul behind every
+packed linear, on hand-written gfx950 HIP kernels.
+
+Public names follow the reference package (epure/__init__.py:31-37) for the
+parts this build covers: the packed store and linear, the fine-tuning
+helpers, and the ``epure.kernels`` backend contract.
+"""
+from .finetune import (
+    ScaleTuner,
+    make_trainable,
+    packed_weights,
+    snapshot_indices,
+    trainable_forward,
+    verify_frozen,
+)
+from .runtime import PackedLinear, PackedWeight, apply_packed
+
+__version__ = "0.2.4+mi355x"
+
+__all__ = [
+    "PackedWeight", "PackedLinear", "apply_packed",
+    "make_trainable", "packed_weights", "snapshot_indices", "verify_frozen",
+    "trainable_forward", "ScaleTuner",
+    "__version__",
+]

@@ -1,0 +1,94 @@
+"""ctypes binding of ``libepure_hip.so`` (the C ABI in ``include/epure_hip.h``).
+
+Loaded after torch so the library resolves to the HIP runtime torch already
+mapped (both carry the soname ``libamdhip64.so.7``): streams and device
+pointers from torch are then valid handles for the library.
+"""
+import ctypes
+import os
+
+import torch
+
+LIB_NAME = "libepure_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "_lib",
+                        LIB_NAME)
+
+ABI_VERSION = 1
+F32, F16, BF16 = 0, 1, 2
+FLAG_ACCUMULATE = 1
+OK = 0
+
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
+
+_c_i64, _c_int, _p, _sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+
+_SIGS = {
+    "ep_abi_version": (_c_int, []),
+    "ep_hip_available": (_c_int, []),
+    "ep_last_error": (ctypes.c_char_p, []),
+    "ep_dequant_matmul_workspace": (_sz, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "ep_dequant_matmul": (_c_int, [
+        _p, _c_int, _c_i64,                      # x, x_dtype, ldx
+        _p, _p, _c_int, _c_i64,                  # packed, scale, scale_dtype, ld_scale
+        _p, _c_int, _c_int, _c_int,              # cb, cb_dtype, levels, group
+        _c_i64, _c_i64, _c_i64,                  # M, N, K
+        _p, _c_int, _c_i64, _c_int,              # y, y_dtype, ldy, flags
+        _p, _sz, _p]),                           # workspace, bytes, stream
+    "ep_dequant_matmul_bwd_workspace": (_sz, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "ep_dequant_matmul_bwd": (_c_int, [
+        _p, _c_int, _c_i64,                      # gy, gy_dtype, ldgy
+        _p, _c_int, _c_i64,                      # x, x_dtype, ldx
+        _p, _p, _c_int, _c_i64,                  # packed, scale, scale_dtype, ld_scale
+        _p, _c_int, _c_int, _c_int,              # cb, cb_dtype, levels, group
+        _c_i64, _c_i64, _c_i64,                  # M, N, K
+        _p, _c_int, _c_i64,                      # grad_x, gx_dtype, ldgx
+        _p, _p, _c_i64,                          # grad_cb, grad_scale, ld_gscale
+        _p, _sz, _p]),                           # workspace, bytes, stream
+    "ep_unpack_indices": (_c_int, [_p, _c_i64, _c_int, _p, _p]),
+    "ep_dequant_tile": (_c_int, [
+        _p, _p, _c_int, _c_i64, _p, _c_int, _c_int, _c_int, _c_i64, _c_i64,
+        _p, _c_int, _c_i64, _p]),
+}
+
+lib = None
+LOAD_ERROR = None
+
+
+def _load():
+    global lib, LOAD_ERROR
+    if lib is not None or LOAD_ERROR is not None:
+        return lib
+    try:
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        if handle.ep_abi_version() != ABI_VERSION:
+            raise ImportError(f"{LIB_NAME} ABI {handle.ep_abi_version()} != {ABI_VERSION}")
+        lib = handle
+    except Exception as exc:                    # noqa: BLE001 - recorded and re-raised by callers
+        LOAD_ERROR = exc
+    return lib
+
+
+def dtype_code(dt):
+    return _DT.get(dt)
+
+
+def stream_handle(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def last_error():
+    msg = lib.ep_last_error() if lib is not None else b""
+    return msg.decode(errors="replace") if msg else ""
+
+
+def check(rc, what):
+    """Map a C ABI return code: 0 -> True, > 0 (decline) -> False, < 0 -> raise."""
+    if rc == OK:
+        return True
+    if rc > 0:
+        return False
+    raise RuntimeError(f"{what} failed ({rc}): {last_error()}")

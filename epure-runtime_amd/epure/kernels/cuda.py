@@ -1,0 +1,206 @@
+"""GPU backend -- hand-written gfx950 HIP kernels behind the reference contract.
+
+Drop-in for ``epure/kernels/cuda.py`` of the reference: the same
+``available()`` and ``linear(x, store) -> Tensor | None`` (cuda.py:49-50,
+:88-117).  ROCm tensors report ``is_cuda``, so the reference's
+``PackedLinear.forward`` (runtime.py:102-117) reaches this module unchanged.
+
+Differences from the reference backend, all deliberate:
+
+* bf16, fp16 and fp32 activations are served (the reference declined every
+  non-fp16 ``x``, cuda.py:101-106, so bf16 models never reached it); the
+  output has ``x.dtype``.
+* every M is served by the library itself (batch-1 GEMV for M <= 4, dequant
+  into LDS + MFMA above), so the caller's ``EPURE_DENSE_ABOVE`` crossover is
+  not needed for speed.
+* the codebook is applied exactly (the reference's default polynomial mode,
+  cuda.py:53-55 / _triton.py:112-185, is an approximation and is not
+  reproduced); ``MODE`` is kept for API compatibility and only "table" exists.
+* with autograd active on ``x``, ``cb`` or ``scale`` the call goes through a
+  custom autograd function with the fused backward, so gradients are never
+  dropped (the reference's fused paths had no backward).
+* if a GPU is present but the library cannot be loaded, importing this
+  module raises: a silent fallback is how the reference once shipped a dead
+  GPU path (cuda.py:26-31).  ``EPURE_ALLOW_FALLBACK=1`` turns that into the
+  reference's RuntimeWarning + decline behaviour.
+"""
+import os
+import warnings
+
+import torch
+
+from . import _abi
+
+MODE = "table"
+IMPORT_ERROR = None
+
+_abi._load()
+if _abi.lib is None:
+    IMPORT_ERROR = _abi.LOAD_ERROR
+    if torch.cuda.is_available():
+        msg = (f"epure: a GPU is present but {_abi.LIB_NAME} failed to load "
+               f"({type(IMPORT_ERROR).__name__}: {IMPORT_ERROR}). Build it with "
+               "__graft_entry__.build().")
+        if os.environ.get("EPURE_ALLOW_FALLBACK") == "1":
+            warnings.warn(msg + " Falling back to the slow path.", RuntimeWarning, stacklevel=2)
+        else:
+            raise ImportError(msg)
+
+_AVAILABLE = None
+
+
+def available():
+    """True when the library is loaded and a gfx950 device is visible."""
+    global _AVAILABLE
+    if _AVAILABLE is None:
+        _AVAILABLE = bool(_abi.lib is not None and torch.cuda.is_available()
+                          and _abi.lib.ep_hip_available() == 1)
+    return _AVAILABLE
+
+
+def library_path():
+    return _abi.LIB_PATH
+
+
+class _Hot:
+    """Per-store launch parameters, resolved once (cuda.py:58-85 ``_hot``).
+
+    Keyed on the identity of the packed/scale/cb tensors: replacing any of
+    them (``make_trainable`` promotes scale/cb to new Parameters) rebuilds
+    the entry.  In-place updates need nothing, since pointers are read per
+    call.
+    """
+    __slots__ = ("packed", "scale", "cb", "N", "K", "group", "levels", "scale_dt", "cb_dt",
+                 "ld_scale")
+
+    def __init__(self, store):
+        self.packed, self.scale, self.cb = store.packed, store.scale, store.cb
+        self.N, self.K = store.out_features, store.in_features
+        self.group, self.levels = int(store.group), int(store.levels)
+        self.scale_dt = _abi.dtype_code(self.scale.dtype)
+        self.cb_dt = _abi.dtype_code(self.cb.dtype)
+        self.ld_scale = self.scale.stride(0) if self.scale.dim() == 2 else self.scale.shape[-1]
+
+    def valid_for(self, store):
+        return (self.packed is store.packed and self.scale is store.scale
+                and self.cb is store.cb)
+
+    def usable(self):
+        return (self.scale_dt is not None and self.cb_dt is not None
+                and self.packed.is_contiguous() and self.cb.is_contiguous()
+                and (self.scale.dim() != 2 or self.scale.stride(1) == 1))
+
+
+def _hot(store):
+    h = store.__dict__.get("_hip_hot")
+    if h is None or not h.valid_for(store):
+        h = _Hot(store)
+        store.__dict__["_hip_hot"] = h
+    return h
+
+
+def forward(x2, h, out=None, accumulate=False):
+    """Launch y = x2 @ W^T for a 2-D ``x2``.  Returns y, or None on decline."""
+    M, K = x2.shape
+    xdt = _abi.dtype_code(x2.dtype)
+    if out is None:
+        out = torch.empty((M, h.N), device=x2.device, dtype=x2.dtype)
+    ydt = _abi.dtype_code(out.dtype)
+    ws_bytes = _abi.lib.ep_dequant_matmul_workspace(M, h.N, K, h.levels, h.group)
+    ws = torch.empty(ws_bytes, device=x2.device, dtype=torch.uint8) if ws_bytes else None
+    rc = _abi.lib.ep_dequant_matmul(
+        x2.data_ptr(), xdt, x2.stride(0),
+        h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+        h.cb.data_ptr(), h.cb_dt, h.levels, h.group,
+        M, h.N, K,
+        out.data_ptr(), ydt, out.stride(0), _abi.FLAG_ACCUMULATE if accumulate else 0,
+        ws.data_ptr() if ws is not None else None, ws_bytes, _abi.stream_handle(x2.device))
+    return out if _abi.check(rc, "ep_dequant_matmul") else None
+
+
+def backward(gy2, x2, h, need_x=True, need_cb=True, need_scale=True):
+    """Fused backward; returns (grad_x, grad_cb, grad_scale) or None on decline."""
+    M, N = gy2.shape
+    K = x2.shape[1]
+    gx = torch.empty((M, K), device=x2.device, dtype=x2.dtype) if need_x else None
+    G = (K + h.group - 1) // h.group
+    gcb = torch.empty(h.levels, device=x2.device, dtype=torch.float32) if need_cb else None
+    gsc = torch.empty((N, G), device=x2.device, dtype=torch.float32) if need_scale else None
+    ws_bytes = _abi.lib.ep_dequant_matmul_bwd_workspace(M, N, K, h.levels, h.group)
+    ws = torch.empty(ws_bytes, device=x2.device, dtype=torch.uint8) if ws_bytes else None
+    rc = _abi.lib.ep_dequant_matmul_bwd(
+        gy2.data_ptr(), _abi.dtype_code(gy2.dtype), gy2.stride(0),
+        x2.data_ptr(), _abi.dtype_code(x2.dtype), x2.stride(0),
+        h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+        h.cb.data_ptr(), h.cb_dt, h.levels, h.group,
+        M, N, K,
+        gx.data_ptr() if gx is not None else None, _abi.dtype_code(x2.dtype), K,
+        gcb.data_ptr() if gcb is not None else None,
+        gsc.data_ptr() if gsc is not None else None, G,
+        ws.data_ptr() if ws is not None else None, ws_bytes, _abi.stream_handle(x2.device))
+    if not _abi.check(rc, "ep_dequant_matmul_bwd"):
+        return None
+    return gx, gcb, gsc
+
+
+class _PackedLinearFn(torch.autograd.Function):
+    """y = x W^T with W = cb[idx] * scale; grads for x, cb and scale."""
+
+    @staticmethod
+    def forward(ctx, x2, cb, scale, h):
+        y = forward(x2, h)
+        if y is None:
+            raise RuntimeError("fused forward declined inside autograd")
+        ctx.h = h
+        ctx.save_for_backward(x2)
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        (x2,) = ctx.saved_tensors
+        h = ctx.h
+        need_x, need_cb, need_sc = ctx.needs_input_grad[0], ctx.needs_input_grad[1], \
+            ctx.needs_input_grad[2]
+        r = backward(gy.contiguous(), x2, h, need_x, need_cb, need_sc)
+        if r is None:
+            raise RuntimeError(f"fused backward declined: {_abi.last_error()}")
+        gx, gcb, gsc = r
+        if gcb is not None:
+            gcb = gcb.to(h.cb.dtype).view_as(h.cb)
+        if gsc is not None:
+            gsc = gsc.to(h.scale.dtype).view_as(h.scale)
+        return gx, gcb, gsc, None
+
+
+def linear(x, store):
+    """``x @ dequant(store).T`` on the GPU, or ``None`` if unsupported."""
+    if not available() or not x.is_cuda or len(store.shape) != 2:
+        return None
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return None
+    h = _hot(store)
+    if not h.usable() or not store.packed.is_cuda:
+        return None
+    shape = x.shape
+    x2 = x.reshape(-1, shape[-1])
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    grad = torch.is_grad_enabled() and (
+        x.requires_grad or store.cb.requires_grad or store.scale.requires_grad)
+    if grad:
+        if not backward_available():
+            return None
+        y = _PackedLinearFn.apply(x2, store.cb, store.scale, h)
+    else:
+        y = forward(x2, h)
+        if y is None:
+            return None
+    return y.reshape(*shape[:-1], h.N)
+
+
+# The fused backward kernels are part of the library build.
+_BWD_BUILT = False
+
+
+def backward_available():
+    return _BWD_BUILT and os.environ.get("EPURE_NO_FUSED_BWD") != "1"

@@ -1,0 +1,152 @@
+"""Packed store and packed linear -- the caller side of the fused kernels.
+
+Mirrors the reference's resident representation and dispatch
+(epure/runtime.py:34-126): ``PackedWeight`` owns ``packed`` / ``scale`` /
+``cb`` buffers, ``PackedLinear.forward`` hands the call to a backend and
+materializes when the backend declines.  Only what the packed-linear path
+needs is here; the ``.ebin`` loader, embeddings and MoE holders are outside
+this build.
+"""
+import os
+
+import numpy as np
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .kernels import cpu as cpu_kernel
+from .kernels import cuda as cuda_kernel
+from .kernels import _abi
+
+_BUFFER_CACHE = {}
+
+# Rows at or above which the GPU path materializes and calls a dense GEMM
+# (reference runtime.py:26-31 defaults to 8).  The HIP backend serves every
+# M itself, so the default keeps the fused path always.
+_DENSE_ABOVE = int(os.environ.get("EPURE_DENSE_ABOVE", str(2**31 - 1)))
+
+
+def _pack4(idx, levels):
+    """Flat index stream -> bytes (runtime.py:34-45 layout).
+
+    Up to 16 levels two indices share a byte, the even position in the low
+    nibble; an odd count gets a zero pad.  Above 16 levels one index per byte.
+    """
+    flat = np.asarray(idx, dtype=np.uint8).reshape(-1)
+    if levels > 16:
+        return np.ascontiguousarray(flat)
+    if flat.size & 1:
+        flat = np.concatenate([flat, np.zeros(1, np.uint8)])
+    pairs = flat.reshape(-1, 2)
+    return np.ascontiguousarray((pairs[:, 0] & 0x0F) | (pairs[:, 1] << 4)).astype(np.uint8)
+
+
+def _unpack4(packed, n, levels):
+    """Bytes -> flat index stream of length n (runtime.py:48-54)."""
+    if levels > 16:
+        return packed[:n]
+    if packed.is_cuda and cuda_kernel.available():
+        out = torch.empty(n, dtype=torch.uint8, device=packed.device)
+        rc = _abi.lib.ep_unpack_indices(packed.data_ptr(), n, levels, out.data_ptr(),
+                                        _abi.stream_handle(packed.device))
+        _abi.check(rc, "ep_unpack_indices")
+        return out
+    both = torch.stack((packed & 0x0F, packed >> 4), dim=-1)
+    return both.reshape(-1)[:n]
+
+
+def _as_tensor(a):
+    return a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a))
+
+
+class PackedWeight(nn.Module):
+    """Indices, per-group scales and a codebook (runtime.py:57-89)."""
+
+    def __init__(self, shape, packed, scale, cb, group, levels):
+        super().__init__()
+        self.levels, self.group = int(levels), int(group)
+        self.shape = tuple(int(d) for d in shape)
+        self.in_features = self.shape[-1]
+        rows = 1
+        for d in self.shape[:-1]:
+            rows *= d
+        self.out_features = rows
+        self.register_buffer("packed", _as_tensor(packed), persistent=False)
+        self.register_buffer("scale", _as_tensor(scale), persistent=False)
+        self.register_buffer("cb", _as_tensor(cb), persistent=False)
+
+    def packed_2d(self):
+        cols = self.in_features if self.levels > 16 else (self.in_features + 1) // 2
+        return self.packed.view(self.out_features, cols)
+
+    def materialize(self, dtype=torch.float16):
+        """Dense weight in ``dtype`` (runtime.py:78-89 semantics).
+
+        ``dtype(cb)[idx] * dtype(scale)`` -- for fp16/bf16 both operands are
+        rounded to ``dtype`` before the product, as the reference does.  On a
+        gfx950 device without autograd this runs the library's dequant
+        kernel; with gradients required it uses differentiable torch ops.
+        """
+        n = self.out_features * self.in_features
+        needs_grad = torch.is_grad_enabled() and (self.cb.requires_grad
+                                                  or self.scale.requires_grad)
+        if (not needs_grad and self.packed.is_cuda and cuda_kernel.available()
+                and dtype in (torch.float32, torch.float16, torch.bfloat16)):
+            h = cuda_kernel._hot(self)
+            if h.usable():
+                w = torch.empty((self.out_features, self.in_features), dtype=dtype,
+                                device=self.packed.device)
+                rc = _abi.lib.ep_dequant_tile(
+                    h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+                    h.cb.data_ptr(), h.cb_dt, h.levels, h.group, h.N, h.K,
+                    w.data_ptr(), _abi.dtype_code(dtype), w.stride(0),
+                    _abi.stream_handle(self.packed.device))
+                if _abi.check(rc, "ep_dequant_tile"):
+                    return w.reshape(self.shape) if len(self.shape) > 2 else w
+        idx = _unpack4(self.packed, n, self.levels).view(self.out_features, self.in_features)
+        table = self.cb.to(dtype).reshape(-1, 1)
+        w = F.embedding(idx.int(), table).squeeze(-1)
+        sc = self.scale.to(dtype).repeat_interleave(self.group, dim=1)[:, :self.in_features]
+        w = w * sc
+        return w.reshape(self.shape) if len(self.shape) > 2 else w
+
+
+class PackedLinear(nn.Module):
+    """Linear layer over a ``PackedWeight`` (runtime.py:92-126)."""
+
+    def __init__(self, store, bias=None):
+        super().__init__()
+        self.store = store
+        self.bias = bias
+
+    def forward(self, x):
+        s = self.store
+        if len(s.shape) == 2 and not s.__dict__.get("_force_materialize", False):
+            out = None
+            if x.is_cuda:
+                if x.reshape(-1, x.shape[-1]).shape[0] < _DENSE_ABOVE:
+                    out = cuda_kernel.linear(x, s)
+            elif s.levels <= 16:
+                out = cpu_kernel.linear(x, s, _BUFFER_CACHE)
+            if out is not None:
+                return out + self.bias if self.bias is not None else out
+        w = s.materialize(x.dtype)
+        out = F.linear(x, w, self.bias)
+        del w
+        return out
+
+
+def apply_packed(model, stores):
+    """Swap ``nn.Linear`` modules for ``PackedLinear`` (runtime.py:261-262).
+
+    ``stores`` maps a module path (``"model.layers.0.mlp.up_proj"``) to a
+    ``PackedWeight``; the linear's bias, if any, is kept.
+    """
+    for name, store in stores.items():
+        parent_name, _, attr = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        target = getattr(parent, attr)
+        if not isinstance(target, nn.Linear):
+            raise TypeError(f"{name} is {type(target).__name__}, not nn.Linear")
+        setattr(parent, attr, PackedLinear(store, getattr(target, "bias", None)))
+    return model

@@ -1,0 +1,138 @@
+/*
+ * epure_hip.h -- C ABI of the MI355X (gfx950) fused codebook dequant-matmul.
+ *
+ * A packed weight W[N, K] is stored the way the reference keeps it resident
+ * (epure/runtime.py:57-89):
+ *   packed  uint8, the FLAT index stream of N*K indices; 4-bit when
+ *           levels <= 16 (two per byte, even position in the low nibble,
+ *           runtime.py:34-45), else one uint8 index per byte;
+ *   scale   [N, ceil(K/group)] fp16 (container) or fp32 (after
+ *           finetune.make_trainable, finetune.py:78), row stride ld_scale;
+ *   cb      [levels] fp32 (container, runtime.py:243) or fp16.
+ *   W[n,k] = cb[idx[n,k]] * scale[n, k / group]; an index >= levels reads 0
+ *   (the Rust LUT, kernel/src/lib.rs:58-59).
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers and sizes; the caller owns every buffer,
+ *     including workspaces; nothing here allocates or frees device memory;
+ *   - work is enqueued on `stream` (a hipStream_t; NULL = the null stream);
+ *     no host synchronisation, so every call is capture-safe;
+ *   - return 0 on success; > 0 = DECLINE (the caller falls back to
+ *     materialize, the `None` of epure/kernels/__init__.py:5-11);
+ *     < 0 = error, with a message from ep_last_error().
+ *
+ * Element type codes are the EP_* values below.
+ */
+#ifndef EPURE_HIP_H
+#define EPURE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EP_ABI_VERSION 1
+
+/* element types */
+#define EP_F32 0
+#define EP_F16 1
+#define EP_BF16 2
+
+/* flags for ep_dequant_matmul */
+#define EP_FLAG_ACCUMULATE 1 /* y += x.W^T instead of y = x.W^T */
+
+/* return codes */
+#define EP_OK 0
+#define EP_DECLINE_DTYPE 1  /* unsupported element type combination */
+#define EP_DECLINE_SHAPE 2  /* shape/stride the kernels do not serve */
+#define EP_DECLINE_LEVELS 3 /* levels outside 1..256 */
+#define EP_ERR_ARG (-1)
+#define EP_ERR_HIP (-2)
+#define EP_ERR_WORKSPACE (-3)
+
+/* Version of this ABI (EP_ABI_VERSION). */
+int ep_abi_version(void);
+
+/*
+ * 1 if a gfx950 device is visible, else 0.  Cheap and side-effect free
+ * after the first call.  Replaces epure/kernels/cuda.py:49-50 available().
+ */
+int ep_hip_available(void);
+
+/* Last error message of the calling thread ("" if none). */
+const char *ep_last_error(void);
+
+/*
+ * Workspace bytes ep_dequant_matmul needs for this shape (a few bytes per
+ * activation row).  The caller passes at least this much.
+ */
+size_t ep_dequant_matmul_workspace(int64_t M, int64_t N, int64_t K, int levels, int group);
+
+/*
+ * y[M, N] (=|+=) x[M, K] . W[N, K]^T
+ *
+ * Replaces the reference's per-packed-linear kernel entry:
+ *   epure/kernels/_triton.py:477-512  dequant_matmul(x, packed, scale, cb,
+ *                                     group, bits, n_out, k_in)
+ *   kernel/src/lib.rs:94-151          epure_kernel.dequant_matmul(x, packed,
+ *                                     scales, cb, group, four_bit)
+ * x: x_dtype (EP_BF16 / EP_F16 / EP_F32), row stride ldx elements.
+ * y: y_dtype, row stride ldy elements.  Accumulation is fp32; weights enter
+ * the products as fp16(cb[idx]) (the dot-product path) or
+ * fp16(cb[idx]*scale) (the MFMA path); x enters as fp16 after an exact
+ * per-row power-of-two rescale, so it cannot overflow fp16.
+ * The kernel is chosen from M (batch-1 GEMV for small M, dequant-to-LDS +
+ * MFMA for large M); both read the packed bytes exactly once per launch.
+ */
+int ep_dequant_matmul(const void *x, int x_dtype, int64_t ldx,
+                      const uint8_t *packed, const void *scale, int scale_dtype,
+                      int64_t ld_scale, const void *cb, int cb_dtype, int levels,
+                      int group, int64_t M, int64_t N, int64_t K,
+                      void *y, int y_dtype, int64_t ldy, int flags,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Compressed-state backward of y = x . W^T with frozen indices
+ * (fine-tuning/README.md:62-68; autograd through runtime.py:84-88):
+ *   grad_x[M, K]            = gy[M, N] . W                (gx_dtype; NULL = skip)
+ *   grad_cb[levels]   (f32) = sum_{idx==l} (gy^T x)[n,k] * scale[n, k/group]
+ *   grad_scale[N, G]  (f32) = sum_{k in g} (gy^T x)[n,k] * cb[idx[n,k]]
+ * (grad_cb / grad_scale NULL = skip).  grad_W is never written to memory.
+ * grad_cb and grad_scale are overwritten, not accumulated, and are
+ * deterministic (fixed-order reductions).  `packed` is only read.
+ */
+size_t ep_dequant_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int levels, int group);
+int ep_dequant_matmul_bwd(const void *gy, int gy_dtype, int64_t ldgy,
+                          const void *x, int x_dtype, int64_t ldx,
+                          const uint8_t *packed, const void *scale, int scale_dtype,
+                          int64_t ld_scale, const void *cb, int cb_dtype, int levels,
+                          int group, int64_t M, int64_t N, int64_t K,
+                          void *grad_x, int gx_dtype, int64_t ldgx,
+                          float *grad_cb, float *grad_scale, int64_t ld_gscale,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * idx[0..n) = the unpacked index stream (epure/runtime.py:48-54 _unpack4),
+ * run by the same device decode the GEMV uses.
+ */
+int ep_unpack_indices(const uint8_t *packed, int64_t n, int levels, uint8_t *idx, void *stream);
+
+/*
+ * out[N, K] (out_dtype, row stride ldo) = dequantized weight, with the
+ * rounding of epure/runtime.py:78-89 materialize(dtype):
+ *   EP_F32: f32(cb[idx]) * f32(scale)  (== container.dequantize,
+ *           epure/container.py:70-88; exact for fp16-valued cb/scale)
+ *   EP_F16 / EP_BF16: dtype(dtype(cb[idx]) * dtype(scale)).
+ */
+int ep_dequant_tile(const uint8_t *packed, const void *scale, int scale_dtype,
+                    int64_t ld_scale, const void *cb, int cb_dtype, int levels,
+                    int group, int64_t N, int64_t K, void *out, int out_dtype,
+                    int64_t ldo, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EPURE_HIP_H */

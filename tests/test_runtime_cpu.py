@@ -1,0 +1,73 @@
+"""Host logic of the drop-in package on CPU: packing helpers, the store, the
+decline contract and the fine-tuning helpers (no GPU, no kernel launch)."""
+import numpy as np
+import pytest
+import torch
+
+from epure import PackedLinear, PackedWeight, make_trainable, snapshot_indices, verify_frozen
+from epure import runtime
+from epure.kernels import cpu, cuda
+from oracle import ref
+
+
+def store(n=16, k=256, levels=16, group=128, seed=0):
+    idx, packed, scale, cb = ref.synth_linear(n, k, levels, group, seed=seed)
+    return idx, PackedWeight((n, k), packed, scale, cb.astype(np.float32), group, levels)
+
+
+@pytest.mark.parametrize("n", [1, 5, 64])
+def test_pack4_matches_oracle(n):
+    idx = np.random.Generator(np.random.PCG64(n)).integers(0, 16, n, dtype=np.uint8)
+    assert np.array_equal(runtime._pack4(idx, 16), ref.pack4(idx, 16))
+    assert np.array_equal(runtime._pack4(idx, 200), ref.pack4(idx, 200))
+
+
+def test_unpack4_cpu_matches_oracle():
+    b = np.random.Generator(np.random.PCG64(3)).integers(0, 256, 77, dtype=np.uint8)
+    got = runtime._unpack4(torch.from_numpy(b), 153, 16).numpy()
+    assert np.array_equal(got, ref.unpack4(b, 153, 16))
+
+
+def test_store_shapes():
+    _, s = store(n=12, k=64)
+    assert s.in_features == 64 and s.out_features == 12
+    assert tuple(s.packed_2d().shape) == (12, 32)
+
+
+@pytest.mark.parametrize("dtype,name", [(torch.float32, "f32"), (torch.float16, "f16"),
+                                        (torch.bfloat16, "bf16")])
+def test_materialize_cpu_matches_oracle(dtype, name):
+    idx, s = store()
+    w = s.materialize(dtype).float().numpy()
+    want = ref.materialize(s.packed.numpy(), s.scale.numpy(), s.cb.numpy(), 16, 256, 128, 16, name)
+    assert np.array_equal(w, want)
+
+
+def test_cpu_backend_declines_and_linear_falls_back():
+    _, s = store()
+    x = torch.randn(3, 256)
+    assert cpu.available() is False and cpu.linear(x, s) is None
+    assert cuda.linear(x, s) is None                    # CPU tensor: decline
+    lin = PackedLinear(s, bias=torch.ones(16))
+    y = lin(x)
+    assert torch.allclose(y, x @ s.materialize(torch.float32).T + 1, rtol=1e-6, atol=1e-6)
+
+
+def test_finetune_index_freeze_cycle():
+    _, s = store()
+    model = torch.nn.Sequential(PackedLinear(s))
+    snap = snapshot_indices(model)
+    params = make_trainable(model, "both", verbose=False)
+    assert len(params) == 2 and all(p.dtype == torch.float32 for p in params)
+    x = torch.randn(4, 256)
+    model(x).square().sum().backward()       # materialize path: autograd reaches cb/scale
+    assert s.cb.grad is not None and s.scale.grad is not None
+    assert verify_frozen(model, snap)
+    s.packed[0] ^= 1
+    with pytest.raises(RuntimeError):
+        verify_frozen(model, snap)
+
+
+def test_make_trainable_rejects_mode():
+    with pytest.raises(ValueError):
+        make_trainable(torch.nn.Sequential(), "nope")
