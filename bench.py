@@ -1,0 +1,187 @@
+"""Headline benchmark: batch-1 greedy decode tok/s of the Llama-3-8B-shaped
+4-bit codebook model on one MI355X, plus the
+dequant-GEMV HBM bandwidth as a fraction of peak.
+
+    python bench.py [--steps K] [--warmup W] [--config llama3-8b|qwen3-1.7b]
+
+One "step" is one decode token: a replay of the captured HIP graph of the
+whole decode step (32 layers x {fused q|k|v GEMV, attention, o GEMV, fused
+gate|up GEMV, down GEMV} + lm_head/argmax).  The prompt (128 random ids) is
+consumed first, untimed; then W warm-up tokens, then K timed tokens, with the
+device synchronised on both sides.  Weights are random-init in the packed
+format (synthetic data; no checkpoints offline).
+
+The roofline entry is for the packed dequant-GEMV: the 128 GEMV launches of
+one step are captured into a second graph that is replayed K times between
+HIP events on the launch stream; achieved = packed bytes per step / time per
+replay.  The CPU baseline is the C restatement of the reference's Rust kernel
+(oracle/rowdot.c, kernel/src/lib.rs semantics) on one layer's 7 linears,
+scaled to the 224 linears of a step.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "epure-runtime_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "batch-1 decode tok/s at 8B shape; dequant-GEMV HBM GB/s as % of peak"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--config", default="llama3-8b", choices=["llama3-8b", "qwen3-1.7b"])
+    ap.add_argument("--prompt", type=int, default=None)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    return ap.parse_args()
+
+
+def cpu_baseline(cfg, threads):
+    """Reference Rust kernel semantics (C port) on one layer's 7 packed
+    linears; tok/s ceiling = 1 / (time per layer * layers)."""
+    import numpy as np
+    from oracle import ref, rowdot
+    shapes = cfg.packed_linear_shapes()
+    data = []
+    for j, (name, n, k) in enumerate(shapes):
+        _, packed, scale, cb = ref.synth_linear(n, k, cfg.levels, cfg.group, seed=100 + j)
+        x = ref.round_bf16(np.random.Generator(np.random.PCG64(j)).standard_normal(
+            (1, k)).astype(np.float32))
+        data.append((x, packed.reshape(n, k // 2), scale.astype(np.float32),
+                     cb.astype(np.float32)))
+    nt = threads or rowdot.threads()
+
+    def layer():
+        for x, p, s, c in data:
+            rowdot.dequant_matmul(x, p, s, c, cfg.group, True, nthreads=nt)
+    layer()                                       # warm-up
+    times = []
+    t_end = time.perf_counter() + 10.0
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        layer()
+        times.append(time.perf_counter() - t0)
+    t_layer = float(np.median(times))
+    return {"value": round(1.0 / (t_layer * cfg.layers), 4), "unit": "tok/s", "cores": nt,
+            "kind": "port",
+            "sample": f"C port of kernel/src/lib.rs on one layer's 7 packed linears "
+                      f"({sum(n * k for _, n, k in shapes) / 1e6:.0f}M weights, f32 x), median of "
+                      f"{len(times)} runs = {t_layer * 1e3:.1f} ms, scaled x{cfg.layers} layers "
+                      f"(linears only, lm_head excluded)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build has "
+              "no multi-GPU path: the packed linears shard by rows with no exchange, see "
+              "DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from epure.decode import LLAMA3_8B, QWEN3_1_7B, Decoder, random_weights
+    from epure.kernels import _abi
+
+    cfg = {"llama3-8b": LLAMA3_8B, "qwen3-1.7b": QWEN3_1_7B}[args.config]
+    n_prompt = args.prompt or (128 if args.config == "llama3-8b" else 32)
+    dev = torch.device("cuda:0")
+    print(f"# building {cfg.name} random weights (seed {args.seed})", file=sys.stderr, flush=True)
+    w = random_weights(cfg, seed=args.seed, device=dev)
+    total_steps = n_prompt - 1 + args.warmup + args.steps
+    dec = Decoder(w, total_steps + 2)
+    import numpy as np
+    prompt = np.random.Generator(np.random.PCG64(args.seed + 1)).integers(
+        0, cfg.vocab, n_prompt).tolist()
+    dec.reset(prompt)
+    dec.capture()
+    for _ in range(n_prompt - 1):
+        dec.step()
+    for _ in range(args.warmup):
+        dec.step()
+    torch.cuda.synchronize()
+    print(f"# prompt + warm-up done; timing {args.steps} decode steps", file=sys.stderr,
+          flush=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dec.step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    tok_s = args.steps / dt
+    toks = dec.tokens[:n_prompt + args.warmup + args.steps].cpu().tolist()
+
+    # dequant-GEMV only: the step's packed GEMV launches, timed with events
+    stream = torch.cuda.current_stream()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        dec.gemv_launches()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(args.steps):
+            g.replay()
+        e1.record(stream)
+    e1.synchronize()
+    gemv_ms = e0.elapsed_time(e1) / args.steps
+    packed = w.packed_bytes()
+    n_gemv = 4 * cfg.layers
+    gemv_gbs = packed / (gemv_ms * 1e-3) / 1e9
+    resident = w.resident_bytes()
+    step_ms = dt / args.steps * 1e3
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{cfg.name}-shaped batch-1 greedy decode, 4-bit codebook packed "
+                        f"linears (16-entry cb, group {cfg.group}), bf16 embed/lm_head, "
+                        f"prompt {n_prompt}",
+            "layers": cfg.layers, "hidden": cfg.hidden, "intermediate": cfg.intermediate,
+            "vocab": cfg.vocab, "prompt": n_prompt, "decoded": args.warmup + args.steps,
+            "packed_linear_bytes": packed, "resident_weight_bytes": resident,
+            "step_hbm_gbs_resident": round(resident / (step_ms * 1e-3) / 1e9, 1),
+            "step_frac_resident": round(resident / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "step_frac_packed": round(packed / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "gemv_ms_per_step": round(gemv_ms, 4),
+            "gemv_launches_per_step": n_gemv,
+            "first_tokens": toks[n_prompt:n_prompt + 8],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gemv_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        print("# CPU baseline (reference Rust semantics, C port)", file=sys.stderr, flush=True)
+        out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_threads)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

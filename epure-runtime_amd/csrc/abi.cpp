@@ -7,6 +7,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include "epure_decode.h"
 #include "epure_hip.h"
 #include "ep_internal.h"
 
@@ -21,6 +22,22 @@ int set_error(int code, const char *fmt, ...)
     vsnprintf(g_err, sizeof(g_err), fmt, ap);
     va_end(ap);
     return code;
+}
+
+static int g_cus = 0;
+
+int device_cus()
+{
+    if (g_cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+            n > 0)
+            g_cus = n;
+        else
+            g_cus = 256;
+    }
+    return g_cus;
 }
 
 static bool valid_dtype(int dt) { return dt == EP_F32 || dt == EP_F16 || dt == EP_BF16; }
@@ -75,6 +92,8 @@ int ep_hip_available(void)
             found = 1;
     }
     cached = found;
+    if (found)
+        (void)device_cus();
     return cached;
 }
 
@@ -179,6 +198,86 @@ int ep_dequant_tile(const uint8_t *packed, const void *scale, int scale_dtype, i
     if (N > 0 && K > 0 && (!out || ldo < K))
         return set_error(EP_ERR_ARG, "bad output buffer");
     return launch_dequant_tile(w, out, out_dtype, ldo, (hipStream_t)stream);
+}
+
+int ep_fused_gemv(int xsrc, const void *x, int x_dtype, const void *x_aux, float eps, int64_t K,
+                  int group, int levels, int scale_dtype, int cb_dtype, int nseg,
+                  const uint8_t *const *packed, const void *const *scale, const void *const *cb,
+                  void *const *y, const int64_t *N, int y_dtype, int accumulate, void *stream)
+{
+    g_err[0] = 0;
+    if (nseg < 1 || nseg > 3 || !packed || !scale || !cb || !y || !N || !x)
+        return set_error(EP_ERR_ARG, "fused GEMV: bad segment arguments");
+    if ((xsrc != EP_XSRC_PLAIN && !x_aux) || !valid_dtype(y_dtype) ||
+        (xsrc == EP_XSRC_PLAIN && !valid_dtype(x_dtype)))
+        return set_error(EP_ERR_ARG, "fused GEMV: bad activation arguments");
+    FusedGemv f{};
+    f.xsrc = xsrc;
+    f.x = x;
+    f.x_dtype = x_dtype;
+    f.x2 = x_aux;
+    f.eps = eps;
+    f.K = K;
+    f.group = group;
+    f.levels = levels;
+    f.scale_dtype = scale_dtype;
+    f.cb_dtype = cb_dtype;
+    f.y_dtype = y_dtype;
+    f.accumulate = accumulate ? 1 : 0;
+    f.nseg = nseg;
+    for (int i = 0; i < nseg; ++i) {
+        PackedDesc w{packed[i], scale[i], scale_dtype, (K + group - 1) / group, cb[i], cb_dtype,
+                     levels, group, N[i], K};
+        int rc = check_weight(w);
+        if (rc != EP_OK)
+            return rc;
+        if (!y[i])
+            return set_error(EP_ERR_ARG, "fused GEMV: null output %d", i);
+        f.seg[i] = FusedSeg{packed[i], scale[i], cb[i], y[i], N[i]};
+    }
+    return launch_gemv_fused(f, (hipStream_t)stream);
+}
+
+size_t ep_attention_workspace(int Hq, int D, int max_pos)
+{
+    return attention_workspace(Hq, D, max_pos);
+}
+
+int ep_decode_attention(const float *q, const float *k, const float *v, const uint16_t *qn_w,
+                        const uint16_t *kn_w, float qk_eps, uint16_t *kcache, uint16_t *vcache,
+                        const float *cos_t, const float *sin_t, const int *state, float *part,
+                        int *counters, uint16_t *out, int Hq, int Hkv, int D, int max_pos,
+                        float scale, void *stream)
+{
+    g_err[0] = 0;
+    if (!q || !k || !v || !kcache || !vcache || !cos_t || !sin_t || !state || !part ||
+        !counters || !out || Hq < 1 || Hkv < 1 || D < 2 || max_pos < 1)
+        return set_error(EP_ERR_ARG, "attention: bad arguments");
+    AttnDesc d{q, k, v, qn_w, kn_w, qk_eps, kcache, vcache, cos_t, sin_t, state, part, counters,
+               out, Hq, Hkv, D, max_pos, scale};
+    return launch_attention(d, (hipStream_t)stream);
+}
+
+int ep_lm_head_argmax(float *h, const uint16_t *norm_w, float eps, const uint16_t *W, float *logits,
+                      int V, int H, float *part_val, int *part_idx, int *counter, int *state,
+                      const int *prompt, int n_prompt, int *tokens, int *argmax_out,
+                      const uint16_t *embed, int max_pos, int grid, void *stream)
+{
+    g_err[0] = 0;
+    if (!h || !norm_w || !W || !part_val || !part_idx || !counter || !state || !tokens ||
+        !argmax_out || !embed || V < 1 || H < 1 || (n_prompt > 0 && !prompt))
+        return set_error(EP_ERR_ARG, "lm_head: bad arguments");
+    HeadDesc d{h, norm_w, eps, W, logits, V, H, part_val, part_idx, counter, state, prompt,
+               n_prompt, tokens, argmax_out, embed, max_pos, grid};
+    return launch_lm_head(d, (hipStream_t)stream);
+}
+
+int ep_embed_token(const uint16_t *embed, const int *state, float *h, int H, void *stream)
+{
+    g_err[0] = 0;
+    if (!embed || !state || !h || H < 1)
+        return set_error(EP_ERR_ARG, "embed: bad arguments");
+    return launch_embed(embed, state, h, H, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,499 @@
+// Decode-step kernels around the packed GEMV: attention over the KV cache
+// and the bf16 lm_head with greedy selection.
+//
+// These are the caller side of the packed linears (the reference leaves
+// them to transformers: runtime.py:389-415 loads a LlamaForCausalLM /
+// Qwen3ForCausalLM whose q/k/v/o/gate/up/down are PackedLinear).  The math
+// follows those modules: per-head RMSNorm on q/k (Qwen3 only), rotate-half
+// RoPE, grouped-query causal softmax attention, RMSNorm before the lm_head,
+// greedy argmax (lowest index on ties, as torch.argmax).
+//
+// Every kernel reads the decode position from device memory (state[0]), so
+// one captured HIP graph replays every step unchanged.  Split-work kernels
+// combine in the workgroup that arrives last on a per-item counter, which
+// that workgroup resets to 0 for the next replay (no memset in the graph).
+#include "ep_common.h"
+#include "ep_internal.h"
+
+namespace ep {
+namespace {
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kChunk = 64;  // KV positions per attention workgroup
+constexpr int kMaxD = 128;  // head_dim served
+
+EP_DEV float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+// Sum of a value held by every thread of a 256-thread workgroup.
+EP_DEV float block_sum256(float v, float *scratch)
+{
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0)
+        scratch[wave] = v;
+    __syncthreads();
+    return scratch[0] + scratch[1] + scratch[2] + scratch[3];
+}
+
+// In-place per-head RMSNorm (optional) and rotate-half RoPE of one head
+// vector held in LDS (D floats), by threads 0..D-1 of the workgroup.
+EP_DEV void norm_rope(float *vec, const uint16_t *nw, float eps, const float *cs, const float *sn,
+                      int D, float *scratch)
+{
+    const int t = threadIdx.x;
+    if (nw) {
+        const float x = t < D ? vec[t] : 0.0f;
+        const float ss = block_sum256(x * x, scratch);
+        const float r = rsqrtf(ss / (float)D + eps);
+        __syncthreads();
+        if (t < D)
+            vec[t] = x * r * bf16_to_f32(nw[t]);
+    }
+    __syncthreads();
+    const int half = D / 2;
+    float out = 0.0f;
+    if (t < D) {
+        const int i = t < half ? t : t - half;
+        const float c = cs[i], s = sn[i];
+        out = t < half ? vec[t] * c - vec[t + half] * s : vec[t] * c + vec[t - half] * s;
+    }
+    __syncthreads();
+    if (t < D)
+        vec[t] = out;
+    __syncthreads();
+}
+
+struct AttnArgs {
+    const float *q;        // [Hq * D] this step's query (GEMV output)
+    const float *k;        // [Hkv * D] this step's key
+    const float *v;        // [Hkv * D] this step's value
+    const uint16_t *qn_w;  // [D] bf16 q RMSNorm weight, or null
+    const uint16_t *kn_w;  // [D] bf16 k RMSNorm weight, or null
+    float qk_eps;
+    uint16_t *kcache;      // [Hkv][max_pos][D] bf16
+    uint16_t *vcache;      // [Hkv][max_pos][D] bf16
+    const float *cos_t;    // [max_pos][D / 2]
+    const float *sin_t;
+    const int *state;      // state[0] = position of this step's token
+    float *part;           // [Hq][max_chunks][D + 2]
+    int *counters;         // [Hq], zero between launches
+    uint16_t *out;         // [Hq * D] bf16
+    int Hq, Hkv, D, max_pos;
+    float scale;
+};
+
+// Grid (Hq, max_pos / kChunk); 256 threads.  Workgroup (h, c) attends query
+// head h over positions [c * 64, c * 64 + 64) ∩ [0, pos]; the last chunk
+// also holds this step's key/value, which the first query head of the
+// group writes to the cache.  Other workgroups never read cache row `pos`,
+// so there is no write/read race on it.
+__global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
+{
+    __shared__ float qs[kMaxD], kn[kMaxD], vn[kMaxD];
+    __shared__ float sc[kChunk];
+    __shared__ float scratch[8];
+    __shared__ float opart[16][kMaxD];
+    __shared__ int s_last;
+
+    const int h = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+    const int D = a.D, pos = a.state[0];
+    if (pos < 0 || pos >= a.max_pos)  // past the cache: nothing to do
+        return;
+    const int nact = pos / kChunk + 1;
+    if (c >= nact)
+        return;
+    const int group = a.Hq / a.Hkv;
+    const int kvh = h / group;
+    const int t0 = c * kChunk;
+    const int t1 = min(t0 + kChunk, pos + 1);
+    const float *cs = a.cos_t + (int64_t)pos * (D / 2);
+    const float *sn = a.sin_t + (int64_t)pos * (D / 2);
+
+    if (t < D)
+        qs[t] = a.q[h * D + t];
+    norm_rope(qs, a.qn_w, a.qk_eps, cs, sn, D, scratch);
+    const bool has_new = (c == nact - 1);
+    if (has_new) {
+        if (t < D) {
+            kn[t] = a.k[kvh * D + t];
+            vn[t] = bf16_round(a.v[kvh * D + t]);
+        }
+        norm_rope(kn, a.kn_w, a.qk_eps, cs, sn, D, scratch);
+        if (t < D) {
+            const float kr = bf16_round(kn[t]);
+            kn[t] = kr;
+            if (h % group == 0) {
+                const int64_t row = ((int64_t)kvh * a.max_pos + pos) * D + t;
+                a.kcache[row] = f32_to_bf16(kr);
+                a.vcache[row] = f32_to_bf16(vn[t]);
+            }
+        }
+        __syncthreads();
+    }
+
+    // scores: 4 threads per position, D/4 dims each
+    {
+        const int tl = t >> 2, part = t & 3;
+        const int tp = t0 + tl;
+        float s = 0.0f;
+        if (tp < t1) {
+            const int dn = D / 4, d0 = part * dn;
+            if (tp == pos) {
+                for (int d = d0; d < d0 + dn; ++d)
+                    s = fmaf(qs[d], kn[d], s);
+            } else {
+                const uint16_t *kr = a.kcache + ((int64_t)kvh * a.max_pos + tp) * D + d0;
+                for (int d = 0; d < dn; d += 8) {
+                    const u32x4_t w = *(const u32x4_t *)(kr + d);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        s = fmaf(qs[d0 + d + 2 * e], __uint_as_float(w[e] << 16), s);
+                        s = fmaf(qs[d0 + d + 2 * e + 1], __uint_as_float(w[e] & 0xffff0000u), s);
+                    }
+                }
+            }
+        }
+        s += __shfl_xor(s, 1, 4);
+        s += __shfl_xor(s, 2, 4);
+        if (part == 0)
+            sc[tl] = tp < t1 ? s * a.scale : -INFINITY;
+    }
+    __syncthreads();
+    // chunk max / exp / sum (wave 0)
+    if (t < 64) {
+        const float s = sc[t];
+        const float m = wave_max(s);
+        const float p = t0 + t < t1 ? __expf(s - m) : 0.0f;
+        const float l = wave_sum(p);
+        sc[t] = p;
+        if (t == 0) {
+            scratch[4] = m;
+            scratch[5] = l;
+        }
+    }
+    __syncthreads();
+    // o[d] = sum_t p[t] v[t][d]: 16 position groups x 16 eight-dim slices,
+    // one 16-byte load per (position, slice), then a fixed-order sum over
+    // the position groups.
+    {
+        const int dc = t & 15, pg = t >> 4;
+        float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (dc * 8 < D) {
+            for (int tl = pg; t0 + tl < t1; tl += 16) {
+                const int tp = t0 + tl;
+                const float p = sc[tl];
+                if (tp == pos) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        o[e] = fmaf(p, vn[dc * 8 + e], o[e]);
+                } else {
+                    const u32x4_t w = *(const u32x4_t *)(a.vcache +
+                                                         ((int64_t)kvh * a.max_pos + tp) * D + dc * 8);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        o[2 * e] = fmaf(p, __uint_as_float(w[e] << 16), o[2 * e]);
+                        o[2 * e + 1] = fmaf(p, __uint_as_float(w[e] & 0xffff0000u), o[2 * e + 1]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                opart[pg][dc * 8 + e] = o[e];
+        }
+    }
+    __syncthreads();
+    if (t < D) {
+        float acc = 0.0f;
+        for (int g = 0; g < 16; ++g)
+            acc += opart[g][t];
+        opart[0][t] = acc;
+    }
+    __syncthreads();
+    float *pp = a.part + ((int64_t)h * (a.max_pos / kChunk) + c) * (D + 2);
+    if (t < D)
+        pp[2 + t] = opart[0][t];
+    if (t == 0) {
+        pp[0] = scratch[4];
+        pp[1] = scratch[5];
+    }
+    // publish, then the last chunk to arrive combines
+    __threadfence();
+    __syncthreads();
+    if (t == 0)
+        s_last = atomicAdd(&a.counters[h], 1) == nact - 1;
+    __syncthreads();
+    if (!s_last)
+        return;
+    __threadfence();
+    const float *base = a.part + (int64_t)h * (a.max_pos / kChunk) * (D + 2);
+    float M = -INFINITY;
+    for (int j = 0; j < nact; ++j)
+        M = fmaxf(M, __builtin_nontemporal_load(base + (int64_t)j * (D + 2)));
+    float L = 0.0f, o = 0.0f;
+    for (int j = 0; j < nact; ++j) {
+        const float *pj = base + (int64_t)j * (D + 2);
+        const float w = __expf(__builtin_nontemporal_load(pj) - M);
+        L = fmaf(__builtin_nontemporal_load(pj + 1), w, L);
+        if (t < D)
+            o = fmaf(__builtin_nontemporal_load(pj + 2 + t), w, o);
+    }
+    if (t < D)
+        a.out[h * D + t] = f32_to_bf16(o / L);
+    if (t == 0)
+        atomicExch(&a.counters[h], 0);
+}
+
+struct HeadArgs {
+    float *h;                // [H] residual (read: final norm input; written: next embedding)
+    const uint16_t *norm_w;  // [H] bf16
+    float eps;
+    const uint16_t *W;       // [V][H] bf16 lm_head
+    float *logits;           // [V] or null
+    int V, H;
+    float *part_val;         // [grid]
+    int *part_idx;           // [grid]
+    int *counter;            // [1], zero between launches
+    int *state;              // [0] pos, [1] token
+    const int *prompt;       // [n_prompt]
+    int n_prompt;
+    int *tokens;             // [max_pos + 1]: tokens[p] = token at position p
+    int *argmax_out;         // [max_pos]: greedy choice after position p
+    const uint16_t *embed;   // [V][H] bf16
+    int max_pos;
+};
+
+constexpr int kHeadPerLane = 64;  // bf16 activations per lane: H <= 4096
+constexpr int kHeadRows = 4;      // rows in flight per wave
+
+template <int CTRL>
+EP_DEV float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of each DPP row, in every lane of the row.
+EP_DEV float row16_sum_dpp(float v)
+{
+    v += dpp_f<0x128>(v);  // row_ror 8
+    v += dpp_f<0x124>(v);  // row_ror 4
+    v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
+    return v;
+}
+
+// lm_head GEMV with the final RMSNorm fused in front and greedy selection
+// behind.  Each wave holds the normalized activation (bf16, as the
+// reference's bf16 model feeds its lm_head) in registers and streams whole
+// rows with 16-byte loads, four rows in flight.
+__global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
+{
+    __shared__ float wv[4];
+    __shared__ int wi[4];
+    __shared__ float ssq_s[4];
+    __shared__ int s_last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.H;
+    const int nld = H / 512;  // 16-byte loads per lane per row
+
+    // RMSNorm of the residual: every wave needs the full row
+    float ss = 0.0f;
+    for (int k = threadIdx.x; k < H; k += 256) {
+        const float v = a.h[k];
+        ss = fmaf(v, v, ss);
+    }
+    ss = wave_sum(ss);
+    if (lane == 0)
+        ssq_s[wave] = ss;
+    __syncthreads();
+    const float rinv = rsqrtf((ssq_s[0] + ssq_s[1] + ssq_s[2] + ssq_s[3]) / (float)H + a.eps);
+
+    bf16x2_t x[kHeadPerLane / 2];
+#pragma unroll
+    for (int i = 0; i < kHeadPerLane / 8; ++i) {
+        if (i < nld) {
+            const int k0 = (lane + 64 * i) * 8;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float v0 = bf16_round(a.h[k0 + 2 * e] * rinv) * bf16_to_f32(a.norm_w[k0 + 2 * e]);
+                const float v1 =
+                    bf16_round(a.h[k0 + 2 * e + 1] * rinv) * bf16_to_f32(a.norm_w[k0 + 2 * e + 1]);
+                x[4 * i + e] = (bf16x2_t){(__bf16)v0, (__bf16)v1};
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                x[4 * i + e] = (bf16x2_t){(__bf16)0.0f, (__bf16)0.0f};
+        }
+    }
+
+    const int gw = blockIdx.x * 4 + wave, nw = gridDim.x * 4;
+    float best = -INFINITY;
+    int besti = 0x7fffffff;
+    for (int rb = gw; rb < a.V; rb += kHeadRows * nw) {
+        u32x4_t w[kHeadRows][kHeadPerLane / 8];
+        int rows[kHeadRows];
+#pragma unroll
+        for (int q = 0; q < kHeadRows; ++q) {
+            const int r = rb + q * nw;
+            rows[q] = r;
+            const int rs = r < a.V ? r : rb;
+#pragma unroll
+            for (int i = 0; i < kHeadPerLane / 8; ++i)
+                if (i < nld)
+                    w[q][i] = __builtin_nontemporal_load(
+                        (const u32x4_t *)(a.W + (int64_t)rs * H + (lane + 64 * i) * 8));
+        }
+#pragma unroll
+        for (int q = 0; q < kHeadRows; ++q) {
+            float sacc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < kHeadPerLane / 8; ++i)
+                if (i < nld) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        sacc = __builtin_amdgcn_fdot2_f32_bf16(
+                            __builtin_bit_cast(bf16x2_t, w[q][i][e]), x[4 * i + e], sacc, false);
+                }
+            // 16-lane rows by DPP, then the four row sums through readlane
+            sacc = row16_sum_dpp(sacc);
+            const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sacc), 0)) +
+                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sacc), 16)) +
+                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sacc), 32)) +
+                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sacc), 48));
+            const int r = rows[q];
+            if (r < a.V) {
+                if (a.logits && lane == 0)
+                    a.logits[r] = tot;
+                if (tot > best || (tot == best && r < besti)) {
+                    best = tot;
+                    besti = r;
+                }
+            }
+        }
+    }
+    if (lane == 0) {
+        wv[wave] = best;
+        wi[wave] = besti;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = wv[0];
+        int bi = wi[0];
+        for (int w = 1; w < 4; ++w)
+            if (wv[w] > b || (wv[w] == b && wi[w] < bi)) {
+                b = wv[w];
+                bi = wi[w];
+            }
+        a.part_val[blockIdx.x] = b;
+        a.part_idx[blockIdx.x] = bi;
+        __threadfence();
+        s_last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!s_last)
+        return;
+    __threadfence();
+    // last workgroup: global argmax, next token, next embedding
+    float b = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int j = threadIdx.x; j < (int)gridDim.x; j += 256) {
+        const float v = __builtin_nontemporal_load(a.part_val + j);
+        const int i = __builtin_nontemporal_load(a.part_idx + j);
+        if (v > b || (v == b && i < bi)) {
+            b = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(b, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (ov > b || (ov == b && oi < bi)) {
+            b = ov;
+            bi = oi;
+        }
+    }
+    if (lane == 0) {
+        wv[wave] = b;
+        wi[wave] = bi;
+    }
+    __syncthreads();
+    __shared__ int s_next;
+    if (threadIdx.x == 0) {
+        float bb = wv[0];
+        int bbi = wi[0];
+        for (int w = 1; w < 4; ++w)
+            if (wv[w] > bb || (wv[w] == bb && wi[w] < bbi)) {
+                bb = wv[w];
+                bbi = wi[w];
+            }
+        const int pos = a.state[0];
+        const int next = pos + 1 < a.n_prompt ? a.prompt[pos + 1] : bbi;
+        if (pos < a.max_pos) {
+            a.argmax_out[pos] = bbi;
+            a.tokens[pos + 1] = next;
+        }
+        a.state[0] = pos + 1;
+        a.state[1] = next;
+        s_next = next;
+        atomicExch(a.counter, 0);
+    }
+    __syncthreads();
+    const int next = s_next;
+    for (int k = threadIdx.x; k < H; k += 256)
+        a.h[k] = bf16_to_f32(a.embed[(int64_t)next * H + k]);
+}
+
+// h = embed[state[1]] (the first step's input).
+__global__ void __launch_bounds__(256) embed_kernel(const uint16_t *embed, const int *state,
+                                                   float *h, int H)
+{
+    const int tok = state[1];
+    for (int k = threadIdx.x; k < H; k += 256)
+        h[k] = bf16_to_f32(embed[(int64_t)tok * H + k]);
+}
+
+}  // namespace
+
+int launch_attention(const AttnDesc &d, hipStream_t stream)
+{
+    if (d.D > kMaxD || d.D % 8 != 0 || d.Hq % d.Hkv != 0 || d.max_pos % kChunk != 0)
+        return set_error(EP_DECLINE_SHAPE, "attention: head_dim %d / heads %d,%d / max_pos %d",
+                         d.D, d.Hq, d.Hkv, d.max_pos);
+    AttnArgs a{d.q, d.k, d.v, d.qn_w, d.kn_w, d.qk_eps, d.kcache, d.vcache, d.cos_t, d.sin_t,
+               d.state, d.part, d.counters, d.out, d.Hq, d.Hkv, d.D, d.max_pos, d.scale};
+    hipLaunchKernelGGL(attention_kernel, dim3(d.Hq, d.max_pos / kChunk), dim3(256), 0, stream, a);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+size_t attention_workspace(int Hq, int D, int max_pos)
+{
+    return (size_t)Hq * (max_pos / kChunk) * (D + 2) * sizeof(float);
+}
+
+int launch_lm_head(const HeadDesc &d, hipStream_t stream)
+{
+    if (d.H % 512 != 0 || d.H > 64 * kHeadPerLane)
+        return set_error(EP_DECLINE_SHAPE, "lm_head: hidden %d must be a multiple of 512, <= %d",
+                         d.H, 64 * kHeadPerLane);
+    if (d.grid < 1 || d.grid > 65535)
+        return set_error(EP_ERR_ARG, "lm_head: grid %d", d.grid);
+    HeadArgs a{d.h, d.norm_w, d.eps, d.W, d.logits, d.V, d.H, d.part_val, d.part_idx,
+               d.counter, d.state, d.prompt, d.n_prompt, d.tokens, d.argmax_out, d.embed,
+               d.max_pos};
+    hipLaunchKernelGGL(lm_head_kernel, dim3(d.grid), dim3(256), 0, stream, a);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+int launch_embed(const uint16_t *embed, const int *state, float *h, int H, hipStream_t stream)
+{
+    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, stream, embed, state, h, H);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+}  // namespace ep

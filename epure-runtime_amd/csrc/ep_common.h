@@ -52,11 +52,12 @@ EP_DEV void store_from_f32(void *p, int dt, int64_t i, float v)
         ((uint16_t *)p)[i] = f32_to_bf16(v);
 }
 
-// Exponent e such that |x| * 2^-e <= 2^14 for the largest |x| of a row
-// (amax), so every element converts to fp16 without overflow; e is also
-// chosen >= -24 so tiny rows are lifted into the normal fp16 range.  2^-e
-// and 2^e are exact, so rescaling changes no bf16 value and the result is
-// multiplied back by 2^e exactly.  Returns 0 for amax == 0 or non-finite.
+// Exponent e such that 2^13 <= amax * 2^-e < 2^14 for the largest |x| of a
+// row (amax): every element converts to fp16 without overflow and rows of
+// tiny values are lifted into the normal fp16 range.  2^-e and 2^e are
+// exact (e is clamped to [-110, 110], inside float32's normal range), so
+// rescaling changes no bf16 value and the result is scaled back exactly.
+// Returns 0 for amax == 0 or non-finite.
 EP_DEV int row_exponent(float amax)
 {
     if (!(amax > 0.0f) || amax > 3.0e38f)
@@ -64,10 +65,10 @@ EP_DEV int row_exponent(float amax)
     int e;
     frexpf(amax, &e);      // amax = f * 2^e, f in [0.5, 1)  ->  amax < 2^e
     int s = e - 14;        // amax * 2^-s < 2^14
-    if (s < -24)
-        s = -24;
-    if (s > 100)
-        s = 100;
+    if (s < -110)
+        s = -110;
+    if (s > 110)
+        s = 110;
     return s;
 }
 

@@ -34,6 +34,10 @@ struct OutDesc {
     int accumulate;
 };
 
+// Compute units of the current device (queried once, at library load or
+// first use; never inside a stream capture after ep_hip_available()).
+int device_cus();
+
 // Sets the calling thread's error message; returns `code`.
 int set_error(int code, const char *fmt, ...);
 
@@ -43,6 +47,68 @@ int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc 
 int launch_gemv_generic(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,
                         hipStream_t stream);
 bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M);
+
+// Decode-step GEMV: M = 1, up to three weights sharing K (fused q/k/v or
+// gate/up), activation taken from a fused prologue.
+struct FusedSeg {
+    const uint8_t *packed;
+    const void *scale;
+    const void *cb;
+    void *y;
+    int64_t N;
+};
+struct FusedGemv {
+    int xsrc;  // 0 plain x (x_dtype), 1 rmsnorm(h f32, w bf16), 2 silu(g) * u (f32)
+    const void *x;
+    int x_dtype;
+    const void *x2;
+    float eps;
+    int64_t K;
+    int group, levels, scale_dtype, cb_dtype, y_dtype, accumulate;
+    int nseg;
+    FusedSeg seg[3];
+};
+int launch_gemv_fused(const FusedGemv &f, hipStream_t stream);
+
+// Decode attention over a bf16 KV cache (decode.hip).
+struct AttnDesc {
+    const float *q, *k, *v;
+    const uint16_t *qn_w, *kn_w;
+    float qk_eps;
+    uint16_t *kcache, *vcache;
+    const float *cos_t, *sin_t;
+    const int *state;
+    float *part;
+    int *counters;
+    uint16_t *out;
+    int Hq, Hkv, D, max_pos;
+    float scale;
+};
+int launch_attention(const AttnDesc &d, hipStream_t stream);
+size_t attention_workspace(int Hq, int D, int max_pos);
+
+// lm_head + final norm + greedy selection + next embedding (decode.hip).
+struct HeadDesc {
+    float *h;
+    const uint16_t *norm_w;
+    float eps;
+    const uint16_t *W;
+    float *logits;
+    int V, H;
+    float *part_val;
+    int *part_idx;
+    int *counter;
+    int *state;
+    const int *prompt;
+    int n_prompt;
+    int *tokens;
+    int *argmax_out;
+    const uint16_t *embed;
+    int max_pos;
+    int grid;
+};
+int launch_lm_head(const HeadDesc &d, hipStream_t stream);
+int launch_embed(const uint16_t *embed, const int *state, float *h, int H, hipStream_t stream);
 
 int launch_mfma(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,
                 void *ws, size_t ws_bytes, hipStream_t stream);

@@ -41,44 +41,58 @@ namespace {
 constexpr int kRepl = 64;                // table replicas (one per lane)
 constexpr int kTabDwords = 256 * kRepl;  // 64 KiB
 constexpr int kSlabBytes = 256;          // bytes of a row covered by 16 lanes
-constexpr int kMaxWaves = 16;
+constexpr int kMaxWaves = 8;   // 512 threads: up to 256 VGPRs per lane
+constexpr int kMaxSeg = 3;
+
+// Where the activation row comes from (template XS).
+constexpr int XS_PLAIN = 0;    // x[m, k] in x_dtype
+constexpr int XS_RMSNORM = 1;  // x = rmsnorm(h) * w: h f32 [K] (x), w bf16 [K] (x2), eps
+constexpr int XS_SWIGLU = 2;   // x = silu(g) * u: g f32 [K] (x), u f32 [K] (x2)
+
+// One weight sharing K / group / levels / dtypes with the others of a launch
+// (e.g. q, k and v of one layer); workgroups [wg_begin, wg_end) serve it.
+struct Seg {
+    const uint8_t *packed;
+    const void *scale;
+    const void *cb;
+    void *y;
+    int N;
+    int wg_begin, wg_end;
+};
 
 struct GemvArgs {
     const void *x;
     int x_dtype;
     int64_t ldx;
     int M;
-    const uint8_t *packed;
+    const void *x2;
+    float eps;
     int64_t row_bytes;
-    const void *scale;
     int scale_dtype;
     int64_t lds;
-    const void *cb;
     int cb_dtype;
     int levels;
-    void *y;
     int y_dtype;
     int64_t ldy;
     int accumulate;
-    int N;
     int64_t K;
     int group;
+    int nseg;
+    Seg seg[kMaxSeg];
 };
 
+// Pair table from the codebook's fp16 bits staged in LDS (cb16[l] = 0 for
+// l >= levels, matching the Rust LUT's zeros).
 template <int BITS>
-EP_DEV void build_table(uint32_t *tab, const void *cb, int cb_dtype, int levels)
+EP_DEV void build_table(uint32_t *tab, const uint16_t *cb16)
 {
     for (int e4 = threadIdx.x; e4 < kTabDwords / 4; e4 += blockDim.x) {
         const int b = (e4 * 4) / kRepl;
         uint32_t v;
         if constexpr (BITS == 4) {
-            const int lo = b & 15, hi = b >> 4;
-            const float clo = lo < levels ? load_as_f32(cb, cb_dtype, lo) : 0.0f;
-            const float chi = hi < levels ? load_as_f32(cb, cb_dtype, hi) : 0.0f;
-            v = (uint32_t)f16_bits((f16_t)clo) | ((uint32_t)f16_bits((f16_t)chi) << 16);
+            v = (uint32_t)cb16[b & 15] | ((uint32_t)cb16[b >> 4] << 16);
         } else {
-            const float c = b < levels ? load_as_f32(cb, cb_dtype, b) : 0.0f;
-            const uint32_t h = f16_bits((f16_t)c);
+            const uint32_t h = cb16[b];
             v = h | (h << 16);
         }
         ((u32x4_t *)tab)[e4] = (u32x4_t){v, v, v, v};
@@ -95,21 +109,27 @@ EP_DEV uint32_t lds_read_u32(const uint32_t *base, uint32_t byte_addr)
     return *(const uint32_t *)((const char *)base + byte_addr);
 }
 
-// Sum over the 16 lanes of a DPP row (lanes 16r..16r+15).
+template <int CTRL>
+EP_DEV float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a DPP row (lanes 16r..16r+15), in every lane:
+// row_ror 8, row_ror 4, quad_perm [2,3,0,1], quad_perm [1,0,3,2].
 EP_DEV float row16_sum(float v)
 {
-    v += __shfl_xor(v, 8, 16);
-    v += __shfl_xor(v, 4, 16);
-    v += __shfl_xor(v, 2, 16);
-    v += __shfl_xor(v, 1, 16);
+    v += dpp_f<0x128>(v);
+    v += dpp_f<0x124>(v);
+    v += dpp_f<0x4e>(v);
+    v += dpp_f<0xb1>(v);
     return v;
 }
 
-// Two raw 16-bit activations (bf16 or fp16, per XDT) -> scaled fp16 pair.
+// Two raw 16-bit activations (bf16 or fp16, per XDT) -> floats.
 template <int XDT>
-EP_DEV f16x2_t cvt_pair(uint32_t raw, float pw)
+EP_DEV void unpack_pair(uint32_t raw, float &lo, float &hi)
 {
-    float lo, hi;
     if constexpr (XDT == EP_BF16) {
         lo = __uint_as_float(raw << 16);
         hi = __uint_as_float(raw & 0xffff0000u);
@@ -117,35 +137,30 @@ EP_DEV f16x2_t cvt_pair(uint32_t raw, float pw)
         lo = (float)f16_from_bits((uint16_t)(raw & 0xffffu));
         hi = (float)f16_from_bits((uint16_t)(raw >> 16));
     }
-    return (f16x2_t){(f16_t)(lo * pw), (f16_t)(hi * pw)};
 }
 
-template <int XDT>
-EP_DEV float pair_amax(uint32_t raw)
+// silu(g) * u with the hardware reciprocal (about 1 ulp; the result is
+// rounded to fp16 right after, so a correctly rounded divide buys nothing).
+EP_DEV float silu_mul(float g, float u)
 {
-    float lo, hi;
-    if constexpr (XDT == EP_BF16) {
-        lo = __uint_as_float(raw << 16);
-        hi = __uint_as_float(raw & 0xffff0000u);
-    } else {
-        lo = (float)f16_from_bits((uint16_t)(raw & 0xffffu));
-        hi = (float)f16_from_bits((uint16_t)(raw >> 16));
-    }
-    return fmaxf(fabsf(lo), fabsf(hi));
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
-template <int BITS, int MT, int RQ, int SPW, int XDT>
-__global__ void __launch_bounds__(1024) gemv_lut_kernel(GemvArgs a)
+template <int BITS, int MT, int RQ, int SPW, int XDT, int XS, bool DB>
+__global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
 {
     constexpr int PAIRS = BITS == 4 ? 16 : 8;  // weight pairs per 16-byte chunk
+    constexpr int KPC = 2 * PAIRS;              // k values per chunk
     constexpr int ROWS = 4 * RQ;                // rows per block
+    static_assert(XS == XS_PLAIN || MT == 1, "fused activation sources serve M = 1");
 
     // Static LDS: the table sits at a compile-time address, so a lookup is
     // one v_perm for the address and the base folds into ds_read's offset.
     __shared__ __align__(16) uint32_t tab[kTabDwords];
     __shared__ float red[kMaxWaves * ROWS * MT];   // [W][ROWS][MT]
-    __shared__ float s_amax[kMaxWaves * MT];       // [W][MT]
-    __shared__ int s_exp[MT];
+    __shared__ float s_part[kMaxWaves];            // sum-of-squares partials
+    __shared__ uint16_t s_cb[256];                 // codebook as fp16 bits
+    __shared__ float s_rinv;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int W = blockDim.x >> 6;
@@ -153,93 +168,202 @@ __global__ void __launch_bounds__(1024) gemv_lut_kernel(GemvArgs a)
     const int64_t KB = BITS == 4 ? a.K / 2 : a.K;
     const int S = (int)((KB + kSlabBytes - 1) / kSlabBytes);
 
-    // ---- stage this lane's activation chunks (raw) and their amax -------
-    f16x2_t xh[SPW][MT][PAIRS];
-    uint32_t xraw[SPW][MT][PAIRS];
-    float amax[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-        amax[m] = 0.0f;
+    // Segment of this workgroup; kept in scalar registers (readfirstlane)
+    // so every per-segment pointer below is uniform.
+    const int bid = (int)blockIdx.x;
+    const int si = __builtin_amdgcn_readfirstlane(
+        (a.nseg > 2 && bid >= a.seg[2].wg_begin) ? 2 : ((a.nseg > 1 && bid >= a.seg[1].wg_begin) ? 1 : 0));
+    const Seg &s0 = a.seg[0], &s1 = a.seg[1], &s2 = a.seg[2];
+    const uint8_t *packed = si == 0 ? s0.packed : (si == 1 ? s1.packed : s2.packed);
+    const void *scale = si == 0 ? s0.scale : (si == 1 ? s1.scale : s2.scale);
+    const void *cbp = si == 0 ? s0.cb : (si == 1 ? s1.cb : s2.cb);
+    void *yseg = si == 0 ? s0.y : (si == 1 ? s1.y : s2.y);
+    const int N = si == 0 ? s0.N : (si == 1 ? s1.N : s2.N);
+    const int wg_begin = si == 0 ? s0.wg_begin : (si == 1 ? s1.wg_begin : s2.wg_begin);
+    const int wg_end = si == 0 ? s0.wg_end : (si == 1 ? s1.wg_end : s2.wg_end);
+    const int nwg = wg_end - wg_begin;
+    const int nblk = (N + ROWS - 1) / ROWS;
+    int blk = bid - wg_begin;
+
+    // This lane's 16-byte chunk of each of its slabs (fixed for the kernel).
+    uint32_t cbyte[SPW];
+    bool act[SPW];
+    int gidx[SPW];
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
         const int s = wave + j * W;
-        const int64_t byte0 = (int64_t)s * kSlabBytes + c * 16;
-        const bool act = s < S && byte0 < KB;
-        const int64_t k0 = BITS == 4 ? byte0 * 2 : byte0;
+        const int64_t b0 = (int64_t)s * kSlabBytes + c * 16;
+        act[j] = s < S && b0 < KB;
+        cbyte[j] = act[j] ? (uint32_t)b0 : 0u;
+        const int64_t k0 = BITS == 4 ? b0 * 2 : b0;
+        gidx[j] = act[j] ? (int)(k0 / a.group) : 0;
+    }
+
+    // Issue the loads of one row block: all SPW x RQ 16-byte chunks and
+    // their scales, from clamped addresses (an out-of-range row reads row 0
+    // and is zeroed through its scale), so they go out back to back.
+    auto load_block = [&](int b, u32x4_t (&wq)[SPW][RQ], float (&sc)[SPW][RQ]) {
+        const int row0 = b * ROWS;
+        uint32_t soff[SPW][RQ];
+#pragma unroll
+        for (int j = 0; j < SPW; ++j)
+#pragma unroll
+            for (int q = 0; q < RQ; ++q) {
+                const int row = row0 + 4 * q + rq;
+                const uint32_t rs = row < N ? (uint32_t)row : 0u;
+                // 32-bit offsets: the host guarantees N * row_bytes < 2^31.
+                wq[j][q] = __builtin_nontemporal_load(
+                    (const u32x4_t *)(packed + (rs * (uint32_t)a.row_bytes + cbyte[j])));
+                soff[j][q] = rs * (uint32_t)a.lds + (uint32_t)gidx[j];
+            }
+        if (a.scale_dtype == EP_F16) {
+#pragma unroll
+            for (int j = 0; j < SPW; ++j)
+#pragma unroll
+                for (int q = 0; q < RQ; ++q)
+                    sc[j][q] = (float)((const f16_t *)scale)[soff[j][q]];
+        } else if (a.scale_dtype == EP_F32) {
+#pragma unroll
+            for (int j = 0; j < SPW; ++j)
+#pragma unroll
+                for (int q = 0; q < RQ; ++q)
+                    sc[j][q] = ((const float *)scale)[soff[j][q]];
+        } else {
+#pragma unroll
+            for (int j = 0; j < SPW; ++j)
+#pragma unroll
+                for (int q = 0; q < RQ; ++q)
+                    sc[j][q] = bf16_to_f32(((const uint16_t *)scale)[soff[j][q]]);
+        }
+#pragma unroll
+        for (int j = 0; j < SPW; ++j)
+#pragma unroll
+            for (int q = 0; q < RQ; ++q)
+                if (!act[j] || row0 + 4 * q + rq >= N)
+                    sc[j][q] = 0.0f;
+    };
+
+    u32x4_t wqA[SPW][RQ], wqB[SPW][RQ];
+    float scA[SPW][RQ], scB[SPW][RQ];
+    if (blk < nblk)
+        load_block(blk, wqA, scA);  // in flight while the table and x are staged
+
+    // ---- stage activations ----------------------------------------------
+    // Each lane converts its own chunk(s) of the activation row to fp16
+    // after an exact power-of-two rescale chosen from that chunk's largest
+    // value; the factor 2^e is folded into the group scale of the chunk's
+    // partial sums, so no cross-lane agreement (and no second pass) is
+    // needed.  RMSNorm's 1/rms is a scalar and is applied to the finished
+    // dot products; its sum of squares is reduced behind the table build.
+    f16x2_t xh[SPW][MT][PAIRS];
+    float fexp[SPW][MT];
+    float ssq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+        // Loads are unconditional from clamped addresses (an idle lane reads
+        // element 0 and zeroes it), keeping each slab straight-line code.
+        const int64_t k0 = act[j] ? (BITS == 4 ? (int64_t)cbyte[j] * 2 : cbyte[j]) : 0;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            const bool live = act && m < a.M;
-            if constexpr (XDT == EP_F32) {
-                const float *xp = (const float *)a.x + (int64_t)m * a.ldx + k0;
+            const bool live = act[j] && m < a.M;
+            const int mm = m < a.M ? m : 0;
+            float v[KPC];
+            if constexpr (XS == XS_RMSNORM) {
+                const float *hp = (const float *)a.x + k0;
+                const uint16_t *wp = (const uint16_t *)a.x2 + k0;
 #pragma unroll
-                for (int p = 0; p < PAIRS; p += 2) {
-                    f32x4_t v = live ? *(const f32x4_t *)(xp + 2 * p) : (f32x4_t){0, 0, 0, 0};
-                    amax[m] = fmaxf(amax[m], fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])),
-                                                   fmaxf(fabsf(v[2]), fabsf(v[3]))));
-                }
-            } else {
-                const uint16_t *xp = (const uint16_t *)a.x + (int64_t)m * a.ldx + k0;
-#pragma unroll
-                for (int p = 0; p < PAIRS; p += 4) {
-                    u32x4_t v = live ? *(const u32x4_t *)(xp + 2 * p) : (u32x4_t){0, 0, 0, 0};
+                for (int p = 0; p < KPC; p += 8) {
+                    const f32x4_t h0 = *(const f32x4_t *)(hp + p);
+                    const f32x4_t h1 = *(const f32x4_t *)(hp + p + 4);
+                    const u32x4_t wv = *(const u32x4_t *)(wp + p);
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        xraw[j][m][p + t] = v[t];
-                        amax[m] = fmaxf(amax[m], pair_amax<XDT>(v[t]));
+                        float w0, w1;
+                        unpack_pair<EP_BF16>(wv[t], w0, w1);
+                        const float x0 = live ? (t < 2 ? h0[2 * t] : h1[2 * t - 4]) : 0.0f;
+                        const float x1 = live ? (t < 2 ? h0[2 * t + 1] : h1[2 * t - 3]) : 0.0f;
+                        ssq = fmaf(x0, x0, fmaf(x1, x1, ssq));
+                        v[p + 2 * t] = x0 * w0;
+                        v[p + 2 * t + 1] = x1 * w1;
+                    }
+                }
+            } else if constexpr (XS == XS_SWIGLU) {
+                const float *gp = (const float *)a.x + k0;
+                const float *up = (const float *)a.x2 + k0;
+#pragma unroll
+                for (int p = 0; p < KPC; p += 4) {
+                    const f32x4_t g = *(const f32x4_t *)(gp + p);
+                    const f32x4_t u = *(const f32x4_t *)(up + p);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        v[p + t] = live ? silu_mul(g[t], u[t]) : 0.0f;
+                }
+            } else if constexpr (XDT == EP_F32) {
+                const float *xp = (const float *)a.x + (int64_t)mm * a.ldx + k0;
+#pragma unroll
+                for (int p = 0; p < KPC; p += 4) {
+                    const f32x4_t t4 = *(const f32x4_t *)(xp + p);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        v[p + t] = live ? t4[t] : 0.0f;
+                }
+            } else {
+                const uint16_t *xp = (const uint16_t *)a.x + (int64_t)mm * a.ldx + k0;
+#pragma unroll
+                for (int p = 0; p < PAIRS; p += 4) {
+                    const u32x4_t t4 = *(const u32x4_t *)(xp + 2 * p);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        unpack_pair<XDT>(live ? t4[t] : 0u, v[2 * (p + t)], v[2 * (p + t) + 1]);
                     }
                 }
             }
+            float am = 0.0f;
+#pragma unroll
+            for (int t = 0; t < KPC; ++t)
+                am = fmaxf(am, fabsf(v[t]));
+            const int e = row_exponent(am);
+            const float pw = ldexpf(1.0f, -e);
+            fexp[j][m] = ldexpf(1.0f, e);
+#pragma unroll
+            for (int p = 0; p < PAIRS; ++p)
+                xh[j][m][p] = (f16x2_t){(f16_t)(v[2 * p] * pw), (f16_t)(v[2 * p + 1] * pw)};
         }
+        // keep one slab's loads live at a time (register pressure)
+        __builtin_amdgcn_sched_barrier(0);
     }
 
-    build_table<BITS>(tab, a.cb, a.cb_dtype, a.levels);
-
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        const float v = wave_max(amax[m]);
+    // codebook -> fp16 bits in LDS (one round trip), then the pair table
+    if (tid < 256)
+        s_cb[tid] = tid < a.levels ? f16_bits((f16_t)load_as_f32(cbp, a.cb_dtype, tid)) : 0;
+    if constexpr (XS == XS_RMSNORM) {
+        // The four row groups of a wave (lanes 16r..16r+15) hold the same
+        // activation chunks: count each element once.
+        const float v = wave_sum(rq == 0 ? ssq : 0.0f);
         if (lane == 0)
-            s_amax[wave * MT + m] = v;
+            s_part[wave] = v;
     }
     __syncthreads();
-    if (tid < MT) {
-        float v = 0.0f;
-        for (int w = 0; w < W; ++w)
-            v = fmaxf(v, s_amax[w * MT + tid]);
-        s_exp[tid] = row_exponent(v);
-    }
-    __syncthreads();
-
-    // ---- convert to scaled fp16 pairs ------------------------------------
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        const float pw = ldexpf(1.0f, -s_exp[m]);
-#pragma unroll
-        for (int j = 0; j < SPW; ++j) {
-            if constexpr (XDT == EP_F32) {
-                const int s = wave + j * W;
-                const int64_t byte0 = (int64_t)s * kSlabBytes + c * 16;
-                const bool live = s < S && byte0 < KB && m < a.M;
-                const int64_t k0 = BITS == 4 ? byte0 * 2 : byte0;
-                const float *xp = (const float *)a.x + (int64_t)m * a.ldx + k0;
-#pragma unroll
-                for (int p = 0; p < PAIRS; p += 2) {
-                    f32x4_t v = live ? *(const f32x4_t *)(xp + 2 * p) : (f32x4_t){0, 0, 0, 0};
-                    xh[j][m][p] = (f16x2_t){(f16_t)(v[0] * pw), (f16_t)(v[1] * pw)};
-                    xh[j][m][p + 1] = (f16x2_t){(f16_t)(v[2] * pw), (f16_t)(v[3] * pw)};
-                }
-            } else {
-#pragma unroll
-                for (int p = 0; p < PAIRS; ++p)
-                    xh[j][m][p] = cvt_pair<XDT>(xraw[j][m][p], pw);
-            }
+    build_table<BITS>(tab, s_cb);
+    if constexpr (XS == XS_RMSNORM) {
+        if (tid == 0) {
+            float q = 0.0f;
+            for (int w = 0; w < W; ++w)
+                q += s_part[w];
+            s_rinv = rsqrtf(q / (float)a.K + a.eps);
         }
     }
+    __syncthreads();
 
     const uint32_t lane4 = (uint32_t)lane << 2;
-    const int nblk = (a.N + ROWS - 1) / ROWS;
 
-    for (int blk = blockIdx.x; blk < nblk; blk += gridDim.x) {
-        const int row0 = blk * ROWS;
+    for (; blk < nblk; blk += nwg) {
+        const int nxt = blk + nwg;
+        if constexpr (DB) {
+            if (nxt < nblk)
+                load_block(nxt, wqB, scB);  // next block in flight during this one
+        }
+
         float acc[RQ][MT];
 #pragma unroll
         for (int q = 0; q < RQ; ++q)
@@ -248,47 +372,7 @@ __global__ void __launch_bounds__(1024) gemv_lut_kernel(GemvArgs a)
                 acc[q][m] = 0.0f;
 
 #pragma unroll
-        for (int j = 0; j < SPW; ++j) {
-            const int s = wave + j * W;
-            const int64_t byte0 = (int64_t)s * kSlabBytes + c * 16;
-            const bool act = s < S && byte0 < KB;
-            const int64_t k0 = BITS == 4 ? byte0 * 2 : byte0;
-            const int g = act ? (int)(k0 / a.group) : 0;
-
-            // Unconditional loads from clamped addresses (an out-of-range lane
-            // reads row 0 / byte 0 and is zeroed through its scale), so the
-            // compiler issues all RQ loads back to back.
-            const uint32_t bsafe = act ? (uint32_t)byte0 : 0u;
-            u32x4_t wq[RQ];
-            uint32_t soff[RQ];
-            float sc[RQ];
-#pragma unroll
-            for (int q = 0; q < RQ; ++q) {
-                const int row = row0 + 4 * q + rq;
-                const uint32_t rsafe = row < a.N ? (uint32_t)row : 0u;
-                // 32-bit offsets: the host guarantees N * row_bytes < 2^31.
-                wq[q] = __builtin_nontemporal_load(
-                    (const u32x4_t *)(a.packed + (rsafe * (uint32_t)a.row_bytes + bsafe)));
-                soff[q] = rsafe * (uint32_t)a.lds + (uint32_t)g;
-            }
-            if (a.scale_dtype == EP_F16) {
-#pragma unroll
-                for (int q = 0; q < RQ; ++q)
-                    sc[q] = (float)((const f16_t *)a.scale)[soff[q]];
-            } else if (a.scale_dtype == EP_F32) {
-#pragma unroll
-                for (int q = 0; q < RQ; ++q)
-                    sc[q] = ((const float *)a.scale)[soff[q]];
-            } else {
-#pragma unroll
-                for (int q = 0; q < RQ; ++q)
-                    sc[q] = bf16_to_f32(((const uint16_t *)a.scale)[soff[q]]);
-            }
-#pragma unroll
-            for (int q = 0; q < RQ; ++q)
-                if (!act || row0 + 4 * q + rq >= a.N)
-                    sc[q] = 0.0f;
-
+        for (int j = 0; j < SPW; ++j)
 #pragma unroll
             for (int q = 0; q < RQ; ++q) {
                 float part[MT];
@@ -297,12 +381,12 @@ __global__ void __launch_bounds__(1024) gemv_lut_kernel(GemvArgs a)
                     part[m] = 0.0f;
 #pragma unroll
                 for (int wd = 0; wd < 4; ++wd) {
-                    const uint32_t w = wq[q][wd];
+                    const uint32_t w = wqA[j][q][wd];
                     if constexpr (BITS == 4) {
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            const uint32_t ad = __builtin_amdgcn_perm(w, lane4, kSelByte[i]);
-                            const uint32_t t = lds_read_u32(tab, ad);
+                            const uint32_t t =
+                                lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[i]));
                             const f16x2_t wv = __builtin_bit_cast(f16x2_t, t);
 #pragma unroll
                             for (int m = 0; m < MT; ++m)
@@ -312,10 +396,10 @@ __global__ void __launch_bounds__(1024) gemv_lut_kernel(GemvArgs a)
                     } else {
 #pragma unroll
                         for (int p = 0; p < 2; ++p) {
-                            const uint32_t a0 = __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p]);
-                            const uint32_t a1 = __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p + 1]);
-                            const uint32_t t0 = lds_read_u32(tab, a0);
-                            const uint32_t t1 = lds_read_u32(tab, a1);
+                            const uint32_t t0 =
+                                lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p]));
+                            const uint32_t t1 = lds_read_u32(
+                                tab, __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p + 1]));
                             const uint32_t pr = __builtin_amdgcn_perm(t1, t0, 0x07060100u);
                             const f16x2_t wv = __builtin_bit_cast(f16x2_t, pr);
 #pragma unroll
@@ -327,10 +411,10 @@ __global__ void __launch_bounds__(1024) gemv_lut_kernel(GemvArgs a)
                 }
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
-                    acc[q][m] = fmaf(part[m], sc[q], acc[q][m]);
+                    acc[q][m] = fmaf(part[m], scA[j][q] * fexp[j][m], acc[q][m]);
             }
-        }
 
+        const int row0 = blk * ROWS;
 #pragma unroll
         for (int q = 0; q < RQ; ++q)
 #pragma unroll
@@ -343,18 +427,33 @@ __global__ void __launch_bounds__(1024) gemv_lut_kernel(GemvArgs a)
         for (int t = tid; t < ROWS * MT; t += blockDim.x) {
             const int r = t / MT, m = t % MT;
             const int row = row0 + r;
-            if (row < a.N && m < a.M) {
+            if (row < N && m < a.M) {
                 float v = 0.0f;
                 for (int w = 0; w < W; ++w)
                     v += red[(w * ROWS + r) * MT + m];
-                v = ldexpf(v, s_exp[m]);
+                if constexpr (XS == XS_RMSNORM)
+                    v *= s_rinv;
                 const int64_t off = (int64_t)m * a.ldy + row;
                 if (a.accumulate)
-                    v += load_as_f32(a.y, a.y_dtype, off);
-                store_from_f32(a.y, a.y_dtype, off, v);
+                    v += load_as_f32(yseg, a.y_dtype, off);
+                store_from_f32(yseg, a.y_dtype, off, v);
             }
         }
         __syncthreads();
+
+        if (nxt < nblk) {
+            if constexpr (DB) {
+#pragma unroll
+                for (int j = 0; j < SPW; ++j)
+#pragma unroll
+                    for (int q = 0; q < RQ; ++q) {
+                        wqA[j][q] = wqB[j][q];
+                        scA[j][q] = scB[j][q];
+                    }
+            } else {
+                load_block(nxt, wqA, scA);
+            }
+        }
     }
 }
 
@@ -364,18 +463,19 @@ __global__ void __launch_bounds__(1024) gemv_lut_kernel(GemvArgs a)
 __global__ void __launch_bounds__(256) gemv_generic_kernel(GemvArgs a)
 {
     const int lane = threadIdx.x & 63;
+    const Seg &sg = a.seg[0];
     const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= a.N)
+    if (row >= sg.N)
         return;
     const bool four = a.levels <= 16;
     for (int m = 0; m < a.M; ++m) {
         float acc = 0.0f;
         for (int64_t k = lane; k < a.K; k += 64) {
             const int64_t p = row * a.K + k;
-            const uint8_t byte = a.packed[four ? (p >> 1) : p];
+            const uint8_t byte = sg.packed[four ? (p >> 1) : p];
             const int idx = four ? ((p & 1) ? (byte >> 4) : (byte & 15)) : byte;
-            const float cbv = idx < a.levels ? load_as_f32(a.cb, a.cb_dtype, idx) : 0.0f;
-            const float w = cbv * load_as_f32(a.scale, a.scale_dtype, row * a.lds + k / a.group);
+            const float cbv = idx < a.levels ? load_as_f32(sg.cb, a.cb_dtype, idx) : 0.0f;
+            const float w = cbv * load_as_f32(sg.scale, a.scale_dtype, row * a.lds + k / a.group);
             acc = fmaf(load_as_f32(a.x, a.x_dtype, (int64_t)m * a.ldx + k), w, acc);
         }
         acc = wave_sum(acc);
@@ -383,33 +483,79 @@ __global__ void __launch_bounds__(256) gemv_generic_kernel(GemvArgs a)
             const int64_t off = (int64_t)m * a.ldy + row;
             float v = acc;
             if (a.accumulate)
-                v += load_as_f32(a.y, a.y_dtype, off);
-            store_from_f32(a.y, a.y_dtype, off, v);
+                v += load_as_f32(sg.y, a.y_dtype, off);
+            store_from_f32(sg.y, a.y_dtype, off, v);
         }
     }
 }
 
-template <int BITS, int MT, int RQ, int SPW, int XDT>
-int launch_lut(const GemvArgs &a, int waves, hipStream_t stream)
+// Row quads per block for a given number of slabs per wave: keeps the
+// 16-byte loads in flight per lane (SPW * RQ, double-buffered) at 8.
+constexpr int rq_for(int spw) { return spw >= 8 ? 1 : (spw >= 4 ? 2 : 4); }
+
+// Activation registers (SPW * MT * pairs-per-chunk) stay within 64 VGPRs,
+// and with several activation rows at most 4 chunk sets are live (the
+// variants beyond that spill).
+constexpr bool fits(int bits, int spw, int mt)
 {
-    constexpr int ROWS = 4 * RQ;
-    constexpr size_t smem = (size_t)kTabDwords * 4 + (size_t)kMaxWaves * ROWS * MT * 4 +
-                            (size_t)kMaxWaves * MT * 4 + (size_t)MT * 4;
-    auto kern = gemv_lut_kernel<BITS, MT, RQ, SPW, XDT>;
-    static int num_cu = 0;
-    if (num_cu == 0) {
-        int dev = 0;
-        EP_HIP_CHECK(hipGetDevice(&dev));
-        EP_HIP_CHECK(hipDeviceGetAttribute(&num_cu, hipDeviceAttributeMultiprocessorCount, dev));
+    return spw * mt * (bits == 4 ? 16 : 8) <= 64 && (mt == 1 || spw * mt <= 4);
+}
+
+// Splits the persistent grid across segments in proportion to their row
+// blocks (every segment gets at least one workgroup).
+void assign_workgroups(GemvArgs &a, int rows_per_block, int per_cu)
+{
+    int blocks[kMaxSeg] = {0, 0, 0};
+    int total = 0;
+    for (int i = 0; i < a.nseg; ++i) {
+        blocks[i] = (a.seg[i].N + rows_per_block - 1) / rows_per_block;
+        total += blocks[i];
     }
-    const int nblk = (a.N + ROWS - 1) / ROWS;
-    const int per_cu = 160 * 1024 / (int)smem;  // workgroups resident per CU by LDS
-    int grid = num_cu * (per_cu > 0 ? per_cu : 1);
-    if (grid > nblk)
-        grid = nblk;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(waves * 64), 0, stream, a);
-    EP_HIP_CHECK(hipGetLastError());
-    return EP_OK;
+    int grid = device_cus() * per_cu;
+    if (grid > total)
+        grid = total;
+    if (grid < a.nseg)
+        grid = a.nseg;
+    int begin = 0;
+    for (int i = 0; i < a.nseg; ++i) {
+        int share = (int)((int64_t)grid * blocks[i] / (total > 0 ? total : 1));
+        if (share < 1)
+            share = 1;
+        if (share > blocks[i] && blocks[i] > 0)
+            share = blocks[i];
+        if (i == a.nseg - 1 && begin + share < grid && grid - begin <= blocks[i])
+            share = grid - begin;
+        a.seg[i].wg_begin = begin;
+        a.seg[i].wg_end = begin + share;
+        begin += share;
+    }
+    for (int i = a.nseg; i < kMaxSeg; ++i)
+        a.seg[i].wg_begin = a.seg[i].wg_end = begin;
+}
+
+template <int BITS, int MT, int SPW, int XDT, int XS>
+int launch_lut(GemvArgs a, int waves, hipStream_t stream)
+{
+    if constexpr (!fits(BITS, SPW, MT)) {
+        return set_error(EP_DECLINE_SHAPE, "GEMV variant does not fit registers");
+    } else {
+        constexpr int RQ = rq_for(SPW);
+        assign_workgroups(a, 4 * RQ, 2);  // 2 workgroups per CU fit the 64 KiB tables
+        const int grid = a.seg[a.nseg - 1].wg_end;
+        // Double-buffer the next block's loads only when a workgroup has more
+        // than one block; otherwise the extra registers buy nothing.
+        bool multi = false;
+        for (int i = 0; i < a.nseg; ++i)
+            multi |= (a.seg[i].N + 4 * RQ - 1) / (4 * RQ) > a.seg[i].wg_end - a.seg[i].wg_begin;
+        if (multi)
+            hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, true>), dim3(grid),
+                               dim3(waves * 64), 0, stream, a);
+        else
+            hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, false>), dim3(grid),
+                               dim3(waves * 64), 0, stream, a);
+        EP_HIP_CHECK(hipGetLastError());
+        return EP_OK;
+    }
 }
 
 template <int BITS, int MT, int SPW>
@@ -417,11 +563,11 @@ int dispatch_xdt(const GemvArgs &a, int xdt, int waves, hipStream_t s)
 {
     switch (xdt) {
     case EP_BF16:
-        return launch_lut<BITS, MT, 4, SPW, EP_BF16>(a, waves, s);
+        return launch_lut<BITS, MT, SPW, EP_BF16, XS_PLAIN>(a, waves, s);
     case EP_F16:
-        return launch_lut<BITS, MT, 4, SPW, EP_F16>(a, waves, s);
+        return launch_lut<BITS, MT, SPW, EP_F16, XS_PLAIN>(a, waves, s);
     default:
-        return launch_lut<BITS, MT, 4, SPW, EP_F32>(a, waves, s);
+        return launch_lut<BITS, MT, SPW, EP_F32, XS_PLAIN>(a, waves, s);
     }
 }
 
@@ -433,33 +579,47 @@ int dispatch_spw(const GemvArgs &a, int xdt, int spw, int waves, hipStream_t s)
         return dispatch_xdt<BITS, MT, 1>(a, xdt, waves, s);
     case 2:
         return dispatch_xdt<BITS, MT, 2>(a, xdt, waves, s);
-    default:
+    case 4:
         return dispatch_xdt<BITS, MT, 4>(a, xdt, waves, s);
+    default:
+        return dispatch_xdt<BITS, MT, 8>(a, xdt, waves, s);
+    }
+}
+
+template <int BITS, int XS>
+int dispatch_fused(const GemvArgs &a, int spw, int waves, hipStream_t s)
+{
+    switch (spw) {
+    case 1:
+        return launch_lut<BITS, 1, 1, EP_F32, XS>(a, waves, s);
+    case 2:
+        return launch_lut<BITS, 1, 2, EP_F32, XS>(a, waves, s);
+    case 4:
+        return launch_lut<BITS, 1, 4, EP_F32, XS>(a, waves, s);
+    default:
+        return launch_lut<BITS, 1, 8, EP_F32, XS>(a, waves, s);
     }
 }
 
 GemvArgs make_args(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y)
 {
-    GemvArgs a;
+    GemvArgs a{};
     a.x = x.ptr;
     a.x_dtype = x.dtype;
     a.ldx = x.ld;
     a.M = (int)M;
-    a.packed = w.packed;
     a.row_bytes = w.bits() == 4 ? w.K / 2 : w.K;
-    a.scale = w.scale;
     a.scale_dtype = w.scale_dtype;
     a.lds = w.ld_scale;
-    a.cb = w.cb;
     a.cb_dtype = w.cb_dtype;
     a.levels = w.levels;
-    a.y = y.ptr;
     a.y_dtype = y.dtype;
     a.ldy = y.ld;
     a.accumulate = y.accumulate;
-    a.N = (int)w.N;
     a.K = w.K;
     a.group = w.group;
+    a.nseg = 1;
+    a.seg[0] = Seg{w.packed, w.scale, w.cb, y.ptr, (int)w.N, 0, 0};
     return a;
 }
 
@@ -475,17 +635,26 @@ void plan(int64_t KB, int &spw, int &waves)
         waves = 1;
 }
 
+bool shape_ok(int bits, int64_t N, int64_t K, int group, int64_t ld_scale)
+{
+    if (N < 1 || N > INT32_MAX || K < 1)
+        return false;
+    if (bits == 4 ? (K % 32 != 0 || group % 32 != 0) : (K % 16 != 0 || group % 16 != 0))
+        return false;
+    const int64_t rb = bits == 4 ? K / 2 : K;
+    if (N * rb >= ((int64_t)1 << 31) || N * ld_scale >= ((int64_t)1 << 31))
+        return false;
+    int spw, waves;
+    plan(rb, spw, waves);
+    return spw <= 8 && fits(bits, spw, 1);
+}
+
 }  // namespace
 
 bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
 {
     const int bits = w.bits();
-    if (M < 1 || M > 4 || w.N < 1 || w.N > INT32_MAX || w.K < 1)
-        return false;
-    const int64_t rb = bits == 4 ? w.K / 2 : w.K;
-    if (w.N * rb >= ((int64_t)1 << 31) || w.N * w.ld_scale >= ((int64_t)1 << 31))
-        return false;
-    if (bits == 4 ? (w.K % 32 != 0 || w.group % 32 != 0) : (w.K % 16 != 0 || w.group % 16 != 0))
+    if (M < 1 || M > 4 || !shape_ok(bits, w.N, w.K, w.group, w.ld_scale))
         return false;
     if (((uintptr_t)w.packed & 15) != 0)
         return false;
@@ -494,10 +663,8 @@ bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
         return false;
     int spw, waves;
     plan(bits == 4 ? w.K / 2 : w.K, spw, waves);
-    if (spw > 4)
-        return false;
     const int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);
-    return spw * mt <= 8;
+    return fits(bits, spw, mt);
 }
 
 int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,
@@ -535,6 +702,53 @@ int launch_gemv_generic(const PackedDesc &w, const ActDesc &x, int64_t M, const 
                        stream, a);
     EP_HIP_CHECK(hipGetLastError());
     return EP_OK;
+}
+
+int launch_gemv_fused(const FusedGemv &f, hipStream_t stream)
+{
+    if (f.nseg < 1 || f.nseg > kMaxSeg)
+        return set_error(EP_ERR_ARG, "fused GEMV: nseg=%d outside 1..%d", f.nseg, kMaxSeg);
+    if (f.xsrc != XS_RMSNORM && f.xsrc != XS_SWIGLU && f.xsrc != XS_PLAIN)
+        return set_error(EP_ERR_ARG, "fused GEMV: unknown activation source %d", f.xsrc);
+    const int bits = f.levels <= 16 ? 4 : 8;
+    GemvArgs a{};
+    a.x = f.x;
+    a.x_dtype = f.xsrc == XS_PLAIN ? f.x_dtype : EP_F32;
+    a.ldx = f.K;
+    a.M = 1;
+    a.x2 = f.x2;
+    a.eps = f.eps;
+    a.row_bytes = bits == 4 ? f.K / 2 : f.K;
+    a.scale_dtype = f.scale_dtype;
+    a.lds = (f.K + f.group - 1) / f.group;
+    a.cb_dtype = f.cb_dtype;
+    a.levels = f.levels;
+    a.y_dtype = f.y_dtype;
+    a.ldy = 0;
+    a.accumulate = f.accumulate;
+    a.K = f.K;
+    a.group = f.group;
+    a.nseg = f.nseg;
+    for (int i = 0; i < f.nseg; ++i) {
+        if (!shape_ok(bits, f.seg[i].N, f.K, f.group, a.lds))
+            return set_error(EP_DECLINE_SHAPE, "fused GEMV: segment %d shape not served", i);
+        if (((uintptr_t)f.seg[i].packed & 15) != 0)
+            return set_error(EP_DECLINE_SHAPE, "fused GEMV: packed not 16-byte aligned");
+        a.seg[i] = Seg{f.seg[i].packed, f.seg[i].scale, f.seg[i].cb, f.seg[i].y, (int)f.seg[i].N,
+                       0, 0};
+    }
+    if (((uintptr_t)f.x & 15) != 0 || (f.x2 && ((uintptr_t)f.x2 & 15) != 0))
+        return set_error(EP_DECLINE_SHAPE, "fused GEMV: activations not 16-byte aligned");
+    int spw, waves;
+    plan(a.row_bytes, spw, waves);
+    if (f.xsrc == XS_PLAIN)
+        return bits == 4 ? dispatch_spw<4, 1>(a, a.x_dtype, spw, waves, stream)
+                         : dispatch_spw<8, 1>(a, a.x_dtype, spw, waves, stream);
+    if (f.xsrc == XS_RMSNORM)
+        return bits == 4 ? dispatch_fused<4, XS_RMSNORM>(a, spw, waves, stream)
+                         : dispatch_fused<8, XS_RMSNORM>(a, spw, waves, stream);
+    return bits == 4 ? dispatch_fused<4, XS_SWIGLU>(a, spw, waves, stream)
+                     : dispatch_fused<8, XS_SWIGLU>(a, spw, waves, stream);
 }
 
 }  // namespace ep

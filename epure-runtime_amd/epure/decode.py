@@ -1,0 +1,316 @@
+"""Batch-1 greedy decode of a packed decoder on the gfx950 kernels.
+
+This is the caller of the packed linears that the reference leaves to
+transformers (epure/runtime.py:373-415 builds a LlamaForCausalLM /
+Qwen3ForCausalLM whose linears are PackedLinear; generation runs through
+``model.generate``, benchmarks/run.py:48-73).  Here one decode step is five
+launches per layer, all through the C ABI of include/epure_decode.h:
+
+    fused q|k|v GEMV   (RMSNorm of the residual fused into the activation load)
+    attention          (q/k norm, RoPE, KV append, split-KV softmax)
+    o GEMV             (accumulates into the f32 residual)
+    fused gate|up GEMV (RMSNorm fused)
+    down GEMV          (SwiGLU fused into the activation load; accumulates)
+
+plus one lm_head launch (final norm, bf16 GEMV, greedy argmax, next-token
+embedding).  The token position lives in device memory, so the step is
+captured once as a HIP graph and replayed per token.
+
+Weights are random-init (there is no network for checkpoints), seeded, in
+the packed format of BASELINE config 0: 4-bit indices two per byte, a sorted
+16-entry fp16-valued codebook per linear (stored fp32 as the container
+does), group-128 fp16 scales |N(0, 0.02)| + 1e-3; embeddings and lm_head
+bf16 N(0, 0.02); norm weights 1.
+"""
+import ctypes
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+from .kernels import _abi
+from .kernels import cuda as cuda_kernel
+from .runtime import PackedWeight
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    hidden: int
+    intermediate: int
+    layers: int
+    n_heads: int
+    n_kv: int
+    head_dim: int
+    vocab: int
+    rope_theta: float
+    rms_eps: float = 1e-5
+    qk_norm: bool = False
+    tie_embeddings: bool = False
+    levels: int = 16
+    group: int = 128
+    name: str = "decoder"
+
+    def packed_linear_shapes(self):
+        """(name, N, K) of the packed linears of one layer."""
+        h, i, d = self.hidden, self.intermediate, self.head_dim
+        return [("q", self.n_heads * d, h), ("k", self.n_kv * d, h), ("v", self.n_kv * d, h),
+                ("o", h, self.n_heads * d), ("gate", i, h), ("up", i, h), ("down", h, i)]
+
+
+# BASELINE.json configs 2 and 1 (Llama-3-8B and Qwen3-1.7B shapes).
+LLAMA3_8B = DecoderConfig(4096, 14336, 32, 32, 8, 128, 128256, 5e5, 1e-5, name="llama3-8b")
+QWEN3_1_7B = DecoderConfig(2048, 6144, 28, 16, 8, 128, 151936, 1e6, 1e-6, qk_norm=True,
+                           tie_embeddings=True, name="qwen3-1.7b")
+
+
+def rope_tables(cfg, max_pos, device):
+    """cos/sin [max_pos, head_dim/2] f32, computed as transformers does
+    (LlamaRotaryEmbedding: inv_freq = theta^(-2i/d) in f32, freqs = pos * inv_freq)."""
+    d = cfg.head_dim
+    inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.int64).float() / d))
+    pos = torch.arange(max_pos, dtype=torch.int64).float()
+    freqs = pos[:, None] * inv_freq[None, :]
+    return freqs.cos().contiguous().to(device), freqs.sin().contiguous().to(device)
+
+
+def _gen(seed, device):
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def random_packed_linear(n, k, cfg, gen, device):
+    """One packed weight with BASELINE config-0 statistics."""
+    nbytes = n * k // 2 if cfg.levels <= 16 else n * k
+    hi = 256 if cfg.levels in (16, 256) else None
+    if hi is None:
+        raise ValueError("random weights are generated for 16 or 256 levels")
+    packed = torch.randint(0, hi, (nbytes,), generator=gen, device=device, dtype=torch.uint8)
+    cb = torch.sort(torch.randn(cfg.levels, generator=gen, device=device)).values
+    cb = cb.half().float()
+    g = (k + cfg.group - 1) // cfg.group
+    scale = (torch.randn(n, g, generator=gen, device=device).abs() * 0.02 + 1e-3).half()
+    return PackedWeight((n, k), packed, scale, cb, cfg.group, cfg.levels)
+
+
+@dataclass
+class Layer:
+    attn_norm: torch.Tensor
+    mlp_norm: torch.Tensor
+    lin: dict
+    q_norm: torch.Tensor = None
+    k_norm: torch.Tensor = None
+
+
+@dataclass
+class DecoderWeights:
+    cfg: DecoderConfig
+    embed: torch.Tensor
+    lm_head: torch.Tensor
+    final_norm: torch.Tensor
+    layers: list = field(default_factory=list)
+
+    def packed_bytes(self):
+        return sum(s.packed.numel() + s.scale.numel() * s.scale.element_size()
+                   + s.cb.numel() * s.cb.element_size()
+                   for L in self.layers for s in L.lin.values())
+
+    def resident_bytes(self):
+        lm = 0 if self.cfg.tie_embeddings else self.lm_head.numel() * 2
+        norms = sum(t.numel() * 2 for L in self.layers
+                    for t in (L.attn_norm, L.mlp_norm, L.q_norm, L.k_norm) if t is not None)
+        return self.packed_bytes() + lm + self.embed.numel() * 2 + norms + \
+            self.final_norm.numel() * 2
+
+
+def random_weights(cfg, seed=0, device="cuda"):
+    device = torch.device(device)
+    gen = _gen(seed, device)
+    h = cfg.hidden
+    embed = (torch.randn(cfg.vocab, h, generator=gen, device=device) * 0.02).to(torch.bfloat16)
+    lm_head = embed if cfg.tie_embeddings else \
+        (torch.randn(cfg.vocab, h, generator=gen, device=device) * 0.02).to(torch.bfloat16)
+    ones = lambda n: torch.ones(n, device=device, dtype=torch.bfloat16)  # noqa: E731
+    layers = []
+    for _ in range(cfg.layers):
+        lin = {name: random_packed_linear(n, k, cfg, gen, device)
+               for name, n, k in cfg.packed_linear_shapes()}
+        layers.append(Layer(ones(h), ones(h), lin,
+                            ones(cfg.head_dim) if cfg.qk_norm else None,
+                            ones(cfg.head_dim) if cfg.qk_norm else None))
+    return DecoderWeights(cfg, embed, lm_head, ones(h), layers)
+
+
+def _ptrs(*tensors):
+    return (ctypes.c_void_p * len(tensors))(*[t.data_ptr() for t in tensors])
+
+
+class Decoder:
+    """Device-resident greedy decoder over ``DecoderWeights``."""
+
+    def __init__(self, weights, max_pos, head_grid=None):
+        if not cuda_kernel.available():
+            raise RuntimeError("the gfx950 HIP backend is not available")
+        self.w = weights
+        cfg = self.cfg = weights.cfg
+        dev = self.device = weights.embed.device
+        if max_pos % 64:
+            max_pos += 64 - max_pos % 64
+        self.max_pos = max_pos
+        f32, bf16, i32 = torch.float32, torch.bfloat16, torch.int32
+        H, D = cfg.hidden, cfg.head_dim
+        self.h = torch.zeros(H, device=dev, dtype=f32)
+        self.q = torch.zeros(cfg.n_heads * D, device=dev, dtype=f32)
+        self.k = torch.zeros(cfg.n_kv * D, device=dev, dtype=f32)
+        self.v = torch.zeros(cfg.n_kv * D, device=dev, dtype=f32)
+        self.attn = torch.zeros(cfg.n_heads * D, device=dev, dtype=bf16)
+        self.g = torch.zeros(cfg.intermediate, device=dev, dtype=f32)
+        self.u = torch.zeros(cfg.intermediate, device=dev, dtype=f32)
+        self.logits = torch.zeros(cfg.vocab, device=dev, dtype=f32)
+        self.kcache = torch.zeros(cfg.layers, cfg.n_kv, max_pos, D, device=dev, dtype=bf16)
+        self.vcache = torch.zeros_like(self.kcache)
+        self.cos, self.sin = rope_tables(cfg, max_pos, dev)
+        self.state = torch.zeros(2, device=dev, dtype=i32)
+        self.tokens = torch.zeros(max_pos + 1, device=dev, dtype=i32)
+        self.argmax = torch.full((max_pos,), -1, device=dev, dtype=i32)
+        self.prompt = torch.zeros(max_pos, device=dev, dtype=i32)
+        self.n_prompt = 0
+        ws = _abi.lib.ep_attention_workspace(cfg.n_heads, D, max_pos)
+        self.attn_part = torch.zeros(ws // 4 + 1, device=dev, dtype=f32)
+        self.attn_ctr = torch.zeros(cfg.n_heads, device=dev, dtype=i32)
+        props = torch.cuda.get_device_properties(dev)
+        self.head_grid = head_grid or 4 * props.multi_processor_count
+        self.head_val = torch.zeros(self.head_grid, device=dev, dtype=f32)
+        self.head_idx = torch.zeros(self.head_grid, device=dev, dtype=i32)
+        self.head_ctr = torch.zeros(1, device=dev, dtype=i32)
+        self._build_launch_args()
+        self.graph = None
+
+    # ------------------------------------------------------------ launch args
+    def _seg(self, names, outs, L):
+        stores = [L.lin[n] for n in names]
+        s0 = stores[0]
+        return dict(
+            K=s0.in_features, group=s0.group, levels=s0.levels,
+            sdt=_abi.dtype_code(s0.scale.dtype), cdt=_abi.dtype_code(s0.cb.dtype),
+            n=len(stores), packed=_ptrs(*[s.packed for s in stores]),
+            scale=_ptrs(*[s.scale for s in stores]), cb=_ptrs(*[s.cb for s in stores]),
+            y=_ptrs(*outs), N=(ctypes.c_int64 * len(stores))(*[s.out_features for s in stores]))
+
+    def _build_launch_args(self):
+        cfg = self.cfg
+        self._layer_args = []
+        for L in self.w.layers:
+            self._layer_args.append(dict(
+                qkv=self._seg(("q", "k", "v"), (self.q, self.k, self.v), L),
+                o=self._seg(("o",), (self.h,), L),
+                gu=self._seg(("gate", "up"), (self.g, self.u), L),
+                down=self._seg(("down",), (self.h,), L),
+                L=L))
+        self.scale = 1.0 / math.sqrt(cfg.head_dim)
+
+    def _gemv(self, a, xsrc, x, xdt, x_aux, accumulate, stream):
+        rc = _abi.lib.ep_fused_gemv(
+            xsrc, x.data_ptr(), xdt, x_aux.data_ptr() if x_aux is not None else None,
+            self.cfg.rms_eps, a["K"], a["group"], a["levels"], a["sdt"], a["cdt"], a["n"],
+            a["packed"], a["scale"], a["cb"], a["y"], a["N"], _abi.F32, int(accumulate), stream)
+        _abi.check(rc, "ep_fused_gemv") or _raise_decline("ep_fused_gemv")
+
+    # ------------------------------------------------------------ one step
+    def step_launches(self):
+        """Enqueue one decode step on the current stream (capturable)."""
+        cfg, lib = self.cfg, _abi.lib
+        stream = _abi.stream_handle(self.device)
+        D = cfg.head_dim
+        for li, a in enumerate(self._layer_args):
+            L = a["L"]
+            self._gemv(a["qkv"], _abi.XSRC_RMSNORM, self.h, _abi.F32, L.attn_norm, False, stream)
+            rc = lib.ep_decode_attention(
+                self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                L.q_norm.data_ptr() if L.q_norm is not None else None,
+                L.k_norm.data_ptr() if L.k_norm is not None else None, cfg.rms_eps,
+                self.kcache[li].data_ptr(), self.vcache[li].data_ptr(), self.cos.data_ptr(),
+                self.sin.data_ptr(), self.state.data_ptr(), self.attn_part.data_ptr(),
+                self.attn_ctr.data_ptr(), self.attn.data_ptr(), cfg.n_heads, cfg.n_kv, D,
+                self.max_pos, self.scale, stream)
+            _abi.check(rc, "ep_decode_attention") or _raise_decline("ep_decode_attention")
+            self._gemv(a["o"], _abi.XSRC_PLAIN, self.attn, _abi.BF16, None, True, stream)
+            self._gemv(a["gu"], _abi.XSRC_RMSNORM, self.h, _abi.F32, L.mlp_norm, False, stream)
+            self._gemv(a["down"], _abi.XSRC_SWIGLU, self.g, _abi.F32, self.u, True, stream)
+        rc = lib.ep_lm_head_argmax(
+            self.h.data_ptr(), self.w.final_norm.data_ptr(), cfg.rms_eps,
+            self.w.lm_head.data_ptr(), self.logits.data_ptr(), cfg.vocab, cfg.hidden,
+            self.head_val.data_ptr(), self.head_idx.data_ptr(), self.head_ctr.data_ptr(),
+            self.state.data_ptr(), self.prompt.data_ptr(), self.n_prompt,
+            self.tokens.data_ptr(), self.argmax.data_ptr(), self.w.embed.data_ptr(),
+            self.max_pos, self.head_grid, stream)
+        _abi.check(rc, "ep_lm_head_argmax") or _raise_decline("ep_lm_head_argmax")
+
+    def gemv_launches(self):
+        """Enqueue only the step's packed GEMVs (4 launches per layer), for
+        timing the dequant-GEMV on its own.  Reads and writes the same
+        buffers as a step; the decode state is left untouched."""
+        stream = _abi.stream_handle(self.device)
+        for a in self._layer_args:
+            L = a["L"]
+            self._gemv(a["qkv"], _abi.XSRC_RMSNORM, self.h, _abi.F32, L.attn_norm, False, stream)
+            self._gemv(a["o"], _abi.XSRC_PLAIN, self.attn, _abi.BF16, None, True, stream)
+            self._gemv(a["gu"], _abi.XSRC_RMSNORM, self.h, _abi.F32, L.mlp_norm, False, stream)
+            self._gemv(a["down"], _abi.XSRC_SWIGLU, self.g, _abi.F32, self.u, True, stream)
+
+    # ------------------------------------------------------------ driving
+    def reset(self, prompt):
+        """Start a new sequence: prompt tokens are forced, then greedy."""
+        prompt = torch.as_tensor(prompt, dtype=torch.int32)
+        n = int(prompt.numel())
+        if n < 1 or n > self.max_pos:
+            raise ValueError("prompt length must be 1..max_pos")
+        self.prompt.zero_()
+        self.prompt[:n].copy_(prompt.to(self.device))
+        if self.n_prompt != n:
+            self.n_prompt = n
+            self.graph = None               # n_prompt is a launch argument
+        self.tokens.zero_()
+        self.tokens[0] = int(prompt[0])
+        self.argmax.fill_(-1)
+        self.state.copy_(torch.tensor([0, int(prompt[0])], dtype=torch.int32))
+        stream = _abi.stream_handle(self.device)
+        _abi.check(_abi.lib.ep_embed_token(self.w.embed.data_ptr(), self.state.data_ptr(),
+                                           self.h.data_ptr(), self.cfg.hidden, stream),
+                   "ep_embed_token")
+
+    def capture(self):
+        """Capture one step as a HIP graph (warm-up launch first)."""
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step_launches()
+        self.graph = g
+        return g
+
+    def step(self, use_graph=True):
+        if use_graph:
+            if self.graph is None:
+                raise RuntimeError("call capture() after reset() before replaying")
+            self.graph.replay()
+        else:
+            self.step_launches()
+
+    def generate(self, prompt, n_new, use_graph=True):
+        """Greedy decode: returns (tokens [n_prompt + n_new], argmax per position)."""
+        self.reset(prompt)
+        steps = self.n_prompt + n_new - 1
+        if steps + 1 > self.max_pos:
+            raise ValueError("max_pos too small for prompt + n_new")
+        if use_graph and self.graph is None:
+            # capture consumes no step: it records launches without running them
+            self.capture()
+        for _ in range(steps):
+            self.step(use_graph)
+        torch.cuda.synchronize(self.device)
+        n = self.n_prompt + n_new
+        return self.tokens[:n].cpu().tolist(), self.argmax[:n - 1].cpu().tolist()
+
+
+def _raise_decline(what):
+    raise RuntimeError(f"{what} declined: {_abi.last_error()}")

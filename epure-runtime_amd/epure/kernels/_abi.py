@@ -48,7 +48,26 @@ _SIGS = {
     "ep_dequant_tile": (_c_int, [
         _p, _p, _c_int, _c_i64, _p, _c_int, _c_int, _c_int, _c_i64, _c_i64,
         _p, _c_int, _c_i64, _p]),
+    # include/epure_decode.h
+    "ep_fused_gemv": (_c_int, [
+        _c_int, _p, _c_int, _p, ctypes.c_float,  # xsrc, x, x_dtype, x_aux, eps
+        _c_i64, _c_int, _c_int, _c_int, _c_int,  # K, group, levels, scale_dtype, cb_dtype
+        _c_int, _p, _p, _p, _p, _p,              # nseg, packed[], scale[], cb[], y[], N[]
+        _c_int, _c_int, _p]),                    # y_dtype, accumulate, stream
+    "ep_attention_workspace": (_sz, [_c_int, _c_int, _c_int]),
+    "ep_decode_attention": (_c_int, [
+        _p, _p, _p, _p, _p, ctypes.c_float,      # q, k, v, qn_w, kn_w, qk_eps
+        _p, _p, _p, _p, _p, _p, _p, _p,          # kcache, vcache, cos, sin, state, part, ctr, out
+        _c_int, _c_int, _c_int, _c_int, ctypes.c_float, _p]),
+    "ep_lm_head_argmax": (_c_int, [
+        _p, _p, ctypes.c_float, _p, _p, _c_int, _c_int,   # h, norm_w, eps, W, logits, V, H
+        _p, _p, _p, _p, _p, _c_int, _p, _p, _p,           # part_val, part_idx, counter, state,
+        _c_int, _c_int, _p]),                             # prompt, n_prompt, tokens, argmax,
+                                                          # embed, max_pos, grid, stream
+    "ep_embed_token": (_c_int, [_p, _p, _p, _c_int, _p]),
 }
+
+XSRC_PLAIN, XSRC_RMSNORM, XSRC_SWIGLU = 0, 1, 2
 
 lib = None
 LOAD_ERROR = None

@@ -1,0 +1,84 @@
+/*
+ * epure_decode.h -- C ABI of the batch-1 decode step built around the fused
+ * packed GEMV (include/epure_hip.h).
+ *
+ * The reference runs decode through transformers with every q/k/v/o/
+ * gate/up/down linear replaced by a PackedLinear (epure/runtime.py:261-262,
+ * :373-415) and calls the fused kernel once per linear per token
+ * (epure/kernels/cuda.py:88-117).  These entry points are the MI355X form
+ * of that step: the packed GEMVs with the RMSNorm / SwiGLU of the decoder
+ * fused into their activation load, grouped-query attention over a bf16 KV
+ * cache, and the bf16 lm_head with greedy selection.
+ *
+ * All entry points follow include/epure_hip.h conventions (device pointers,
+ * caller-owned buffers, return codes, no host synchronisation).  The token
+ * position is read from device memory (`state[0]`), so a captured HIP graph
+ * of one step replays for every token.
+ */
+#ifndef EPURE_DECODE_H
+#define EPURE_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* activation sources for ep_fused_gemv */
+#define EP_XSRC_PLAIN 0   /* x[K] in x_dtype */
+#define EP_XSRC_RMSNORM 1 /* x = rmsnorm(h) * w: h f32 [K] (x), w bf16 [K] (x_aux), eps */
+#define EP_XSRC_SWIGLU 2  /* x = silu(g) * u: g f32 [K] (x), u f32 [K] (x_aux) */
+
+/*
+ * y_i[N_i] (=|+=) W_i[N_i, K] . x for nseg (1..3) packed weights sharing K,
+ * group, levels and element types (q/k/v of one layer, or gate/up), with x
+ * built by the fused activation source.  Same arithmetic as
+ * ep_dequant_matmul at M = 1.  Replaces, per segment, one call of
+ * epure/kernels/cuda.py:88-117 linear(x, store) at batch 1.
+ * Scale rows are dense: ld_scale = ceil(K / group).
+ */
+int ep_fused_gemv(int xsrc, const void *x, int x_dtype, const void *x_aux, float eps,
+                  int64_t K, int group, int levels, int scale_dtype, int cb_dtype, int nseg,
+                  const uint8_t *const *packed, const void *const *scale, const void *const *cb,
+                  void *const *y, const int64_t *N, int y_dtype, int accumulate, void *stream);
+
+/*
+ * Grouped-query decode attention for one layer at position p = state[0]:
+ * optional per-head RMSNorm of q and k (weights qn_w / kn_w, bf16, NULL =
+ * none), rotate-half RoPE with cos/sin rows p of [max_pos][D/2] f32
+ * tables, append of this step's k/v (rounded to bf16) at row p of the
+ * [Hkv][max_pos][D] bf16 caches, causal softmax over rows 0..p scaled by
+ * `scale`, output [Hq * D] bf16.  `part` needs ep_attention_workspace()
+ * bytes; `counters` holds Hq ints that are zero before the first call and
+ * are left zero by every call.  head_dim <= 128, max_pos % 64 == 0.
+ */
+size_t ep_attention_workspace(int Hq, int D, int max_pos);
+int ep_decode_attention(const float *q, const float *k, const float *v, const uint16_t *qn_w,
+                        const uint16_t *kn_w, float qk_eps, uint16_t *kcache, uint16_t *vcache,
+                        const float *cos_t, const float *sin_t, const int *state, float *part,
+                        int *counters, uint16_t *out, int Hq, int Hkv, int D, int max_pos,
+                        float scale, void *stream);
+
+/*
+ * logits = W[V, H] (bf16) . bf16(rmsnorm(h) * norm_w), then greedy
+ * selection: with p = state[0], argmax_out[p] = argmax (lowest index on
+ * ties), the next token is prompt[p + 1] while p + 1 < n_prompt, else the
+ * argmax; tokens[p + 1] = next; state = {p + 1, next}; h = embed[next]
+ * (f32).  `logits` may be NULL.  part_val / part_idx hold `grid` entries;
+ * `counter` is one int, zero before the first call and left zero.
+ * H % 512 == 0, H <= 4096.
+ */
+int ep_lm_head_argmax(float *h, const uint16_t *norm_w, float eps, const uint16_t *W,
+                      float *logits, int V, int H, float *part_val, int *part_idx, int *counter,
+                      int *state, const int *prompt, int n_prompt, int *tokens, int *argmax_out,
+                      const uint16_t *embed, int max_pos, int grid, void *stream);
+
+/* h[H] = embed[state[1]] as f32 (the first step's input). */
+int ep_embed_token(const uint16_t *embed, const int *state, float *h, int H, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EPURE_DECODE_H */
