@@ -18,7 +18,6 @@
 namespace ep {
 namespace {
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kChunk = 64;  // KV positions per attention workgroup
 constexpr int kMaxD = 128;  // head_dim served
@@ -354,7 +353,7 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         sacc = __builtin_amdgcn_fdot2_f32_bf16(
-                            __builtin_bit_cast(bf16x2_t, w[q][i][e]), x[4 * i + e], sacc, false);
+                            as_bf16x2(w[q][i][e]), x[4 * i + e], sacc, false);
                 }
             // 16-lane rows by DPP, then the four row sums through readlane
             sacc = row16_sum_dpp(sacc);

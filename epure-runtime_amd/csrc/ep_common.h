@@ -29,8 +29,35 @@ EP_DEV uint16_t f32_to_bf16(float f)
     return (uint16_t)(u >> 16);
 }
 
-EP_DEV uint16_t f16_bits(f16_t h) { return __builtin_bit_cast(uint16_t, h); }
-EP_DEV f16_t f16_from_bits(uint16_t b) { return __builtin_bit_cast(f16_t, b); }
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// Bit reinterpretations go through memcpy: __builtin_bit_cast of an
+// ext-vector element to a 16-bit-lane vector is lowered to element 0 by this
+// compiler (every lane of a u32x4 read as lane 0).
+EP_DEV uint16_t f16_bits(f16_t h)
+{
+    uint16_t u;
+    __builtin_memcpy(&u, &h, 2);
+    return u;
+}
+EP_DEV f16_t f16_from_bits(uint16_t b)
+{
+    f16_t h;
+    __builtin_memcpy(&h, &b, 2);
+    return h;
+}
+EP_DEV f16x2_t as_f16x2(uint32_t u)
+{
+    f16x2_t v;
+    __builtin_memcpy(&v, &u, 4);
+    return v;
+}
+EP_DEV bf16x2_t as_bf16x2(uint32_t u)
+{
+    bf16x2_t v;
+    __builtin_memcpy(&v, &u, 4);
+    return v;
+}
 
 // Load element i of a buffer of element type `dt` as float.
 EP_DEV float load_as_f32(const void *p, int dt, int64_t i)

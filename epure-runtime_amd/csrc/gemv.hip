@@ -334,8 +334,8 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     }
 
     // codebook -> fp16 bits in LDS (one round trip), then the pair table
-    if (tid < 256)
-        s_cb[tid] = tid < a.levels ? f16_bits((f16_t)load_as_f32(cbp, a.cb_dtype, tid)) : 0;
+    for (int i = tid; i < 256; i += blockDim.x)
+        s_cb[i] = i < a.levels ? f16_bits((f16_t)load_as_f32(cbp, a.cb_dtype, i)) : 0;
     if constexpr (XS == XS_RMSNORM) {
         // The four row groups of a wave (lanes 16r..16r+15) hold the same
         // activation chunks: count each element once.
@@ -387,7 +387,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                         for (int i = 0; i < 4; ++i) {
                             const uint32_t t =
                                 lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[i]));
-                            const f16x2_t wv = __builtin_bit_cast(f16x2_t, t);
+                            const f16x2_t wv = as_f16x2(t);
 #pragma unroll
                             for (int m = 0; m < MT; ++m)
                                 part[m] = __builtin_amdgcn_fdot2(wv, xh[j][m][wd * 4 + i], part[m],
@@ -401,7 +401,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                             const uint32_t t1 = lds_read_u32(
                                 tab, __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p + 1]));
                             const uint32_t pr = __builtin_amdgcn_perm(t1, t0, 0x07060100u);
-                            const f16x2_t wv = __builtin_bit_cast(f16x2_t, pr);
+                            const f16x2_t wv = as_f16x2(pr);
 #pragma unroll
                             for (int m = 0; m < MT; ++m)
                                 part[m] = __builtin_amdgcn_fdot2(wv, xh[j][m][wd * 2 + p], part[m],

@@ -198,7 +198,7 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
                         const uint32_t t = tab[(w >> (8 * b)) & 0xffu];
-                        o[wd * 4 + b] = __builtin_bit_cast(f16x2_t, t) * s2;
+                        o[wd * 4 + b] = as_f16x2(t) * s2;
                     }
                 } else {
 #pragma unroll
@@ -206,7 +206,7 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
                         const uint32_t t0 = tab[(w >> (16 * p)) & 0xffu];
                         const uint32_t t1 = tab[(w >> (16 * p + 8)) & 0xffu];
                         const f16x2_t pr =
-                            __builtin_bit_cast(f16x2_t, (t0 & 0xffffu) | (t1 << 16));
+                            as_f16x2((t0 & 0xffffu) | (t1 << 16));
                         o[wd * 2 + p] = pr * s2;
                     }
                 }

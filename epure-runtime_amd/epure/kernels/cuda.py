@@ -188,7 +188,7 @@ def linear(x, store):
     grad = torch.is_grad_enabled() and (
         x.requires_grad or store.cb.requires_grad or store.scale.requires_grad)
     if grad:
-        if not backward_available():
+        if not backward_available() or not backward_serves(store, x):
             return None
         y = _PackedLinearFn.apply(x2, store.cb, store.scale, h)
     else:
@@ -198,9 +198,14 @@ def linear(x, store):
     return y.reshape(*shape[:-1], h.N)
 
 
-# The fused backward kernels are part of the library build.
-_BWD_BUILT = False
-
-
 def backward_available():
-    return _BWD_BUILT and os.environ.get("EPURE_NO_FUSED_BWD") != "1"
+    return os.environ.get("EPURE_NO_FUSED_BWD") != "1"
+
+
+def backward_serves(store, x):
+    """Shapes the fused backward covers (the C ABI declines the rest):
+    levels <= 16, K % 128 == 0, N % 16 == 0, group in {32, 64, 128}, bf16
+    activations."""
+    return (store.levels <= 16 and store.in_features % 128 == 0
+            and store.out_features % 16 == 0
+            and store.group in (32, 64, 128) and x.dtype == torch.bfloat16)

@@ -1,0 +1,124 @@
+"""Fused compressed-state backward against the closed forms
+(fine-tuning/README.md:62-68), float64 references.
+
+grad_x = gy W; G = gy^T x (never stored); grad_scale[n, g] = sum_{k in g}
+G[n, k] cb[idx[n, k]]; grad_cb[l] = sum_{idx == l} G[n, k] scale[n, g(k)].
+Indices must be bit-identical before and after.
+"""
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from epure import PackedLinear, PackedWeight, make_trainable, snapshot_indices, verify_frozen
+from epure.kernels import _abi, cuda
+from oracle import ref
+from oracle.decoder import dense_tile
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def make(n, k, group=128, seed=0):
+    idx, packed, scale, cb = ref.synth_linear(n, k, 16, group, seed=seed)
+    s = PackedWeight((n, k), packed, scale, cb.astype(np.float32), group, 16).to(DEV)
+    return idx, packed, scale, cb, s
+
+
+def bf16(shape, seed, std=1.0):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return (torch.randn(*shape, generator=g, device=DEV) * std).to(torch.bfloat16)
+
+
+def closed_forms_t64(gy, x, s):
+    """float64 torch restatement of the closed forms (on the GPU)."""
+    n, k, grp = s.out_features, s.in_features, s.group
+    w = dense_tile(s.packed, s.scale, s.cb, n, k, grp, 16).double()
+    gy64, x64 = gy.double(), x.double()
+    gx = gy64 @ w
+    G = gy64.t() @ x64
+    both = torch.stack((s.packed & 0x0F, s.packed >> 4), -1).reshape(-1)[:n * k]
+    idx = both.reshape(n, k).long()
+    cbd = s.cb.double()
+    gsc = (G * cbd[idx]).view(n, k // grp, grp).sum(-1)
+    sfull = s.scale.double().repeat_interleave(grp, 1)
+    gcb = torch.zeros(16, dtype=torch.float64, device=DEV).index_add_(
+        0, idx.reshape(-1), (G * sfull).reshape(-1))
+    return gx, gcb, gsc
+
+
+def rel(a, b):
+    return float((a.double() - b).abs().max() / b.abs().max())
+
+
+def run_bwd(s, gy, x):
+    h = cuda._hot(s)
+    r = cuda.backward(gy, x, h)
+    assert r is not None, _abi.last_error()
+    torch.cuda.synchronize()
+    return r
+
+
+@pytest.mark.parametrize("n,k,m,group", [(256, 512, 64, 128), (384, 1024, 100, 64),
+                                         (208, 256, 33, 32), (128, 128, 1, 128)])
+def test_backward_small_vs_closed_forms(n, k, m, group):
+    idx, packed, scale, cb, s = make(n, k, group, seed=n + k)
+    x, gy = bf16((m, k), 1), bf16((m, n), 2, 1e-2)
+    gx, gcb, gsc = run_bwd(s, gy, x)
+    # numpy float64 oracle (oracle/ref.py backward_f64) on the same bf16 values
+    wgx, wgcb, wgsc = ref.backward_f64(gy.float().cpu().numpy(), x.float().cpu().numpy(), idx,
+                                       scale, cb, group)
+    assert rel(gx.float().cpu(), torch.from_numpy(wgx)) < 2e-3
+    assert rel(gsc.cpu(), torch.from_numpy(wgsc)) < 1e-4
+    assert rel(gcb.cpu(), torch.from_numpy(wgcb)) < 1e-4
+
+
+@pytest.mark.parametrize("n,k", [(2048, 6144), (6144, 2048)])
+def test_backward_config4(n, k):
+    _, packed, _, _, s = make(n, k, seed=7)
+    before = hashlib.blake2b(s.packed.cpu().numpy().tobytes(), digest_size=16).hexdigest()
+    x, gy = bf16((2048, k), 3), bf16((2048, n), 4, 1e-2)
+    gx, gcb, gsc = run_bwd(s, gy, x)
+    wgx, wgcb, wgsc = closed_forms_t64(gy, x, s)
+    assert rel(gx.float(), wgx) < 2e-3
+    assert rel(gsc, wgsc) < 1e-4
+    assert rel(gcb, wgcb) < 1e-4
+    after = hashlib.blake2b(s.packed.cpu().numpy().tobytes(), digest_size=16).hexdigest()
+    assert before == after
+    a = run_bwd(s, gy, x)
+    assert all(torch.equal(p, q) for p, q in zip((gx, gcb, gsc), a))   # deterministic
+
+
+def test_autograd_through_packed_linear():
+    n, k, m = 512, 1024, 48
+    _, _, _, _, s = make(n, k, seed=9)
+    lin = PackedLinear(s)
+    model = torch.nn.Sequential(lin)
+    snap = snapshot_indices(model)
+    make_trainable(model, "both", verbose=False)
+    x = bf16((m, k), 5).requires_grad_(True)
+    gy = bf16((m, n), 6, 1e-2)
+    y = lin(x)
+    assert y.grad_fn is not None and "PackedLinearFn" in type(y.grad_fn).__name__
+    y.backward(gy)
+    # reference: autograd through a float64 materialize of the same weight
+    cb64 = s.cb.detach().double().requires_grad_(True)
+    sc64 = s.scale.detach().double().requires_grad_(True)
+    both = torch.stack((s.packed & 0x0F, s.packed >> 4), -1).reshape(-1)[:n * k]
+    w = cb64[both.reshape(n, k).long()] * sc64.repeat_interleave(128, 1)
+    x64 = x.detach().double().requires_grad_(True)
+    (x64 @ w.t()).backward(gy.double())
+    assert rel(x.grad.float(), x64.grad) < 2e-3
+    assert rel(s.cb.grad, cb64.grad) < 1e-4
+    assert rel(s.scale.grad, sc64.grad) < 1e-4
+    assert verify_frozen(model, snap)
+
+
+def test_backward_declines_unserved():
+    _, _, _, _, s = make(128, 256, seed=1)
+    h = cuda._hot(s)
+    x = torch.randn(4, 256, device=DEV)                 # f32 activations: declined
+    gy = torch.randn(4, 128, device=DEV)
+    assert cuda.backward(gy, x, h) is None
+    assert cuda.linear(x.requires_grad_(True), s) is None   # autograd: falls back to materialize
