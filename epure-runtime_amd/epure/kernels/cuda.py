@@ -161,14 +161,15 @@ class _PackedLinearFn(torch.autograd.Function):
         h = ctx.h
         need_x, need_cb, need_sc = ctx.needs_input_grad[0], ctx.needs_input_grad[1], \
             ctx.needs_input_grad[2]
-        r = backward(gy.contiguous(), x2, h, need_x, need_cb, need_sc)
+        # grad_cb comes out of the same pass as grad_scale, which is then kept
+        r = backward(gy.contiguous(), x2, h, need_x, need_cb, need_sc or need_cb)
         if r is None:
             raise RuntimeError(f"fused backward declined: {_abi.last_error()}")
         gx, gcb, gsc = r
         if gcb is not None:
             gcb = gcb.to(h.cb.dtype).view_as(h.cb)
         if gsc is not None:
-            gsc = gsc.to(h.scale.dtype).view_as(h.scale)
+            gsc = gsc.to(h.scale.dtype).view_as(h.scale) if need_sc else None
         return gx, gcb, gsc, None
 
 
