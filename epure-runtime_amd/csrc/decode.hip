@@ -264,7 +264,6 @@ struct HeadArgs {
 };
 
 constexpr int kHeadPerLane = 64;  // bf16 activations per lane: H <= 4096
-constexpr int kHeadRows = 4;      // rows in flight per wave
 
 template <int CTRL>
 EP_DEV float dpp_f(float v)
@@ -283,85 +282,87 @@ EP_DEV float row16_sum_dpp(float v)
 }
 
 // lm_head GEMV with the final RMSNorm fused in front and greedy selection
-// behind.  Each wave holds the normalized activation (bf16, as the
-// reference's bf16 model feeds its lm_head) in registers and streams whole
-// rows with 16-byte loads, four rows in flight.
+// behind.  The workgroup normalizes the residual once into LDS (bf16, as the
+// reference's bf16 model feeds its lm_head); each wave keeps its 64 values
+// in registers and streams whole rows with 16-byte loads, two rows in
+// flight; row sums use DPP within 16-lane rows and readlane across them.
 __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
 {
     __shared__ float wv[4];
     __shared__ int wi[4];
     __shared__ float ssq_s[4];
     __shared__ int s_last;
+    __shared__ __align__(16) uint16_t xs[64 * kHeadPerLane];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = a.H;
     const int nld = H / 512;  // 16-byte loads per lane per row
 
-    // RMSNorm of the residual: every wave needs the full row
-    float ss = 0.0f;
-    for (int k = threadIdx.x; k < H; k += 256) {
-        const float v = a.h[k];
-        ss = fmaf(v, v, ss);
-    }
-    ss = wave_sum(ss);
-    if (lane == 0)
-        ssq_s[wave] = ss;
-    __syncthreads();
-    const float rinv = rsqrtf((ssq_s[0] + ssq_s[1] + ssq_s[2] + ssq_s[3]) / (float)H + a.eps);
-
-    bf16x2_t x[kHeadPerLane / 2];
-#pragma unroll
-    for (int i = 0; i < kHeadPerLane / 8; ++i) {
-        if (i < nld) {
-            const int k0 = (lane + 64 * i) * 8;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float v0 = bf16_round(a.h[k0 + 2 * e] * rinv) * bf16_to_f32(a.norm_w[k0 + 2 * e]);
-                const float v1 =
-                    bf16_round(a.h[k0 + 2 * e + 1] * rinv) * bf16_to_f32(a.norm_w[k0 + 2 * e + 1]);
-                x[4 * i + e] = (bf16x2_t){(__bf16)v0, (__bf16)v1};
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                x[4 * i + e] = (bf16x2_t){(__bf16)0.0f, (__bf16)0.0f};
-        }
-    }
-
     const int gw = blockIdx.x * 4 + wave, nw = gridDim.x * 4;
-    float best = -INFINITY;
-    int besti = 0x7fffffff;
-    for (int rb = gw; rb < a.V; rb += kHeadRows * nw) {
-        u32x4_t w[kHeadRows][kHeadPerLane / 8];
-        int rows[kHeadRows];
+    // first rows' loads go out before the normalization
+    u32x4_t w[2][kHeadPerLane / 8];
+    auto load_rows = [&](int r0) {
 #pragma unroll
-        for (int q = 0; q < kHeadRows; ++q) {
-            const int r = rb + q * nw;
-            rows[q] = r;
-            const int rs = r < a.V ? r : rb;
+        for (int q = 0; q < 2; ++q) {
+            const int r = r0 + q * nw;
+            const int rs = r < a.V ? r : (r0 < a.V ? r0 : 0);
 #pragma unroll
             for (int i = 0; i < kHeadPerLane / 8; ++i)
                 if (i < nld)
                     w[q][i] = __builtin_nontemporal_load(
                         (const u32x4_t *)(a.W + (int64_t)rs * H + (lane + 64 * i) * 8));
         }
+    };
+    if (gw < a.V)
+        load_rows(gw);
+
+    float ss = 0.0f;
+    for (int k = threadIdx.x * 4; k < H; k += 1024) {
+        const f32x4_t v = *(const f32x4_t *)(a.h + k);
+        ss = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], fmaf(v[3], v[3], ss))));
+    }
+    ss = wave_sum(ss);
+    if (lane == 0)
+        ssq_s[wave] = ss;
+    __syncthreads();
+    const float rinv = rsqrtf((ssq_s[0] + ssq_s[1] + ssq_s[2] + ssq_s[3]) / (float)H + a.eps);
+    for (int k = threadIdx.x; k < H; k += 256)
+        xs[k] = f32_to_bf16(bf16_round(a.h[k] * rinv) * bf16_to_f32(a.norm_w[k]));
+    __syncthreads();
+    bf16x2_t x[kHeadPerLane / 2];
 #pragma unroll
-        for (int q = 0; q < kHeadRows; ++q) {
-            float sacc = 0.0f;
+    for (int i = 0; i < kHeadPerLane / 8; ++i) {
+        u32x4_t q4 = (u32x4_t){0, 0, 0, 0};
+        if (i < nld)
+            q4 = *(const u32x4_t *)(xs + (lane + 64 * i) * 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            x[4 * i + e] = as_bf16x2(q4[e]);
+    }
+
+    float best = -INFINITY;
+    int besti = 0x7fffffff;
+    for (int rb = gw; rb < a.V; rb += 2 * nw) {
+        float sacc[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
 #pragma unroll
             for (int i = 0; i < kHeadPerLane / 8; ++i)
                 if (i < nld) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        sacc = __builtin_amdgcn_fdot2_f32_bf16(
-                            as_bf16x2(w[q][i][e]), x[4 * i + e], sacc, false);
+                        sacc[q] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w[q][i][e]),
+                                                                  x[4 * i + e], sacc[q], false);
                 }
-            // 16-lane rows by DPP, then the four row sums through readlane
-            sacc = row16_sum_dpp(sacc);
-            const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sacc), 0)) +
-                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sacc), 16)) +
-                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sacc), 32)) +
-                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sacc), 48));
-            const int r = rows[q];
+        if (rb + 2 * nw < a.V)
+            load_rows(rb + 2 * nw);  // next rows in flight during the reduction
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const float v = row16_sum_dpp(sacc[q]);
+            const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)) +
+                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)) +
+                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)) +
+                              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+            const int r = rb + q * nw;
             if (r < a.V) {
                 if (a.logits && lane == 0)
                     a.logits[r] = tot;

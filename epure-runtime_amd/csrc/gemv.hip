@@ -146,7 +146,7 @@ EP_DEV float silu_mul(float g, float u)
     return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
-template <int BITS, int MT, int RQ, int SPW, int XDT, int XS, bool DB>
+template <int BITS, int MT, int RQ, int SPW, int XDT, int XS, bool DB, int XCAP>
 __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
 {
     constexpr int PAIRS = BITS == 4 ? 16 : 8;  // weight pairs per 16-byte chunk
@@ -161,6 +161,8 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     __shared__ float s_part[kMaxWaves];            // sum-of-squares partials
     __shared__ uint16_t s_cb[256];                 // codebook as fp16 bits
     __shared__ float s_rinv;
+    __shared__ __align__(16) uint32_t xs[XCAP * MT];      // staged activations, fp16 pairs
+    __shared__ float xf[(2 * XCAP / (BITS == 4 ? 32 : 16)) * MT];  // 2^e per chunk
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int W = blockDim.x >> 6;
@@ -249,24 +251,20 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
         load_block(blk, wqA, scA);  // in flight while the table and x are staged
 
     // ---- stage activations ----------------------------------------------
-    // Each lane converts its own chunk(s) of the activation row to fp16
-    // after an exact power-of-two rescale chosen from that chunk's largest
-    // value; the factor 2^e is folded into the group scale of the chunk's
-    // partial sums, so no cross-lane agreement (and no second pass) is
-    // needed.  RMSNorm's 1/rms is a scalar and is applied to the finished
-    // dot products; its sum of squares is reduced behind the table build.
-    f16x2_t xh[SPW][MT][PAIRS];
-    float fexp[SPW][MT];
+    // The workgroup converts the activation row(s) once, cooperatively: one
+    // chunk of KPC values per thread, scaled by an exact power of two chosen
+    // from the chunk's largest value and stored to LDS as fp16 pairs; the
+    // factor 2^e is folded into the group scale of the chunk's partial sums,
+    // so no cross-lane agreement is needed.  RMSNorm's 1/rms is a scalar
+    // and is applied to the finished dot products.
+    constexpr int NCH = 2 * XCAP / KPC;  // chunk slots per activation row
+    const int nchunk = (int)(a.K / KPC);
     float ssq = 0.0f;
 #pragma unroll
-    for (int j = 0; j < SPW; ++j) {
-        // Loads are unconditional from clamped addresses (an idle lane reads
-        // element 0 and zeroes it), keeping each slab straight-line code.
-        const int64_t k0 = act[j] ? (BITS == 4 ? (int64_t)cbyte[j] * 2 : cbyte[j]) : 0;
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            const bool live = act[j] && m < a.M;
-            const int mm = m < a.M ? m : 0;
+    for (int m = 0; m < MT; ++m) {
+        const bool live_m = m < a.M;
+        for (int cc = tid; cc < nchunk; cc += blockDim.x) {
+            const int64_t k0 = (int64_t)cc * KPC;
             float v[KPC];
             if constexpr (XS == XS_RMSNORM) {
                 const float *hp = (const float *)a.x + k0;
@@ -280,8 +278,8 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                     for (int t = 0; t < 4; ++t) {
                         float w0, w1;
                         unpack_pair<EP_BF16>(wv[t], w0, w1);
-                        const float x0 = live ? (t < 2 ? h0[2 * t] : h1[2 * t - 4]) : 0.0f;
-                        const float x1 = live ? (t < 2 ? h0[2 * t + 1] : h1[2 * t - 3]) : 0.0f;
+                        const float x0 = t < 2 ? h0[2 * t] : h1[2 * t - 4];
+                        const float x1 = t < 2 ? h0[2 * t + 1] : h1[2 * t - 3];
                         ssq = fmaf(x0, x0, fmaf(x1, x1, ssq));
                         v[p + 2 * t] = x0 * w0;
                         v[p + 2 * t + 1] = x1 * w1;
@@ -296,26 +294,25 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                     const f32x4_t u = *(const f32x4_t *)(up + p);
 #pragma unroll
                     for (int t = 0; t < 4; ++t)
-                        v[p + t] = live ? silu_mul(g[t], u[t]) : 0.0f;
+                        v[p + t] = silu_mul(g[t], u[t]);
                 }
             } else if constexpr (XDT == EP_F32) {
-                const float *xp = (const float *)a.x + (int64_t)mm * a.ldx + k0;
+                const float *xp = (const float *)a.x + (int64_t)(live_m ? m : 0) * a.ldx + k0;
 #pragma unroll
                 for (int p = 0; p < KPC; p += 4) {
                     const f32x4_t t4 = *(const f32x4_t *)(xp + p);
 #pragma unroll
                     for (int t = 0; t < 4; ++t)
-                        v[p + t] = live ? t4[t] : 0.0f;
+                        v[p + t] = live_m ? t4[t] : 0.0f;
                 }
             } else {
-                const uint16_t *xp = (const uint16_t *)a.x + (int64_t)mm * a.ldx + k0;
+                const uint16_t *xp = (const uint16_t *)a.x + (int64_t)(live_m ? m : 0) * a.ldx + k0;
 #pragma unroll
                 for (int p = 0; p < PAIRS; p += 4) {
                     const u32x4_t t4 = *(const u32x4_t *)(xp + 2 * p);
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        unpack_pair<XDT>(live ? t4[t] : 0u, v[2 * (p + t)], v[2 * (p + t) + 1]);
-                    }
+                    for (int t = 0; t < 4; ++t)
+                        unpack_pair<XDT>(live_m ? t4[t] : 0u, v[2 * (p + t)], v[2 * (p + t) + 1]);
                 }
             }
             float am = 0.0f;
@@ -324,22 +321,25 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                 am = fmaxf(am, fabsf(v[t]));
             const int e = row_exponent(am);
             const float pw = ldexpf(1.0f, -e);
-            fexp[j][m] = ldexpf(1.0f, e);
+            uint32_t *dst = xs + m * XCAP + cc * PAIRS;
 #pragma unroll
-            for (int p = 0; p < PAIRS; ++p)
-                xh[j][m][p] = (f16x2_t){(f16_t)(v[2 * p] * pw), (f16_t)(v[2 * p + 1] * pw)};
+            for (int p = 0; p < PAIRS; p += 4) {
+                u32x4_t q4;
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    q4[t] = (uint32_t)f16_bits((f16_t)(v[2 * (p + t)] * pw)) |
+                            ((uint32_t)f16_bits((f16_t)(v[2 * (p + t) + 1] * pw)) << 16);
+                *(u32x4_t *)(dst + p) = q4;
+            }
+            xf[m * NCH + cc] = ldexpf(1.0f, e);
         }
-        // keep one slab's loads live at a time (register pressure)
-        __builtin_amdgcn_sched_barrier(0);
     }
 
-    // codebook -> fp16 bits in LDS (one round trip), then the pair table
+    // codebook -> fp16 bits in LDS, then the pair table
     for (int i = tid; i < 256; i += blockDim.x)
         s_cb[i] = i < a.levels ? f16_bits((f16_t)load_as_f32(cbp, a.cb_dtype, i)) : 0;
     if constexpr (XS == XS_RMSNORM) {
-        // The four row groups of a wave (lanes 16r..16r+15) hold the same
-        // activation chunks: count each element once.
-        const float v = wave_sum(rq == 0 ? ssq : 0.0f);
+        const float v = wave_sum(ssq);
         if (lane == 0)
             s_part[wave] = v;
     }
@@ -351,6 +351,25 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
             for (int w = 0; w < W; ++w)
                 q += s_part[w];
             s_rinv = rsqrtf(q / (float)a.K + a.eps);
+        }
+    }
+    // this lane's activation chunks, from LDS into registers
+    f16x2_t xh[SPW][MT][PAIRS];
+    float fexp[SPW][MT];
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+        const int cc = act[j] ? (int)(cbyte[j] / 16) : 0;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const uint32_t *src = xs + m * XCAP + cc * PAIRS;
+#pragma unroll
+            for (int p = 0; p < PAIRS; p += 4) {
+                const u32x4_t q4 = *(const u32x4_t *)(src + p);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    xh[j][m][p + t] = as_f16x2(q4[t]);
+            }
+            fexp[j][m] = act[j] ? xf[m * NCH + cc] : 0.0f;
         }
     }
     __syncthreads();
@@ -494,11 +513,11 @@ __global__ void __launch_bounds__(256) gemv_generic_kernel(GemvArgs a)
 constexpr int rq_for(int spw) { return spw >= 8 ? 1 : (spw >= 4 ? 2 : 4); }
 
 // Activation registers (SPW * MT * pairs-per-chunk) stay within 64 VGPRs,
-// and with several activation rows at most 4 chunk sets are live (the
-// variants beyond that spill).
+// and several activation rows are served with one slab per wave (the other
+// variants spill).
 constexpr bool fits(int bits, int spw, int mt)
 {
-    return spw * mt * (bits == 4 ? 16 : 8) <= 64 && (mt == 1 || spw * mt <= 4);
+    return spw * mt * (bits == 4 ? 16 : 8) <= 64 && (mt == 1 || spw == 1);
 }
 
 // Splits the persistent grid across segments in proportion to their row
@@ -533,28 +552,57 @@ void assign_workgroups(GemvArgs &a, int rows_per_block, int per_cu)
         a.seg[i].wg_begin = a.seg[i].wg_end = begin;
 }
 
+// LDS bytes of one workgroup of a variant (table + staged activations).
+constexpr size_t lds_bytes(int bits, int mt, int rq, int xcap)
+{
+    return (size_t)kTabDwords * 4 + (size_t)kMaxWaves * 4 * rq * mt * 4 + (size_t)xcap * mt * 4 +
+           (size_t)(2 * xcap / (bits == 4 ? 32 : 16)) * mt * 4 + 1024;
+}
+
+template <int BITS, int MT, int SPW, int XDT, int XS, int XCAP>
+int launch_xcap(GemvArgs a, int waves, hipStream_t stream)
+{
+    constexpr int RQ = rq_for(SPW);
+    constexpr size_t lds = lds_bytes(BITS, MT, RQ, XCAP);
+    static_assert(lds <= 160 * 1024, "LDS budget");
+    // persistent grid: as many workgroups per CU as LDS and registers allow
+    int per_cu = (int)((160 * 1024) / lds);
+    if (SPW >= 2 || MT >= 2)
+        per_cu = 1;  // ~200+ VGPRs: one 8-wave workgroup per CU
+    if (per_cu < 1)
+        per_cu = 1;
+    assign_workgroups(a, 4 * RQ, per_cu);
+    const int grid = a.seg[a.nseg - 1].wg_end;
+    // Double-buffer the next block's loads only when a workgroup has more
+    // than one block; otherwise the extra registers buy nothing.
+    bool multi = false;
+    for (int i = 0; i < a.nseg; ++i)
+        multi |= (a.seg[i].N + 4 * RQ - 1) / (4 * RQ) > a.seg[i].wg_end - a.seg[i].wg_begin;
+    if (multi)
+        hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, true, XCAP>), dim3(grid),
+                           dim3(waves * 64), 0, stream, a);
+    else
+        hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, false, XCAP>),
+                           dim3(grid), dim3(waves * 64), 0, stream, a);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
 template <int BITS, int MT, int SPW, int XDT, int XS>
 int launch_lut(GemvArgs a, int waves, hipStream_t stream)
 {
     if constexpr (!fits(BITS, SPW, MT)) {
         return set_error(EP_DECLINE_SHAPE, "GEMV variant does not fit registers");
     } else {
-        constexpr int RQ = rq_for(SPW);
-        assign_workgroups(a, 4 * RQ, 2);  // 2 workgroups per CU fit the 64 KiB tables
-        const int grid = a.seg[a.nseg - 1].wg_end;
-        // Double-buffer the next block's loads only when a workgroup has more
-        // than one block; otherwise the extra registers buy nothing.
-        bool multi = false;
-        for (int i = 0; i < a.nseg; ++i)
-            multi |= (a.seg[i].N + 4 * RQ - 1) / (4 * RQ) > a.seg[i].wg_end - a.seg[i].wg_begin;
-        if (multi)
-            hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, true>), dim3(grid),
-                               dim3(waves * 64), 0, stream, a);
-        else
-            hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, false>), dim3(grid),
-                               dim3(waves * 64), 0, stream, a);
-        EP_HIP_CHECK(hipGetLastError());
-        return EP_OK;
+        const int64_t pairs = a.K / 2;
+        if (pairs <= 2048)
+            return launch_xcap<BITS, MT, SPW, XDT, XS, 2048>(a, waves, stream);
+        if constexpr (MT <= 2) {
+            if (pairs <= 8192)
+                return launch_xcap<BITS, MT, SPW, XDT, XS, 8192>(a, waves, stream);
+        }
+        return set_error(EP_DECLINE_SHAPE, "GEMV: K=%lld x M too large to stage",
+                         (long long)a.K);
     }
 }
 
@@ -644,6 +692,8 @@ bool shape_ok(int bits, int64_t N, int64_t K, int group, int64_t ld_scale)
     const int64_t rb = bits == 4 ? K / 2 : K;
     if (N * rb >= ((int64_t)1 << 31) || N * ld_scale >= ((int64_t)1 << 31))
         return false;
+    if (K > 16384)
+        return false;
     int spw, waves;
     plan(rb, spw, waves);
     return spw <= 8 && fits(bits, spw, 1);
@@ -664,6 +714,8 @@ bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
     int spw, waves;
     plan(bits == 4 ? w.K / 2 : w.K, spw, waves);
     const int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);
+    if (mt > 2 && w.K > 4096)
+        return false;  // activations of 4 rows staged in LDS: K <= 4096
     return fits(bits, spw, mt);
 }
 

@@ -118,11 +118,13 @@ def forward(x2, h, out=None, accumulate=False):
     return out if _abi.check(rc, "ep_dequant_matmul") else None
 
 
-def backward(gy2, x2, h, need_x=True, need_cb=True, need_scale=True):
-    """Fused backward; returns (grad_x, grad_cb, grad_scale) or None on decline."""
+def backward(gy2, x2, h, need_x=True, need_cb=True, need_scale=True, gx_dtype=None):
+    """Fused backward; returns (grad_x, grad_cb, grad_scale) or None on decline.
+
+    grad_x has ``gx_dtype`` (default: x's dtype)."""
     M, N = gy2.shape
     K = x2.shape[1]
-    gx = torch.empty((M, K), device=x2.device, dtype=x2.dtype) if need_x else None
+    gx = torch.empty((M, K), device=x2.device, dtype=gx_dtype or x2.dtype) if need_x else None
     G = (K + h.group - 1) // h.group
     gcb = torch.empty(h.levels, device=x2.device, dtype=torch.float32) if need_cb else None
     gsc = torch.empty((N, G), device=x2.device, dtype=torch.float32) if need_scale else None
@@ -134,7 +136,8 @@ def backward(gy2, x2, h, need_x=True, need_cb=True, need_scale=True):
         h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
         h.cb.data_ptr(), h.cb_dt, h.levels, h.group,
         M, N, K,
-        gx.data_ptr() if gx is not None else None, _abi.dtype_code(x2.dtype), K,
+        gx.data_ptr() if gx is not None else None,
+        _abi.dtype_code(gx.dtype if gx is not None else x2.dtype), K,
         gcb.data_ptr() if gcb is not None else None,
         gsc.data_ptr() if gsc is not None else None, G,
         ws.data_ptr() if ws is not None else None, ws_bytes, _abi.stream_handle(x2.device))

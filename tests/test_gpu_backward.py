@@ -52,9 +52,9 @@ def rel(a, b):
     return float((a.double() - b).abs().max() / b.abs().max())
 
 
-def run_bwd(s, gy, x):
+def run_bwd(s, gy, x, gx_dtype=torch.float32):
     h = cuda._hot(s)
-    r = cuda.backward(gy, x, h)
+    r = cuda.backward(gy, x, h, gx_dtype=gx_dtype)
     assert r is not None, _abi.last_error()
     torch.cuda.synchronize()
     return r
@@ -88,6 +88,8 @@ def test_backward_config4(n, k):
     assert before == after
     a = run_bwd(s, gy, x)
     assert all(torch.equal(p, q) for p, q in zip((gx, gcb, gsc), a))   # deterministic
+    gxb = run_bwd(s, gy, x, torch.bfloat16)[0]
+    assert rel(gxb.float(), wgx) < 2e-3 + 2.0 ** -8
 
 
 def test_autograd_through_packed_linear():
@@ -109,7 +111,7 @@ def test_autograd_through_packed_linear():
     w = cb64[both.reshape(n, k).long()] * sc64.repeat_interleave(128, 1)
     x64 = x.detach().double().requires_grad_(True)
     (x64 @ w.t()).backward(gy.double())
-    assert rel(x.grad.float(), x64.grad) < 2e-3
+    assert rel(x.grad.float(), x64.grad) < 2e-3 + 2.0 ** -8    # bf16 output
     assert rel(s.cb.grad, cb64.grad) < 1e-4
     assert rel(s.scale.grad, sc64.grad) < 1e-4
     assert verify_frozen(model, snap)
