@@ -109,55 +109,81 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
     const int t1 = min(t0 + kChunk, pos + 1);
     const float *cs = a.cos_t + (int64_t)pos * (D / 2);
     const float *sn = a.sin_t + (int64_t)pos * (D / 2);
+    const uint16_t *kbase = a.kcache + (int64_t)kvh * a.max_pos * D;
+    const uint16_t *vbase = a.vcache + (int64_t)kvh * a.max_pos * D;
+
+    // K and V tiles go out first: they depend only on the position.
+    // K: thread -> (position t/4, D/4-dim quarter t%4); V: thread ->
+    // (8-dim slice t%16, positions t/16 + 16 i).  Cache row `pos` is not read
+    // (this step's k/v come from the projections below).
+    const int ktl = t >> 2, kq = t & 3, kdn = D / 4;
+    const bool kok = t0 + ktl < t1 && t0 + ktl != pos;
+    u32x4_t kr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = kq * kdn + i * 8;
+        kr[i] = (kok && d < (kq + 1) * kdn)
+                    ? *(const u32x4_t *)(kbase + (int64_t)(t0 + ktl) * D + d)
+                    : (u32x4_t){0, 0, 0, 0};
+    }
+    const int vdc = t & 15, vpg = t >> 4;
+    u32x4_t vr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tl = vpg + 16 * i;
+        const bool ok = t0 + tl < t1 && t0 + tl != pos && vdc * 8 < D;
+        vr[i] = ok ? *(const u32x4_t *)(vbase + (int64_t)(t0 + tl) * D + vdc * 8)
+                   : (u32x4_t){0, 0, 0, 0};
+    }
 
     if (t < D)
         qs[t] = a.q[h * D + t];
-    norm_rope(qs, a.qn_w, a.qk_eps, cs, sn, D, scratch);
     const bool has_new = (c == nact - 1);
+    if (has_new && t < D) {
+        kn[t] = a.k[kvh * D + t];
+        vn[t] = bf16_round(a.v[kvh * D + t]);
+    }
+    norm_rope(qs, a.qn_w, a.qk_eps, cs, sn, D, scratch);
     if (has_new) {
-        if (t < D) {
-            kn[t] = a.k[kvh * D + t];
-            vn[t] = bf16_round(a.v[kvh * D + t]);
-        }
         norm_rope(kn, a.kn_w, a.qk_eps, cs, sn, D, scratch);
         if (t < D) {
-            const float kr = bf16_round(kn[t]);
-            kn[t] = kr;
+            const float kr16 = bf16_round(kn[t]);
+            kn[t] = kr16;
             if (h % group == 0) {
                 const int64_t row = ((int64_t)kvh * a.max_pos + pos) * D + t;
-                a.kcache[row] = f32_to_bf16(kr);
+                a.kcache[row] = f32_to_bf16(kr16);
                 a.vcache[row] = f32_to_bf16(vn[t]);
             }
         }
         __syncthreads();
     }
 
-    // scores: 4 threads per position, D/4 dims each
+    // scores
     {
-        const int tl = t >> 2, part = t & 3;
-        const int tp = t0 + tl;
+        const int tp = t0 + ktl;
         float s = 0.0f;
         if (tp < t1) {
-            const int dn = D / 4, d0 = part * dn;
+            const int d0 = kq * kdn;
             if (tp == pos) {
-                for (int d = d0; d < d0 + dn; ++d)
+                for (int d = d0; d < d0 + kdn; ++d)
                     s = fmaf(qs[d], kn[d], s);
             } else {
-                const uint16_t *kr = a.kcache + ((int64_t)kvh * a.max_pos + tp) * D + d0;
-                for (int d = 0; d < dn; d += 8) {
-                    const u32x4_t w = *(const u32x4_t *)(kr + d);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        s = fmaf(qs[d0 + d + 2 * e], __uint_as_float(w[e] << 16), s);
-                        s = fmaf(qs[d0 + d + 2 * e + 1], __uint_as_float(w[e] & 0xffff0000u), s);
+                for (int i = 0; i < 4; ++i)
+                    if (i * 8 < kdn) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int d = d0 + i * 8 + 2 * e;
+                            s = fmaf(qs[d], __uint_as_float(kr[i][e] << 16), s);
+                            s = fmaf(qs[d + 1], __uint_as_float(kr[i][e] & 0xffff0000u), s);
+                        }
                     }
-                }
             }
         }
         s += __shfl_xor(s, 1, 4);
         s += __shfl_xor(s, 2, 4);
-        if (part == 0)
-            sc[tl] = tp < t1 ? s * a.scale : -INFINITY;
+        if (kq == 0)
+            sc[ktl] = tp < t1 ? s * a.scale : -INFINITY;
     }
     __syncthreads();
     // chunk max / exp / sum (wave 0)
@@ -173,34 +199,32 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
         }
     }
     __syncthreads();
-    // o[d] = sum_t p[t] v[t][d]: 16 position groups x 16 eight-dim slices,
-    // one 16-byte load per (position, slice), then a fixed-order sum over
-    // the position groups.
-    {
-        const int dc = t & 15, pg = t >> 4;
+    // o[d] = sum_t p[t] v[t][d] from the V registers, then a fixed-order sum
+    // over the 16 position groups
+    if (vdc * 8 < D) {
         float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (dc * 8 < D) {
-            for (int tl = pg; t0 + tl < t1; tl += 16) {
-                const int tp = t0 + tl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tl = vpg + 16 * i;
+            const int tp = t0 + tl;
+            if (tp < t1) {
                 const float p = sc[tl];
                 if (tp == pos) {
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
-                        o[e] = fmaf(p, vn[dc * 8 + e], o[e]);
+                        o[e] = fmaf(p, vn[vdc * 8 + e], o[e]);
                 } else {
-                    const u32x4_t w = *(const u32x4_t *)(a.vcache +
-                                                         ((int64_t)kvh * a.max_pos + tp) * D + dc * 8);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        o[2 * e] = fmaf(p, __uint_as_float(w[e] << 16), o[2 * e]);
-                        o[2 * e + 1] = fmaf(p, __uint_as_float(w[e] & 0xffff0000u), o[2 * e + 1]);
+                        o[2 * e] = fmaf(p, __uint_as_float(vr[i][e] << 16), o[2 * e]);
+                        o[2 * e + 1] = fmaf(p, __uint_as_float(vr[i][e] & 0xffff0000u), o[2 * e + 1]);
                     }
                 }
             }
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                opart[pg][dc * 8 + e] = o[e];
         }
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            opart[vpg][vdc * 8 + e] = o[e];
     }
     __syncthreads();
     if (t < D) {

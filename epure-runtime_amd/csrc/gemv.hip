@@ -249,6 +249,10 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     float scA[SPW][RQ], scB[SPW][RQ];
     if (blk < nblk)
         load_block(blk, wqA, scA);  // in flight while the table and x are staged
+    // the codebook load goes out now too (its own round trip otherwise)
+    float cbv = 0.0f;
+    if (tid < a.levels)
+        cbv = load_as_f32(cbp, a.cb_dtype, tid);
 
     // ---- stage activations ----------------------------------------------
     // The workgroup converts the activation row(s) once, cooperatively: one
@@ -337,7 +341,8 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
 
     // codebook -> fp16 bits in LDS, then the pair table
     for (int i = tid; i < 256; i += blockDim.x)
-        s_cb[i] = i < a.levels ? f16_bits((f16_t)load_as_f32(cbp, a.cb_dtype, i)) : 0;
+        s_cb[i] = i < a.levels ? f16_bits((f16_t)(i == tid ? cbv : load_as_f32(cbp, a.cb_dtype, i)))
+                               : 0;
     if constexpr (XS == XS_RMSNORM) {
         const float v = wave_sum(ssq);
         if (lane == 0)
