@@ -11,7 +11,9 @@
 // Every kernel reads the decode position from device memory (state[0]), so
 // one captured HIP graph replays every step unchanged.  Split-work kernels
 // combine in the workgroup that arrives last on a per-item counter, which
-// that workgroup resets to 0 for the next replay (no memset in the graph).
+// that workgroup resets to 0 for the next replay (no memset in the graph);
+// the partials go through coherent agent-scope stores/loads rather than
+// device-scope fences (which would flush the XCD's L2).
 #include "ep_common.h"
 #include "ep_internal.h"
 
@@ -236,36 +238,35 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
     __syncthreads();
     float *pp = a.part + ((int64_t)h * (a.max_pos / kChunk) + c) * (D + 2);
     if (t < D)
-        pp[2 + t] = opart[0][t];
+        st_agent(pp + 2 + t, opart[0][t]);
     if (t == 0) {
-        pp[0] = scratch[4];
-        pp[1] = scratch[5];
+        st_agent(pp, scratch[4]);
+        st_agent(pp + 1, scratch[5]);
     }
     // publish, then the last chunk to arrive combines
-    __threadfence();
+    wait_stores();
     __syncthreads();
     if (t == 0)
-        s_last = atomicAdd(&a.counters[h], 1) == nact - 1;
+        s_last = counter_add(&a.counters[h], 1) == nact - 1;
     __syncthreads();
     if (!s_last)
         return;
-    __threadfence();
-    const float *base = a.part + (int64_t)h * (a.max_pos / kChunk) * (D + 2);
+    float *base = a.part + (int64_t)h * (a.max_pos / kChunk) * (D + 2);
     float M = -INFINITY;
     for (int j = 0; j < nact; ++j)
-        M = fmaxf(M, __builtin_nontemporal_load(base + (int64_t)j * (D + 2)));
+        M = fmaxf(M, ld_agent(base + (int64_t)j * (D + 2)));
     float L = 0.0f, o = 0.0f;
     for (int j = 0; j < nact; ++j) {
-        const float *pj = base + (int64_t)j * (D + 2);
-        const float w = __expf(__builtin_nontemporal_load(pj) - M);
-        L = fmaf(__builtin_nontemporal_load(pj + 1), w, L);
+        float *pj = base + (int64_t)j * (D + 2);
+        const float w = __expf(ld_agent(pj) - M);
+        L = fmaf(ld_agent(pj + 1), w, L);
         if (t < D)
-            o = fmaf(__builtin_nontemporal_load(pj + 2 + t), w, o);
+            o = fmaf(ld_agent(pj + 2 + t), w, o);
     }
     if (t < D)
         a.out[h * D + t] = f32_to_bf16(o / L);
     if (t == 0)
-        atomicExch(&a.counters[h], 0);
+        st_agent(&a.counters[h], 0);
 }
 
 struct HeadArgs {
@@ -410,21 +411,20 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
                 b = wv[w];
                 bi = wi[w];
             }
-        a.part_val[blockIdx.x] = b;
-        a.part_idx[blockIdx.x] = bi;
-        __threadfence();
-        s_last = atomicAdd(a.counter, 1) == (int)gridDim.x - 1;
+        st_agent(a.part_val + blockIdx.x, b);
+        st_agent(a.part_idx + blockIdx.x, bi);
+        wait_stores();
+        s_last = counter_add(a.counter, 1) == (int)gridDim.x - 1;
     }
     __syncthreads();
     if (!s_last)
         return;
-    __threadfence();
     // last workgroup: global argmax, next token, next embedding
     float b = -INFINITY;
     int bi = 0x7fffffff;
     for (int j = threadIdx.x; j < (int)gridDim.x; j += 256) {
-        const float v = __builtin_nontemporal_load(a.part_val + j);
-        const int i = __builtin_nontemporal_load(a.part_idx + j);
+        const float v = ld_agent(a.part_val + j);
+        const int i = ld_agent(a.part_idx + j);
         if (v > b || (v == b && i < bi)) {
             b = v;
             bi = i;
@@ -462,7 +462,7 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
         a.state[0] = pos + 1;
         a.state[1] = next;
         s_next = next;
-        atomicExch(a.counter, 0);
+        st_agent(a.counter, 0);
     }
     __syncthreads();
     const int next = s_next;

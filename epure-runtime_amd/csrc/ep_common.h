@@ -99,6 +99,27 @@ EP_DEV int row_exponent(float amax)
     return s;
 }
 
+// Cross-workgroup hand-off without device-scope fences.  On gfx950 a
+// device-scope fence writes back and invalidates the whole L2 of the XCD;
+// instead, values another workgroup will read are stored and loaded as
+// relaxed agent-scope atomics (coherent sc1 accesses), and the writer waits
+// for its stores to complete before it bumps the hand-off counter.
+template <typename T>
+EP_DEV void st_agent(T *p, T v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+EP_DEV T ld_agent(T *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+EP_DEV void wait_stores() { __builtin_amdgcn_s_waitcnt(0); }
+EP_DEV int counter_add(int *p, int v)
+{
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Sum over the 64 lanes of a wave (result valid in every lane).
 EP_DEV float wave_sum(float v)
 {
