@@ -38,6 +38,17 @@
 namespace ep {
 namespace {
 
+// Tuning knobs (compile-time; the defaults are the measured choice).
+#ifndef EP_GEMV_NT_LOADS
+#define EP_GEMV_NT_LOADS 1      // weight loads marked non-temporal (streamed once)
+#endif
+#ifndef EP_GEMV_RQ1
+#define EP_GEMV_RQ1 4           // row quads per block when a wave holds one slab
+#endif
+#ifndef EP_GEMV_PER_CU
+#define EP_GEMV_PER_CU 2        // workgroups per CU for one-slab variants
+#endif
+
 constexpr int kRepl = 64;                // table replicas (one per lane)
 constexpr int kTabDwords = 256 * kRepl;  // 64 KiB
 constexpr int kSlabBytes = 256;          // bytes of a row covered by 16 lanes
@@ -214,8 +225,12 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                 const int row = row0 + 4 * q + rq;
                 const uint32_t rs = row < N ? (uint32_t)row : 0u;
                 // 32-bit offsets: the host guarantees N * row_bytes < 2^31.
+#if EP_GEMV_NT_LOADS
                 wq[j][q] = __builtin_nontemporal_load(
                     (const u32x4_t *)(packed + (rs * (uint32_t)a.row_bytes + cbyte[j])));
+#else
+                wq[j][q] = *(const u32x4_t *)(packed + (rs * (uint32_t)a.row_bytes + cbyte[j]));
+#endif
                 soff[j][q] = rs * (uint32_t)a.lds + (uint32_t)gidx[j];
             }
         if (a.scale_dtype == EP_F16) {
@@ -515,7 +530,7 @@ __global__ void __launch_bounds__(256) gemv_generic_kernel(GemvArgs a)
 
 // Row quads per block for a given number of slabs per wave: keeps the
 // 16-byte loads in flight per lane (SPW * RQ, double-buffered) at 8.
-constexpr int rq_for(int spw) { return spw >= 8 ? 1 : (spw >= 4 ? 2 : 4); }
+constexpr int rq_for(int spw) { return spw >= 8 ? 1 : (spw >= 4 ? 2 : (spw >= 2 ? 4 : EP_GEMV_RQ1)); }
 
 // Activation registers (SPW * MT * pairs-per-chunk) stay within 64 VGPRs,
 // and several activation rows are served with one slab per wave (the other
@@ -572,6 +587,8 @@ int launch_xcap(GemvArgs a, int waves, hipStream_t stream)
     static_assert(lds <= 160 * 1024, "LDS budget");
     // persistent grid: as many workgroups per CU as LDS and registers allow
     int per_cu = (int)((160 * 1024) / lds);
+    if (per_cu > EP_GEMV_PER_CU)
+        per_cu = EP_GEMV_PER_CU;
     if (SPW >= 2 || MT >= 2)
         per_cu = 1;  // ~200+ VGPRs: one 8-wave workgroup per CU
     if (per_cu < 1)
