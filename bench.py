@@ -5,18 +5,23 @@ dequant-GEMV HBM bandwidth as a fraction of peak.
     python bench.py [--steps K] [--warmup W] [--config llama3-8b|qwen3-1.7b]
 
 One "step" is one decode token: a replay of the captured HIP graph of the
-whole decode step (32 layers x {fused q|k|v GEMV, attention, o GEMV, fused
-gate|up GEMV, down GEMV} + lm_head/argmax).  The prompt (128 random ids) is
-consumed first, untimed; then W warm-up tokens, then K timed tokens, with the
-device synchronised on both sides.  Weights are random-init in the packed
-format (synthetic data; no checkpoints offline).
+whole decode step -- the one-launch decode-step kernel (all 32 layers: fused
+q|k|v dequant-GEMV with RMSNorm, attention, o GEMV, gate|up GEMV with
+SwiGLU, down GEMV; grid barriers between phases) and the lm_head/argmax
+launch.  The prompt (128 random ids) is consumed first, untimed; then W
+warm-up tokens, then K timed tokens, with the device synchronised on both
+sides.  Weights are random-init in the packed format (synthetic data; no
+checkpoints offline).  --per-layer times the five-launches-per-layer path
+instead.
 
-The roofline entry is for the packed dequant-GEMV: the 128 GEMV launches of
-one step are captured into a second graph that is replayed K times between
-HIP events on the launch stream; achieved = packed bytes per step / time per
-replay.  The CPU baseline is the C restatement of the reference's Rust kernel
-(oracle/rowdot.c, kernel/src/lib.rs semantics) on one layer's 7 linears,
-scaled to the 224 linears of a step.
+The roofline entry is for the dominant kernel, the decode-step kernel: it is
+captured alone into a second graph (at the final position) and replayed K
+times between HIP events on the launch stream; achieved = its algorithmic
+bytes (packed indices + group scales + codebooks of the 224 linears, RMSNorm
+weights, and the KV rows attention reads at that position) / time per
+replay.  The CPU baseline is the C restatement of the reference's Rust
+kernel (oracle/rowdot.c, kernel/src/lib.rs semantics) on one layer's 7
+linears, scaled to the 224 linears of a step.
 """
 import argparse
 import json
@@ -43,6 +48,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--per-layer", action="store_true",
+                    help="five launches per layer instead of the one-launch step kernel")
     return ap.parse_args()
 
 
@@ -98,7 +105,7 @@ def main():
     print(f"# building {cfg.name} random weights (seed {args.seed})", file=sys.stderr, flush=True)
     w = random_weights(cfg, seed=args.seed, device=dev)
     total_steps = n_prompt - 1 + args.warmup + args.steps
-    dec = Decoder(w, total_steps + 2)
+    dec = Decoder(w, total_steps + 2, persistent=False if args.per_layer else None)
     import numpy as np
     prompt = np.random.Generator(np.random.PCG64(args.seed + 1)).integers(
         0, cfg.vocab, n_prompt).tolist()
@@ -119,12 +126,17 @@ def main():
     tok_s = args.steps / dt
     toks = dec.tokens[:n_prompt + args.warmup + args.steps].cpu().tolist()
 
-    # dequant-GEMV only: the step's packed GEMV launches, timed with events
+    if dec.step_failed():
+        raise RuntimeError("a grid barrier of the decode-step kernel timed out")
+
+    # dominant kernel alone: the layers of one step (one launch, or the 160
+    # per-layer launches), replayed at the final position between events on
+    # the launch stream
     stream = torch.cuda.current_stream()
     g = torch.cuda.CUDAGraph()
     torch.cuda.synchronize()
     with torch.cuda.graph(g):
-        dec.gemv_launches()
+        dec.layer_launches()
     g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -134,10 +146,14 @@ def main():
             g.replay()
         e1.record(stream)
     e1.synchronize()
-    gemv_ms = e0.elapsed_time(e1) / args.steps
+    kern_ms = e0.elapsed_time(e1) / args.steps
+    pos = int(dec.state[0].item())
     packed = w.packed_bytes()
-    n_gemv = 4 * cfg.layers
-    gemv_gbs = packed / (gemv_ms * 1e-3) / 1e9
+    norm_bytes = sum(t.numel() * 2 for L in w.layers
+                     for t in (L.attn_norm, L.mlp_norm, L.q_norm, L.k_norm) if t is not None)
+    kv_bytes = 2 * cfg.layers * cfg.n_kv * pos * cfg.head_dim * 2
+    alg = packed + norm_bytes + kv_bytes
+    kern_gbs = alg / (kern_ms * 1e-3) / 1e9
     resident = w.resident_bytes()
     step_ms = dt / args.steps * 1e3
 
@@ -164,16 +180,19 @@ def main():
             "step_hbm_gbs_resident": round(resident / (step_ms * 1e-3) / 1e9, 1),
             "step_frac_resident": round(resident / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "step_frac_packed": round(packed / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "gemv_ms_per_step": round(gemv_ms, 4),
-            "gemv_launches_per_step": n_gemv,
+            "layers_path": "per-layer launches" if args.per_layer else "one-launch step kernel",
+            "layers_ms_per_step": round(kern_ms, 4),
+            "layers_alg_bytes": alg,
+            "layers_kv_position": pos,
             "first_tokens": toks[n_prompt:n_prompt + 8],
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(gemv_gbs, 1),
+            "kernel": "decode_step_kernel" if not args.per_layer else "per-layer launches",
+            "achieved": round(kern_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+            "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
         },
     }

@@ -280,4 +280,68 @@ int ep_embed_token(const uint16_t *embed, const int *state, float *h, int H, voi
     return launch_embed(embed, state, h, H, (hipStream_t)stream);
 }
 
+size_t ep_decode_step_layer_bytes(void) { return decode_step_layer_bytes(); }
+
+size_t ep_decode_step_workspace(int H, int I, int Hq, int Hkv, int D, int max_pos)
+{
+    if (H < 1 || I < 1 || Hq < 1 || Hkv < 1 || D < 1 || max_pos < 1)
+        return 0;
+    return decode_step_workspace(H, I, Hq, Hkv, D, max_pos);
+}
+
+static StepDesc step_desc(int H, int I, int Hq, int Hkv, int D, int max_pos, int levels, int group,
+                          int scale_dtype, int cb_dtype)
+{
+    StepDesc d{};
+    d.H = H;
+    d.I = I;
+    d.Hq = Hq;
+    d.Hkv = Hkv;
+    d.D = D;
+    d.max_pos = max_pos;
+    d.levels = levels;
+    d.group = group;
+    d.scale_dtype = scale_dtype;
+    d.cb_dtype = cb_dtype;
+    return d;
+}
+
+int ep_decode_step_serves(int H, int I, int Hq, int Hkv, int D, int max_pos, int levels, int group,
+                          int scale_dtype, int cb_dtype)
+{
+    g_err[0] = 0;
+    if (H < 1 || I < 1 || Hq < 1 || Hkv < 1 || D < 1 || max_pos < 1 || group < 1)
+        return 0;
+    return decode_step_serves(step_desc(H, I, Hq, Hkv, D, max_pos, levels, group, scale_dtype,
+                                        cb_dtype)) == EP_OK;
+}
+
+int ep_decode_step(const void *layers, int n_layers, float *h, void *workspace,
+                   size_t workspace_bytes, const float *cos_t, const float *sin_t, const int *state,
+                   int H, int I, int Hq, int Hkv, int D, int max_pos, int levels, int group,
+                   int scale_dtype, int cb_dtype, float eps, float qk_eps, float att_scale,
+                   long long *trace, void *stream)
+{
+    g_err[0] = 0;
+    if (!layers || n_layers < 1 || !h || !workspace || !cos_t || !sin_t || !state || H < 1 ||
+        I < 1 || Hq < 1 || Hkv < 1 || D < 1 || max_pos < 1 || group < 1)
+        return set_error(EP_ERR_ARG, "decode step: bad arguments");
+    if (((uintptr_t)h | (uintptr_t)workspace) & 15)
+        return set_error(EP_ERR_ARG, "decode step: h/workspace not 16-byte aligned");
+    StepDesc d = step_desc(H, I, Hq, Hkv, D, max_pos, levels, group, scale_dtype, cb_dtype);
+    d.layers = layers;
+    d.n_layers = n_layers;
+    d.h = h;
+    d.ws = workspace;
+    d.ws_bytes = workspace_bytes;
+    d.cos_t = cos_t;
+    d.sin_t = sin_t;
+    d.state = state;
+    d.eps = eps;
+    d.qk_eps = qk_eps;
+    d.att_scale = att_scale;
+    d.trace = trace;
+    return launch_decode_step(d, (hipStream_t)stream);
+}
+
 }  // extern "C"

@@ -110,6 +110,26 @@ struct HeadDesc {
 int launch_lm_head(const HeadDesc &d, hipStream_t stream);
 int launch_embed(const uint16_t *embed, const int *state, float *h, int H, hipStream_t stream);
 
+// Persistent decode step (step.hip): every layer of one batch-1 step in one
+// launch.  `layers` points to n_layers device-side descriptors of
+// decode_step_layer_bytes() each.
+struct StepDesc {
+    const void *layers;
+    int n_layers;
+    float *h;   // [H] f32 in (embedding) / out (final residual)
+    void *ws;   // decode_step_workspace() bytes, zeroed before the first launch
+    size_t ws_bytes;
+    const float *cos_t, *sin_t;
+    const int *state;
+    int H, I, Hq, Hkv, D, max_pos, levels, group, scale_dtype, cb_dtype;
+    float eps, qk_eps, att_scale;
+    long long *trace;
+};
+int launch_decode_step(const StepDesc &d, hipStream_t stream);
+int decode_step_serves(const StepDesc &d);
+size_t decode_step_workspace(int H, int I, int Hq, int Hkv, int D, int max_pos);
+size_t decode_step_layer_bytes();
+
 int launch_mfma(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,
                 void *ws, size_t ws_bytes, hipStream_t stream);
 bool mfma_serves(const PackedDesc &w, const ActDesc &x, int64_t M);

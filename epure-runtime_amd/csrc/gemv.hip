@@ -34,6 +34,7 @@
 
 #include "ep_common.h"
 #include "ep_internal.h"
+#include "gemv_core.h"
 
 namespace ep {
 namespace {
@@ -49,9 +50,6 @@ namespace {
 #define EP_GEMV_PER_CU 2        // workgroups per CU for one-slab variants
 #endif
 
-constexpr int kRepl = 64;                // table replicas (one per lane)
-constexpr int kTabDwords = 256 * kRepl;  // 64 KiB
-constexpr int kSlabBytes = 256;          // bytes of a row covered by 16 lanes
 constexpr int kMaxWaves = 8;   // 512 threads: up to 256 VGPRs per lane
 constexpr int kMaxSeg = 3;
 
@@ -91,71 +89,6 @@ struct GemvArgs {
     int nseg;
     Seg seg[kMaxSeg];
 };
-
-// Pair table from the codebook's fp16 bits staged in LDS (cb16[l] = 0 for
-// l >= levels, matching the Rust LUT's zeros).
-template <int BITS>
-EP_DEV void build_table(uint32_t *tab, const uint16_t *cb16)
-{
-    for (int e4 = threadIdx.x; e4 < kTabDwords / 4; e4 += blockDim.x) {
-        const int b = (e4 * 4) / kRepl;
-        uint32_t v;
-        if constexpr (BITS == 4) {
-            v = (uint32_t)cb16[b & 15] | ((uint32_t)cb16[b >> 4] << 16);
-        } else {
-            const uint32_t h = cb16[b];
-            v = h | (h << 16);
-        }
-        ((u32x4_t *)tab)[e4] = (u32x4_t){v, v, v, v};
-    }
-}
-
-// v_perm selectors building the LDS byte address (byte_i << 8) | lane4:
-// result byte0 = lane4 (src1 byte 0), byte1 = byte i of the packed word
-// (src0 byte i = selector 4 + i), bytes 2-3 = 0 (selector 12).
-constexpr uint32_t kSelByte[4] = {0x0c0c0400u, 0x0c0c0500u, 0x0c0c0600u, 0x0c0c0700u};
-
-EP_DEV uint32_t lds_read_u32(const uint32_t *base, uint32_t byte_addr)
-{
-    return *(const uint32_t *)((const char *)base + byte_addr);
-}
-
-template <int CTRL>
-EP_DEV float dpp_f(float v)
-{
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-// Sum over the 16 lanes of a DPP row (lanes 16r..16r+15), in every lane:
-// row_ror 8, row_ror 4, quad_perm [2,3,0,1], quad_perm [1,0,3,2].
-EP_DEV float row16_sum(float v)
-{
-    v += dpp_f<0x128>(v);
-    v += dpp_f<0x124>(v);
-    v += dpp_f<0x4e>(v);
-    v += dpp_f<0xb1>(v);
-    return v;
-}
-
-// Two raw 16-bit activations (bf16 or fp16, per XDT) -> floats.
-template <int XDT>
-EP_DEV void unpack_pair(uint32_t raw, float &lo, float &hi)
-{
-    if constexpr (XDT == EP_BF16) {
-        lo = __uint_as_float(raw << 16);
-        hi = __uint_as_float(raw & 0xffff0000u);
-    } else {
-        lo = (float)f16_from_bits((uint16_t)(raw & 0xffffu));
-        hi = (float)f16_from_bits((uint16_t)(raw >> 16));
-    }
-}
-
-// silu(g) * u with the hardware reciprocal (about 1 ulp; the result is
-// rounded to fp16 right after, so a correctly rounded divide buys nothing).
-EP_DEV float silu_mul(float g, float u)
-{
-    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
-}
 
 template <int BITS, int MT, int RQ, int SPW, int XDT, int XS, bool DB, int XCAP>
 __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)

@@ -1,0 +1,1375 @@
+// Persistent batch-1 decode step for gfx950: one launch runs every layer of
+// a decoder step (the caller side of the packed linears; the reference runs
+// it through transformers with each q/k/v/o/gate/up/down a PackedLinear,
+// epure/runtime.py:92-126, :373-415, one fused-kernel call per linear,
+// epure/kernels/cuda.py:88-117).
+//
+// Why one launch: at batch 1 a layer moves ~112 MB of packed weights
+// (Llama-3-8B shape), i.e. ~14 us at 8 TB/s, while a separate launch per
+// linear pays its own ramp, prologue and drain (several us each).  Here one
+// workgroup per CU stays resident for the whole step; the phases of a layer
+//
+//     qkv GEMV (RMSNorm in the activation load) -> attention ->
+//     o GEMV (+= residual) -> gate|up GEMV (RMSNorm; SwiGLU at the output) ->
+//     down GEMV (+= residual)
+//
+// follow each other without grid barriers: every workgroup issues the loads
+// of its share of the NEXT phase's packed weights (which do not depend on
+// activations) and builds that phase's LDS pair tables, then waits for the
+// activations it needs, so HBM keeps streaming through each dependency.
+//
+// Cross-workgroup data (residual, q/k/v, attention output, SwiGLU output,
+// split-KV partials) is tagged: each 32-bit value is stored together with a
+// 32-bit tag (launch sequence, layer, phase) in one coherent 8-byte store,
+// and a consumer re-reads (coherent sc1 loads) until every tag it needs is
+// current.  A phase transition is then one memory round trip -- no store
+// completion wait, counter or barrier -- and no device-scope fence is used
+// (on gfx950 that writes back and invalidates the XCD's whole L2).  The
+// phases' data dependencies are all-to-all, so a buffer is never rewritten
+// while a consumer of its previous contents is still reading.  The launch
+// sequence advances when the last workgroup finishes; every wait is bounded:
+// a wait that outlasts ~0.1 s marks the step failed (sync[2]) and all
+// waits then give up, so the grid always drains.
+//
+// GEMV arithmetic is the LUT dequant-GEMV of gemv.hip (pair table per
+// codebook, v_dot2_f32_f16 with f32 accumulation, group scale per 32
+// weights, DPP row sums, fixed-order cross-wave sums: deterministic), with
+// the activations compensated: after an exact power-of-two factor per 32
+// values each activation is split into two fp16 terms, hi = fp16(x) and
+// lo = fp16(x - hi) (~22 significant bits together), and every table lookup
+// feeds two dot products.  The codebook entries are exact fp16 values, so
+// the GEMV then agrees with float32 arithmetic to f32 accumulation order,
+// which keeps bf16 storage roundings downstream (KV rows, attention output)
+// on the same side as a float32 reference's.
+#include "ep_common.h"
+#include "ep_internal.h"
+#include "gemv_core.h"
+
+namespace ep {
+namespace {
+
+constexpr int kThreads = 512;
+constexpr int kWaves = 8;
+constexpr int kSpinLimit = 1 << 16;  // polls (~1-2 us each) before the step fails
+constexpr int kD = 128;              // head_dim served
+constexpr int kChunk = 64;           // KV positions per attention item (8 waves x 8)
+constexpr int kEvents = 16;          // trace events per layer (debug)
+
+// Geometry of a GEMV phase whose rows are S 256-byte slabs long: waves per
+// row group (WPR), row groups per workgroup (RG) and slabs per wave (SPW).
+// All 8 waves busy where possible, at most 4 slabs (64 activation VGPRs) per
+// wave.
+constexpr int geo_wpr(int S)
+{
+    return (S % 8 == 0 && S / 8 <= 4)   ? 8
+           : (S <= 4 && 8 % S == 0)     ? S
+           : (S % 4 == 0 && S / 4 <= 4) ? 4
+           : (S % 7 == 0 && S / 7 <= 4) ? 7
+                                        : 8;
+}
+constexpr int geo_rg(int S) { return 8 % geo_wpr(S) == 0 ? 8 / geo_wpr(S) : 1; }
+constexpr int geo_spw(int S) { return (S + geo_wpr(S) - 1) / geo_wpr(S); }
+constexpr int imax(int a, int b) { return a > b ? a : b; }
+
+// A decoder shape served by the persistent step.  RQ_* = row quads per row
+// group per block of each GEMV phase (blocks are pipelined three deep, the
+// first two issued before the phase's barrier); MQ_* = the most row quads a
+// workgroup's share of the phase may hold (the LDS accumulator is sized by
+// it; the launch checks it against the grid).
+template <int H_, int HQD_, int I_, int GQ_, int RQ_QKV_, int RQ_O_, int RQ_GU_, int RQ_D_,
+          int MQ_QKV_, int MQ_O_, int MQ_GU_, int MQ_D_>
+struct Model {
+    static constexpr int H = H_, HQD = HQD_, I = I_, GQ = GQ_;
+    static constexpr int SH = H / 512, SO = HQD / 512, SI = I / 512;
+    static constexpr int RQ_QKV = RQ_QKV_, RQ_O = RQ_O_, RQ_GU = RQ_GU_, RQ_D = RQ_D_;
+    static constexpr int MQ_QKV = MQ_QKV_, MQ_O = MQ_O_, MQ_GU = MQ_GU_, MQ_D = MQ_D_;
+    // Per phase the region holds: activations as fp16 pairs (K / 2 dwords),
+    // their lo terms (same size; the down phase, which uses one table, keeps
+    // them in the second table slot instead), one factor per 32 values, then
+    // the accumulator [8 waves][rows].
+    static constexpr int phase_bytes(int K, int red, bool lo) { return (lo ? K * 4 : K * 2) + K / 32 * 4 + red; }
+    // attention scratch: q [GQ][D], k, v [D], S [GQ][256], m, l [GQ], o [8][GQ][D]
+    static constexpr int ATT_BYTES =
+        (GQ * kD + 2 * kD + GQ * kChunk + 2 * GQ + kWaves * GQ * kD) * 4 + 16;
+    static constexpr int REGION =
+        imax(imax(imax(phase_bytes(H, kWaves * 4 * MQ_QKV * 4, true),
+                       phase_bytes(HQD, kWaves * 4 * MQ_O * 4, true)),
+                  imax(phase_bytes(H, kWaves * 8 * MQ_GU * 4, true),
+                       phase_bytes(I, kWaves * 4 * MQ_D * 4, false))),
+             ATT_BYTES);
+    static_assert(I * 2 <= kTabBytes, "down-phase lo terms fit a table slot");
+    static constexpr int LDS = 2 * kTabBytes + REGION + 32 * 2 + 16 * 4 + 64 * 4;
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    static_assert(H % 512 == 0 && HQD % 512 == 0 && I % 512 == 0, "rows of whole slabs");
+};
+
+// Llama-3-8B and Qwen3-1.7B (config 1) shapes; shares
+// at 256 workgroups: q|k|v 6 / 4 quads, o 4 / 2, gate|up 14 / 6, down 4 / 2.
+using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 1, 6, 4, 14, 4>;
+using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 2, 6, 2>;
+
+// Where a phase of contraction length K keeps its activations, factors and
+// accumulator inside the region.
+struct PhaseLds {
+    uint32_t *xs, *xl;  // hi and lo terms, fp16 pairs
+    float *xf, *red;
+};
+EP_DEV PhaseLds phase_lds(char *region, int K, uint32_t *lo_elsewhere = nullptr)
+{
+    PhaseLds p;
+    const int lo = lo_elsewhere ? 0 : K * 2;
+    p.xs = (uint32_t *)region;
+    p.xl = lo_elsewhere ? lo_elsewhere : (uint32_t *)(region + K * 2);
+    p.xf = (float *)(region + K * 2 + lo);
+    p.red = (float *)(region + K * 2 + lo + K / 32 * 4);
+    return p;
+}
+
+// ---------------------------------------------------------------- memory
+// Global-address-space accesses.  A generic (flat) access may complete out
+// of order with other vector memory operations, so the compiler waits for
+// ALL loads in flight (vmcnt(0)) before using any flat load's result -- which
+// would drain the weight prefetch.  Every device-memory access here is
+// therefore global (address space 1) or a buffer access.
+template <class T>
+EP_DEV T ldg(const T *p)
+{
+    return *(const __attribute__((address_space(1))) T *)p;
+}
+template <class T>
+EP_DEV void stg(T *p, T v)
+{
+    *(__attribute__((address_space(1))) T *)p = v;
+}
+EP_DEV float ldg_as_f32(const void *p, int dt, int64_t i)
+{
+    if (dt == EP_F32)
+        return ldg((const float *)p + i);
+    if (dt == EP_F16)
+        return (float)f16_from_bits(ldg((const uint16_t *)p + i));
+    return bf16_to_f32(ldg((const uint16_t *)p + i));
+}
+
+// Buffer descriptor of a wave-uniform base pointer.  The base goes through
+// readfirstlane so the descriptor is known to live in scalar registers (a
+// descriptor the compiler cannot prove uniform turns every load into a
+// per-lane waterfall loop).
+EP_DEV __amdgpu_buffer_rsrc_t rsrc(const void *p, uint32_t bytes = 0x7fffffffu)
+{
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
+                                             (int)__builtin_amdgcn_readfirstlane(bytes),
+                                             0x00020000);
+}
+// 16-byte load with sc1 (coherent at agent scope: sees other XCDs' sc1 stores).
+EP_DEV u32x4_t ldc16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 16);
+}
+EP_DEV float ldc_f32(const float *p) { return ld_agent(const_cast<float *>(p)); }
+
+// Tagged values: value bits in the low word, tag in the high word.
+constexpr int PH_QKV = 0, PH_ATT = 1, PH_PART = 2, PH_O = 3, PH_ACT = 4, PH_DOWN = 5;
+EP_DEV uint32_t tag_of(uint32_t seq, int layer, int phase)
+{
+    return (seq << 10) | (uint32_t)(layer * 8 + phase + 1);  // never 0 (zeroed buffers)
+}
+EP_DEV void st_tag(uint64_t *p, uint32_t bits, uint32_t tag)
+{
+    st_agent(p, (uint64_t)bits | ((uint64_t)tag << 32));
+}
+EP_DEV uint64_t ld_tag(const uint64_t *p) { return ld_agent(const_cast<uint64_t *>(p)); }
+
+// Bounded wait: `again` sleeps briefly and returns true while the caller
+// should keep polling.  After kSpinLimit polls it marks the step failed;
+// any wait also gives up once the step is marked failed.
+struct Spin {
+    int it = 0;
+    EP_DEV bool again(int *err)
+    {
+        if (++it > kSpinLimit) {
+            st_agent(err, 1);
+            return false;
+        }
+        if ((it & 31) == 0 && ld_agent(err) != 0)
+            return false;
+        __builtin_amdgcn_s_sleep(1);
+        return true;
+    }
+};
+
+// One tagged f32 value (polled until its tag is current).
+EP_DEV float ld_tag_f32(const uint64_t *p, uint32_t tag, int *err)
+{
+    Spin sp;
+    uint64_t v = ld_tag(p);
+    while ((uint32_t)(v >> 32) != tag && sp.again(err))
+        v = ld_tag(p);
+    return __uint_as_float((uint32_t)v);
+}
+
+// threadIdx.x through an opaque move: values derived from it are recomputed
+// per phase instead of being hoisted out of the layer loop and kept live
+// (registers) for the whole step.
+EP_DEV int tid_fresh()
+{
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+// Wave index in a scalar register (buffer descriptors built from it stay
+// uniform).
+EP_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(tid_fresh() >> 6); }
+
+// ---------------------------------------------------------------- segments
+// The virtual row-quad space of one GEMV phase of a layer: up to three
+// weights stacked (q|k|v), or a gate/up pair sharing quad indices.
+struct Segs {
+    const uint8_t *pk0, *pk1, *pk2;
+    const char *sc0, *sc1, *sc2;
+    const void *cb0, *cb1, *cb2;
+    uint64_t *y0, *y1, *y2;  // tagged outputs (q|k|v phase)
+    int q1, q2;    // first virtual quad of segments 1 and 2 (INT_MAX: absent)
+    int nq;        // virtual quads
+    int qa, qb;    // this workgroup's share [qa, qb)
+    int sfirst;    // segment of quad qa (LDS table slot 0)
+    int ntab;      // tables the share needs (1 or 2)
+    int ldsb;      // scale row bytes (fp16 scales)
+};
+
+template <class T>
+EP_DEV T sel3(int s, T a, T b, T c)
+{
+    return s == 0 ? a : (s == 1 ? b : c);
+}
+
+EP_DEV void share(Segs &g, int b, int G, bool paired)
+{
+    g.qa = (int)((int64_t)b * g.nq / G);
+    g.qb = (int)((int64_t)(b + 1) * g.nq / G);
+    if (paired) {
+        g.sfirst = 0;
+        g.ntab = 2;
+    } else {
+        g.sfirst = g.qa >= g.q2 ? 2 : (g.qa >= g.q1 ? 1 : 0);
+        const int nxt = g.sfirst == 0 ? g.q1 : (g.sfirst == 1 ? g.q2 : 0x7fffffff);
+        g.ntab = (g.qb > g.qa && g.qb - 1 >= nxt) ? 2 : 1;
+    }
+}
+
+// ---------------------------------------------------------------- layer
+struct StepLayer {
+    const uint8_t *packed[7];  // q, k, v, o, gate, up, down
+    const void *scale[7];      // fp16 [N][K / group]
+    const void *cb[7];         // [levels] f32 or fp16
+    const uint16_t *attn_norm, *mlp_norm, *q_norm, *k_norm;  // bf16 (q/k norm may be null)
+    uint16_t *kcache, *vcache;  // [Hkv][max_pos][D] bf16
+};
+
+struct StepArgs {
+    const StepLayer *layers;
+    int n_layers;
+    float *h0;          // [H] f32: the step's input embedding; the final residual on exit
+    uint64_t *ht;       // [H] tagged residual
+    uint64_t *qt, *kt, *vt;  // [Hq * D], [Hkv * D], [Hkv * D] tagged f32
+    uint64_t *at;       // [Hq * D / 2] tagged bf16 pairs: attention output
+    uint64_t *actt;     // [I] tagged f32: silu(gate) * up
+    uint64_t *part;     // [Hq][max_pos / kChunk + 1][D + 2] tagged split-KV partials
+    int *sync;          // [0] finished workgroups, [1] launch sequence, [2] error flag
+    const float *cos_t, *sin_t;  // [max_pos][D / 2]
+    const int *state;            // [0] position
+    int Hkv, max_pos, levels, group, cb_dtype;
+    float eps, qk_eps, att_scale;
+    long long *trace;  // optional [layers][kEvents][grid] wall-clock stamps
+};
+
+// ---------------------------------------------------------------- GEMV phase
+constexpr int MODE_STORE = 0;   // y_seg[row] = dot * rinv
+constexpr int MODE_ACC = 1;     // h[row] += dot
+constexpr int MODE_SWIGLU = 2;  // act[row] = silu(gate * rinv) * (up * rinv)
+
+// One GEMV phase.  A workgroup's share [qa, qb) of virtual row quads (at
+// most MAXQ) is cut into blocks of QPB quads; lane (wave, lane) covers row
+// 4 q + (lane >> 4) of each quad q of its row group, 16 bytes (32 weights)
+// of each of its slabs.  Blocks are pipelined three deep: blocks 0 and 1
+// are issued by the caller (before the barrier), block i + 2 while block i
+// is computed.  Waves run their blocks independently: each row's 16-lane
+// sum goes to an LDS accumulator (one slot per wave and row), and the
+// cross-wave sums and outputs are formed once, after the last block.
+template <int S, int RQ, bool PAIRED, int MAXQ>
+struct Gemv {
+    static constexpr int WPR = geo_wpr(S), RG = geo_rg(S), SPW = geo_spw(S);
+    static constexpr int NQ = PAIRED ? 2 * RQ : RQ;  // row quads per lane per block
+    static constexpr int QPB = RG * RQ;              // virtual quads per block
+    static constexpr int RB = S * kSlabBytes;        // packed row bytes
+    static constexpr bool XREG = SPW == 1;           // activations held in registers
+    static constexpr int NPAIR = PAIRED ? 2 : 1;
+    static constexpr int RED_ROWS = 4 * MAXQ * NPAIR;  // accumulator slots per wave
+    static constexpr int RED_BYTES = kWaves * RED_ROWS * 4;
+    // fp16 scales a wave needs per block: NQ quads x SPW slabs x 4 rows x up
+    // to 4 groups per slab (group >= 128) -- one 2-byte load per lane
+    static_assert(NQ * SPW * 4 * 4 <= 64, "one scale load per wave and block");
+    static_assert(RG * WPR <= kWaves, "waves");
+
+    struct Blk {
+        u32x4_t w[SPW][NQ];
+        uint32_t s;  // one fp16 scale (bits) per lane, spread to the lanes that
+                     // use it at compute time; converted there (a conversion
+                     // right after the load would wait for every load in flight)
+    };
+
+    // This lane's place in the phase (cheap; recomputed where needed so it
+    // holds no registers across phases).
+    static EP_DEV bool wave_on(int wv) { return wv / WPR < RG; }
+    static EP_DEV bool slab_on(int j, int wv) { return wave_on(wv) && (wv % WPR) + j * WPR < S; }
+    static EP_DEV int slab(int j, int wv) { return slab_on(j, wv) ? (wv % WPR) + j * WPR : 0; }
+    // byte offset of the lane's 16-byte chunk of slab j within a row
+    static EP_DEV uint32_t chunk_byte(int j, int wv)
+    {
+        return (uint32_t)(slab(j, wv) * kSlabBytes + (tid_fresh() & 15) * 16);
+    }
+
+    static EP_DEV int nblocks(const Segs &sg) { return (sg.qb - sg.qa + QPB - 1) / QPB; }
+
+    // Virtual quad of slot i of the block starting at virtual quad vb.
+    static EP_DEV int vquad(int vb, int i, int wv)
+    {
+        return vb + (wv / WPR) * RQ + (PAIRED ? (i % RQ) : i);
+    }
+    static EP_DEV int seg_of(const Segs &sg, int vq, int i)
+    {
+        if constexpr (PAIRED)
+            return i >= RQ ? 1 : 0;
+        else
+            return vq >= sg.q2 ? 2 : (vq >= sg.q1 ? 1 : 0);
+    }
+    static EP_DEV int first_quad(const Segs &sg, int s)
+    {
+        return PAIRED ? 0 : (s == 2 ? sg.q2 : (s == 1 ? sg.q1 : 0));
+    }
+    // groups of a 256-byte slab (512 weights); group >= 128
+    static EP_DEV int gps(int group) { return group >= 512 ? 1 : 512 / group; }
+
+    // Issues the packed-weight loads of block bi (non-temporal: every weight
+    // byte is read once per step) and the wave's one scale load.  Buffer
+    // loads for the weights: the quad's base is a scalar offset, the lane's
+    // place a 32-bit vector offset.  Nothing is loaded for a block past the
+    // share or by an idle wave (the block is then never read); a quad past
+    // the share reads the segment's first quad and an idle slab reads slab
+    // 0 -- both are weighted 0 at use -- so the loads carry no branch.
+    static EP_DEV void issue(Blk &bk, const Segs &sg, int bi, int group)
+    {
+        const int wv = wave_id();
+        if (bi >= nblocks(sg) || !wave_on(wv))
+            return;
+        const int vb = sg.qa + bi * QPB;
+        const int lane = tid_fresh() & 63;
+        const uint32_t rq = (uint32_t)lane >> 4;
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) {
+            const int vq = vquad(vb, i, wv);
+            const bool ok = vq < sg.qb;
+            const int s = seg_of(sg, ok ? vq : sg.qa, i);
+            const int quad = ok ? vq - first_quad(sg, s) : 0;
+            const auto rp = rsrc(sel3(s, sg.pk0, sg.pk1, sg.pk2));
+            const int sp = quad * 4 * RB;
+#pragma unroll
+            for (int j = 0; j < SPW; ++j)
+                bk.w[j][i] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rp, (int)(rq * RB + chunk_byte(j, wv)), sp, 2);
+        }
+        // scale entry n = ((j * NQ + i) * 4 + r) * G + g of this lane
+        const int G = gps(group);
+        int n = lane;
+        const int g = n % G;
+        n /= G;
+        const int r = n % 4;
+        n /= 4;
+        const int i = n % NQ, j = n / NQ;
+        const bool live = j < SPW;
+        const int vq = vquad(vb, live ? i : 0, wv);
+        const bool ok = live && vq < sg.qb;
+        const int s = seg_of(sg, ok ? vq : sg.qa, live ? i : 0);
+        const int row = ok ? (vq - first_quad(sg, s)) * 4 + r : 0;
+        const int gi = ok ? (slab(j, wv) * 512) / group + g : 0;
+        const char *sc = sel3(s, sg.sc0, sg.sc1, sg.sc2) + (int64_t)row * sg.ldsb + gi * 2;
+        bk.s = ldg((const uint16_t *)sc);
+    }
+
+    // Runs the share; outputs are tagged (`tag`).  MODE_ACC adds the share's
+    // residual rows (hv, one per thread, loaded with the staging) and writes
+    // the sum to ht (and to h0 when `last`).
+    template <int MODE>
+    static EP_DEV void run(Blk &b0, Blk &b1, const Segs &sg, int group, const uint32_t *tab,
+                           const uint32_t *xs, const uint32_t *xlo, const float *xf, float *red,
+                           float *hrow, float hv, float rinv, uint64_t *ht, float *h0, bool last,
+                           uint64_t *act, uint32_t tag)
+    {
+        // activations (hi and lo terms): in registers for one slab per wave
+        // (32 VGPRs); with more slabs per wave they are read from LDS at use
+        f16x2_t xh[XREG ? SPW : 1][32];
+        const int wv = wave_id();
+        if constexpr (XREG) {
+#pragma unroll
+            for (int j = 0; j < SPW; ++j) {
+                const uint32_t xo = chunk_byte(j, wv);  // pair index = byte index
+#pragma unroll
+                for (int p = 0; p < 16; p += 4) {
+                    const u32x4_t q4 = *(const u32x4_t *)(xs + xo + p);
+                    const u32x4_t l4 = *(const u32x4_t *)(xlo + xo + p);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        xh[j][p + t] = as_f16x2(q4[t]);
+                        xh[j][16 + p + t] = as_f16x2(l4[t]);
+                    }
+                }
+            }
+        }
+        // residual rows of the share (loaded by the caller with the staging)
+        if constexpr (MODE == MODE_ACC) {
+            if (tid_fresh() < (sg.qb - sg.qa) * 4)
+                hrow[tid_fresh()] = hv;
+        }
+        // three buffers rotated by unrolling (a register copy of a block
+        // would wait for its loads)
+        const int nb = nblocks(sg);
+        Blk b2;
+        for (int bi = 0; bi < nb; bi += 3) {
+            issue(b2, sg, bi + 2, group);
+            block(b0, sg, bi, group, xh, xs, xlo, xf, tab, red);
+            if (bi + 1 >= nb)
+                break;
+            issue(b0, sg, bi + 3, group);
+            block(b1, sg, bi + 1, group, xh, xs, xlo, xf, tab, red);
+            if (bi + 2 >= nb)
+                break;
+            issue(b1, sg, bi + 4, group);
+            block(b2, sg, bi + 2, group, xh, xs, xlo, xf, tab, red);
+        }
+        __syncthreads();
+        // cross-wave sums (fixed order) and outputs, one thread per row
+        const int t = tid_fresh();
+        const int nrow = (sg.qb - sg.qa) * 4;
+        if (t < nrow) {
+            const int q = t / 4;
+            const int gg = (q % QPB) / RQ;  // row group that computed the row
+            float v = 0.0f, u = 0.0f;
+#pragma unroll
+            for (int wr = 0; wr < WPR; ++wr) {
+                v += red[(gg * WPR + wr) * RED_ROWS + t];
+                if constexpr (PAIRED)
+                    u += red[(gg * WPR + wr) * RED_ROWS + RED_ROWS / 2 + t];
+            }
+            const int row = sg.qa * 4 + t;
+            if constexpr (MODE == MODE_STORE) {
+                const int vq = sg.qa + q;
+                const int s = vq >= sg.q2 ? 2 : (vq >= sg.q1 ? 1 : 0);
+                st_tag(sel3(s, sg.y0, sg.y1, sg.y2) + (row - first_quad(sg, s) * 4),
+                       __float_as_uint(v * rinv), tag);
+            } else if constexpr (MODE == MODE_ACC) {
+                const float hn = hrow[t] + v;
+                st_tag(ht + row, __float_as_uint(hn), tag);
+                if (last)
+                    stg(h0 + row, hn);  // the lm_head's input (read by a later launch)
+            } else {
+                st_tag(act + row, __float_as_uint(silu_mul(v * rinv, u * rinv)), tag);
+            }
+        }
+        __syncthreads();  // LDS (tables, accumulator) free for the next phase
+    }
+
+    // Dot products of one block; each row's sum into the LDS accumulator.
+    static EP_DEV void block(const Blk &bk, const Segs &sg, int bi, int group,
+                             const f16x2_t (&xh)[XREG ? SPW : 1][32], const uint32_t *xs,
+                             const uint32_t *xlo, const float *xf, const uint32_t *tab, float *red)
+    {
+        const int lane = tid_fresh() & 63, wave = wave_id();
+        const int rq = lane >> 4, c = lane & 15;
+        const uint32_t lane4 = (uint32_t)lane << 2;
+        const int vb = sg.qa + bi * QPB;
+        const int G = gps(group);
+        const int gl = group >= 512 ? 0 : (c * 32) / group;  // this lane's group within its slab
+        if (!wave_on(wave))
+            return;
+        float acc[NQ];
+#pragma unroll
+        for (int i = 0; i < NQ; ++i)
+            acc[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < SPW; ++j) {
+            if (!slab_on(j, wave))
+                continue;
+            const uint32_t xo = chunk_byte(j, wave);
+            const float fxj = xf[xo / 16];
+            f16x2_t xl[32];  // hi terms, then lo terms
+#pragma unroll
+            for (int p = 0; p < 16; p += 4) {
+                if constexpr (XREG) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        xl[p + t] = xh[j][p + t];
+                        xl[16 + p + t] = xh[j][16 + p + t];
+                    }
+                } else {
+                    const u32x4_t q4 = *(const u32x4_t *)(xs + xo + p);
+                    const u32x4_t l4 = *(const u32x4_t *)(xlo + xo + p);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        xl[p + t] = as_f16x2(q4[t]);
+                        xl[16 + p + t] = as_f16x2(l4[t]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < NQ; ++i) {
+                const int vq = vquad(vb, i, wave);
+                const int slot =
+                    PAIRED ? (i >= RQ ? 1 : 0) : (vq < sg.qb ? seg_of(sg, vq, i) - sg.sfirst : 0);
+                const uint32_t l4s = lane4 | ((uint32_t)slot << 16);
+                // the 16 lookups of the chunk are issued back to back, then
+                // consumed (source order is kept where registers are tight)
+                uint32_t tv[16];
+#pragma unroll
+                for (int wd = 0; wd < 4; ++wd)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        tv[wd * 4 + q] = lds_read_u32(
+                            tab, __builtin_amdgcn_perm(bk.w[j][i][wd], l4s, kSelByteSlot[q]));
+                float part = 0.0f, plo = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    part = __builtin_amdgcn_fdot2(as_f16x2(tv[k]), xl[k], part, false);
+                    plo = __builtin_amdgcn_fdot2(as_f16x2(tv[k]), xl[16 + k], plo, false);
+                }
+                part += plo;
+                const uint32_t sb = (uint32_t)__shfl((int)bk.s, ((j * NQ + i) * 4 + rq) * G + gl, 64);
+                const float sc = vq < sg.qb ? (float)f16_from_bits((uint16_t)sb) : 0.0f;
+                acc[i] = fmaf(part, sc * fxj, acc[i]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) {
+            const float v = row16_sum(acc[i]);
+            const int vq = vquad(vb, i, wave);
+            if (c == 0 && vq < sg.qb)
+                red[wave * RED_ROWS + (PAIRED && i >= RQ ? RED_ROWS / 2 : 0) + (vq - sg.qa) * 4 + rq] = v;
+        }
+    }
+};
+
+// ---------------------------------------------------------------- tables
+// The 16 codebook entries of one table through the scalar cache (one
+// 64-byte scalar load): the codebooks are constant during the launch, and a
+// scalar load is waited for on its own counter (a vector load's wait could
+// also wait for the weight prefetch issued around it).
+EP_DEV float cb_pick(const void *cb, int dt, int l)
+{
+    float out = 0.0f;
+    if (dt == EP_F32) {
+        const __attribute__((address_space(4))) float *c =
+            (const __attribute__((address_space(4))) float *)cb;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            v[i] = c[i];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            out = l == i ? v[i] : out;
+    } else {
+        const __attribute__((address_space(4))) uint32_t *c =
+            (const __attribute__((address_space(4))) uint32_t *)cb;
+        uint32_t v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = c[i];
+        uint32_t h = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            h = l == i ? (v[i / 2] >> (16 * (i & 1))) & 0xffffu : h;
+        out = dt == EP_F16 ? (float)f16_from_bits((uint16_t)h) : bf16_to_f32((uint16_t)h);
+    }
+    return out;
+}
+
+// Thread t < 32 gets entry t & 15 of table slot t >> 4 of the phase (0 for
+// entries >= levels and absent slots).  A codebook holds 16 entries
+// (levels <= 16 is required).
+EP_DEV float load_cb(const Segs &sg, int ntab, int levels, int cb_dtype)
+{
+    const int t = tid_fresh();
+    const int slot = t >> 4, l = t & 15;
+    const float v0 = cb_pick(sel3(sg.sfirst, sg.cb0, sg.cb1, sg.cb2), cb_dtype, l);
+    float v1 = 0.0f;
+    if (ntab > 1)
+        v1 = cb_pick(sel3(sg.sfirst + 1, sg.cb0, sg.cb1, sg.cb2), cb_dtype, l);
+    const float v = slot == 0 ? v0 : v1;
+    return (t < 32 && l < levels && slot < ntab) ? v : 0.0f;
+}
+
+EP_DEV void build_tables(uint32_t *tab, uint16_t *cb16, float cbv, int ntab)
+{
+    if (tid_fresh() < 32)
+        cb16[tid_fresh()] = f16_bits((f16_t)cbv);
+    __syncthreads();
+    build_table<4>(tab, cb16);
+    if (ntab > 1)
+        build_table<4>(tab + kTabDwords, cb16 + 16);
+}
+
+// ---------------------------------------------------------------- activations
+constexpr int XS_RMS_H0 = 0;  // h0 (f32, untagged: written by an earlier launch) * norm weight
+constexpr int XS_RMS = 1;     // tagged residual * norm weight (bf16); 1/rms returned
+constexpr int XS_BF16 = 2;    // tagged bf16 pairs (attention output)
+constexpr int XS_F32 = 3;     // tagged f32 (SwiGLU output)
+
+// Converts the K-vector to fp16 pairs in LDS with one exact power-of-two
+// factor per 32 values (the 4 threads of a 32-value chunk agree on it
+// through a quad max), the same staging as gemv.hip's.  Tagged sources are
+// re-read until every tag is `tag`.
+template <int XS, int K>
+EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, uint32_t *xs,
+                   uint32_t *xl, float *xf, float *part8, int *err)
+{
+    const auto rs = rsrc(x);
+    float ssq = 0.0f;
+    for (int e = tid_fresh(); e < K / 8; e += kThreads) {
+        float v[8];
+        if constexpr (XS == XS_RMS_H0) {
+            const u32x4_t h0 = ldc16(rs, (uint32_t)e * 32);
+            const u32x4_t h1 = ldc16(rs, (uint32_t)e * 32 + 16);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                v[t] = __uint_as_float(h0[t]);
+                v[4 + t] = __uint_as_float(h1[t]);
+            }
+        } else if constexpr (XS == XS_BF16) {
+            u32x4_t q0, q1;  // 4 entries: 2 bf16 + tag each
+            Spin sp;
+            do {
+                q0 = ldc16(rs, (uint32_t)e * 32);
+                q1 = ldc16(rs, (uint32_t)e * 32 + 16);
+            } while ((q0[1] != tag || q0[3] != tag || q1[1] != tag || q1[3] != tag) && sp.again(err));
+            unpack_pair<EP_BF16>(q0[0], v[0], v[1]);
+            unpack_pair<EP_BF16>(q0[2], v[2], v[3]);
+            unpack_pair<EP_BF16>(q1[0], v[4], v[5]);
+            unpack_pair<EP_BF16>(q1[2], v[6], v[7]);
+        } else {  // XS_RMS, XS_F32: 8 tagged f32 = 64 bytes
+            u32x4_t q[4];
+            Spin sp;
+            bool ok;
+            do {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    q[t] = ldc16(rs, (uint32_t)e * 64 + 16 * t);
+                ok = true;
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    ok = ok && q[t][1] == tag && q[t][3] == tag;
+            } while (!ok && sp.again(err));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                v[2 * t] = __uint_as_float(q[t][0]);
+                v[2 * t + 1] = __uint_as_float(q[t][2]);
+            }
+        }
+        if constexpr (XS == XS_RMS_H0 || XS == XS_RMS) {
+            const u32x4_t wv = ldg((const u32x4_t *)(w + e * 8));
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                float w0, w1;
+                unpack_pair<EP_BF16>(wv[t], w0, w1);
+                ssq = fmaf(v[2 * t], v[2 * t], fmaf(v[2 * t + 1], v[2 * t + 1], ssq));
+                v[2 * t] *= w0;
+                v[2 * t + 1] *= w1;
+            }
+        }
+        float am = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            am = fmaxf(am, fabsf(v[t]));
+        am = fmaxf(am, __shfl_xor(am, 1, 64));
+        am = fmaxf(am, __shfl_xor(am, 2, 64));
+        const int ex = row_exponent(am);
+        const float pw = ldexpf(1.0f, -ex);
+        u32x4_t q4, l4;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const float a0 = v[2 * p] * pw, a1 = v[2 * p + 1] * pw;
+            const f16_t h0 = (f16_t)a0, h1 = (f16_t)a1;
+            q4[p] = (uint32_t)f16_bits(h0) | ((uint32_t)f16_bits(h1) << 16);
+            l4[p] = (uint32_t)f16_bits((f16_t)(a0 - (float)h0)) |
+                    ((uint32_t)f16_bits((f16_t)(a1 - (float)h1)) << 16);
+        }
+        *(u32x4_t *)(xs + e * 4) = q4;
+        *(u32x4_t *)(xl + e * 4) = l4;
+        if ((e & 3) == 0)
+            xf[e >> 2] = ldexpf(1.0f, ex);
+    }
+    float rinv = 1.0f;
+    if constexpr (XS == XS_RMS_H0 || XS == XS_RMS) {
+        const float s = wave_sum(ssq);
+        if ((tid_fresh() & 63) == 0)
+            part8[tid_fresh() >> 6] = s;
+    }
+    __syncthreads();
+    if constexpr (XS == XS_RMS_H0 || XS == XS_RMS) {
+        float q = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w)
+            q += part8[w];
+        rinv = rsqrtf(q / (float)K + eps);
+    }
+    return rinv;
+}
+
+// ---------------------------------------------------------------- attention
+EP_DEV void stamp(const StepArgs &a, int l, int ev)
+{
+    if (a.trace && tid_fresh() == 0)
+        a.trace[((int64_t)l * kEvents + ev) * gridDim.x + blockIdx.x] = (long long)wall_clock64();
+}
+
+// Item (kv head j, chunk c) covers positions [c * 64, c * 64 + 64) ∩
+// [0, pos] for the GQ query heads of group j (short chunks spread the KV
+// reads over many CUs: one CU streams only a few tens of GB/s).  Wave w
+// owns the chunk's positions 8 w .. 8 w + 7; lane (r = lane >> 4,
+// e = lane & 15) holds dims 8 e .. 8 e + 7 of rows 8 w + 4 k + r (k = 0, 1),
+// so every K or V load instruction reads four whole rows (1 KB,
+// contiguous).  Row pos is this step's k/v (from LDS), rows past pos are
+// weighted 0.
+constexpr int kRowsPerWave = kChunk / kWaves;  // 8
+constexpr int kLoadsPerWave = kRowsPerWave / 4;  // 2
+struct AttnRegs {
+    u32x4_t k[kLoadsPerWave];  // K rows (bf16)
+    u32x4_t v[kLoadsPerWave];  // V rows (bf16)
+};
+
+// K/V rows of item (j, c); a wave whose positions all lie past pos gets a
+// zero-length descriptor (its loads return 0 and touch no memory).  The
+// wave's rows pw0 .. pw0 + 7 exist when pw0 <= pos: pw0 is a multiple of 8,
+// max_pos of 64.
+EP_DEV void attn_load(AttnRegs &r, const uint16_t *kc, const uint16_t *vc, int j, int c, int pos,
+                      int max_pos)
+{
+    const int lane = tid_fresh() & 63, wave = wave_id();
+    const int pw0 = c * kChunk + wave * kRowsPerWave;
+    const uint32_t bytes = pw0 <= pos ? kRowsPerWave * kD * 2u : 0u;
+    const int64_t row0 = pw0 <= pos ? (int64_t)j * max_pos + pw0 : 0;
+    const auto rk = rsrc(kc + row0 * kD, bytes);
+    const auto rv = rsrc(vc + row0 * kD, bytes);
+    const uint32_t off = (uint32_t)lane * 16;  // row lane >> 4, dims 8 (lane & 15)
+#pragma unroll
+    for (int k = 0; k < kLoadsPerWave; ++k)
+        r.k[k] = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)off, k * 4 * kD * 2, 0);
+#pragma unroll
+    for (int k = 0; k < kLoadsPerWave; ++k)
+        r.v[k] = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)off, k * 4 * kD * 2, 0);
+}
+
+EP_DEV float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+template <int GQ>
+EP_DEV void attn_item(const StepArgs &a, const StepLayer &L, int l, uint32_t seq, int j, int c,
+                      int nchunk, int pos, char *scratch)
+{
+    const int tid = tid_fresh(), lane = tid & 63, wave = wave_id();
+    const int rr = lane >> 4, e16 = lane & 15;
+    float *qs = (float *)scratch;        // [GQ][D]
+    float *kn = qs + GQ * kD;            // [D]
+    float *vn = kn + kD;                 // [D]
+    float *S = vn + kD;                  // [GQ][kChunk] scores, then probabilities
+    float *mw = S + GQ * kChunk;         // [GQ] chunk max
+    float *lw = mw + GQ;                 // [GQ] chunk sum
+    float *ow = lw + GQ;                 // [8][GQ][D]
+    const int hq0 = j * GQ;
+    int *err = a.sync + 2;
+
+    AttnRegs r;
+    attn_load(r, L.kcache, L.vcache, j, c, pos, a.max_pos);
+
+    // this step's q (GQ heads), k and v rows: per-head RMSNorm (Qwen3) and
+    // rotate-half RoPE on q and k; k and v rounded to bf16 as cached.  Lane l
+    // holds dims l and l + 64, the pair RoPE rotates together.
+    if (wave < GQ + 2) {
+        const uint64_t *src = wave < GQ ? a.qt + (hq0 + wave) * kD
+                                        : (wave == GQ ? a.kt + j * kD : a.vt + j * kD);
+        const uint32_t tq = tag_of(seq, l, PH_QKV);
+        uint64_t v0, v1;
+        Spin sp;
+        do {
+            v0 = ld_tag(src + lane);
+            v1 = ld_tag(src + lane + 64);
+        } while (((uint32_t)(v0 >> 32) != tq || (uint32_t)(v1 >> 32) != tq) && sp.again(err));
+        float x0 = __uint_as_float((uint32_t)v0), x1 = __uint_as_float((uint32_t)v1);
+        if (wave <= GQ) {
+            const uint16_t *nw = wave < GQ ? L.q_norm : L.k_norm;
+            if (nw) {
+                const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+                const float rn = rsqrtf(ss / (float)kD + a.qk_eps);
+                x0 = x0 * rn * bf16_to_f32(ldg(nw + lane));
+                x1 = x1 * rn * bf16_to_f32(ldg(nw + lane + 64));
+            }
+            const float cs = ldg(a.cos_t + (int64_t)pos * (kD / 2) + lane);
+            const float sn = ldg(a.sin_t + (int64_t)pos * (kD / 2) + lane);
+            float y0 = x0 * cs - x1 * sn;
+            float y1 = x1 * cs + x0 * sn;
+            float *dst = wave < GQ ? qs + wave * kD : kn;
+            if (wave == GQ) {
+                y0 = bf16r(y0);
+                y1 = bf16r(y1);
+            }
+            dst[lane] = y0;
+            dst[lane + 64] = y1;
+        } else {
+            vn[lane] = bf16r(x0);
+            vn[lane + 64] = bf16r(x1);
+        }
+    }
+    __syncthreads();
+    stamp(a, l, 10);  // q/k/v received
+    if (c == nchunk - 1 && tid < kD) {  // append this step's row (read by later steps only)
+        const int64_t row = ((int64_t)j * a.max_pos + pos) * kD + tid;
+        stg(L.kcache + row, f32_to_bf16(kn[tid]));
+        stg(L.vcache + row, f32_to_bf16(vn[tid]));
+    }
+
+    // scores: 8 dims per lane, then the sum over the row's 16 lanes
+    const int pw0 = c * kChunk + wave * kRowsPerWave;
+    const bool wave_live = pw0 <= pos;  // wave-uniform
+    if (wave_live) {
+        float qv[GQ][8];
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+            const f32x4_t a0 = *(const f32x4_t *)(qs + g * kD + e16 * 8);
+            const f32x4_t a1 = *(const f32x4_t *)(qs + g * kD + e16 * 8 + 4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                qv[g][t] = a0[t];
+                qv[g][4 + t] = a1[t];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kLoadsPerWave; ++k) {
+            const int p = pw0 + 4 * k + rr;
+            u32x4_t kw = r.k[k];
+            if (p == pos) {  // this step's key (bf16-exact)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    kw[t] = (uint32_t)f32_to_bf16(kn[e16 * 8 + 2 * t]) |
+                            ((uint32_t)f32_to_bf16(kn[e16 * 8 + 2 * t + 1]) << 16);
+            }
+            float sg[GQ];
+#pragma unroll
+            for (int g = 0; g < GQ; ++g) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    acc = fmaf(qv[g][2 * t], __uint_as_float(kw[t] << 16), acc);
+                    acc = fmaf(qv[g][2 * t + 1], __uint_as_float(kw[t] & 0xffff0000u), acc);
+                }
+                sg[g] = row16_sum(acc);
+            }
+            if (e16 == 0) {
+#pragma unroll
+                for (int g = 0; g < GQ; ++g)
+                    S[g * kChunk + wave * kRowsPerWave + 4 * k + rr] =
+                        p <= pos ? sg[g] * a.att_scale : -INFINITY;
+            }
+        }
+    } else if (e16 == 0) {
+#pragma unroll
+        for (int k = 0; k < kLoadsPerWave; ++k)
+#pragma unroll
+            for (int g = 0; g < GQ; ++g)
+                S[g * kChunk + wave * kRowsPerWave + 4 * k + rr] = -INFINITY;
+    }
+    __syncthreads();
+    // softmax over the chunk, one wave per head: one score per lane
+    static_assert(kChunk == 64, "one score per lane");
+    if (wave < GQ) {
+        const float sv = S[wave * kChunk + lane];
+        const float m = wave_max(sv);
+        const float pe = sv == -INFINITY ? 0.0f : __expf(sv - m);
+        S[wave * kChunk + lane] = pe;
+        const float lsum = wave_sum(pe);
+        if (lane == 0) {
+            mw[wave] = m;
+            lw[wave] = lsum;
+        }
+    }
+    __syncthreads();
+    // P.V: 8 dims per lane over its 8 rows, then over the wave's 4 row
+    // groups (lanes l, l ^ 16, l ^ 32, l ^ 48), then over the 8 waves
+    float o[GQ][8];
+#pragma unroll
+    for (int g = 0; g < GQ; ++g)
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            o[g][t] = 0.0f;
+    if (wave_live) {
+        const uint32_t vnew[4] = {
+            (uint32_t)f32_to_bf16(vn[e16 * 8 + 0]) | ((uint32_t)f32_to_bf16(vn[e16 * 8 + 1]) << 16),
+            (uint32_t)f32_to_bf16(vn[e16 * 8 + 2]) | ((uint32_t)f32_to_bf16(vn[e16 * 8 + 3]) << 16),
+            (uint32_t)f32_to_bf16(vn[e16 * 8 + 4]) | ((uint32_t)f32_to_bf16(vn[e16 * 8 + 5]) << 16),
+            (uint32_t)f32_to_bf16(vn[e16 * 8 + 6]) | ((uint32_t)f32_to_bf16(vn[e16 * 8 + 7]) << 16)};
+#pragma unroll
+        for (int k = 0; k < kLoadsPerWave; ++k) {
+            const int p = pw0 + 4 * k + rr;
+            const int pl = wave * kRowsPerWave + 4 * k + rr;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t vv = p == pos ? vnew[t] : (p < pos ? r.v[k][t] : 0u);
+                const float v0 = __uint_as_float(vv << 16), v1 = __uint_as_float(vv & 0xffff0000u);
+#pragma unroll
+                for (int g = 0; g < GQ; ++g) {
+                    const float pe = S[g * kChunk + pl];
+                    o[g][2 * t] = fmaf(pe, v0, o[g][2 * t]);
+                    o[g][2 * t + 1] = fmaf(pe, v1, o[g][2 * t + 1]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < GQ; ++g)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            float x = o[g][t];
+            x += __shfl_xor(x, 16, 64);
+            x += __shfl_xor(x, 32, 64);
+            o[g][t] = x;
+        }
+    if (rr == 0) {
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+            *(f32x4_t *)(ow + (wave * GQ + g) * kD + e16 * 8) =
+                (f32x4_t){o[g][0], o[g][1], o[g][2], o[g][3]};
+            *(f32x4_t *)(ow + (wave * GQ + g) * kD + e16 * 8 + 4) =
+                (f32x4_t){o[g][4], o[g][5], o[g][6], o[g][7]};
+        }
+    }
+    __syncthreads();
+    stamp(a, l, 11);  // scores, softmax, P.V done
+    // sum over the 8 waves; thread (g, dims 2dd, 2dd + 1)
+    const bool cth = tid < GQ * 64;
+    const int g = tid / 64, dd = 2 * (tid % 64);
+    float M = 0.0f, Ls = 0.0f, n0 = 0.0f, n1 = 0.0f;
+    if (cth) {
+        M = mw[g];
+        Ls = lw[g];
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            n0 += ow[(w * GQ + g) * kD + dd];
+            n1 += ow[(w * GQ + g) * kD + dd + 1];
+        }
+    }
+    uint64_t *outp = a.at + ((hq0 + g) * kD + dd) / 2;
+    const uint32_t tatt = tag_of(seq, l, PH_ATT), tpart = tag_of(seq, l, PH_PART);
+    const int maxch = a.max_pos / kChunk + 1;
+    if (nchunk > 1 && c > 0) {
+        // publish the partial; chunk 0 of this kv head combines
+        if (cth) {
+            uint64_t *pp = a.part + ((int64_t)(hq0 + g) * maxch + c) * (kD + 2);
+            st_tag(pp + 2 + dd, __float_as_uint(n0), tpart);
+            st_tag(pp + 3 + dd, __float_as_uint(n1), tpart);
+            if (dd == 0) {
+                st_tag(pp, __float_as_uint(M), tpart);
+                st_tag(pp + 1, __float_as_uint(Ls), tpart);
+            }
+        }
+        return;
+    }
+    if (cth) {
+        for (int cc = 1; cc < nchunk; ++cc) {  // running combine, chunk order
+            const uint64_t *pc = a.part + ((int64_t)(hq0 + g) * maxch + cc) * (kD + 2);
+            uint64_t e0, e1, e2, e3;
+            Spin sp;
+            do {
+                e0 = ld_tag(pc);
+                e1 = ld_tag(pc + 1);
+                e2 = ld_tag(pc + 2 + dd);
+                e3 = ld_tag(pc + 3 + dd);
+            } while (((uint32_t)(e0 >> 32) != tpart || (uint32_t)(e1 >> 32) != tpart ||
+                      (uint32_t)(e2 >> 32) != tpart || (uint32_t)(e3 >> 32) != tpart) &&
+                     sp.again(err));
+            const float Mc = __uint_as_float((uint32_t)e0);
+            const float Mn = fmaxf(M, Mc);
+            const float fa = __expf(M - Mn), fb = __expf(Mc - Mn);
+            Ls = Ls * fa + __uint_as_float((uint32_t)e1) * fb;
+            n0 = n0 * fa + __uint_as_float((uint32_t)e2) * fb;
+            n1 = n1 * fa + __uint_as_float((uint32_t)e3) * fb;
+            M = Mn;
+        }
+        st_tag(outp, (uint32_t)f32_to_bf16(n0 / Ls) | ((uint32_t)f32_to_bf16(n1 / Ls) << 16), tatt);
+    }
+    stamp(a, l, 12);  // output written (combined)
+}
+
+// ---------------------------------------------------------------- kernel
+// The residual rows an accumulating phase owns (one per thread), read with
+// its activation staging: layer 0's o reads the untagged input h0, later
+// phases the tagged residual.
+EP_DEV float residual_rows(const Segs &sg, const StepArgs &a, bool from_h0, uint32_t tag)
+{
+    const int t = tid_fresh();
+    if (t >= (sg.qb - sg.qa) * 4)
+        return 0.0f;
+    const int row = sg.qa * 4 + t;
+    return from_h0 ? ldg(a.h0 + row) : ld_tag_f32(a.ht + row, tag, a.sync + 2);
+}
+
+
+// Segment tables of the four GEMV phases of a layer (scalar loads of the
+// layer descriptor; recomputed where needed).
+struct Shape {
+    int Nq, Nkv, H, I, ldsb_h, ldsb_o, ldsb_i, b, G;
+};
+
+EP_DEV Segs segs_qkv(const StepLayer &L, const StepArgs &a, const Shape &sh)
+{
+    Segs s;
+    s.pk0 = L.packed[0];
+    s.pk1 = L.packed[1];
+    s.pk2 = L.packed[2];
+    s.sc0 = (const char *)L.scale[0];
+    s.sc1 = (const char *)L.scale[1];
+    s.sc2 = (const char *)L.scale[2];
+    s.cb0 = L.cb[0];
+    s.cb1 = L.cb[1];
+    s.cb2 = L.cb[2];
+    s.y0 = a.qt;
+    s.y1 = a.kt;
+    s.y2 = a.vt;
+    s.q1 = sh.Nq / 4;
+    s.q2 = (sh.Nq + sh.Nkv) / 4;
+    s.nq = (sh.Nq + 2 * sh.Nkv) / 4;
+    s.ldsb = sh.ldsb_h;
+    share(s, sh.b, sh.G, false);
+    return s;
+}
+
+EP_DEV Segs segs_one(const StepLayer &L, int li, int N, int ldsb, const Shape &sh)
+{
+    Segs s;
+    s.pk0 = s.pk1 = s.pk2 = L.packed[li];
+    s.sc0 = s.sc1 = s.sc2 = (const char *)L.scale[li];
+    s.cb0 = s.cb1 = s.cb2 = L.cb[li];
+    s.y0 = s.y1 = s.y2 = nullptr;
+    s.q1 = s.q2 = 0x7fffffff;
+    s.nq = N / 4;
+    s.ldsb = ldsb;
+    share(s, sh.b, sh.G, false);
+    return s;
+}
+
+EP_DEV Segs segs_gu(const StepLayer &L, const Shape &sh)
+{
+    Segs s;
+    s.pk0 = L.packed[4];
+    s.pk1 = s.pk2 = L.packed[5];
+    s.sc0 = (const char *)L.scale[4];
+    s.sc1 = s.sc2 = (const char *)L.scale[5];
+    s.cb0 = L.cb[4];
+    s.cb1 = s.cb2 = L.cb[5];
+    s.y0 = s.y1 = s.y2 = nullptr;
+    s.q1 = s.q2 = 0x7fffffff;
+    s.nq = sh.I / 4;
+    s.ldsb = sh.ldsb_h;
+    share(s, sh.b, sh.G, true);
+    return s;
+}
+
+template <class M>
+__global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
+{
+    __shared__ __align__(16) char smem[M::LDS];
+    uint32_t *tab = (uint32_t *)smem;
+    char *region = smem + 2 * kTabBytes;
+    uint16_t *cb16 = (uint16_t *)(region + M::REGION);
+    float *part8 = (float *)(cb16 + 32);
+    float *hrow = part8 + 16;
+    const PhaseLds lh = phase_lds(region, M::H), lo = phase_lds(region, M::HQD),
+                   li = phase_lds(region, M::I, tab + kTabDwords);  // down: one table
+
+    using PQ = Gemv<M::SH, M::RQ_QKV, false, M::MQ_QKV>;
+    using PO = Gemv<M::SO, M::RQ_O, false, M::MQ_O>;
+    using PG = Gemv<M::SH, M::RQ_GU, true, M::MQ_GU>;
+    using PD = Gemv<M::SI, M::RQ_D, false, M::MQ_D>;
+
+    const int pos = ldg(a.state);
+    if (pos < 0 || pos >= a.max_pos)
+        return;  // uniform: past the cache, nothing to do
+    const int G = gridDim.x, b = blockIdx.x;
+    const uint32_t seq = (uint32_t)ld_agent(a.sync + 1);
+    int *err = a.sync + 2;
+
+    Shape sh;
+    sh.Nq = M::HQD;
+    sh.Nkv = a.Hkv * kD;
+    sh.H = M::H;
+    sh.I = M::I;
+    sh.ldsb_h = (M::H / a.group) * 2;
+    sh.ldsb_o = (M::HQD / a.group) * 2;
+    sh.ldsb_i = (M::I / a.group) * 2;
+    sh.b = b;
+    sh.G = G;
+
+    const int nchunk = pos / kChunk + 1;
+    const int nitems = a.Hkv * nchunk;
+
+    typename PQ::Blk q0, q1;
+    typename PO::Blk o0, o1;
+    typename PG::Blk g0, g1;
+    typename PD::Blk d0, d1;
+
+    // Each phase's codebooks are loaded one phase ahead (a wait on a load
+    // issued after the weight prefetch would wait for the whole prefetch).
+    float cbv;
+    {
+        const Segs sq = segs_qkv(a.layers[0], a, sh);
+        cbv = load_cb(sq, sq.ntab, a.levels, a.cb_dtype);
+        __builtin_amdgcn_sched_barrier(0);
+        PQ::issue(q0, sq, 0, a.group);
+        PQ::issue(q1, sq, 1, a.group);
+        build_tables(tab, cb16, cbv, sq.ntab);
+        const Segs so = segs_one(a.layers[0], 3, M::H, sh.ldsb_o, sh);
+        cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
+    }
+
+    for (int l = 0; l < a.n_layers; ++l) {
+        const StepLayer &L = a.layers[l];
+        const bool last = l + 1 == a.n_layers;
+        stamp(a, l, 0);
+        // ---- q|k|v (RMSNorm of the residual in the activation load)
+        {
+            const Segs sq = segs_qkv(L, a, sh);
+            const float rinv =
+                l == 0 ? stage<XS_RMS_H0, M::H>(a.h0, L.attn_norm, a.eps, 0, lh.xs, lh.xl, lh.xf, part8, err)
+                       : stage<XS_RMS, M::H>(a.ht, L.attn_norm, a.eps, tag_of(seq, l - 1, PH_DOWN),
+                                             lh.xs, lh.xl, lh.xf, part8, err);
+            PQ::template run<MODE_STORE>(q0, q1, sq, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
+                                         rinv, a.ht, a.h0, false, nullptr, tag_of(seq, l, PH_QKV));
+        }
+        stamp(a, l, 1);
+        // o weights go out and the o table is built before any attention
+        // wait; then the attention items (K/V loads issued at item start)
+        {
+            const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
+            PO::issue(o0, so, 0, a.group);
+            PO::issue(o1, so, 1, a.group);
+            stamp(a, l, 13);
+            build_tables(tab, cb16, cbv, so.ntab);
+            stamp(a, l, 14);
+            const Segs sg = segs_gu(L, sh);
+            cbv = load_cb(sg, sg.ntab, a.levels, a.cb_dtype);
+        }
+        stamp(a, l, 9);
+        // ---- attention
+        for (int it = b; it < nitems; it += G) {
+            attn_item<M::GQ>(a, L, l, seq, it % a.Hkv, it / a.Hkv, nchunk, pos, region);
+            __syncthreads();
+        }
+        stamp(a, l, 2);
+        // ---- o (+= residual)
+        {
+            const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
+            const float hv = residual_rows(so, a, l == 0, tag_of(seq, l - 1, PH_DOWN));
+            stage<XS_BF16, M::HQD>(a.at, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf, part8,
+                                   err);
+            stamp(a, l, 3);
+            PO::template run<MODE_ACC>(o0, o1, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
+                                       1.0f, a.ht, a.h0, false, nullptr, tag_of(seq, l, PH_O));
+        }
+        stamp(a, l, 4);
+        {
+            const Segs sg = segs_gu(L, sh);
+            PG::issue(g0, sg, 0, a.group);
+            PG::issue(g1, sg, 1, a.group);
+            build_tables(tab, cb16, cbv, sg.ntab);
+            const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
+            cbv = load_cb(sd, sd.ntab, a.levels, a.cb_dtype);
+        }
+        // ---- gate|up -> silu(gate) * up
+        {
+            const Segs sg = segs_gu(L, sh);
+            const float rinv = stage<XS_RMS, M::H>(a.ht, L.mlp_norm, a.eps, tag_of(seq, l, PH_O),
+                                                   lh.xs, lh.xl, lh.xf, part8, err);
+            stamp(a, l, 5);
+            PG::template run<MODE_SWIGLU>(g0, g1, sg, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
+                                          rinv, a.ht, a.h0, false, a.actt, tag_of(seq, l, PH_ACT));
+        }
+        stamp(a, l, 6);
+        {
+            const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
+            PD::issue(d0, sd, 0, a.group);
+            PD::issue(d1, sd, 1, a.group);
+            build_tables(tab, cb16, cbv, sd.ntab);
+            if (!last) {
+                const Segs sq = segs_qkv(a.layers[l + 1], a, sh);
+                cbv = load_cb(sq, sq.ntab, a.levels, a.cb_dtype);
+            }
+        }
+        // ---- down (+= residual)
+        {
+            const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
+            const float hv = residual_rows(sd, a, false, tag_of(seq, l, PH_O));
+            stage<XS_F32, M::I>(a.actt, nullptr, 0.0f, tag_of(seq, l, PH_ACT), li.xs, li.xl, li.xf, part8,
+                                err);
+            stamp(a, l, 7);
+            PD::template run<MODE_ACC>(d0, d1, sd, a.group, tab, li.xs, li.xl, li.xf, li.red, hrow, hv,
+                                       1.0f, a.ht, a.h0, last, nullptr, tag_of(seq, l, PH_DOWN));
+        }
+        stamp(a, l, 8);
+        if (!last) {
+            const Segs sq = segs_qkv(a.layers[l + 1], a, sh);
+            PQ::issue(q0, sq, 0, a.group);
+            PQ::issue(q1, sq, 1, a.group);
+            build_tables(tab, cb16, cbv, sq.ntab);
+            const Segs so = segs_one(a.layers[l + 1], 3, M::H, sh.ldsb_o, sh);
+            cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
+        }
+    }
+    // the last workgroup to finish advances the launch sequence (every
+    // workgroup has read it by then)
+    __syncthreads();
+    if (tid_fresh() == 0 && counter_add(a.sync, 1) == G - 1) {
+        st_agent(a.sync, 0);
+        st_agent(a.sync + 1, (int)(seq + 1));
+    }
+}
+
+template <class M>
+int launch_model(const StepArgs &a, hipStream_t stream)
+{
+    static int grid = 0;
+    if (grid == 0) {
+        int per_cu = 0;
+        EP_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_kernel<M>,
+                                                                  kThreads, 0));
+        if (per_cu < 1)
+            return set_error(EP_DECLINE_SHAPE, "decode step: kernel does not fit a CU");
+        grid = device_cus();  // one resident workgroup per CU (LDS > half a CU's)
+    }
+    // every qkv share must touch at most two of q, k, v (two LDS tables)
+    const int Nkv = a.Hkv * kD;
+    const int maxshare = ((M::HQD + 2 * Nkv) / 4 + grid - 1) / grid;
+    if (maxshare >= Nkv / 4)
+        return set_error(EP_DECLINE_SHAPE, "decode step: qkv share spans three weights");
+    // every share must fit its LDS accumulator (and an accumulating share
+    // the 64 residual slots)
+    auto quads = [&](int rows) { return (rows / 4 + grid - 1) / grid; };
+    if (quads(M::HQD + 2 * Nkv) > M::MQ_QKV || quads(M::H) > M::MQ_O ||
+        quads(M::I) > M::MQ_GU || quads(M::H) > M::MQ_D || quads(M::H) * 4 > 64)
+        return set_error(EP_DECLINE_SHAPE, "decode step: %d workgroups too few for the shape",
+                         grid);
+    hipLaunchKernelGGL(decode_step_kernel<M>, dim3(grid), dim3(kThreads), 0, stream, a);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+}  // namespace
+
+// Which persistent variant serves the shape (0: none) and why not.
+static int variant_of(const StepDesc &d)
+{
+    if (d.D != kD || d.levels > 16 || d.levels < 1 ||
+        !(d.group == 128 || d.group == 256 || (d.group >= 512 && d.group % 512 == 0)) ||
+        d.scale_dtype != EP_F16 || (d.cb_dtype != EP_F32 && d.cb_dtype != EP_F16) || d.Hkv < 1 ||
+        d.Hq % d.Hkv != 0 || d.max_pos < 64 || d.max_pos % 64 != 0) {
+        set_error(EP_DECLINE_SHAPE,
+                  "decode step: head_dim %d, levels %d, group %d, scale dtype %d, cb dtype %d, "
+                  "max_pos %d not served",
+                  d.D, d.levels, d.group, d.scale_dtype, d.cb_dtype, d.max_pos);
+        return 0;
+    }
+    if (d.H % d.group != 0 || d.I % d.group != 0 || (d.Hq * d.D) % d.group != 0) {
+        set_error(EP_DECLINE_SHAPE, "decode step: K not a multiple of the group");
+        return 0;
+    }
+    const int GQ = d.Hq / d.Hkv;
+    if (d.H == ModelL8B::H && d.Hq * d.D == ModelL8B::HQD && d.I == ModelL8B::I &&
+        GQ == ModelL8B::GQ)
+        return 1;
+    if (d.H == ModelQ17::H && d.Hq * d.D == ModelQ17::HQD && d.I == ModelQ17::I &&
+        GQ == ModelQ17::GQ)
+        return 2;
+    set_error(EP_DECLINE_SHAPE,
+              "decode step: no persistent variant for hidden %d, heads %d/%d, intermediate %d",
+              d.H, d.Hq, d.Hkv, d.I);
+    return 0;
+}
+
+int decode_step_serves(const StepDesc &d) { return variant_of(d) != 0 ? EP_OK : EP_DECLINE_SHAPE; }
+
+// Workspace: sync words, then the tagged buffers (8 bytes per value).
+struct StepWs {
+    size_t sync, ht, qt, kt, vt, at, actt, part, total;
+};
+static StepWs step_ws(int H, int I, int Hq, int Hkv, int D, int max_pos)
+{
+    StepWs w;
+    size_t o = 0;
+    auto take = [&](size_t n) {
+        const size_t at = o;
+        o += (n * 8 + 255) / 256 * 256;
+        return at;
+    };
+    w.sync = take(8);
+    w.ht = take((size_t)H);
+    w.qt = take((size_t)Hq * D);
+    w.kt = take((size_t)Hkv * D);
+    w.vt = take((size_t)Hkv * D);
+    w.at = take((size_t)Hq * D / 2);
+    w.actt = take((size_t)I);
+    w.part = take((size_t)Hq * (max_pos / kChunk + 1) * (D + 2));
+    w.total = o;
+    return w;
+}
+
+size_t decode_step_workspace(int H, int I, int Hq, int Hkv, int D, int max_pos)
+{
+    return step_ws(H, I, Hq, Hkv, D, max_pos).total;
+}
+
+int launch_decode_step(const StepDesc &d, hipStream_t stream)
+{
+    const int var = variant_of(d);
+    if (var == 0)
+        return EP_DECLINE_SHAPE;
+    if (d.n_layers > 100)
+        return set_error(EP_DECLINE_SHAPE, "decode step: %d layers (at most 100)", d.n_layers);
+    const StepWs w = step_ws(d.H, d.I, d.Hq, d.Hkv, d.D, d.max_pos);
+    if (d.ws_bytes < w.total)
+        return set_error(EP_ERR_ARG, "decode step: workspace %zu < %zu bytes", d.ws_bytes, w.total);
+    char *ws = (char *)d.ws;
+    StepArgs a{};
+    a.layers = (const StepLayer *)d.layers;
+    a.n_layers = d.n_layers;
+    a.h0 = d.h;
+    a.ht = (uint64_t *)(ws + w.ht);
+    a.qt = (uint64_t *)(ws + w.qt);
+    a.kt = (uint64_t *)(ws + w.kt);
+    a.vt = (uint64_t *)(ws + w.vt);
+    a.at = (uint64_t *)(ws + w.at);
+    a.actt = (uint64_t *)(ws + w.actt);
+    a.part = (uint64_t *)(ws + w.part);
+    a.sync = (int *)(ws + w.sync);
+    a.cos_t = d.cos_t;
+    a.sin_t = d.sin_t;
+    a.state = d.state;
+    a.Hkv = d.Hkv;
+    a.max_pos = d.max_pos;
+    a.levels = d.levels;
+    a.group = d.group;
+    a.cb_dtype = d.cb_dtype;
+    a.eps = d.eps;
+    a.qk_eps = d.qk_eps;
+    a.att_scale = d.att_scale;
+    a.trace = d.trace;
+    return var == 1 ? launch_model<ModelL8B>(a, stream) : launch_model<ModelQ17>(a, stream);
+}
+
+size_t decode_step_layer_bytes() { return sizeof(StepLayer); }
+
+}  // namespace ep

@@ -146,9 +146,15 @@ def _ptrs(*tensors):
 
 
 class Decoder:
-    """Device-resident greedy decoder over ``DecoderWeights``."""
+    """Device-resident greedy decoder over ``DecoderWeights``.
 
-    def __init__(self, weights, max_pos, head_grid=None):
+    ``persistent`` selects how the layers run: True = one launch per step
+    (ep_decode_step, a resident workgroup per CU with grid barriers), False =
+    five launches per layer (ep_fused_gemv / ep_decode_attention), None =
+    the persistent kernel when it serves the shape.  Either way the step ends
+    with ep_lm_head_argmax and is replayed from one captured graph."""
+
+    def __init__(self, weights, max_pos, head_grid=None, persistent=None):
         if not cuda_kernel.available():
             raise RuntimeError("the gfx950 HIP backend is not available")
         self.w = weights
@@ -184,6 +190,14 @@ class Decoder:
         self.head_idx = torch.zeros(self.head_grid, device=dev, dtype=i32)
         self.head_ctr = torch.zeros(1, device=dev, dtype=i32)
         self._build_launch_args()
+        served = bool(_abi.lib.ep_decode_step_serves(
+            H, cfg.intermediate, cfg.n_heads, cfg.n_kv, D, max_pos, cfg.levels, cfg.group,
+            self._step_dtype("scale"), self._step_dtype("cb")))
+        if persistent and not served:
+            raise RuntimeError(f"persistent decode step declined: {_abi.last_error()}")
+        self.persistent = served if persistent is None else bool(persistent)
+        if self.persistent:
+            self._build_step_table()
         self.graph = None
 
     # ------------------------------------------------------------ launch args
@@ -209,6 +223,59 @@ class Decoder:
                 L=L))
         self.scale = 1.0 / math.sqrt(cfg.head_dim)
 
+    def _step_dtype(self, which):
+        s = self.w.layers[0].lin["q"]
+        return _abi.dtype_code(s.scale.dtype if which == "scale" else s.cb.dtype)
+
+    # Order of the 27 pointers of one layer descriptor (include/epure_decode.h).
+    _STEP_LINEARS = ("q", "k", "v", "o", "gate", "up", "down")
+
+    def _build_step_table(self):
+        nbytes = _abi.lib.ep_decode_step_layer_bytes()
+        if nbytes != 27 * 8:
+            raise RuntimeError(f"unexpected decode-step layer descriptor size {nbytes}")
+        rows = []
+        self._cb16 = []  # 16-entry copies of shorter codebooks (the kernel reads 16)
+        for li, L in enumerate(self.w.layers):
+            st = [L.lin[n] for n in self._STEP_LINEARS]
+            ptr = lambda t: 0 if t is None else t.data_ptr()  # noqa: E731
+            cbs = []
+            for s in st:
+                cb = s.cb.reshape(-1)
+                if cb.numel() < 16 or not cb.is_contiguous():
+                    pad = torch.zeros(16, device=cb.device, dtype=cb.dtype)
+                    pad[:cb.numel()] = cb
+                    self._cb16.append(pad)
+                    cb = pad
+                cbs.append(cb.data_ptr())
+            rows.append([s.packed.data_ptr() for s in st] + [s.scale.data_ptr() for s in st]
+                        + cbs
+                        + [ptr(L.attn_norm), ptr(L.mlp_norm), ptr(L.q_norm), ptr(L.k_norm),
+                           self.kcache[li].data_ptr(), self.vcache[li].data_ptr()])
+        self.step_table = torch.tensor(rows, dtype=torch.int64).to(self.device)
+        cfg = self.cfg
+        ws = _abi.lib.ep_decode_step_workspace(cfg.hidden, cfg.intermediate, cfg.n_heads,
+                                               cfg.n_kv, cfg.head_dim, self.max_pos)
+        self.step_ws = torch.zeros((ws + 15) // 16 * 4, device=self.device, dtype=torch.int32)
+        self.step_trace = None
+
+    def step_failed(self):
+        """True if a hand-over wait of the persistent step timed out (its
+        results are garbage).  Synchronizes."""
+        return self.persistent and int(self.step_ws[2].item()) != 0
+
+    def _step_kernel(self, stream):
+        cfg = self.cfg
+        rc = _abi.lib.ep_decode_step(
+            self.step_table.data_ptr(), cfg.layers, self.h.data_ptr(), self.step_ws.data_ptr(),
+            self.step_ws.numel() * 4, self.cos.data_ptr(),
+            self.sin.data_ptr(), self.state.data_ptr(), cfg.hidden, cfg.intermediate,
+            cfg.n_heads, cfg.n_kv, cfg.head_dim, self.max_pos, cfg.levels, cfg.group,
+            self._step_dtype("scale"), self._step_dtype("cb"), cfg.rms_eps, cfg.rms_eps,
+            self.scale,
+            self.step_trace.data_ptr() if self.step_trace is not None else None, stream)
+        _abi.check(rc, "ep_decode_step") or _raise_decline("ep_decode_step")
+
     def _gemv(self, a, xsrc, x, xdt, x_aux, accumulate, stream):
         rc = _abi.lib.ep_fused_gemv(
             xsrc, x.data_ptr(), xdt, x_aux.data_ptr() if x_aux is not None else None,
@@ -221,6 +288,32 @@ class Decoder:
         """Enqueue one decode step on the current stream (capturable)."""
         cfg, lib = self.cfg, _abi.lib
         stream = _abi.stream_handle(self.device)
+        D = cfg.head_dim
+        if self.persistent:
+            self._step_kernel(stream)
+        else:
+            self._layers_multi(stream)
+        rc = lib.ep_lm_head_argmax(
+            self.h.data_ptr(), self.w.final_norm.data_ptr(), cfg.rms_eps,
+            self.w.lm_head.data_ptr(), self.logits.data_ptr(), cfg.vocab, cfg.hidden,
+            self.head_val.data_ptr(), self.head_idx.data_ptr(), self.head_ctr.data_ptr(),
+            self.state.data_ptr(), self.prompt.data_ptr(), self.n_prompt,
+            self.tokens.data_ptr(), self.argmax.data_ptr(), self.w.embed.data_ptr(),
+            self.max_pos, self.head_grid, stream)
+        _abi.check(rc, "ep_lm_head_argmax") or _raise_decline("ep_lm_head_argmax")
+
+    def layer_launches(self):
+        """Enqueue only the layers of one step (no lm_head): the persistent
+        step kernel, or the 5 launches per layer.  The decode position is
+        not advanced, so replays repeat the same position."""
+        stream = _abi.stream_handle(self.device)
+        if self.persistent:
+            self._step_kernel(stream)
+        else:
+            self._layers_multi(stream)
+
+    def _layers_multi(self, stream):
+        cfg, lib = self.cfg, _abi.lib
         D = cfg.head_dim
         for li, a in enumerate(self._layer_args):
             L = a["L"]
@@ -237,14 +330,6 @@ class Decoder:
             self._gemv(a["o"], _abi.XSRC_PLAIN, self.attn, _abi.BF16, None, True, stream)
             self._gemv(a["gu"], _abi.XSRC_RMSNORM, self.h, _abi.F32, L.mlp_norm, False, stream)
             self._gemv(a["down"], _abi.XSRC_SWIGLU, self.g, _abi.F32, self.u, True, stream)
-        rc = lib.ep_lm_head_argmax(
-            self.h.data_ptr(), self.w.final_norm.data_ptr(), cfg.rms_eps,
-            self.w.lm_head.data_ptr(), self.logits.data_ptr(), cfg.vocab, cfg.hidden,
-            self.head_val.data_ptr(), self.head_idx.data_ptr(), self.head_ctr.data_ptr(),
-            self.state.data_ptr(), self.prompt.data_ptr(), self.n_prompt,
-            self.tokens.data_ptr(), self.argmax.data_ptr(), self.w.embed.data_ptr(),
-            self.max_pos, self.head_grid, stream)
-        _abi.check(rc, "ep_lm_head_argmax") or _raise_decline("ep_lm_head_argmax")
 
     def gemv_launches(self):
         """Enqueue only the step's packed GEMVs (4 launches per layer), for

@@ -65,6 +65,16 @@ _SIGS = {
         _c_int, _c_int, _p]),                             # prompt, n_prompt, tokens, argmax,
                                                           # embed, max_pos, grid, stream
     "ep_embed_token": (_c_int, [_p, _p, _p, _c_int, _p]),
+    "ep_decode_step_layer_bytes": (_sz, []),
+    "ep_decode_step_workspace": (_sz, [_c_int] * 6),
+    "ep_decode_step_serves": (_c_int, [_c_int] * 10),
+    "ep_decode_step": (_c_int, [
+        _p, _c_int, _p, _p, _sz,                 # layers, n_layers, h, workspace, bytes
+        _p, _p, _p,                              # cos, sin, state
+        _c_int, _c_int, _c_int, _c_int, _c_int,  # H, I, Hq, Hkv, D
+        _c_int, _c_int, _c_int, _c_int, _c_int,  # max_pos, levels, group, scale_dtype, cb_dtype
+        ctypes.c_float, ctypes.c_float, ctypes.c_float,  # eps, qk_eps, att_scale
+        _p, _p]),                                # trace, stream
 }
 
 XSRC_PLAIN, XSRC_RMSNORM, XSRC_SWIGLU = 0, 1, 2

@@ -74,6 +74,43 @@ int ep_lm_head_argmax(float *h, const uint16_t *norm_w, float eps, const uint16_
                       int *state, const int *prompt, int n_prompt, int *tokens, int *argmax_out,
                       const uint16_t *embed, int max_pos, int grid, void *stream);
 
+/*
+ * Persistent decode step: every layer of one batch-1 step in ONE launch (one
+ * resident workgroup per CU; phases hand over through tagged data, see
+ * below; the next phase's packed weights are in flight across each hand-
+ * over).  Same math as the per-layer sequence ep_fused_gemv(q|k|v, RMSNorm)
+ * -> ep_decode_attention -> ep_fused_gemv(o, +=) -> ep_fused_gemv(gate|up,
+ * RMSNorm) -> ep_fused_gemv(down, SwiGLU, +=), i.e. the transformers
+ * decoder layer whose linears the reference replaces with PackedLinear
+ * (epure/runtime.py:261-262, :373-415), at batch 1.  Follow it with
+ * ep_lm_head_argmax on the same h.
+ *
+ * `layers` (device memory) holds n_layers (<= 100) descriptors of
+ * ep_decode_step_layer_bytes() bytes: 27 device pointers in this order --
+ * packed[7], scale[7] (fp16 [N][K/group]), cb[7] (16 entries f32 or fp16,
+ * entries >= levels ignored) for
+ * q, k, v, o, gate, up, down; attn_norm, mlp_norm, q_norm, k_norm (bf16
+ * [H], [H], [D], [D]; q/k norm NULL for Llama); kcache, vcache (bf16
+ * [Hkv][max_pos][D]).  h [H] f32 holds the step's input embedding and
+ * receives the final residual (the lm_head's input).  `workspace`
+ * (ep_decode_step_workspace bytes: the tagged hand-over buffers) must be
+ * zeroed before the first call and is left valid for the next; its int
+ * word 2 becomes nonzero if a hand-over wait timed out (the step's results
+ * are then garbage).  `trace`, when not NULL, receives wall-clock stamps
+ * [n_layers][10][grid] (debug).  Declines (> 0) shapes without a
+ * persistent variant (ep_decode_step_serves; group 128, 256 or a multiple
+ * of 512, fp16 scales, 4-bit indices).  Position = state[0].
+ */
+size_t ep_decode_step_layer_bytes(void);
+size_t ep_decode_step_workspace(int H, int I, int Hq, int Hkv, int D, int max_pos);
+int ep_decode_step_serves(int H, int I, int Hq, int Hkv, int D, int max_pos, int levels,
+                          int group, int scale_dtype, int cb_dtype);
+int ep_decode_step(const void *layers, int n_layers, float *h, void *workspace,
+                   size_t workspace_bytes, const float *cos_t, const float *sin_t,
+                   const int *state, int H, int I, int Hq, int Hkv, int D, int max_pos,
+                   int levels, int group, int scale_dtype, int cb_dtype, float eps,
+                   float qk_eps, float att_scale, long long *trace, void *stream);
+
 /* h[H] = embed[state[1]] as f32 (the first step's input). */
 int ep_embed_token(const uint16_t *embed, const int *state, float *h, int H, void *stream);
 

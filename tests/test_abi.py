@@ -96,3 +96,50 @@ def test_check_maps_codes(lib):
 def test_workspace_sizes(lib):
     assert lib.ep_dequant_matmul_workspace(1, 4096, 4096, 16, 128) >= 4
     assert lib.ep_dequant_matmul_workspace(512, 4096, 4096, 16, 128) >= 512 * 4
+
+
+# ---- persistent decode step (include/epure_decode.h): host-side contract
+LLAMA8B = dict(H=4096, I=14336, Hq=32, Hkv=8, D=128)
+QWEN17B = dict(H=2048, I=6144, Hq=16, Hkv=8, D=128)
+
+
+def _serves(lib, H, I, Hq, Hkv, D, max_pos=448, levels=16, group=128, sdt=_abi.F16, cdt=_abi.F32):
+    return lib.ep_decode_step_serves(H, I, Hq, Hkv, D, max_pos, levels, group, sdt, cdt)
+
+
+def test_decode_step_layer_descriptor_is_27_pointers(lib):
+    assert lib.ep_decode_step_layer_bytes() == 27 * 8
+
+
+def test_decode_step_workspace_size(lib):
+    # 8-byte tagged values, each buffer 256-byte aligned: sync, h, q, k, v,
+    # attention output (bf16 pairs), SwiGLU output, split-KV partials
+    def r(n):
+        return (n * 8 + 255) // 256 * 256
+    H, I, Hq, Hkv, D, P = 4096, 14336, 32, 8, 128, 448
+    want = r(8) + r(H) + r(Hq * D) + 2 * r(Hkv * D) + r(Hq * D // 2) + r(I) + \
+        r(Hq * (P // 64 + 1) * (D + 2))
+    assert lib.ep_decode_step_workspace(H, I, Hq, Hkv, D, P) == want
+    assert lib.ep_decode_step_workspace(H, I, 0, Hkv, D, P) == 0
+
+
+@pytest.mark.parametrize("shape", [LLAMA8B, QWEN17B], ids=["llama3-8b", "qwen3-1.7b"])
+def test_decode_step_serves_baseline_shapes(lib, shape):
+    assert _serves(lib, **shape) == 1
+    assert _serves(lib, **shape, cdt=_abi.F16) == 1
+
+
+@pytest.mark.parametrize("change", [
+    dict(H=1024), dict(I=8192), dict(Hq=16), dict(D=64), dict(levels=256), dict(group=64),
+    dict(sdt=_abi.F32), dict(max_pos=100), dict(max_pos=32)])
+def test_decode_step_declines_other_shapes(lib, change):
+    shape = dict(LLAMA8B)
+    kw = {k: v for k, v in change.items() if k in ("max_pos", "levels", "group", "sdt", "cdt")}
+    shape.update({k: v for k, v in change.items() if k in shape})
+    assert _serves(lib, **shape, **kw) == 0
+
+
+def test_decode_step_rejects_bad_arguments_without_launch(lib):
+    rc = lib.ep_decode_step(None, 32, None, None, 0, None, None, None, 4096, 14336, 32, 8, 128,
+                            448, 16, 128, _abi.F16, _abi.F32, 1e-5, 1e-5, 0.088, None, None)
+    assert rc < 0 and "bad arguments" in _abi.last_error()

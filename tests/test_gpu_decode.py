@@ -69,17 +69,19 @@ def test_graph_replay_matches_eager():
     assert torch.equal(la, dec.logits)
 
 
+@pytest.mark.parametrize("persistent", [True, False], ids=["one-launch", "per-layer"])
 @pytest.mark.parametrize("cfg,n_prompt", [(QWEN3_1_7B, 32), (LLAMA3_8B, 128)],
                          ids=["qwen3-1.7b", "llama3-8b"])
-def test_greedy_64_steps_identical(cfg, n_prompt):
+def test_greedy_64_steps_identical(cfg, n_prompt, persistent):
     w = random_weights(cfg, seed=0, device=DEV)
-    dec = Decoder(w, n_prompt + 64 + 1)
+    dec = Decoder(w, n_prompt + 64 + 1, persistent=persistent)
     prompt = prompt_ids(n_prompt, cfg.vocab, 1)
     toks, _ = dec.generate(prompt, 64)
     ref = RefDecoder.from_weights(w, dec.max_pos)
     want, _, margins = ref.generate(prompt, 64)
     gen_m = margins[n_prompt - 1:]
     print(f"{cfg.name}: min oracle margin over the 64 greedy steps {min(gen_m):.3e}")
+    assert not dec.step_failed(), "a grid barrier of the one-launch step timed out"
     first = next((i for i, (x, y) in enumerate(zip(toks, want)) if x != y), None)
     assert first is None, (f"diverged at position {first}: got {toks[first]} want {want[first]}, "
                            f"oracle margin there {margins[first - 1]:.3e}")
