@@ -50,6 +50,8 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = 8;
+// cache policy of the weight loads: nt (streamed, read once per step)
+constexpr int kAuxStream = 2;
 constexpr int kSpinLimit = 1 << 16;  // polls (~1-2 us each) before the step fails
 constexpr int kD = 128;              // head_dim served
 constexpr int kChunk = 64;           // KV positions per attention item (8 waves x 8)
@@ -72,13 +74,16 @@ constexpr int geo_spw(int S) { return (S + geo_wpr(S) - 1) / geo_wpr(S); }
 constexpr int imax(int a, int b) { return a > b ? a : b; }
 
 // A decoder shape served by the persistent step.  RQ_* = row quads per row
-// group per block of each GEMV phase (blocks are pipelined three deep, the
-// first two issued before the phase's barrier); MQ_* = the most row quads a
+// group per block of each GEMV phase (blocks are pipelined, the first ones
+// issued before the phase's hand-over wait); MQ_* = the most row quads a
 // workgroup's share of the phase may hold (the LDS accumulator is sized by
 // it; the launch checks it against the grid).
 template <int H_, int HQD_, int I_, int GQ_, int RQ_QKV_, int RQ_O_, int RQ_GU_, int RQ_D_,
-          int MQ_QKV_, int MQ_O_, int MQ_GU_, int MQ_D_>
+          int MQ_QKV_, int MQ_O_, int MQ_GU_, int MQ_D_, int NB_QKV_ = 0, int NB_O_ = 0, int NB_GU_ = 0,
+          int NB_D_ = 0>
 struct Model {
+    // NB_* = block buffers of each phase (0: sized for the loads in flight)
+    static constexpr int NB_QKV = NB_QKV_, NB_O = NB_O_, NB_GU = NB_GU_, NB_D = NB_D_;
     static constexpr int H = H_, HQD = HQD_, I = I_, GQ = GQ_;
     static constexpr int SH = H / 512, SO = HQD / 512, SI = I / 512;
     static constexpr int RQ_QKV = RQ_QKV_, RQ_O = RQ_O_, RQ_GU = RQ_GU_, RQ_D = RQ_D_;
@@ -103,9 +108,9 @@ struct Model {
     static_assert(H % 512 == 0 && HQD % 512 == 0 && I % 512 == 0, "rows of whole slabs");
 };
 
-// Llama-3-8B and Qwen3-1.7B (config 1) shapes; shares
+// Llama-3-8B and Qwen3-1.7B shapes; shares
 // at 256 workgroups: q|k|v 6 / 4 quads, o 4 / 2, gate|up 14 / 6, down 4 / 2.
-using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 1, 6, 4, 14, 4>;
+using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 4, 14, 4, 0, 0, 0, 2>;
 using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 2, 6, 2>;
 
 // Where a phase of contraction length K keeps its activations, factors and
@@ -291,31 +296,44 @@ constexpr int MODE_ACC = 1;     // h[row] += dot
 constexpr int MODE_SWIGLU = 2;  // act[row] = silu(gate * rinv) * (up * rinv)
 
 // One GEMV phase.  A workgroup's share [qa, qb) of virtual row quads (at
-// most MAXQ) is cut into blocks of QPB quads; lane (wave, lane) covers row
-// 4 q + (lane >> 4) of each quad q of its row group, 16 bytes (32 weights)
-// of each of its slabs.  Blocks are pipelined three deep: blocks 0 and 1
-// are issued by the caller (before the barrier), block i + 2 while block i
-// is computed.  Waves run their blocks independently: each row's 16-lane
-// sum goes to an LDS accumulator (one slot per wave and row), and the
-// cross-wave sums and outputs are formed once, after the last block.
-template <int S, int RQ, bool PAIRED, int MAXQ>
+// most MAXQ) is cut into quad groups of QPB quads; lane (wave, lane) covers
+// row 4 q + (lane >> 4) of each quad q of its row group, 16 bytes (32
+// weights) of each of its SPW slabs.  A block is one slab of one quad group
+// (NQ loads per lane), blocks run slab-major: a wave's activation chunk of
+// a slab is read once for all the share's quads, and each row's partial sum
+// stays in a register until the wave's last slab.  Blocks are pipelined
+// NBUF deep: blocks 0 .. NBUF - 2 are issued by the caller (before the
+// hand-over wait), block i + NBUF - 1 while block i is computed.  Waves run
+// their blocks independently: each row's 16-lane sum goes to an LDS
+// accumulator (one slot per wave and row), and the cross-wave sums and
+// outputs are formed once, after the last block.
+template <int S, int RQ, bool PAIRED, int MAXQ, int NBUF_SET = 0>
 struct Gemv {
     static constexpr int WPR = geo_wpr(S), RG = geo_rg(S), SPW = geo_spw(S);
-    static constexpr int NQ = PAIRED ? 2 * RQ : RQ;  // row quads per lane per block
-    static constexpr int QPB = RG * RQ;              // virtual quads per block
-    static constexpr int RB = S * kSlabBytes;        // packed row bytes
-    static constexpr bool XREG = SPW == 1;           // activations held in registers
+    static constexpr int NQ = PAIRED ? 2 * RQ : RQ;  // loads (row quads) per lane per block
+    static constexpr int QPB = RG * RQ;              // virtual quads per quad group
+    static constexpr int QB = (MAXQ + QPB - 1) / QPB;  // quad groups of the largest share
+    static constexpr int MAXB = SPW * QB;              // blocks of the largest share
+    static constexpr int RB = S * kSlabBytes;          // packed row bytes
+    static constexpr bool XREG = SPW == 1;             // one activation chunk for the phase
     static constexpr int NPAIR = PAIRED ? 2 : 1;
     static constexpr int RED_ROWS = 4 * MAXQ * NPAIR;  // accumulator slots per wave
     static constexpr int RED_BYTES = kWaves * RED_ROWS * 4;
-    // fp16 scales a wave needs per block: NQ quads x SPW slabs x 4 rows x up
-    // to 4 groups per slab (group >= 128) -- one 2-byte load per lane
-    static_assert(NQ * SPW * 4 * 4 <= 64, "one scale load per wave and block");
+    // fp16 scales a wave needs per block: NQ quads x 4 rows x up to 4 groups
+    // per slab (group >= 128) -- one 2-byte load per lane
+    static_assert(NQ * 4 * 4 <= 64, "one scale load per wave and block");
     static_assert(RG * WPR <= kWaves, "waves");
+    // Block buffers: enough blocks in flight to keep ~48 KiB of a CU's loads
+    // requested (more than the CU's L1 holds in flight), the whole share at
+    // most; NBUF - 1 of them are issued ahead of the phase's hand-over.
+    static constexpr int BLOCK_BYTES = RG * WPR * 64 * 16 * NQ;
+    static constexpr int NBUF_WANT = 1 + (49152 + BLOCK_BYTES - 1) / BLOCK_BYTES;
+    static constexpr int NBUF_AUTO = NBUF_WANT < 2 ? 2 : (NBUF_WANT > MAXB + 1 ? MAXB + 1 : NBUF_WANT);
+    static constexpr int NBUF = NBUF_SET > 0 ? NBUF_SET : NBUF_AUTO;
 
     struct Blk {
-        u32x4_t w[SPW][NQ];
-        uint32_t s;  // one fp16 scale (bits) per lane, spread to the lanes that
+        u32x4_t w[NQ];
+        uint16_t s;  // one fp16 scale (bits) per lane, spread to the lanes that
                      // use it at compute time; converted there (a conversion
                      // right after the load would wait for every load in flight)
     };
@@ -331,12 +349,12 @@ struct Gemv {
         return (uint32_t)(slab(j, wv) * kSlabBytes + (tid_fresh() & 15) * 16);
     }
 
-    static EP_DEV int nblocks(const Segs &sg) { return (sg.qb - sg.qa + QPB - 1) / QPB; }
+    static EP_DEV int ngroups(const Segs &sg) { return (sg.qb - sg.qa + QPB - 1) / QPB; }
 
-    // Virtual quad of slot i of the block starting at virtual quad vb.
-    static EP_DEV int vquad(int vb, int i, int wv)
+    // Virtual quad of slot i of quad group qg.
+    static EP_DEV int vquad(const Segs &sg, int qg, int i, int wv)
     {
-        return vb + (wv / WPR) * RQ + (PAIRED ? (i % RQ) : i);
+        return sg.qa + qg * QPB + (wv / WPR) * RQ + (PAIRED ? (i % RQ) : i);
     }
     static EP_DEV int seg_of(const Segs &sg, int vq, int i)
     {
@@ -349,104 +367,132 @@ struct Gemv {
     {
         return PAIRED ? 0 : (s == 2 ? sg.q2 : (s == 1 ? sg.q1 : 0));
     }
-    // groups of a 256-byte slab (512 weights); group >= 128
-    static EP_DEV int gps(int group) { return group >= 512 ? 1 : 512 / group; }
+
+    // Lane constants of the block scale loads (fixed for a phase): the lane
+    // loads scale entry (i * 4 + r) * G + g of a block -- quad slot i, row
+    // r of the quad, group g of the block's slab (G = 4, 2, 1 groups per
+    // slab for groups of 128, 256, >= 512 weights; groups are powers of two).
+    struct SLane {
+        int i, r, g;  // quad slot (i < NQ: live), row, group within the slab
+        int lgroup;   // log2(group)
+    };
+    static EP_DEV int lg_gps(int lgroup) { return lgroup <= 9 ? 9 - lgroup : 0; }
+    static EP_DEV SLane slane(int group)
+    {
+        SLane sl;
+        sl.lgroup = 31 - __builtin_clz((unsigned)group);
+        const int lg = lg_gps(sl.lgroup);
+        int n = tid_fresh() & 63;
+        sl.g = n & ((1 << lg) - 1);
+        n >>= lg;
+        sl.r = n & 3;
+        n >>= 2;
+        sl.i = n < NQ ? n : NQ;
+        return sl;
+    }
+    // first group of slab j in a scale row
+    static EP_DEV int slab_group(int j, int wv, int lgroup)
+    {
+        const int sl = slab(j, wv);
+        return lgroup <= 9 ? sl << (9 - lgroup) : sl >> (lgroup - 9);
+    }
 
     // Issues the packed-weight loads of block bi (non-temporal: every weight
     // byte is read once per step) and the wave's one scale load.  Buffer
     // loads for the weights: the quad's base is a scalar offset, the lane's
-    // place a 32-bit vector offset.  Nothing is loaded for a block past the
-    // share or by an idle wave (the block is then never read); a quad past
-    // the share reads the segment's first quad and an idle slab reads slab
-    // 0 -- both are weighted 0 at use -- so the loads carry no branch.
-    static EP_DEV void issue(Blk &bk, const Segs &sg, int bi, int group)
+    // place a 32-bit vector offset.  The loads are issued for every block
+    // index, also past the share or for an idle slab: there the descriptor
+    // has no records, so they return zeros without touching memory -- a load
+    // issued on one path only would make the compiler's wait counts after
+    // the join assume the worst, and waits on in-order counters then drain
+    // the whole pipeline.  A quad past the share reads the segment's first
+    // quad, weighted 0 at use.  Idle waves never call it.
+    static EP_DEV void issue(Blk &bk, const Segs &sg, int bi, const SLane &sl)
     {
         const int wv = wave_id();
-        if (bi >= nblocks(sg) || !wave_on(wv))
-            return;
-        const int vb = sg.qa + bi * QPB;
+        const int j = bi / QB, qg = bi % QB;
+        const bool live = qg < ngroups(sg) && slab_on(j, wv);
         const int lane = tid_fresh() & 63;
         const uint32_t rq = (uint32_t)lane >> 4;
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
-            const int vq = vquad(vb, i, wv);
-            const bool ok = vq < sg.qb;
+            const int vq = vquad(sg, qg, i, wv);
+            const bool ok = live && vq < sg.qb;
             const int s = seg_of(sg, ok ? vq : sg.qa, i);
             const int quad = ok ? vq - first_quad(sg, s) : 0;
-            const auto rp = rsrc(sel3(s, sg.pk0, sg.pk1, sg.pk2));
-            const int sp = quad * 4 * RB;
-#pragma unroll
-            for (int j = 0; j < SPW; ++j)
-                bk.w[j][i] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rp, (int)(rq * RB + chunk_byte(j, wv)), sp, 2);
+            const auto rp = rsrc(sel3(s, sg.pk0, sg.pk1, sg.pk2), live ? 0x7fffffffu : 0u);
+            bk.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)(rq * RB + chunk_byte(j, wv)),
+                                                            quad * 4 * RB, kAuxStream);
         }
-        // scale entry n = ((j * NQ + i) * 4 + r) * G + g of this lane
-        const int G = gps(group);
-        int n = lane;
-        const int g = n % G;
-        n /= G;
-        const int r = n % 4;
-        n /= 4;
-        const int i = n % NQ, j = n / NQ;
-        const bool live = j < SPW;
-        const int vq = vquad(vb, live ? i : 0, wv);
-        const bool ok = live && vq < sg.qb;
-        const int s = seg_of(sg, ok ? vq : sg.qa, live ? i : 0);
-        const int row = ok ? (vq - first_quad(sg, s)) * 4 + r : 0;
-        const int gi = ok ? (slab(j, wv) * 512) / group + g : 0;
+        const bool sok = sl.i < NQ;
+        const int vq = vquad(sg, qg, sok ? sl.i : 0, wv);
+        const bool ok = sok && live && vq < sg.qb;
+        const int s = seg_of(sg, ok ? vq : sg.qa, sok ? sl.i : 0);
+        const int row = ok ? (vq - first_quad(sg, s)) * 4 + sl.r : 0;
+        const int gi = ok ? slab_group(j, wv, sl.lgroup) + sl.g : 0;
+        // one scale row may belong to another segment than the lane's
+        // neighbours' (q|k|v): a per-lane address, row 0 of the segment
+        // where the entry is not used
         const char *sc = sel3(s, sg.sc0, sg.sc1, sg.sc2) + (int64_t)row * sg.ldsb + gi * 2;
         bk.s = ldg((const uint16_t *)sc);
+    }
+
+    // Blocks 0 .. NBUF - 2 of a phase, issued ahead of its hand-over wait.
+    static EP_DEV void prefetch(Blk (&bb)[NBUF], const Segs &sg, int group)
+    {
+        if (!wave_on(wave_id()))
+            return;
+        const SLane sl = slane(group);
+#pragma unroll
+        for (int k = 0; k + 1 < NBUF; ++k)
+            issue(bb[k], sg, k, sl);
     }
 
     // Runs the share; outputs are tagged (`tag`).  MODE_ACC adds the share's
     // residual rows (hv, one per thread, loaded with the staging) and writes
     // the sum to ht (and to h0 when `last`).
     template <int MODE>
-    static EP_DEV void run(Blk &b0, Blk &b1, const Segs &sg, int group, const uint32_t *tab,
+    static EP_DEV void run(Blk (&bb)[NBUF], const Segs &sg, int group, const uint32_t *tab,
                            const uint32_t *xs, const uint32_t *xlo, const float *xf, float *red,
                            float *hrow, float hv, float rinv, uint64_t *ht, float *h0, bool last,
                            uint64_t *act, uint32_t tag)
     {
-        // activations (hi and lo terms): in registers for one slab per wave
-        // (32 VGPRs); with more slabs per wave they are read from LDS at use
-        f16x2_t xh[XREG ? SPW : 1][32];
         const int wv = wave_id();
-        if constexpr (XREG) {
-#pragma unroll
-            for (int j = 0; j < SPW; ++j) {
-                const uint32_t xo = chunk_byte(j, wv);  // pair index = byte index
-#pragma unroll
-                for (int p = 0; p < 16; p += 4) {
-                    const u32x4_t q4 = *(const u32x4_t *)(xs + xo + p);
-                    const u32x4_t l4 = *(const u32x4_t *)(xlo + xo + p);
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        xh[j][p + t] = as_f16x2(q4[t]);
-                        xh[j][16 + p + t] = as_f16x2(l4[t]);
-                    }
-                }
-            }
-        }
         // residual rows of the share (loaded by the caller with the staging)
         if constexpr (MODE == MODE_ACC) {
             if (tid_fresh() < (sg.qb - sg.qa) * 4)
                 hrow[tid_fresh()] = hv;
         }
-        // three buffers rotated by unrolling (a register copy of a block
-        // would wait for its loads)
-        const int nb = nblocks(sg);
-        Blk b2;
-        for (int bi = 0; bi < nb; bi += 3) {
-            issue(b2, sg, bi + 2, group);
-            block(b0, sg, bi, group, xh, xs, xlo, xf, tab, red);
-            if (bi + 1 >= nb)
-                break;
-            issue(b0, sg, bi + 3, group);
-            block(b1, sg, bi + 1, group, xh, xs, xlo, xf, tab, red);
-            if (bi + 2 >= nb)
-                break;
-            issue(b1, sg, bi + 4, group);
-            block(b2, sg, bi + 2, group, xh, xs, xlo, xf, tab, red);
+        // Straight-line over the most blocks a share can hold, NBUF buffers
+        // rotated (a register copy of a block would wait for its loads):
+        // block bi + NBUF - 1 is issued into the buffer block bi - 1 left,
+        // then block bi is computed.  Every block's loads are issued
+        // (zero-length where not live), only live blocks computed: with no
+        // loop and no conditional loads the compiler's wait before each
+        // block counts exactly the younger blocks still in flight.
+        if (wave_on(wv)) {
+            const int ng = ngroups(sg);
+            const SLane sl = slane(group);
+            float acc[QB][NQ];
+            f16x2_t xh[32];  // the slab's activations: hi terms, then lo terms
+            float fx = 0.0f;
+#pragma unroll
+            for (int bi = 0; bi < MAXB; ++bi) {
+                const int j = bi / QB, qg = bi % QB;
+                if (bi + NBUF - 1 < MAXB)
+                    issue(bb[(bi + NBUF - 1) % NBUF], sg, bi + NBUF - 1, sl);
+                if (qg == 0 && slab_on(j, wv))
+                    fx = load_x(j, wv, xs, xlo, xf, xh);
+                if (j == 0) {
+#pragma unroll
+                    for (int i = 0; i < NQ; ++i)
+                        acc[qg][i] = 0.0f;
+                }
+                if (qg < ng && slab_on(j, wv))
+                    block(bb[bi % NBUF], sg, qg, sl, xh, fx, tab, acc[qg]);
+                if (j == SPW - 1 && qg < ng)
+                    reduce(sg, qg, acc[qg], red);
+            }
         }
         __syncthreads();
         // cross-wave sums (fixed order) and outputs, one thread per row
@@ -480,79 +526,69 @@ struct Gemv {
         __syncthreads();  // LDS (tables, accumulator) free for the next phase
     }
 
-    // Dot products of one block; each row's sum into the LDS accumulator.
-    static EP_DEV void block(const Blk &bk, const Segs &sg, int bi, int group,
-                             const f16x2_t (&xh)[XREG ? SPW : 1][32], const uint32_t *xs,
-                             const uint32_t *xlo, const float *xf, const uint32_t *tab, float *red)
+    // The lane's activation chunk of slab j (hi and lo fp16 pairs) and its
+    // factor.
+    static EP_DEV float load_x(int j, int wv, const uint32_t *xs, const uint32_t *xlo, const float *xf,
+                               f16x2_t (&xh)[32])
+    {
+        const uint32_t xo = chunk_byte(j, wv);  // pair index = byte index
+#pragma unroll
+        for (int p = 0; p < 16; p += 4) {
+            const u32x4_t q4 = *(const u32x4_t *)(xs + xo + p);
+            const u32x4_t l4 = *(const u32x4_t *)(xlo + xo + p);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                xh[p + t] = as_f16x2(q4[t]);
+                xh[16 + p + t] = as_f16x2(l4[t]);
+            }
+        }
+        return xf[xo / 16];
+    }
+
+    // Dot products of one block into the rows' partial sums.
+    static EP_DEV void block(const Blk &bk, const Segs &sg, int qg, const SLane &sl,
+                             const f16x2_t (&xh)[32], float fx, const uint32_t *tab, float (&acc)[NQ])
     {
         const int lane = tid_fresh() & 63, wave = wave_id();
         const int rq = lane >> 4, c = lane & 15;
         const uint32_t lane4 = (uint32_t)lane << 2;
-        const int vb = sg.qa + bi * QPB;
-        const int G = gps(group);
-        const int gl = group >= 512 ? 0 : (c * 32) / group;  // this lane's group within its slab
-        if (!wave_on(wave))
-            return;
-        float acc[NQ];
+        const int lg = lg_gps(sl.lgroup);
+        const int gl = (c >> (4 - lg)) & ((1 << lg) - 1);  // this lane's group within the slab
 #pragma unroll
-        for (int i = 0; i < NQ; ++i)
-            acc[i] = 0.0f;
+        for (int i = 0; i < NQ; ++i) {
+            const int vq = vquad(sg, qg, i, wave);
+            const int slot = PAIRED ? (i >= RQ ? 1 : 0) : (vq < sg.qb ? seg_of(sg, vq, i) - sg.sfirst : 0);
+            const uint32_t l4s = lane4 | ((uint32_t)slot << 16);
+            // the 16 lookups of the chunk are issued back to back, then
+            // consumed (source order is kept where registers are tight)
+            uint32_t tv[16];
 #pragma unroll
-        for (int j = 0; j < SPW; ++j) {
-            if (!slab_on(j, wave))
-                continue;
-            const uint32_t xo = chunk_byte(j, wave);
-            const float fxj = xf[xo / 16];
-            f16x2_t xl[32];  // hi terms, then lo terms
+            for (int wd = 0; wd < 4; ++wd)
 #pragma unroll
-            for (int p = 0; p < 16; p += 4) {
-                if constexpr (XREG) {
+                for (int q = 0; q < 4; ++q)
+                    tv[wd * 4 + q] = lds_read_u32(tab, __builtin_amdgcn_perm(bk.w[i][wd], l4s, kSelByteSlot[q]));
+            float part = 0.0f, plo = 0.0f;
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        xl[p + t] = xh[j][p + t];
-                        xl[16 + p + t] = xh[j][16 + p + t];
-                    }
-                } else {
-                    const u32x4_t q4 = *(const u32x4_t *)(xs + xo + p);
-                    const u32x4_t l4 = *(const u32x4_t *)(xlo + xo + p);
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        xl[p + t] = as_f16x2(q4[t]);
-                        xl[16 + p + t] = as_f16x2(l4[t]);
-                    }
-                }
+            for (int k = 0; k < 16; ++k) {
+                part = __builtin_amdgcn_fdot2(as_f16x2(tv[k]), xh[k], part, false);
+                plo = __builtin_amdgcn_fdot2(as_f16x2(tv[k]), xh[16 + k], plo, false);
             }
-#pragma unroll
-            for (int i = 0; i < NQ; ++i) {
-                const int vq = vquad(vb, i, wave);
-                const int slot =
-                    PAIRED ? (i >= RQ ? 1 : 0) : (vq < sg.qb ? seg_of(sg, vq, i) - sg.sfirst : 0);
-                const uint32_t l4s = lane4 | ((uint32_t)slot << 16);
-                // the 16 lookups of the chunk are issued back to back, then
-                // consumed (source order is kept where registers are tight)
-                uint32_t tv[16];
-#pragma unroll
-                for (int wd = 0; wd < 4; ++wd)
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        tv[wd * 4 + q] = lds_read_u32(
-                            tab, __builtin_amdgcn_perm(bk.w[j][i][wd], l4s, kSelByteSlot[q]));
-                float part = 0.0f, plo = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) {
-                    part = __builtin_amdgcn_fdot2(as_f16x2(tv[k]), xl[k], part, false);
-                    plo = __builtin_amdgcn_fdot2(as_f16x2(tv[k]), xl[16 + k], plo, false);
-                }
-                part += plo;
-                const uint32_t sb = (uint32_t)__shfl((int)bk.s, ((j * NQ + i) * 4 + rq) * G + gl, 64);
-                const float sc = vq < sg.qb ? (float)f16_from_bits((uint16_t)sb) : 0.0f;
-                acc[i] = fmaf(part, sc * fxj, acc[i]);
-            }
+            part += plo;
+            const uint32_t sb = (uint32_t)__shfl((int)bk.s, (((i * 4 + rq) << lg) | gl), 64);
+            const float sc = vq < sg.qb ? (float)f16_from_bits((uint16_t)sb) : 0.0f;
+            acc[i] = fmaf(part, sc * fx, acc[i]);
         }
+    }
+
+    // Each row's 16-lane sum of quad group qg into the LDS accumulator.
+    static EP_DEV void reduce(const Segs &sg, int qg, const float (&acc)[NQ], float *red)
+    {
+        const int lane = tid_fresh() & 63, wave = wave_id();
+        const int rq = lane >> 4, c = lane & 15;
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
             const float v = row16_sum(acc[i]);
-            const int vq = vquad(vb, i, wave);
+            const int vq = vquad(sg, qg, i, wave);
             if (c == 0 && vq < sg.qb)
                 red[wave * RED_ROWS + (PAIRED && i >= RQ ? RED_ROWS / 2 : 0) + (vq - sg.qa) * 4 + rq] = v;
         }
@@ -725,9 +761,9 @@ EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, ui
 }
 
 // ---------------------------------------------------------------- attention
-EP_DEV void stamp(const StepArgs &a, int l, int ev)
+EP_DEV void stamp(const StepArgs &a, int l, int ev, int thread = 0)
 {
-    if (a.trace && tid_fresh() == 0)
+    if (a.trace && tid_fresh() == thread)
         a.trace[((int64_t)l * kEvents + ev) * gridDim.x + blockIdx.x] = (long long)wall_clock64();
 }
 
@@ -1092,10 +1128,10 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
     const PhaseLds lh = phase_lds(region, M::H), lo = phase_lds(region, M::HQD),
                    li = phase_lds(region, M::I, tab + kTabDwords);  // down: one table
 
-    using PQ = Gemv<M::SH, M::RQ_QKV, false, M::MQ_QKV>;
-    using PO = Gemv<M::SO, M::RQ_O, false, M::MQ_O>;
-    using PG = Gemv<M::SH, M::RQ_GU, true, M::MQ_GU>;
-    using PD = Gemv<M::SI, M::RQ_D, false, M::MQ_D>;
+    using PQ = Gemv<M::SH, M::RQ_QKV, false, M::MQ_QKV, M::NB_QKV>;
+    using PO = Gemv<M::SO, M::RQ_O, false, M::MQ_O, M::NB_O>;
+    using PG = Gemv<M::SH, M::RQ_GU, true, M::MQ_GU, M::NB_GU>;
+    using PD = Gemv<M::SI, M::RQ_D, false, M::MQ_D, M::NB_D>;
 
     const int pos = ldg(a.state);
     if (pos < 0 || pos >= a.max_pos)
@@ -1118,10 +1154,10 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
     const int nchunk = pos / kChunk + 1;
     const int nitems = a.Hkv * nchunk;
 
-    typename PQ::Blk q0, q1;
-    typename PO::Blk o0, o1;
-    typename PG::Blk g0, g1;
-    typename PD::Blk d0, d1;
+    typename PQ::Blk qb[PQ::NBUF];
+    typename PO::Blk ob[PO::NBUF];
+    typename PG::Blk gb[PG::NBUF];
+    typename PD::Blk db[PD::NBUF];
 
     // Each phase's codebooks are loaded one phase ahead (a wait on a load
     // issued after the weight prefetch would wait for the whole prefetch).
@@ -1130,8 +1166,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         const Segs sq = segs_qkv(a.layers[0], a, sh);
         cbv = load_cb(sq, sq.ntab, a.levels, a.cb_dtype);
         __builtin_amdgcn_sched_barrier(0);
-        PQ::issue(q0, sq, 0, a.group);
-        PQ::issue(q1, sq, 1, a.group);
+        PQ::prefetch(qb, sq, a.group);
         build_tables(tab, cb16, cbv, sq.ntab);
         const Segs so = segs_one(a.layers[0], 3, M::H, sh.ldsb_o, sh);
         cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
@@ -1148,7 +1183,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
                 l == 0 ? stage<XS_RMS_H0, M::H>(a.h0, L.attn_norm, a.eps, 0, lh.xs, lh.xl, lh.xf, part8, err)
                        : stage<XS_RMS, M::H>(a.ht, L.attn_norm, a.eps, tag_of(seq, l - 1, PH_DOWN),
                                              lh.xs, lh.xl, lh.xf, part8, err);
-            PQ::template run<MODE_STORE>(q0, q1, sq, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
+            PQ::template run<MODE_STORE>(qb, sq, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
                                          rinv, a.ht, a.h0, false, nullptr, tag_of(seq, l, PH_QKV));
         }
         stamp(a, l, 1);
@@ -1156,11 +1191,8 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // wait; then the attention items (K/V loads issued at item start)
         {
             const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
-            PO::issue(o0, so, 0, a.group);
-            PO::issue(o1, so, 1, a.group);
-            stamp(a, l, 13);
+            PO::prefetch(ob, so, a.group);
             build_tables(tab, cb16, cbv, so.ntab);
-            stamp(a, l, 14);
             const Segs sg = segs_gu(L, sh);
             cbv = load_cb(sg, sg.ntab, a.levels, a.cb_dtype);
         }
@@ -1178,15 +1210,17 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             stage<XS_BF16, M::HQD>(a.at, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf, part8,
                                    err);
             stamp(a, l, 3);
-            PO::template run<MODE_ACC>(o0, o1, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
+            PO::template run<MODE_ACC>(ob, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
                                        1.0f, a.ht, a.h0, false, nullptr, tag_of(seq, l, PH_O));
         }
         stamp(a, l, 4);
         {
             const Segs sg = segs_gu(L, sh);
-            PG::issue(g0, sg, 0, a.group);
-            PG::issue(g1, sg, 1, a.group);
+            PG::prefetch(gb, sg, a.group);
+            stamp(a, l, 13);
+            stamp(a, l, 14, 448);
             build_tables(tab, cb16, cbv, sg.ntab);
+            stamp(a, l, 15);
             const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
             cbv = load_cb(sd, sd.ntab, a.levels, a.cb_dtype);
         }
@@ -1196,14 +1230,13 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             const float rinv = stage<XS_RMS, M::H>(a.ht, L.mlp_norm, a.eps, tag_of(seq, l, PH_O),
                                                    lh.xs, lh.xl, lh.xf, part8, err);
             stamp(a, l, 5);
-            PG::template run<MODE_SWIGLU>(g0, g1, sg, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
+            PG::template run<MODE_SWIGLU>(gb, sg, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
                                           rinv, a.ht, a.h0, false, a.actt, tag_of(seq, l, PH_ACT));
         }
         stamp(a, l, 6);
         {
             const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
-            PD::issue(d0, sd, 0, a.group);
-            PD::issue(d1, sd, 1, a.group);
+            PD::prefetch(db, sd, a.group);
             build_tables(tab, cb16, cbv, sd.ntab);
             if (!last) {
                 const Segs sq = segs_qkv(a.layers[l + 1], a, sh);
@@ -1217,14 +1250,13 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             stage<XS_F32, M::I>(a.actt, nullptr, 0.0f, tag_of(seq, l, PH_ACT), li.xs, li.xl, li.xf, part8,
                                 err);
             stamp(a, l, 7);
-            PD::template run<MODE_ACC>(d0, d1, sd, a.group, tab, li.xs, li.xl, li.xf, li.red, hrow, hv,
+            PD::template run<MODE_ACC>(db, sd, a.group, tab, li.xs, li.xl, li.xf, li.red, hrow, hv,
                                        1.0f, a.ht, a.h0, last, nullptr, tag_of(seq, l, PH_DOWN));
         }
         stamp(a, l, 8);
         if (!last) {
             const Segs sq = segs_qkv(a.layers[l + 1], a, sh);
-            PQ::issue(q0, sq, 0, a.group);
-            PQ::issue(q1, sq, 1, a.group);
+            PQ::prefetch(qb, sq, a.group);
             build_tables(tab, cb16, cbv, sq.ntab);
             const Segs so = segs_one(a.layers[l + 1], 3, M::H, sh.ldsb_o, sh);
             cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
@@ -1274,7 +1306,7 @@ int launch_model(const StepArgs &a, hipStream_t stream)
 static int variant_of(const StepDesc &d)
 {
     if (d.D != kD || d.levels > 16 || d.levels < 1 ||
-        !(d.group == 128 || d.group == 256 || (d.group >= 512 && d.group % 512 == 0)) ||
+        d.group < 128 || (d.group & (d.group - 1)) != 0 ||
         d.scale_dtype != EP_F16 || (d.cb_dtype != EP_F32 && d.cb_dtype != EP_F16) || d.Hkv < 1 ||
         d.Hq % d.Hkv != 0 || d.max_pos < 64 || d.max_pos % 64 != 0) {
         set_error(EP_DECLINE_SHAPE,
