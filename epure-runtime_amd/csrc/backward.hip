@@ -66,7 +66,7 @@ __global__ void __launch_bounds__(256)
     float amax = 0.0f;
     for (int64_t n = lane; n < N; n += 64)
         amax = fmaxf(amax, fabsf(load_as_f32(gy, dt, row * ld + n)));
-    amax = wave_max(amax);
+    amax = wave_max_bfly(amax);
     if (lane == 0)
         rexp[row] = row_exponent(amax);
 }

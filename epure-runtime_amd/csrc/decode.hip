@@ -29,7 +29,7 @@ EP_DEV float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 // Sum of a value held by every thread of a 256-thread workgroup.
 EP_DEV float block_sum256(float v, float *scratch)
 {
-    v = wave_sum(v);
+    v = wave_sum_bfly(v);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     __syncthreads();
     if (lane == 0)
@@ -191,9 +191,9 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
     // chunk max / exp / sum (wave 0)
     if (t < 64) {
         const float s = sc[t];
-        const float m = wave_max(s);
+        const float m = wave_max_bfly(s);
         const float p = t0 + t < t1 ? __expf(s - m) : 0.0f;
-        const float l = wave_sum(p);
+        const float l = wave_sum_bfly(p);
         sc[t] = p;
         if (t == 0) {
             scratch[4] = m;
@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
         const f32x4_t v = *(const f32x4_t *)(a.h + k);
         ss = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], fmaf(v[3], v[3], ss))));
     }
-    ss = wave_sum(ss);
+    ss = wave_sum_bfly(ss);
     if (lane == 0)
         ssq_s[wave] = ss;
     __syncthreads();

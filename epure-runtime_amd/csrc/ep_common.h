@@ -120,19 +120,70 @@ EP_DEV int counter_add(int *p, int v)
     return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Sum over the 64 lanes of a wave (result valid in every lane).
-EP_DEV float wave_sum(float v)
+// Cross-lane reductions without the LDS unit (a ds_bpermute round trip
+// costs ~100 cycles, and a butterfly chains six of them): DPP within 16-lane
+// rows (row_ror 8, row_ror 4, quad_perm [2,3,0,1], quad_perm [1,0,3,2]),
+// then lanes l ^ 16 and l ^ 32 through v_permlane16/32_swap (gfx950).
+// Every lane ends with the same value (each step pairs commutatively).
+// All 64 lanes must be active.
+template <int CTRL>
+EP_DEV float dpp_mov(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+EP_DEV float xor16_sum(float v)
+{
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+EP_DEV float xor32_sum(float v)
+{
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+EP_DEV float xor16_max(float v)
+{
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+EP_DEV float xor32_max(float v)
+{
+    const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
+// Butterfly sums over the 64 lanes through ds_bpermute (the per-layer
+// kernels' order of additions).
+EP_DEV float wave_sum_bfly(float v)
 {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1)
         v += __shfl_xor(v, o, 64);
     return v;
 }
-
-EP_DEV float wave_max(float v)
+EP_DEV float wave_max_bfly(float v)
 {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1)
         v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
+}
+
+// Sum over the 64 lanes of a wave (result valid in every lane).
+EP_DEV float wave_sum(float v)
+{
+    v += dpp_mov<0x128>(v);
+    v += dpp_mov<0x124>(v);
+    v += dpp_mov<0x4e>(v);
+    v += dpp_mov<0xb1>(v);
+    return xor32_sum(xor16_sum(v));
+}
+
+EP_DEV float wave_max(float v)
+{
+    v = fmaxf(v, dpp_mov<0x128>(v));
+    v = fmaxf(v, dpp_mov<0x124>(v));
+    v = fmaxf(v, dpp_mov<0x4e>(v));
+    v = fmaxf(v, dpp_mov<0xb1>(v));
+    return xor32_max(xor16_max(v));
 }

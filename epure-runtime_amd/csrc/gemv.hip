@@ -292,7 +292,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
         s_cb[i] = i < a.levels ? f16_bits((f16_t)(i == tid ? cbv : load_as_f32(cbp, a.cb_dtype, i)))
                                : 0;
     if constexpr (XS == XS_RMSNORM) {
-        const float v = wave_sum(ssq);
+        const float v = wave_sum_bfly(ssq);
         if (lane == 0)
             s_part[wave] = v;
     }
@@ -450,7 +450,7 @@ __global__ void __launch_bounds__(256) gemv_generic_kernel(GemvArgs a)
             const float w = cbv * load_as_f32(sg.scale, a.scale_dtype, row * a.lds + k / a.group);
             acc = fmaf(load_as_f32(a.x, a.x_dtype, (int64_t)m * a.ldx + k), w, acc);
         }
-        acc = wave_sum(acc);
+        acc = wave_sum_bfly(acc);
         if (lane == 0) {
             const int64_t off = (int64_t)m * a.ldy + row;
             float v = acc;

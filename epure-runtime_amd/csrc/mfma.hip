@@ -57,7 +57,7 @@ __global__ void __launch_bounds__(256)
     float amax = 0.0f;
     for (int64_t k = lane; k < K; k += 64)
         amax = fmaxf(amax, fabsf(load_as_f32(x, xdt, row * ldx + k)));
-    amax = wave_max(amax);
+    amax = wave_max_bfly(amax);
     if (lane == 0)
         rexp[row] = row_exponent(amax);
 }

@@ -55,7 +55,7 @@ constexpr int kAuxStream = 2;
 constexpr int kSpinLimit = 1 << 16;  // polls (~1-2 us each) before the step fails
 constexpr int kD = 128;              // head_dim served
 constexpr int kChunk = 64;           // KV positions per attention item (8 waves x 8)
-constexpr int kEvents = 16;          // trace events per layer (debug)
+constexpr int kEvents = 24;          // trace events per layer (debug)
 
 // Geometry of a GEMV phase whose rows are S 256-byte slabs long: waves per
 // row group (WPR), row groups per workgroup (RG) and slabs per wave (SPW).
@@ -110,7 +110,7 @@ struct Model {
 
 // Llama-3-8B and Qwen3-1.7B shapes; shares
 // at 256 workgroups: q|k|v 6 / 4 quads, o 4 / 2, gate|up 14 / 6, down 4 / 2.
-using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 4, 14, 4, 0, 0, 0, 2>;
+using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 4, 14, 4, 2, 0, 0, 2>;
 using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 2, 6, 2>;
 
 // Where a phase of contraction length K keeps its activations, factors and
@@ -129,6 +129,14 @@ EP_DEV PhaseLds phase_lds(char *region, int K, uint32_t *lo_elsewhere = nullptr)
     p.red = (float *)(region + K * 2 + lo + K / 32 * 4);
     return p;
 }
+
+// ---------------------------------------------------------------- barrier
+// Workgroup barrier for LDS hand-offs: waits for this wave's LDS (and
+// scalar) operations only.  __syncthreads() also fences global memory, i.e.
+// waits for every global load and store of the wave still in flight -- the
+// weight prefetch, the tagged stores -- which nothing here orders through a
+// barrier (tagged data carries its own check).
+EP_DEV void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ---------------------------------------------------------------- memory
 // Global-address-space accesses.  A generic (flat) access may complete out
@@ -272,6 +280,11 @@ struct StepLayer {
     const uint16_t *attn_norm, *mlp_norm, *q_norm, *k_norm;  // bf16 (q/k norm may be null)
     uint16_t *kcache, *vcache;  // [Hkv][max_pos][D] bf16
 };
+
+// A layer descriptor as the kernel reads it: through the constant address
+// space, so its pointers come in by scalar loads (waited for on their own
+// counter; a vector load's wait would also wait for the weight prefetch).
+using LayerC = const __attribute__((address_space(4))) StepLayer;
 
 struct StepArgs {
     const StepLayer *layers;
@@ -494,7 +507,7 @@ struct Gemv {
                     reduce(sg, qg, acc[qg], red);
             }
         }
-        __syncthreads();
+        lds_sync();
         // cross-wave sums (fixed order) and outputs, one thread per row
         const int t = tid_fresh();
         const int nrow = (sg.qb - sg.qa) * 4;
@@ -523,7 +536,7 @@ struct Gemv {
                 st_tag(act + row, __float_as_uint(silu_mul(v * rinv, u * rinv)), tag);
             }
         }
-        __syncthreads();  // LDS (tables, accumulator) free for the next phase
+        lds_sync();  // LDS (tables, accumulator) free for the next phase
     }
 
     // The lane's activation chunk of slab j (hi and lo fp16 pairs) and its
@@ -648,7 +661,7 @@ EP_DEV void build_tables(uint32_t *tab, uint16_t *cb16, float cbv, int ntab)
 {
     if (tid_fresh() < 32)
         cb16[tid_fresh()] = f16_bits((f16_t)cbv);
-    __syncthreads();
+    lds_sync();
     build_table<4>(tab, cb16);
     if (ntab > 1)
         build_table<4>(tab + kTabDwords, cb16 + 16);
@@ -725,8 +738,8 @@ EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, ui
 #pragma unroll
         for (int t = 0; t < 8; ++t)
             am = fmaxf(am, fabsf(v[t]));
-        am = fmaxf(am, __shfl_xor(am, 1, 64));
-        am = fmaxf(am, __shfl_xor(am, 2, 64));
+        am = fmaxf(am, dpp_mov<0xb1>(am));  // lanes ^ 1
+        am = fmaxf(am, dpp_mov<0x4e>(am));  // lanes ^ 2
         const int ex = row_exponent(am);
         const float pw = ldexpf(1.0f, -ex);
         u32x4_t q4, l4;
@@ -749,7 +762,7 @@ EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, ui
         if ((tid_fresh() & 63) == 0)
             part8[tid_fresh() >> 6] = s;
     }
-    __syncthreads();
+    lds_sync();
     if constexpr (XS == XS_RMS_H0 || XS == XS_RMS) {
         float q = 0.0f;
 #pragma unroll
@@ -807,8 +820,8 @@ EP_DEV void attn_load(AttnRegs &r, const uint16_t *kc, const uint16_t *vc, int j
 EP_DEV float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 template <int GQ>
-EP_DEV void attn_item(const StepArgs &a, const StepLayer &L, int l, uint32_t seq, int j, int c,
-                      int nchunk, int pos, char *scratch)
+EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, int c,
+                      int nchunk, int pos, char *scratch, const AttnRegs &r)
 {
     const int tid = tid_fresh(), lane = tid & 63, wave = wave_id();
     const int rr = lane >> 4, e16 = lane & 15;
@@ -822,8 +835,6 @@ EP_DEV void attn_item(const StepArgs &a, const StepLayer &L, int l, uint32_t seq
     const int hq0 = j * GQ;
     int *err = a.sync + 2;
 
-    AttnRegs r;
-    attn_load(r, L.kcache, L.vcache, j, c, pos, a.max_pos);
 
     // this step's q (GQ heads), k and v rows: per-head RMSNorm (Qwen3) and
     // rotate-half RoPE on q and k; k and v rounded to bf16 as cached.  Lane l
@@ -863,7 +874,7 @@ EP_DEV void attn_item(const StepArgs &a, const StepLayer &L, int l, uint32_t seq
             vn[lane + 64] = bf16r(x1);
         }
     }
-    __syncthreads();
+    lds_sync();
     stamp(a, l, 10);  // q/k/v received
     if (c == nchunk - 1 && tid < kD) {  // append this step's row (read by later steps only)
         const int64_t row = ((int64_t)j * a.max_pos + pos) * kD + tid;
@@ -921,7 +932,8 @@ EP_DEV void attn_item(const StepArgs &a, const StepLayer &L, int l, uint32_t seq
             for (int g = 0; g < GQ; ++g)
                 S[g * kChunk + wave * kRowsPerWave + 4 * k + rr] = -INFINITY;
     }
-    __syncthreads();
+    lds_sync();
+    stamp(a, l, 16);  // scores
     // softmax over the chunk, one wave per head: one score per lane
     static_assert(kChunk == 64, "one score per lane");
     if (wave < GQ) {
@@ -935,7 +947,8 @@ EP_DEV void attn_item(const StepArgs &a, const StepLayer &L, int l, uint32_t seq
             lw[wave] = lsum;
         }
     }
-    __syncthreads();
+    lds_sync();
+    stamp(a, l, 17);  // softmax
     // P.V: 8 dims per lane over its 8 rows, then over the wave's 4 row
     // groups (lanes l, l ^ 16, l ^ 32, l ^ 48), then over the 8 waves
     float o[GQ][8];
@@ -972,8 +985,7 @@ EP_DEV void attn_item(const StepArgs &a, const StepLayer &L, int l, uint32_t seq
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             float x = o[g][t];
-            x += __shfl_xor(x, 16, 64);
-            x += __shfl_xor(x, 32, 64);
+            x = xor32_sum(xor16_sum(x));
             o[g][t] = x;
         }
     if (rr == 0) {
@@ -985,7 +997,7 @@ EP_DEV void attn_item(const StepArgs &a, const StepLayer &L, int l, uint32_t seq
                 (f32x4_t){o[g][4], o[g][5], o[g][6], o[g][7]};
         }
     }
-    __syncthreads();
+    lds_sync();
     stamp(a, l, 11);  // scores, softmax, P.V done
     // sum over the 8 waves; thread (g, dims 2dd, 2dd + 1)
     const bool cth = tid < GQ * 64;
@@ -1062,7 +1074,7 @@ struct Shape {
     int Nq, Nkv, H, I, ldsb_h, ldsb_o, ldsb_i, b, G;
 };
 
-EP_DEV Segs segs_qkv(const StepLayer &L, const StepArgs &a, const Shape &sh)
+EP_DEV Segs segs_qkv(LayerC &L, const StepArgs &a, const Shape &sh)
 {
     Segs s;
     s.pk0 = L.packed[0];
@@ -1085,7 +1097,7 @@ EP_DEV Segs segs_qkv(const StepLayer &L, const StepArgs &a, const Shape &sh)
     return s;
 }
 
-EP_DEV Segs segs_one(const StepLayer &L, int li, int N, int ldsb, const Shape &sh)
+EP_DEV Segs segs_one(LayerC &L, int li, int N, int ldsb, const Shape &sh)
 {
     Segs s;
     s.pk0 = s.pk1 = s.pk2 = L.packed[li];
@@ -1099,7 +1111,7 @@ EP_DEV Segs segs_one(const StepLayer &L, int li, int N, int ldsb, const Shape &s
     return s;
 }
 
-EP_DEV Segs segs_gu(const StepLayer &L, const Shape &sh)
+EP_DEV Segs segs_gu(LayerC &L, const Shape &sh)
 {
     Segs s;
     s.pk0 = L.packed[4];
@@ -1133,6 +1145,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
     using PG = Gemv<M::SH, M::RQ_GU, true, M::MQ_GU, M::NB_GU>;
     using PD = Gemv<M::SI, M::RQ_D, false, M::MQ_D, M::NB_D>;
 
+    LayerC *layers = (LayerC *)a.layers;
     const int pos = ldg(a.state);
     if (pos < 0 || pos >= a.max_pos)
         return;  // uniform: past the cache, nothing to do
@@ -1163,17 +1176,17 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
     // issued after the weight prefetch would wait for the whole prefetch).
     float cbv;
     {
-        const Segs sq = segs_qkv(a.layers[0], a, sh);
+        const Segs sq = segs_qkv(layers[0], a, sh);
         cbv = load_cb(sq, sq.ntab, a.levels, a.cb_dtype);
         __builtin_amdgcn_sched_barrier(0);
         PQ::prefetch(qb, sq, a.group);
         build_tables(tab, cb16, cbv, sq.ntab);
-        const Segs so = segs_one(a.layers[0], 3, M::H, sh.ldsb_o, sh);
+        const Segs so = segs_one(layers[0], 3, M::H, sh.ldsb_o, sh);
         cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
     }
 
     for (int l = 0; l < a.n_layers; ++l) {
-        const StepLayer &L = a.layers[l];
+        LayerC &L = layers[l];
         const bool last = l + 1 == a.n_layers;
         stamp(a, l, 0);
         // ---- q|k|v (RMSNorm of the residual in the activation load)
@@ -1187,8 +1200,12 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
                                          rinv, a.ht, a.h0, false, nullptr, tag_of(seq, l, PH_QKV));
         }
         stamp(a, l, 1);
-        // o weights go out and the o table is built before any attention
-        // wait; then the attention items (K/V loads issued at item start)
+        // the first attention item's K/V rows (cached by earlier steps) go
+        // out first, then the o weights, and the o table is built before any
+        // attention wait
+        AttnRegs ar;
+        if (b < nitems)
+            attn_load(ar, L.kcache, L.vcache, b % a.Hkv, b / a.Hkv, pos, a.max_pos);
         {
             const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
             PO::prefetch(ob, so, a.group);
@@ -1198,9 +1215,17 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         }
         stamp(a, l, 9);
         // ---- attention
-        for (int it = b; it < nitems; it += G) {
-            attn_item<M::GQ>(a, L, l, seq, it % a.Hkv, it / a.Hkv, nchunk, pos, region);
-            __syncthreads();
+        // (the first item apart: a loop-carried merge of its preloaded rows
+        // with a later item's loads would wait for every load in flight)
+        if (b < nitems) {
+            attn_item<M::GQ>(a, L, l, seq, b % a.Hkv, b / a.Hkv, nchunk, pos, region, ar);
+            lds_sync();
+            for (int it = b + G; it < nitems; it += G) {
+                AttnRegs r2;
+                attn_load(r2, L.kcache, L.vcache, it % a.Hkv, it / a.Hkv, pos, a.max_pos);
+                attn_item<M::GQ>(a, L, l, seq, it % a.Hkv, it / a.Hkv, nchunk, pos, region, r2);
+                lds_sync();
+            }
         }
         stamp(a, l, 2);
         // ---- o (+= residual)
@@ -1239,7 +1264,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             PD::prefetch(db, sd, a.group);
             build_tables(tab, cb16, cbv, sd.ntab);
             if (!last) {
-                const Segs sq = segs_qkv(a.layers[l + 1], a, sh);
+                const Segs sq = segs_qkv(layers[l + 1], a, sh);
                 cbv = load_cb(sq, sq.ntab, a.levels, a.cb_dtype);
             }
         }
@@ -1255,16 +1280,16 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         }
         stamp(a, l, 8);
         if (!last) {
-            const Segs sq = segs_qkv(a.layers[l + 1], a, sh);
+            const Segs sq = segs_qkv(layers[l + 1], a, sh);
             PQ::prefetch(qb, sq, a.group);
             build_tables(tab, cb16, cbv, sq.ntab);
-            const Segs so = segs_one(a.layers[l + 1], 3, M::H, sh.ldsb_o, sh);
+            const Segs so = segs_one(layers[l + 1], 3, M::H, sh.ldsb_o, sh);
             cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
         }
     }
     // the last workgroup to finish advances the launch sequence (every
     // workgroup has read it by then)
-    __syncthreads();
+    __syncthreads();  // the step's stores complete before the count
     if (tid_fresh() == 0 && counter_add(a.sync, 1) == G - 1) {
         st_agent(a.sync, 0);
         st_agent(a.sync + 1, (int)(seq + 1));

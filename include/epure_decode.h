@@ -97,7 +97,7 @@ int ep_lm_head_argmax(float *h, const uint16_t *norm_w, float eps, const uint16_
  * zeroed before the first call and is left valid for the next; its int
  * word 2 becomes nonzero if a hand-over wait timed out (the step's results
  * are then garbage).  `trace`, when not NULL, receives wall-clock stamps
- * [n_layers][16][grid] (debug).  Declines (> 0) shapes without a
+ * [n_layers][24][grid] (debug).  Declines (> 0) shapes without a
  * persistent variant (ep_decode_step_serves; groups a power of two >= 128,
  * fp16 scales, 4-bit indices).  Position = state[0].
  */
