@@ -110,7 +110,7 @@ struct Model {
 
 // Llama-3-8B and Qwen3-1.7B shapes; shares
 // at 256 workgroups: q|k|v 6 / 4 quads, o 4 / 2, gate|up 14 / 6, down 4 / 2.
-using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 4, 14, 4, 2, 0, 0, 2>;
+using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 4, 14, 4, 0, 0, 0, 2>;
 using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 2, 6, 2>;
 
 // Where a phase of contraction length K keeps its activations, factors and
@@ -356,10 +356,11 @@ struct Gemv {
     static EP_DEV bool wave_on(int wv) { return wv / WPR < RG; }
     static EP_DEV bool slab_on(int j, int wv) { return wave_on(wv) && (wv % WPR) + j * WPR < S; }
     static EP_DEV int slab(int j, int wv) { return slab_on(j, wv) ? (wv % WPR) + j * WPR : 0; }
-    // byte offset of the lane's 16-byte chunk of slab j within a row
+    // byte offset of the lane's 16-byte chunk of slab j within a row: lane
+    // l covers chunk l >> 2 of row l & 3 of a quad (the 4x4x4 MFMA layout)
     static EP_DEV uint32_t chunk_byte(int j, int wv)
     {
-        return (uint32_t)(slab(j, wv) * kSlabBytes + (tid_fresh() & 15) * 16);
+        return (uint32_t)(slab(j, wv) * kSlabBytes + ((tid_fresh() & 63) >> 2) * 16);
     }
 
     static EP_DEV int ngroups(const Segs &sg) { return (sg.qb - sg.qa + QPB - 1) / QPB; }
@@ -426,7 +427,7 @@ struct Gemv {
         const int j = bi / QB, qg = bi % QB;
         const bool live = qg < ngroups(sg) && slab_on(j, wv);
         const int lane = tid_fresh() & 63;
-        const uint32_t rq = (uint32_t)lane >> 4;
+        const uint32_t rq = (uint32_t)lane & 3;
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
             const int vq = vquad(sg, qg, i, wv);
@@ -487,7 +488,7 @@ struct Gemv {
             const int ng = ngroups(sg);
             const SLane sl = slane(group);
             float acc[QB][NQ];
-            f16x2_t xh[32];  // the slab's activations: hi terms, then lo terms
+            f16x2_t xa[16];  // the slab's activations (MFMA A operand: hi, lo or 0)
             float fx = 0.0f;
 #pragma unroll
             for (int bi = 0; bi < MAXB; ++bi) {
@@ -495,14 +496,14 @@ struct Gemv {
                 if (bi + NBUF - 1 < MAXB)
                     issue(bb[(bi + NBUF - 1) % NBUF], sg, bi + NBUF - 1, sl);
                 if (qg == 0 && slab_on(j, wv))
-                    fx = load_x(j, wv, xs, xlo, xf, xh);
+                    fx = load_x(j, wv, xs, xlo, xf, xa);
                 if (j == 0) {
 #pragma unroll
                     for (int i = 0; i < NQ; ++i)
                         acc[qg][i] = 0.0f;
                 }
                 if (qg < ng && slab_on(j, wv))
-                    block(bb[bi % NBUF], sg, qg, sl, xh, fx, tab, acc[qg]);
+                    block(bb[bi % NBUF], sg, qg, sl, xa, fx, tab, acc[qg]);
                 if (j == SPW - 1 && qg < ng)
                     reduce(sg, qg, acc[qg], red);
             }
@@ -539,31 +540,36 @@ struct Gemv {
         lds_sync();  // LDS (tables, accumulator) free for the next phase
     }
 
-    // The lane's activation chunk of slab j (hi and lo fp16 pairs) and its
-    // factor.
+    // The lane's A operand for slab j: lanes 4 b + 0 and 4 b + 1 hold the hi
+    // and lo fp16 terms of the slab's activation chunk b (32 values as 16
+    // pairs), lanes 4 b + 2 and 4 b + 3 zeros; and the chunk's factor.
     static EP_DEV float load_x(int j, int wv, const uint32_t *xs, const uint32_t *xlo, const float *xf,
-                               f16x2_t (&xh)[32])
+                               f16x2_t (&xa)[16])
     {
+        const int ai = tid_fresh() & 3;
         const uint32_t xo = chunk_byte(j, wv);  // pair index = byte index
+        const uint32_t *src = ai == 0 ? xs : xlo;
 #pragma unroll
         for (int p = 0; p < 16; p += 4) {
-            const u32x4_t q4 = *(const u32x4_t *)(xs + xo + p);
-            const u32x4_t l4 = *(const u32x4_t *)(xlo + xo + p);
+            const u32x4_t q4 = *(const u32x4_t *)(src + xo + p);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                xh[p + t] = as_f16x2(q4[t]);
-                xh[16 + p + t] = as_f16x2(l4[t]);
-            }
+            for (int t = 0; t < 4; ++t)
+                xa[p + t] = as_f16x2(ai < 2 ? q4[t] : 0u);
         }
         return xf[xo / 16];
     }
 
-    // Dot products of one block into the rows' partial sums.
+    // Dot products of one block into the rows' partial sums on the matrix
+    // cores: v_mfma_f32_4x4x4_16b_f16 with block b = the lane's chunk, A =
+    // activations (rows hi, lo, 0, 0), B = the quad's dequantized weights
+    // (columns = its 4 rows); eight MFMAs take the chunk's 32 weights.  Lane
+    // 4 b + r then holds the chunk's hi and lo dot products of row r (D rows
+    // 0 and 1), scaled by the row's group scale and the chunk's factor.
     static EP_DEV void block(const Blk &bk, const Segs &sg, int qg, const SLane &sl,
-                             const f16x2_t (&xh)[32], float fx, const uint32_t *tab, float (&acc)[NQ])
+                             const f16x2_t (&xa)[16], float fx, const uint32_t *tab, float (&acc)[NQ])
     {
         const int lane = tid_fresh() & 63, wave = wave_id();
-        const int rq = lane >> 4, c = lane & 15;
+        const int rq = lane & 3, c = lane >> 2;
         const uint32_t lane4 = (uint32_t)lane << 2;
         const int lg = lg_gps(sl.lgroup);
         const int gl = (c >> (4 - lg)) & ((1 << lg) - 1);  // this lane's group within the slab
@@ -580,29 +586,36 @@ struct Gemv {
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                     tv[wd * 4 + q] = lds_read_u32(tab, __builtin_amdgcn_perm(bk.w[i][wd], l4s, kSelByteSlot[q]));
-            float part = 0.0f, plo = 0.0f;
+            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                part = __builtin_amdgcn_fdot2(as_f16x2(tv[k]), xh[k], part, false);
-                plo = __builtin_amdgcn_fdot2(as_f16x2(tv[k]), xh[16 + k], plo, false);
+            for (int n = 0; n < 8; ++n) {
+                const f16x2_t a0 = xa[2 * n], a1 = xa[2 * n + 1];
+                const f16x2_t b0 = as_f16x2(tv[2 * n]), b1 = as_f16x2(tv[2 * n + 1]);
+                const f16x4_t av = {a0[0], a0[1], a1[0], a1[1]};
+                const f16x4_t bv = {b0[0], b0[1], b1[0], b1[1]};
+                d = __builtin_amdgcn_mfma_f32_4x4x4f16(av, bv, d, 0, 0, 0);
             }
-            part += plo;
             const uint32_t sb = (uint32_t)__shfl((int)bk.s, (((i * 4 + rq) << lg) | gl), 64);
             const float sc = vq < sg.qb ? (float)f16_from_bits((uint16_t)sb) : 0.0f;
-            acc[i] = fmaf(part, sc * fx, acc[i]);
+            acc[i] = fmaf(d[0] + d[1], sc * fx, acc[i]);
         }
     }
 
-    // Each row's 16-lane sum of quad group qg into the LDS accumulator.
+    // Each row's sum over the 16 chunks (lanes r, r + 4, .., r + 60) of quad
+    // group qg into the LDS accumulator: DPP row_ror 4 and 8, then lanes
+    // l ^ 16 and l ^ 32.
     static EP_DEV void reduce(const Segs &sg, int qg, const float (&acc)[NQ], float *red)
     {
         const int lane = tid_fresh() & 63, wave = wave_id();
-        const int rq = lane >> 4, c = lane & 15;
+        const int rq = lane & 3;
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
-            const float v = row16_sum(acc[i]);
+            float v = acc[i];
+            v += dpp_mov<0x124>(v);
+            v += dpp_mov<0x128>(v);
+            v = xor32_sum(xor16_sum(v));
             const int vq = vquad(sg, qg, i, wave);
-            if (c == 0 && vq < sg.qb)
+            if (lane < 4 && vq < sg.qb)
                 red[wave * RED_ROWS + (PAIRED && i >= RQ ? RED_ROWS / 2 : 0) + (vq - sg.qa) * 4 + rq] = v;
         }
     }
@@ -819,9 +832,10 @@ EP_DEV void attn_load(AttnRegs &r, const uint16_t *kc, const uint16_t *vc, int j
 
 EP_DEV float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
-template <int GQ>
+// `received` runs once this step's q|k|v rows are in.
+template <int GQ, class F>
 EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, int c,
-                      int nchunk, int pos, char *scratch, const AttnRegs &r)
+                      int nchunk, int pos, char *scratch, const AttnRegs &r, F received)
 {
     const int tid = tid_fresh(), lane = tid & 63, wave = wave_id();
     const int rr = lane >> 4, e16 = lane & 15;
@@ -876,6 +890,7 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
     }
     lds_sync();
     stamp(a, l, 10);  // q/k/v received
+    received();
     if (c == nchunk - 1 && tid < kD) {  // append this step's row (read by later steps only)
         const int64_t row = ((int64_t)j * a.max_pos + pos) * kD + tid;
         stg(L.kcache + row, f32_to_bf16(kn[tid]));
@@ -1029,25 +1044,41 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
         return;
     }
     if (cth) {
-        for (int cc = 1; cc < nchunk; ++cc) {  // running combine, chunk order
-            const uint64_t *pc = a.part + ((int64_t)(hq0 + g) * maxch + cc) * (kD + 2);
-            uint64_t e0, e1, e2, e3;
-            Spin sp;
-            do {
-                e0 = ld_tag(pc);
-                e1 = ld_tag(pc + 1);
-                e2 = ld_tag(pc + 2 + dd);
-                e3 = ld_tag(pc + 3 + dd);
-            } while (((uint32_t)(e0 >> 32) != tpart || (uint32_t)(e1 >> 32) != tpart ||
-                      (uint32_t)(e2 >> 32) != tpart || (uint32_t)(e3 >> 32) != tpart) &&
-                     sp.again(err));
-            const float Mc = __uint_as_float((uint32_t)e0);
-            const float Mn = fmaxf(M, Mc);
-            const float fa = __expf(M - Mn), fb = __expf(Mc - Mn);
-            Ls = Ls * fa + __uint_as_float((uint32_t)e1) * fb;
-            n0 = n0 * fa + __uint_as_float((uint32_t)e2) * fb;
-            n1 = n1 * fa + __uint_as_float((uint32_t)e3) * fb;
-            M = Mn;
+        // running combine in chunk order; the partials of up to kCombine
+        // chunks are requested at once, then re-read where not yet there
+        constexpr int kCombine = 8;
+        const uint64_t *pg = a.part + (int64_t)(hq0 + g) * maxch * (kD + 2);
+        auto ready = [&](const uint64_t (&e)[4]) {
+            return (uint32_t)(e[0] >> 32) == tpart && (uint32_t)(e[1] >> 32) == tpart &&
+                   (uint32_t)(e[2] >> 32) == tpart && (uint32_t)(e[3] >> 32) == tpart;
+        };
+        auto fetch = [&](uint64_t (&e)[4], int cc) {
+            const uint64_t *pc = pg + (int64_t)cc * (kD + 2);
+            e[0] = ld_tag(pc);
+            e[1] = ld_tag(pc + 1);
+            e[2] = ld_tag(pc + 2 + dd);
+            e[3] = ld_tag(pc + 3 + dd);
+        };
+        for (int c0 = 1; c0 < nchunk; c0 += kCombine) {
+            uint64_t e[kCombine][4];
+#pragma unroll
+            for (int k = 0; k < kCombine; ++k)
+                fetch(e[k], c0 + k < nchunk ? c0 + k : c0);
+#pragma unroll
+            for (int k = 0; k < kCombine; ++k) {
+                if (c0 + k >= nchunk)
+                    break;
+                Spin sp;
+                while (!ready(e[k]) && sp.again(err))
+                    fetch(e[k], c0 + k);
+                const float Mc = __uint_as_float((uint32_t)e[k][0]);
+                const float Mn = fmaxf(M, Mc);
+                const float fa = __expf(M - Mn), fb = __expf(Mc - Mn);
+                Ls = Ls * fa + __uint_as_float((uint32_t)e[k][1]) * fb;
+                n0 = n0 * fa + __uint_as_float((uint32_t)e[k][2]) * fb;
+                n1 = n1 * fa + __uint_as_float((uint32_t)e[k][3]) * fb;
+                M = Mn;
+            }
         }
         st_tag(outp, (uint32_t)f32_to_bf16(n0 / Ls) | ((uint32_t)f32_to_bf16(n1 / Ls) << 16), tatt);
     }
@@ -1200,32 +1231,37 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
                                          rinv, a.ht, a.h0, false, nullptr, tag_of(seq, l, PH_QKV));
         }
         stamp(a, l, 1);
-        // the first attention item's K/V rows (cached by earlier steps) go
-        // out first, then the o weights, and the o table is built before any
-        // attention wait
-        AttnRegs ar;
-        if (b < nitems)
-            attn_load(ar, L.kcache, L.vcache, b % a.Hkv, b / a.Hkv, pos, a.max_pos);
-        {
-            const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
-            PO::prefetch(ob, so, a.group);
-            build_tables(tab, cb16, cbv, so.ntab);
-            const Segs sg = segs_gu(L, sh);
-            cbv = load_cb(sg, sg.ntab, a.levels, a.cb_dtype);
-        }
-        stamp(a, l, 9);
-        // ---- attention
-        // (the first item apart: a loop-carried merge of its preloaded rows
-        // with a later item's loads would wait for every load in flight)
+        // Attention workgroups issue their first item's K/V rows (cached by
+        // earlier steps) and wait for q|k|v at once; their o weights go out
+        // once q|k|v are in (loads issued before the wait would delay it:
+        // results return in order) and the o table is built after the
+        // attention.  The other workgroups prefetch o and build its table now.
+        const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
         if (b < nitems) {
-            attn_item<M::GQ>(a, L, l, seq, b % a.Hkv, b / a.Hkv, nchunk, pos, region, ar);
+            AttnRegs ar;
+            attn_load(ar, L.kcache, L.vcache, b % a.Hkv, b / a.Hkv, pos, a.max_pos);
+            stamp(a, l, 9);
+            // (the first item apart: a loop-carried merge of its preloaded
+            // rows with a later item's loads would wait for every load in
+            // flight)
+            attn_item<M::GQ>(a, L, l, seq, b % a.Hkv, b / a.Hkv, nchunk, pos, region, ar,
+                             [&] { PO::prefetch(ob, so, a.group); });
             lds_sync();
             for (int it = b + G; it < nitems; it += G) {
                 AttnRegs r2;
                 attn_load(r2, L.kcache, L.vcache, it % a.Hkv, it / a.Hkv, pos, a.max_pos);
-                attn_item<M::GQ>(a, L, l, seq, it % a.Hkv, it / a.Hkv, nchunk, pos, region, r2);
+                attn_item<M::GQ>(a, L, l, seq, it % a.Hkv, it / a.Hkv, nchunk, pos, region, r2, [] {});
                 lds_sync();
             }
+            build_tables(tab, cb16, cbv, so.ntab);
+        } else {
+            PO::prefetch(ob, so, a.group);
+            build_tables(tab, cb16, cbv, so.ntab);
+            stamp(a, l, 9);
+        }
+        {
+            const Segs sg = segs_gu(L, sh);
+            cbv = load_cb(sg, sg.ntab, a.levels, a.cb_dtype);
         }
         stamp(a, l, 2);
         // ---- o (+= residual)
