@@ -52,6 +52,13 @@ constexpr int kThreads = 512;
 constexpr int kWaves = 8;
 // cache policy of the weight loads: nt (streamed, read once per step)
 constexpr int kAuxStream = 2;
+// Hand-over vectors every workgroup reads whole (the residual, the
+// attention output, the SwiGLU output) are read through the L2 of each XCD
+// first, which is only safe where no stale copy can be cached there -- so
+// each rotates through kRing slots per layer (a slot comes back kRing
+// layers later, long evicted by then); an entry whose tag is not current
+// yet is re-read coherently (sc1).
+constexpr int kRing = 32;
 constexpr int kSpinLimit = 1 << 16;  // polls (~1-2 us each) before the step fails
 constexpr int kD = 128;              // head_dim served
 constexpr int kChunk = 64;           // KV positions per attention item (8 waves x 8)
@@ -290,10 +297,10 @@ struct StepArgs {
     const StepLayer *layers;
     int n_layers;
     float *h0;          // [H] f32: the step's input embedding; the final residual on exit
-    uint64_t *ht;       // [H] tagged residual
+    uint64_t *ht;       // [2 kRing][H] tagged residual: o and down outputs of each layer
     uint64_t *qt, *kt, *vt;  // [Hq * D], [Hkv * D], [Hkv * D] tagged f32
-    uint64_t *at;       // [Hq * D / 2] tagged bf16 pairs: attention output
-    uint64_t *actt;     // [I] tagged f32: silu(gate) * up
+    uint64_t *at;       // [kRing][Hq * D / 2] tagged bf16 pairs: attention output
+    uint64_t *actt;     // [kRing][I] tagged f32: silu(gate) * up
     uint64_t *part;     // [Hq][max_pos / kChunk + 1][D + 2] tagged split-KV partials
     int *sync;          // [0] finished workgroups, [1] launch sequence, [2] error flag
     const float *cos_t, *sin_t;  // [max_pos][D / 2]
@@ -707,12 +714,14 @@ EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, ui
                 v[4 + t] = __uint_as_float(h1[t]);
             }
         } else if constexpr (XS == XS_BF16) {
-            u32x4_t q0, q1;  // 4 entries: 2 bf16 + tag each
+            // 4 entries: 2 bf16 + tag each; a ring slot: first through the caches
+            u32x4_t q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)e * 32, 0, 0);
+            u32x4_t q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)e * 32 + 16, 0, 0);
             Spin sp;
-            do {
+            while ((q0[1] != tag || q0[3] != tag || q1[1] != tag || q1[3] != tag) && sp.again(err)) {
                 q0 = ldc16(rs, (uint32_t)e * 32);
                 q1 = ldc16(rs, (uint32_t)e * 32 + 16);
-            } while ((q0[1] != tag || q0[3] != tag || q1[1] != tag || q1[3] != tag) && sp.again(err));
+            }
             unpack_pair<EP_BF16>(q0[0], v[0], v[1]);
             unpack_pair<EP_BF16>(q0[2], v[2], v[3]);
             unpack_pair<EP_BF16>(q1[0], v[4], v[5]);
@@ -720,16 +729,21 @@ EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, ui
         } else {  // XS_RMS, XS_F32: 8 tagged f32 = 64 bytes
             u32x4_t q[4];
             Spin sp;
-            bool ok;
-            do {
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    q[t] = ldc16(rs, (uint32_t)e * 64 + 16 * t);
-                ok = true;
+            auto ready = [&] {
+                bool ok = true;
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
                     ok = ok && q[t][1] == tag && q[t][3] == tag;
-            } while (!ok && sp.again(err));
+                return ok;
+            };
+#pragma unroll
+            for (int t = 0; t < 4; ++t)  // a ring slot: first through the caches
+                q[t] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)e * 64 + 16 * t, 0, 0);
+            while (!ready() && sp.again(err)) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    q[t] = ldc16(rs, (uint32_t)e * 64 + 16 * t);
+            }
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 v[2 * t] = __uint_as_float(q[t][0]);
@@ -835,7 +849,7 @@ EP_DEV float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 // `received` runs once this step's q|k|v rows are in.
 template <int GQ, class F>
 EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, int c,
-                      int nchunk, int pos, char *scratch, const AttnRegs &r, F received)
+                      int nchunk, int pos, char *scratch, uint64_t *at, const AttnRegs &r, F received)
 {
     const int tid = tid_fresh(), lane = tid & 63, wave = wave_id();
     const int rr = lane >> 4, e16 = lane & 15;
@@ -1027,7 +1041,7 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
             n1 += ow[(w * GQ + g) * kD + dd + 1];
         }
     }
-    uint64_t *outp = a.at + ((hq0 + g) * kD + dd) / 2;
+    uint64_t *outp = at + ((hq0 + g) * kD + dd) / 2;
     const uint32_t tatt = tag_of(seq, l, PH_ATT), tpart = tag_of(seq, l, PH_PART);
     const int maxch = a.max_pos / kChunk + 1;
     if (nchunk > 1 && c > 0) {
@@ -1089,13 +1103,13 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
 // The residual rows an accumulating phase owns (one per thread), read with
 // its activation staging: layer 0's o reads the untagged input h0, later
 // phases the tagged residual.
-EP_DEV float residual_rows(const Segs &sg, const StepArgs &a, bool from_h0, uint32_t tag)
+EP_DEV float residual_rows(const Segs &sg, const StepArgs &a, const uint64_t *hsrc, uint32_t tag)
 {
     const int t = tid_fresh();
     if (t >= (sg.qb - sg.qa) * 4)
         return 0.0f;
     const int row = sg.qa * 4 + t;
-    return from_h0 ? ldg(a.h0 + row) : ld_tag_f32(a.ht + row, tag, a.sync + 2);
+    return hsrc ? ld_tag_f32(hsrc + row, tag, a.sync + 2) : ldg(a.h0 + row);
 }
 
 
@@ -1218,6 +1232,14 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
 
     for (int l = 0; l < a.n_layers; ++l) {
         LayerC &L = layers[l];
+        // this layer's ring slots: residual after o and after down, the
+        // attention output, the SwiGLU output; the previous layer's residual
+        const uint32_t gl = seq * (uint32_t)a.n_layers + (uint32_t)l;
+        uint64_t *h_o = a.ht + (size_t)((2 * gl) % (2 * kRing)) * M::H;
+        uint64_t *h_d = a.ht + (size_t)((2 * gl + 1) % (2 * kRing)) * M::H;
+        const uint64_t *h_prev = l == 0 ? nullptr : a.ht + (size_t)((2 * gl - 1) % (2 * kRing)) * M::H;
+        uint64_t *at_l = a.at + (size_t)(gl % kRing) * (M::HQD / 2);
+        uint64_t *actl = a.actt + (size_t)(gl % kRing) * M::I;
         const bool last = l + 1 == a.n_layers;
         stamp(a, l, 0);
         // ---- q|k|v (RMSNorm of the residual in the activation load)
@@ -1225,10 +1247,10 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             const Segs sq = segs_qkv(L, a, sh);
             const float rinv =
                 l == 0 ? stage<XS_RMS_H0, M::H>(a.h0, L.attn_norm, a.eps, 0, lh.xs, lh.xl, lh.xf, part8, err)
-                       : stage<XS_RMS, M::H>(a.ht, L.attn_norm, a.eps, tag_of(seq, l - 1, PH_DOWN),
+                       : stage<XS_RMS, M::H>(h_prev, L.attn_norm, a.eps, tag_of(seq, l - 1, PH_DOWN),
                                              lh.xs, lh.xl, lh.xf, part8, err);
             PQ::template run<MODE_STORE>(qb, sq, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
-                                         rinv, a.ht, a.h0, false, nullptr, tag_of(seq, l, PH_QKV));
+                                         rinv, nullptr, a.h0, false, nullptr, tag_of(seq, l, PH_QKV));
         }
         stamp(a, l, 1);
         // Attention workgroups issue their first item's K/V rows (cached by
@@ -1244,13 +1266,14 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             // (the first item apart: a loop-carried merge of its preloaded
             // rows with a later item's loads would wait for every load in
             // flight)
-            attn_item<M::GQ>(a, L, l, seq, b % a.Hkv, b / a.Hkv, nchunk, pos, region, ar,
+            attn_item<M::GQ>(a, L, l, seq, b % a.Hkv, b / a.Hkv, nchunk, pos, region, at_l, ar,
                              [&] { PO::prefetch(ob, so, a.group); });
             lds_sync();
             for (int it = b + G; it < nitems; it += G) {
                 AttnRegs r2;
                 attn_load(r2, L.kcache, L.vcache, it % a.Hkv, it / a.Hkv, pos, a.max_pos);
-                attn_item<M::GQ>(a, L, l, seq, it % a.Hkv, it / a.Hkv, nchunk, pos, region, r2, [] {});
+                attn_item<M::GQ>(a, L, l, seq, it % a.Hkv, it / a.Hkv, nchunk, pos, region, at_l, r2,
+                                 [] {});
                 lds_sync();
             }
             build_tables(tab, cb16, cbv, so.ntab);
@@ -1267,12 +1290,12 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // ---- o (+= residual)
         {
             const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
-            const float hv = residual_rows(so, a, l == 0, tag_of(seq, l - 1, PH_DOWN));
-            stage<XS_BF16, M::HQD>(a.at, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf, part8,
+            const float hv = residual_rows(so, a, h_prev, tag_of(seq, l - 1, PH_DOWN));
+            stage<XS_BF16, M::HQD>(at_l, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf, part8,
                                    err);
             stamp(a, l, 3);
             PO::template run<MODE_ACC>(ob, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
-                                       1.0f, a.ht, a.h0, false, nullptr, tag_of(seq, l, PH_O));
+                                       1.0f, h_o, a.h0, false, nullptr, tag_of(seq, l, PH_O));
         }
         stamp(a, l, 4);
         {
@@ -1288,11 +1311,11 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // ---- gate|up -> silu(gate) * up
         {
             const Segs sg = segs_gu(L, sh);
-            const float rinv = stage<XS_RMS, M::H>(a.ht, L.mlp_norm, a.eps, tag_of(seq, l, PH_O),
+            const float rinv = stage<XS_RMS, M::H>(h_o, L.mlp_norm, a.eps, tag_of(seq, l, PH_O),
                                                    lh.xs, lh.xl, lh.xf, part8, err);
             stamp(a, l, 5);
             PG::template run<MODE_SWIGLU>(gb, sg, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
-                                          rinv, a.ht, a.h0, false, a.actt, tag_of(seq, l, PH_ACT));
+                                          rinv, nullptr, a.h0, false, actl, tag_of(seq, l, PH_ACT));
         }
         stamp(a, l, 6);
         {
@@ -1307,12 +1330,12 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // ---- down (+= residual)
         {
             const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
-            const float hv = residual_rows(sd, a, false, tag_of(seq, l, PH_O));
-            stage<XS_F32, M::I>(a.actt, nullptr, 0.0f, tag_of(seq, l, PH_ACT), li.xs, li.xl, li.xf, part8,
+            const float hv = residual_rows(sd, a, h_o, tag_of(seq, l, PH_O));
+            stage<XS_F32, M::I>(actl, nullptr, 0.0f, tag_of(seq, l, PH_ACT), li.xs, li.xl, li.xf, part8,
                                 err);
             stamp(a, l, 7);
             PD::template run<MODE_ACC>(db, sd, a.group, tab, li.xs, li.xl, li.xf, li.red, hrow, hv,
-                                       1.0f, a.ht, a.h0, last, nullptr, tag_of(seq, l, PH_DOWN));
+                                       1.0f, h_d, a.h0, last, nullptr, tag_of(seq, l, PH_DOWN));
         }
         stamp(a, l, 8);
         if (!last) {
@@ -1409,12 +1432,12 @@ static StepWs step_ws(int H, int I, int Hq, int Hkv, int D, int max_pos)
         return at;
     };
     w.sync = take(8);
-    w.ht = take((size_t)H);
+    w.ht = take((size_t)2 * kRing * H);
     w.qt = take((size_t)Hq * D);
     w.kt = take((size_t)Hkv * D);
     w.vt = take((size_t)Hkv * D);
-    w.at = take((size_t)Hq * D / 2);
-    w.actt = take((size_t)I);
+    w.at = take((size_t)kRing * Hq * D / 2);
+    w.actt = take((size_t)kRing * I);
     w.part = take((size_t)Hq * (max_pos / kChunk + 1) * (D + 2));
     w.total = o;
     return w;
