@@ -22,11 +22,10 @@ EP_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16)
 // float -> bfloat16, round to nearest even (NaN stays NaN).
 EP_DEV uint16_t f32_to_bf16(float f)
 {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u)
-        return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    const uint32_t u = __float_as_uint(f);
+    const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const uint32_t nan = (u >> 16) | 0x40u;
+    return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? nan : rounded);  // a select, no branch
 }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

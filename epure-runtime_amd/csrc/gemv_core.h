@@ -41,9 +41,12 @@ EP_DEV void build_table(uint32_t *tab, const uint16_t *cb16)
 // result byte0 = lane4 (src1 byte 0), byte1 = byte i of the packed word
 // (src0 byte i = selector 4 + i), bytes 2-3 = 0 (selector 12).
 constexpr uint32_t kSelByte[4] = {0x0c0c0400u, 0x0c0c0500u, 0x0c0c0600u, 0x0c0c0700u};
-// Same, with result byte 2 taken from src1 byte 2: src1 = lane4 | slot << 16
-// selects table `slot` (64 KiB apart) at no extra instruction.
-constexpr uint32_t kSelByteSlot[4] = {0x0c020400u, 0x0c020500u, 0x0c020600u, 0x0c020700u};
+// Two pair tables interleaved in 64 KiB (the one-launch step): entry b of
+// table `slot`, copy c (of 32) at dword b * 64 + slot * 32 + c, i.e. byte
+// (b << 8) | (slot << 7) | (c << 2) -- the kSelByte address with src1 =
+// slot << 7 | (lane & 31) << 2.  32 copies serve a wave as fast as 64 (a
+// ds_read_b32 takes 32 lanes per cycle).
+constexpr int kPairTabBytes = 256 * 2 * 32 * 4;
 
 EP_DEV uint32_t lds_read_u32(const uint32_t *base, uint32_t byte_addr)
 {

@@ -96,21 +96,19 @@ struct Model {
     static constexpr int RQ_QKV = RQ_QKV_, RQ_O = RQ_O_, RQ_GU = RQ_GU_, RQ_D = RQ_D_;
     static constexpr int MQ_QKV = MQ_QKV_, MQ_O = MQ_O_, MQ_GU = MQ_GU_, MQ_D = MQ_D_;
     // Per phase the region holds: activations as fp16 pairs (K / 2 dwords),
-    // their lo terms (same size; the down phase, which uses one table, keeps
-    // them in the second table slot instead), one factor per 32 values, then
-    // the accumulator [8 waves][rows].
-    static constexpr int phase_bytes(int K, int red, bool lo) { return (lo ? K * 4 : K * 2) + K / 32 * 4 + red; }
+    // their lo terms (same size), one factor per 32 values, then the
+    // accumulator [8 waves][rows].
+    static constexpr int phase_bytes(int K, int red) { return K * 4 + K / 32 * 4 + red; }
     // attention scratch: q [GQ][D], k, v [D], S [GQ][256], m, l [GQ], o [8][GQ][D]
     static constexpr int ATT_BYTES =
         (GQ * kD + 2 * kD + GQ * kChunk + 2 * GQ + kWaves * GQ * kD) * 4 + 16;
     static constexpr int REGION =
-        imax(imax(imax(phase_bytes(H, kWaves * 4 * MQ_QKV * 4, true),
-                       phase_bytes(HQD, kWaves * 4 * MQ_O * 4, true)),
-                  imax(phase_bytes(H, kWaves * 8 * MQ_GU * 4, true),
-                       phase_bytes(I, kWaves * 4 * MQ_D * 4, false))),
+        imax(imax(imax(phase_bytes(H, kWaves * 4 * MQ_QKV * 4),
+                       phase_bytes(HQD, kWaves * 4 * MQ_O * 4)),
+                  imax(phase_bytes(H, kWaves * 8 * MQ_GU * 4),
+                       phase_bytes(I, kWaves * 4 * MQ_D * 4))),
              ATT_BYTES);
-    static_assert(I * 2 <= kTabBytes, "down-phase lo terms fit a table slot");
-    static constexpr int LDS = 2 * kTabBytes + REGION + 32 * 2 + 16 * 4 + 64 * 4;
+    static constexpr int LDS = kPairTabBytes + REGION + 32 * 2 + 16 * 4 + 64 * 4;
     static_assert(LDS <= 160 * 1024, "LDS budget");
     static_assert(H % 512 == 0 && HQD % 512 == 0 && I % 512 == 0, "rows of whole slabs");
 };
@@ -126,14 +124,13 @@ struct PhaseLds {
     uint32_t *xs, *xl;  // hi and lo terms, fp16 pairs
     float *xf, *red;
 };
-EP_DEV PhaseLds phase_lds(char *region, int K, uint32_t *lo_elsewhere = nullptr)
+EP_DEV PhaseLds phase_lds(char *region, int K)
 {
     PhaseLds p;
-    const int lo = lo_elsewhere ? 0 : K * 2;
     p.xs = (uint32_t *)region;
-    p.xl = lo_elsewhere ? lo_elsewhere : (uint32_t *)(region + K * 2);
-    p.xf = (float *)(region + K * 2 + lo);
-    p.red = (float *)(region + K * 2 + lo + K / 32 * 4);
+    p.xl = (uint32_t *)(region + K * 2);
+    p.xf = (float *)(region + K * 4);
+    p.red = (float *)(region + K * 4 + K / 32 * 4);
     return p;
 }
 
@@ -577,14 +574,14 @@ struct Gemv {
     {
         const int lane = tid_fresh() & 63, wave = wave_id();
         const int rq = lane & 3, c = lane >> 2;
-        const uint32_t lane4 = (uint32_t)lane << 2;
+        const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
         const int lg = lg_gps(sl.lgroup);
         const int gl = (c >> (4 - lg)) & ((1 << lg) - 1);  // this lane's group within the slab
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
             const int vq = vquad(sg, qg, i, wave);
             const int slot = PAIRED ? (i >= RQ ? 1 : 0) : (vq < sg.qb ? seg_of(sg, vq, i) - sg.sfirst : 0);
-            const uint32_t l4s = lane4 | ((uint32_t)slot << 16);
+            const uint32_t l4s = lane4 | ((uint32_t)slot << 7);
             // the 16 lookups of the chunk are issued back to back, then
             // consumed (source order is kept where registers are tight)
             uint32_t tv[16];
@@ -592,7 +589,7 @@ struct Gemv {
             for (int wd = 0; wd < 4; ++wd)
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
-                    tv[wd * 4 + q] = lds_read_u32(tab, __builtin_amdgcn_perm(bk.w[i][wd], l4s, kSelByteSlot[q]));
+                    tv[wd * 4 + q] = lds_read_u32(tab, __builtin_amdgcn_perm(bk.w[i][wd], l4s, kSelByte[q]));
             f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int n = 0; n < 8; ++n) {
@@ -682,9 +679,25 @@ EP_DEV void build_tables(uint32_t *tab, uint16_t *cb16, float cbv, int ntab)
     if (tid_fresh() < 32)
         cb16[tid_fresh()] = f16_bits((f16_t)cbv);
     lds_sync();
-    build_table<4>(tab, cb16);
-    if (ntab > 1)
-        build_table<4>(tab + kTabDwords, cb16 + 16);
+    // Thread t writes dwords 4 e4 .. 4 e4 + 3, e4 = t + 512 it: entry
+    // b = t / 16 + 32 it, slot (t / 8) & 1 -- so its low index is the same
+    // for every it and its high index is t / 256 + 2 it: nine reads, all in
+    // flight at once, then eight 16-byte writes.
+    const int t = tid_fresh();
+    const int slot = (t >> 3) & 1;
+    if (slot >= ntab)
+        return;
+    const uint16_t *cb = cb16 + slot * 16;
+    const uint32_t lo = cb[(t >> 4) & 15];
+    uint32_t hi[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it)
+        hi[it] = cb[(t >> 8) + 2 * it];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+        const uint32_t v = lo | (hi[it] << 16);
+        ((u32x4_t *)tab)[t + kThreads * it] = (u32x4_t){v, v, v, v};
+    }
 }
 
 // ---------------------------------------------------------------- activations
@@ -1178,12 +1191,12 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
 {
     __shared__ __align__(16) char smem[M::LDS];
     uint32_t *tab = (uint32_t *)smem;
-    char *region = smem + 2 * kTabBytes;
+    char *region = smem + kPairTabBytes;
     uint16_t *cb16 = (uint16_t *)(region + M::REGION);
     float *part8 = (float *)(cb16 + 32);
     float *hrow = part8 + 16;
     const PhaseLds lh = phase_lds(region, M::H), lo = phase_lds(region, M::HQD),
-                   li = phase_lds(region, M::I, tab + kTabDwords);  // down: one table
+                   li = phase_lds(region, M::I);
 
     using PQ = Gemv<M::SH, M::RQ_QKV, false, M::MQ_QKV, M::NB_QKV>;
     using PO = Gemv<M::SO, M::RQ_O, false, M::MQ_O, M::NB_O>;
