@@ -59,7 +59,7 @@ constexpr int kAuxStream = 2;
 // layers later, long evicted by then); an entry whose tag is not current
 // yet is re-read coherently (sc1).
 constexpr int kRing = 32;
-constexpr int kSpinLimit = 1 << 16;  // polls (~1-2 us each) before the step fails
+constexpr int kSpinLimit = 1 << 16;  // polls (~0.3-2 us each) before the step fails
 constexpr int kD = 128;              // head_dim served
 constexpr int kChunk = 64;           // KV positions per attention item (8 waves x 8)
 constexpr int kEvents = 24;          // trace events per layer (debug)
@@ -212,7 +212,12 @@ struct Spin {
         }
         if ((it & 31) == 0 && ld_agent(err) != 0)
             return false;
-        __builtin_amdgcn_s_sleep(1);
+        // back off after the first polls: every poll of every thread is a
+        // memory-side read that competes with the producers' traffic
+        if (it < 4)
+            __builtin_amdgcn_s_sleep(1);
+        else
+            __builtin_amdgcn_s_sleep(6);  // ~400 cycles
         return true;
     }
 };
@@ -859,10 +864,10 @@ EP_DEV void attn_load(AttnRegs &r, const uint16_t *kc, const uint16_t *vc, int j
 
 EP_DEV float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
-// `received` runs once this step's q|k|v rows are in.
+// `done` runs once the item's partial or output is stored.
 template <int GQ, class F>
 EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, int c,
-                      int nchunk, int pos, char *scratch, uint64_t *at, const AttnRegs &r, F received)
+                      int nchunk, int pos, char *scratch, uint64_t *at, const AttnRegs &r, F done)
 {
     const int tid = tid_fresh(), lane = tid & 63, wave = wave_id();
     const int rr = lane >> 4, e16 = lane & 15;
@@ -917,7 +922,6 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
     }
     lds_sync();
     stamp(a, l, 10);  // q/k/v received
-    received();
     if (c == nchunk - 1 && tid < kD) {  // append this step's row (read by later steps only)
         const int64_t row = ((int64_t)j * a.max_pos + pos) * kD + tid;
         stg(L.kcache + row, f32_to_bf16(kn[tid]));
@@ -1068,6 +1072,7 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
                 st_tag(pp + 1, __float_as_uint(Ls), tpart);
             }
         }
+        done();
         return;
     }
     if (cth) {
@@ -1091,13 +1096,25 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
 #pragma unroll
             for (int k = 0; k < kCombine; ++k)
                 fetch(e[k], c0 + k < nchunk ? c0 + k : c0);
+            // re-read every chunk not there yet in the same round (one round
+            // trip per round, not one per chunk)
+            Spin sp;
+            for (;;) {
+                bool all = true;
+#pragma unroll
+                for (int k = 0; k < kCombine; ++k)
+                    all = all && (c0 + k >= nchunk || ready(e[k]));
+                if (all || !sp.again(err))
+                    break;
+#pragma unroll
+                for (int k = 0; k < kCombine; ++k)
+                    if (c0 + k < nchunk && !ready(e[k]))
+                        fetch(e[k], c0 + k);
+            }
 #pragma unroll
             for (int k = 0; k < kCombine; ++k) {
                 if (c0 + k >= nchunk)
                     break;
-                Spin sp;
-                while (!ready(e[k]) && sp.again(err))
-                    fetch(e[k], c0 + k);
                 const float Mc = __uint_as_float((uint32_t)e[k][0]);
                 const float Mn = fmaxf(M, Mc);
                 const float fa = __expf(M - Mn), fb = __expf(Mc - Mn);
@@ -1110,6 +1127,7 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
         st_tag(outp, (uint32_t)f32_to_bf16(n0 / Ls) | ((uint32_t)f32_to_bf16(n1 / Ls) << 16), tatt);
     }
     stamp(a, l, 12);  // output written (combined)
+    done();
 }
 
 // ---------------------------------------------------------------- kernel
@@ -1268,9 +1286,10 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         stamp(a, l, 1);
         // Attention workgroups issue their first item's K/V rows (cached by
         // earlier steps) and wait for q|k|v at once; their o weights go out
-        // once q|k|v are in (loads issued before the wait would delay it:
-        // results return in order) and the o table is built after the
-        // attention.  The other workgroups prefetch o and build its table now.
+        // once the item's result is stored (loads issued before a wait
+        // would delay it: results return in order) and the o table is built
+        // after the attention.  The other workgroups prefetch o and build
+        // its table now.
         const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
         if (b < nitems) {
             AttnRegs ar;
