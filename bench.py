@@ -1,16 +1,16 @@
 """Headline benchmark: batch-1 greedy decode tok/s of the Llama-3-8B-shaped
-4-bit codebook model on one MI355X, plus the
-dequant-GEMV HBM bandwidth as a fraction of peak.
+4-bit codebook model (the reference's headline decode configuration) on one
+MI355X, plus the dequant-GEMV HBM bandwidth as a fraction of peak.
 
     python bench.py [--steps K] [--warmup W] [--config llama3-8b|qwen3-1.7b]
 
 One "step" is one decode token: a replay of the captured HIP graph of the
 whole decode step -- the one-launch decode-step kernel (all 32 layers: fused
 q|k|v dequant-GEMV with RMSNorm, attention, o GEMV, gate|up GEMV with
-SwiGLU, down GEMV; grid barriers between phases) and the lm_head/argmax
-launch.  The prompt (128 random ids) is consumed first, untimed; then W
-warm-up tokens, then K timed tokens, with the device synchronised on both
-sides.  Weights are random-init in the packed format (synthetic data; no
+SwiGLU, down GEMV; phases hand over through tagged data, no grid barrier)
+and the lm_head/argmax launch.  The prompt (128 random ids) is consumed
+first, untimed; then W warm-up tokens, then K timed tokens, with the device
+synchronised on both sides.  Weights are random-init in the packed format (synthetic data; no
 checkpoints offline).  --per-layer times the five-launches-per-layer path
 instead.
 
@@ -19,9 +19,13 @@ captured alone into a second graph (at the final position) and replayed K
 times between HIP events on the launch stream; achieved = its algorithmic
 bytes (packed indices + group scales + codebooks of the 224 linears, RMSNorm
 weights, and the KV rows attention reads at that position) / time per
-replay.  The CPU baseline is the C restatement of the reference's Rust
-kernel (oracle/rowdot.c, kernel/src/lib.rs semantics) on one layer's 7
-linears, scaled to the 224 linears of a step.
+replay.  `traffic` is the HBM bytes per launch of the same replays from the
+FETCH_SIZE/WRITE_SIZE passes summarised in
+profiles/decode_step_llama3_8b_traffic.md (calibrated against a copy of
+known size; `--copy-probe` runs that copy).  The CPU baseline is the C
+restatement of the reference's Rust kernel (oracle/rowdot.c,
+kernel/src/lib.rs semantics) on one layer's 7 linears, scaled to the 224
+linears of a step.
 """
 import argparse
 import json
@@ -50,7 +54,33 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--per-layer", action="store_true",
                     help="five launches per layer instead of the one-launch step kernel")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only copy a BYTES-long device buffer 10 times (the known-size "
+                         "kernel that calibrates rocprofv3's FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def copy_probe(nbytes):
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": nbytes, "copies": 10}), flush=True)
+
+
+def traffic_from_profile():
+    """HBM bytes per launch of the step kernel, as measured by the
+    FETCH_SIZE/WRITE_SIZE passes summarised in profiles/ (None if absent)."""
+    path = os.path.join(ROOT, "profiles", "decode_step_llama3_8b_traffic.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(cfg, threads):
@@ -89,10 +119,13 @@ def cpu_baseline(cfg, threads):
 
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this build has "
-              "no multi-GPU path: the packed linears shard by rows with no exchange, see "
-              "DESIGN.md).", file=sys.stderr)
+              "no multi-GPU path: column-parallel linears would shard by rows with no "
+              "exchange, row-parallel ones by K with one all-reduce).", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -193,7 +226,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": None if args.per_layer else traffic_from_profile(),
         },
     }
     if not args.no_cpu_baseline:

@@ -17,7 +17,7 @@ embedding).  The token position lives in device memory, so the step is
 captured once as a HIP graph and replayed per token.
 
 Weights are random-init (there is no network for checkpoints), seeded, in
-the packed format of BASELINE config 0: 4-bit indices two per byte, a sorted
+the reference's packed format: 4-bit indices two per byte, a sorted
 16-entry fp16-valued codebook per linear (stored fp32 as the container
 does), group-128 fp16 scales |N(0, 0.02)| + 1e-3; embeddings and lm_head
 bf16 N(0, 0.02); norm weights 1.
@@ -57,7 +57,7 @@ class DecoderConfig:
                 ("o", h, self.n_heads * d), ("gate", i, h), ("up", i, h), ("down", h, i)]
 
 
-# BASELINE.json configs 2 and 1 (Llama-3-8B and Qwen3-1.7B shapes).
+# The two decode shapes served by the one-launch step: Llama-3-8B and Qwen3-1.7B.
 LLAMA3_8B = DecoderConfig(4096, 14336, 32, 32, 8, 128, 128256, 5e5, 1e-5, name="llama3-8b")
 QWEN3_1_7B = DecoderConfig(2048, 6144, 28, 16, 8, 128, 151936, 1e6, 1e-6, qk_norm=True,
                            tie_embeddings=True, name="qwen3-1.7b")
@@ -80,7 +80,8 @@ def _gen(seed, device):
 
 
 def random_packed_linear(n, k, cfg, gen, device):
-    """One packed weight with BASELINE config-0 statistics."""
+    """One packed weight: uniform indices, sorted N(0, 1) fp16-valued codebook,
+    |N(0, 0.02)| + 1e-3 fp16 group scales."""
     nbytes = n * k // 2 if cfg.levels <= 16 else n * k
     hi = 256 if cfg.levels in (16, 256) else None
     if hi is None:

@@ -76,9 +76,12 @@ int ep_lm_head_argmax(float *h, const uint16_t *norm_w, float eps, const uint16_
 
 /*
  * Persistent decode step: every layer of one batch-1 step in ONE launch (one
- * resident workgroup per CU; phases hand over through tagged data, see
- * below; the next phase's packed weights are in flight across each hand-
- * over).  Same math as the per-layer sequence ep_fused_gemv(q|k|v, RMSNorm)
+ * resident workgroup per CU).  Phases hand over through tagged data in the
+ * workspace: each value a workgroup produces for others is stored with the
+ * (launch, layer, phase) tag, and consumers poll the values until every tag
+ * is current -- no grid barrier; the next phase's packed weights are in
+ * flight across each hand-over.  Same math as the per-layer sequence
+ * ep_fused_gemv(q|k|v, RMSNorm)
  * -> ep_decode_attention -> ep_fused_gemv(o, +=) -> ep_fused_gemv(gate|up,
  * RMSNorm) -> ep_fused_gemv(down, SwiGLU, +=), i.e. the transformers
  * decoder layer whose linears the reference replaces with PackedLinear
@@ -98,8 +101,10 @@ int ep_lm_head_argmax(float *h, const uint16_t *norm_w, float eps, const uint16_
  * word 2 becomes nonzero if a hand-over wait timed out (the step's results
  * are then garbage).  `trace`, when not NULL, receives wall-clock stamps
  * [n_layers][24][grid] (debug).  Declines (> 0) shapes without a
- * persistent variant (ep_decode_step_serves; groups a power of two >= 128,
- * fp16 scales, 4-bit indices).  Position = state[0].
+ * persistent variant (ep_decode_step_serves: the Llama-3-8B and Qwen3-1.7B
+ * shapes, D = 128, groups a power of two >= 128, fp16 scales, 4-bit
+ * indices).  Position = state[0].  Launches that share a workspace must be
+ * stream-ordered (two in flight on one workspace race).
  */
 size_t ep_decode_step_layer_bytes(void);
 size_t ep_decode_step_workspace(int H, int I, int Hq, int Hkv, int D, int max_pos);

@@ -219,7 +219,7 @@ def snapshot_digest(packed_bytes):
 
 # ---------------------------------------------------------------- synthetic inputs
 def synth_linear(n, k, levels=16, group=128, seed=0, cb_sorted=True):
-    """BASELINE config 0/3 generators (numpy PCG64, machine-independent).
+    """Synthetic packed linear (numpy PCG64, machine-independent).
 
     idx uniform over 0..levels-1; cb = sort(N(0,1) draws) as fp16; scales
     |N(0, 0.02)| + 1e-3 as fp16 [n, ceil(k/group)].  Returns

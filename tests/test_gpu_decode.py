@@ -1,7 +1,7 @@
 """Greedy-decode parity of the gfx950 decoder against the dense float32
 oracle (oracle/decoder.py, itself pinned against transformers on CPU).
 
-Bar (BASELINE.json north_star): greedy decode gives identical argmax tokens
+Bar: greedy decode gives identical argmax tokens
 for 64 steps.  The oracle rounds to bf16 where the GPU decoder stores bf16
 (KV rows, attention output, lm_head input); everything else is float32, so
 the remaining differences are the GEMV's fp16 operands and summation order.

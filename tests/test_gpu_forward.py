@@ -1,6 +1,6 @@
 """GPU parity of the forward path through the C ABI, against the CPU oracle.
 
-Bars (BASELINE.json north_star): unpacked indices and dequantized tiles are
+Bars: unpacked indices and dequantized tiles are
 bit-exact; matmul outputs are within max relative error 2e-3 of the
 reference's fp32-accumulated result (kernel/src/lib.rs order, computed by the
 oracle), measured normwise (max|y-r| / max|r|) and per element with an
