@@ -25,7 +25,16 @@ profiles/decode_step_llama3_8b_traffic.md (calibrated against a copy of
 known size; `--copy-probe` runs that copy).  The CPU baseline is the C
 restatement of the reference's Rust kernel (oracle/rowdot.c,
 kernel/src/lib.rs semantics) on one layer's 7 linears, scaled to the 224
-linears of a step.
+linears of a step.  The line also carries `gemv`: the config-0 dequant-GEMV
+(4096x4096 4-bit, batch 1) over 64 rotating weight sets, GB/s per launch.
+
+    python bench.py --workload gemv|prefill|backward
+
+prints one line for the other configurations instead: config 0 alone (GEMV
+GB/s, with the C port timed on the same linear), config 3 (the 8-bit M sweep;
+GB/s and MFMA utilisation per case) and config 4 (the compressed-state
+backward; TFLOP/s against the dense bf16 MFMA peak, indices hashed before and
+after).
 """
 import argparse
 import json
@@ -57,7 +66,188 @@ def parse():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only copy a BYTES-long device buffer 10 times (the known-size "
                          "kernel that calibrates rocprofv3's FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--workload", default="decode",
+                    choices=["decode", "gemv", "prefill", "backward"],
+                    help="decode: the headline (config 2); gemv: one 4096x4096 4-bit GEMV "
+                         "over a rotating sweep (config 0); prefill: the 8-bit M sweep "
+                         "(config 3); backward: the compressed-state backward (config 4)")
+    ap.add_argument("--no-gemv", action="store_true",
+                    help="decode: skip the config-0 GEMV sweep reported beside the step")
     return ap.parse_args()
+
+
+# ---------------------------------------------------------------- standalone linears
+class _Linear:
+    """One packed linear bound to the C ABI with preallocated buffers, so a
+    launch is graph-capturable (ep_dequant_matmul / ep_dequant_matmul_bwd)."""
+
+    def __init__(self, store, x, out_dtype=None, bwd_gy=None):
+        import torch
+        from epure.kernels import _abi, cuda
+        self.h = cuda._hot(store)
+        self.x = x
+        M, K = x.shape
+        self.y = torch.empty((M, self.h.N), device=x.device, dtype=out_dtype or x.dtype)
+        nb = _abi.lib.ep_dequant_matmul_workspace(M, self.h.N, K, self.h.levels, self.h.group)
+        self.ws = torch.empty(max(nb, 256), device=x.device, dtype=torch.uint8)
+        self.gy = bwd_gy
+        if bwd_gy is not None:
+            G = (K + self.h.group - 1) // self.h.group
+            self.gx = torch.empty((M, K), device=x.device, dtype=torch.bfloat16)
+            self.gcb = torch.empty(self.h.levels, device=x.device, dtype=torch.float32)
+            self.gsc = torch.empty((self.h.N, G), device=x.device, dtype=torch.float32)
+            nb = _abi.lib.ep_dequant_matmul_bwd_workspace(M, self.h.N, K, self.h.levels,
+                                                          self.h.group)
+            self.bws = torch.empty(max(nb, 256), device=x.device, dtype=torch.uint8)
+
+    def fwd(self, stream):
+        from epure.kernels import _abi
+        h, x, y = self.h, self.x, self.y
+        rc = _abi.lib.ep_dequant_matmul(
+            x.data_ptr(), _abi.dtype_code(x.dtype), x.stride(0),
+            h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+            h.cb.data_ptr(), h.cb_dt, h.levels, h.group, x.shape[0], h.N, x.shape[1],
+            y.data_ptr(), _abi.dtype_code(y.dtype), y.stride(0), 0,
+            self.ws.data_ptr(), self.ws.numel(), stream)
+        if rc != 0:
+            raise RuntimeError(f"ep_dequant_matmul: {rc} {_abi.last_error()}")
+
+    def bwd(self, stream):
+        from epure.kernels import _abi
+        h, x, gy = self.h, self.x, self.gy
+        M, K = x.shape
+        rc = _abi.lib.ep_dequant_matmul_bwd(
+            gy.data_ptr(), _abi.dtype_code(gy.dtype), gy.stride(0),
+            x.data_ptr(), _abi.dtype_code(x.dtype), x.stride(0),
+            h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+            h.cb.data_ptr(), h.cb_dt, h.levels, h.group, M, h.N, K,
+            self.gx.data_ptr(), _abi.BF16, K, self.gcb.data_ptr(), self.gsc.data_ptr(),
+            self.gsc.shape[1], self.bws.data_ptr(), self.bws.numel(), stream)
+        if rc != 0:
+            raise RuntimeError(f"ep_dequant_matmul_bwd: {rc} {_abi.last_error()}")
+
+
+def _graph_time(launches, replays):
+    """Captures `launches` (callables taking the stream handle) into one HIP
+    graph and returns the mean ms per replay, timed with HIP events on the
+    capture stream."""
+    import ctypes
+    import torch
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        h = ctypes.c_void_p(stream.cuda_stream)
+        for f in launches:          # eager pass: warms caches of launch parameters
+            f(h)
+        stream.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for f in launches:
+                f(h)
+        g.replay()
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(replays):
+            g.replay()
+        e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / replays
+
+
+def _spec(levels):
+    from epure.decode import DecoderConfig
+    return DecoderConfig(0, 0, 0, 1, 1, 128, 0, 1.0, levels=levels, group=128)
+
+
+def _weight_bytes(n, k, levels, group=128):
+    idx = n * k // 2 if levels <= 16 else n * k
+    return idx + n * ((k + group - 1) // group) * 2 + levels * 4
+
+
+def gemv_sweep(seed=0, sets=64, replays=20):
+    """Config 0: y = x.W^T, W 4096x4096 4-bit (16-entry codebook, group-128
+    fp16 scales), x bf16 [1, 4096].  `sets` distinct weight sets (64 x 8.65 MB
+    = 553 MB, more than the 256 MB MALL holds) are launched round-robin from
+    one graph, so every launch streams its weights from HBM."""
+    import torch
+    from epure.decode import _gen, random_packed_linear
+    dev = torch.device("cuda:0")
+    n = k = 4096
+    gen = _gen(seed, dev)
+    x = torch.randn(1, k, generator=gen, device=dev).to(torch.bfloat16)
+    lins = [_Linear(random_packed_linear(n, k, _spec(16), gen, dev), x) for _ in range(sets)]
+    ms = _graph_time([L.fwd for L in lins], replays) / sets
+    wb = _weight_bytes(n, k, 16)
+    gbs = wb / (ms * 1e-3) / 1e9
+    return {"kernel": "gemv_lut_kernel", "shape": "4096x4096 4-bit, M=1, bf16 x/y",
+            "rotating_sets": sets, "us_per_launch": round(ms * 1e3, 3),
+            "alg_bytes_per_launch": wb, "achieved_gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def prefill_sweep(seed=0, replays=10):
+    """Config 3: 8-bit indices (256-entry fp16-valued codebook, group-128 fp16
+    scales), (N, K) in {4096x4096, 14336x4096, 4096x14336}, bf16 x with M in
+    {1, 4, 16, 64, 512, 2048}.  Weight sets rotate so at least ~512 MB are
+    touched per replay (HBM, not the MALL, serves the small-M cases)."""
+    import torch
+    from epure.decode import _gen, random_packed_linear
+    dev = torch.device("cuda:0")
+    gen = _gen(seed, dev)
+    rows = []
+    for n, k in [(4096, 4096), (14336, 4096), (4096, 14336)]:
+        wb = _weight_bytes(n, k, 256)
+        sets = max(1, -(-512 * 2 ** 20 // wb))
+        stores = [random_packed_linear(n, k, _spec(256), gen, dev) for _ in range(sets)]
+        for m in (1, 4, 16, 64, 512, 2048):
+            x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
+            lins = [_Linear(s, x) for s in stores]
+            ms = _graph_time([L.fwd for L in lins], replays) / sets
+            byt = wb + m * k * 2 + m * n * 2
+            flop = 2.0 * m * n * k
+            rows.append({"N": n, "K": k, "M": m, "us": round(ms * 1e3, 2),
+                         "gbs": round(byt / (ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(byt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                         "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+                         "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                         "kernel": "gemv_lut_kernel" if m <= 4 else "mm_kernel"})
+            del lins, x
+        del stores
+        torch.cuda.empty_cache()
+    return rows
+
+
+def backward_sweep(seed=0, replays=10):
+    """Config 4: grad_x, grad_codebook and grad_scales of one 2048x6144 and one
+    6144x2048 packed linear (4-bit, 16 levels, group 128), x bf16 [2048, K]
+    ~ N(0, 1), gy bf16 [2048, N] ~ N(0, 1e-2).  The indices are hashed before
+    and after: they must be bit-identical."""
+    import hashlib
+    import torch
+    from epure.decode import _gen, random_packed_linear
+    dev = torch.device("cuda:0")
+    gen = _gen(seed, dev)
+    t = 2048
+    rows = []
+    for n, k in [(2048, 6144), (6144, 2048)]:
+        s = random_packed_linear(n, k, _spec(16), gen, dev)
+        x = torch.randn(t, k, generator=gen, device=dev).to(torch.bfloat16)
+        gy = (torch.randn(t, n, generator=gen, device=dev) * 1e-2).to(torch.bfloat16)
+        digest = lambda: hashlib.blake2b(s.packed.cpu().numpy().tobytes(),  # noqa: E731
+                                         digest_size=16).hexdigest()
+        before = digest()
+        L = _Linear(s, x, bwd_gy=gy)
+        ms = _graph_time([L.bwd], replays)
+        flop = 4.0 * t * n * k
+        rows.append({"N": n, "K": k, "T": t, "us": round(ms * 1e3, 2),
+                     "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+                     "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                     "indices_frozen": digest() == before})
+    return rows
 
 
 def copy_probe(nbytes):
@@ -117,6 +307,89 @@ def cpu_baseline(cfg, threads):
                       f"(linears only, lm_head excluded)"}
 
 
+def cpu_gemv_baseline(n, k, levels, ms, threads):
+    """The C port of the reference Rust kernel (kernel/src/lib.rs) on one
+    N x K linear with M rows of f32 x (bf16-valued): GB/s of packed weights."""
+    import numpy as np
+    from oracle import ref, rowdot
+    _, packed, scale, cb = ref.synth_linear(n, k, levels, 128, seed=0)
+    row = k // 2 if levels <= 16 else k
+    rng = np.random.Generator(np.random.PCG64(1))
+    nt = threads or rowdot.threads()
+    out = []
+    for m in ms:
+        x = ref.round_bf16(rng.standard_normal((m, k)).astype(np.float32))
+        args = (x, packed.reshape(n, row), scale.astype(np.float32), cb.astype(np.float32), 128,
+                levels <= 16)
+        rowdot.dequant_matmul(*args, nthreads=nt)
+        times = []
+        t_end = time.perf_counter() + 4.0
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+            t0 = time.perf_counter()
+            rowdot.dequant_matmul(*args, nthreads=nt)
+            times.append(time.perf_counter() - t0)
+        t = float(np.median(times))
+        out.append((m, t, len(times)))
+    wb = _weight_bytes(n, k, levels)
+    m, t, runs = out[0]
+    return {"value": round(wb / t / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+            "sample": f"C port of kernel/src/lib.rs, {n}x{k} {'4' if levels <= 16 else '8'}-bit "
+                      f"linear, f32 x; " + "; ".join(
+                          f"M={m_}: {t_ * 1e3:.2f} ms (median of {r_})" for m_, t_, r_ in out)}
+
+
+def side_workload(args):
+    """The non-headline configurations: one JSON line each."""
+    base = {"n_gpus": 1, "steps": args.steps, "warmup": 2, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "data": "synthetic"}
+    if args.workload == "gemv":
+        g = gemv_sweep(args.seed, replays=args.steps)
+        out = dict(metric="dequant-GEMV HBM GB/s (4096x4096 4-bit, batch 1)",
+                   value=g["achieved_gbs"], unit="GB/s", ms_per_step=g["us_per_launch"] / 1e3,
+                   dtype="f16", **base)
+        out["config"] = {"workload": "config 0: one 4096x4096 4-bit packed linear, x bf16 [1,4096], "
+                                     f"{g['rotating_sets']} rotating weight sets", **g}
+        out["roofline"] = {"bound": "hbm", "kernel": g["kernel"], "achieved": g["achieved_gbs"],
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
+                           "traffic": None}
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_gemv_baseline(4096, 4096, 16, [1], args.cpu_threads)
+    elif args.workload == "prefill":
+        rows = prefill_sweep(args.seed, replays=min(args.steps, 20))
+        top = max(rows, key=lambda r: r["tflops"])
+        out = dict(metric="8-bit packed linear prefill sweep: TFLOP/s (large M), GB/s (small M)",
+                   value=top["tflops"], unit="TFLOP/s", ms_per_step=top["us"] / 1e3,
+                   dtype="f16", **base)
+        out["config"] = {"workload": "config 3: 8-bit codebook (256 levels), group 128; "
+                                     "(N,K) in {4096x4096, 14336x4096, 4096x14336}, "
+                                     "M in {1,4,16,64,512,2048}", "rows": rows}
+        out["roofline"] = {"bound": "mfma", "kernel": top["kernel"],
+                           "achieved": top["tflops"], "peak": MFMA_PEAK_TFLOPS,
+                           "unit": "TFLOP/s", "frac": top["mfma_frac"], "traffic": None,
+                           "case": f"N={top['N']} K={top['K']} M={top['M']}"}
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_gemv_baseline(4096, 4096, 256, [1, 4, 16],
+                                                    args.cpu_threads)
+    else:
+        rows = backward_sweep(args.seed, replays=min(args.steps, 20))
+        flop = sum(4.0 * r["T"] * r["N"] * r["K"] for r in rows)
+        us = sum(r["us"] for r in rows)
+        tf = flop / (us * 1e-6) / 1e12
+        out = dict(metric="compressed-state backward TFLOP/s (grad_x + implicit grad_W)",
+                   value=round(tf, 2), unit="TFLOP/s", ms_per_step=round(us / 1e3, 4),
+                   dtype="bf16", **base)
+        out["config"] = {"workload": "config 4: 2048x6144 and 6144x2048 4-bit packed linears, "
+                                     "T=2048, grad_x + grad_codebook + grad_scales",
+                         "rows": rows,
+                         "indices_frozen": all(r["indices_frozen"] for r in rows)}
+        out["roofline"] = {"bound": "mfma", "kernel": "dx_kernel + dw_kernel",
+                           "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS,
+                           "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                           "traffic": None}
+        out["cpu_baseline"] = None  # the reference backward is torch autograd, no CPU kernel
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_probe:
@@ -127,6 +400,9 @@ def main():
               "no multi-GPU path: column-parallel linears would shard by rows with no "
               "exchange, row-parallel ones by K with one all-reduce).", file=sys.stderr)
         sys.exit(2)
+    if args.workload != "decode":
+        side_workload(args)
+        return
 
     import torch
     from epure.decode import LLAMA3_8B, QWEN3_1_7B, Decoder, random_weights
@@ -229,6 +505,11 @@ def main():
             "traffic": None if args.per_layer else traffic_from_profile(),
         },
     }
+    if not args.no_gemv:
+        del dec, w, g
+        torch.cuda.empty_cache()
+        print("# config-0 GEMV sweep", file=sys.stderr, flush=True)
+        out["gemv"] = gemv_sweep(args.seed)
     if not args.no_cpu_baseline:
         print("# CPU baseline (reference Rust semantics, C port)", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_threads)
