@@ -99,13 +99,13 @@ int ep_hip_available(void)
 
 size_t ep_dequant_matmul_workspace(int64_t M, int64_t N, int64_t K, int levels, int group)
 {
-    (void)N;
-    (void)K;
-    (void)levels;
     (void)group;
     // Any M may land on the MFMA path (shapes the GEMV does not serve), so
-    // the per-row exponent buffer is always requested.
-    return mfma_workspace(M);
+    // the per-row exponent buffer is always requested; 2..64 rows may take
+    // the split-K path and its partial sums.
+    const size_t a = mfma_workspace(M);
+    const size_t b = (M >= 2 && M <= 64) ? skinny_workspace(M, N, K, levels) : 0;
+    return a > b ? a : b;
 }
 
 int ep_dequant_matmul(const void *x, int x_dtype, int64_t ldx, const uint8_t *packed,
@@ -132,8 +132,12 @@ int ep_dequant_matmul(const void *x, int x_dtype, int64_t ldx, const uint8_t *pa
     ActDesc xa{x, x_dtype, M > 1 ? ldx : K};
     OutDesc ya{y, y_dtype, M > 1 ? ldy : N, (flags & EP_FLAG_ACCUMULATE) ? 1 : 0};
     hipStream_t s = (hipStream_t)stream;
+    // 1..4 rows: the LUT GEMV (one launch) where it serves; 2..64 rows: the
+    // split-K MFMA path; more: the MFMA tiles
     if (gemv_serves(w, xa, M))
         return launch_gemv(w, xa, M, ya, s);
+    if (skinny_serves(w, xa, M))
+        return launch_skinny(w, xa, M, ya, workspace, workspace_bytes, s);
     if (mfma_serves(w, xa, M))
         return launch_mfma(w, xa, M, ya, workspace, workspace_bytes, s);
     if (M <= 64)

@@ -135,6 +135,12 @@ int launch_mfma(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc 
 bool mfma_serves(const PackedDesc &w, const ActDesc &x, int64_t M);
 size_t mfma_workspace(int64_t M);
 
+// Small-M (2..64 rows) split-K dequant-matmul on MFMA (skinny.hip).
+int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y, void *ws,
+                  size_t ws_bytes, hipStream_t stream);
+bool skinny_serves(const PackedDesc &w, const ActDesc &x, int64_t M);
+size_t skinny_workspace(int64_t M, int64_t N, int64_t K, int levels);
+
 int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, int64_t M,
                     const OutDesc &gx, float *grad_cb, float *grad_scale, int64_t ld_gscale,
                     void *ws, size_t ws_bytes, hipStream_t stream);

@@ -1,0 +1,459 @@
+// Small-M (2 <= M <= 64) fused codebook dequant-matmul on gfx950 MFMA.
+//
+// y[M, N] = x[M, K] . W[N, K]^T with W[n, k] = cb[idx[n, k]] * scale[n, k / group],
+// for the row counts between the batch-1 GEMV and the compute-bound prefill
+// tiles.  Reference behaviour: the table kernel epure/kernels/_triton.py:54-107
+// (fp16 operands, fp32 accumulation; its grid had one program per 16x64
+// output tile, too few at small M, _triton.py:260-263) and the reference's
+// split-K experiments (_triton.py:239-315, :317-400).
+//
+// At these M the contraction is HBM-bound: the packed bytes must stream at
+// full rate while the MFMA units and LDS are mostly idle.  So:
+//  * a workgroup (8 waves) owns one K split of KS values and up to kTpw row
+//    tiles of 128 rows (16 per wave); every one of its weight loads (16
+//    bytes per lane, kLoads per tile) is issued at kernel entry, before the
+//    activation staging and the table build, so HBM streams from the first
+//    cycle;
+//  * weights are dequantized in registers straight into the B operand of
+//    v_mfma_f32_16x16x32_f16: lane (j = lane & 15, q = lane >> 4) loads 16
+//    bytes of row j -- 32 (4-bit) or 16 (8-bit) consecutive weights -- looks
+//    each byte up in the 64-replica LDS pair table of gemv_core.h and
+//    multiplies by the chunk's group scale in fp16 (the tile of
+//    materialize(float16), runtime.py:78-89); the MFMA's k index of lane q,
+//    element e maps to the weight 8 s + e of the lane's chunk (sub-step s),
+//    and the activation operand is read from LDS with the same mapping;
+//  * activations of the split (M rows x KS) are staged once in LDS as fp16
+//    after an exact power-of-two rescale per row (exponent of the row's
+//    largest |x| within the split), and the partial sums are scaled back
+//    exactly before they leave the workgroup;
+//  * with one split the results go straight to y; otherwise each split
+//    writes f32 partials [S][M][N] and sk_reduce_kernel sums them in split
+//    order (deterministic; no atomics, no counters).
+#include "ep_common.h"
+#include "ep_internal.h"
+#include "gemv_core.h"
+
+namespace ep {
+namespace {
+
+constexpr int kSkThreads = 512;
+constexpr int kSkWaves = kSkThreads / 64;
+constexpr int kSkRows = 16 * kSkWaves;  // rows of a row tile
+constexpr int kLoads = 4;               // 16-byte weight loads per lane and tile
+constexpr int kTpw = 4;                 // most row tiles one workgroup covers
+
+template <int BITS>
+constexpr int sk_kpl()
+{
+    return BITS == 4 ? 32 : 16;  // weights per 16-byte load
+}
+template <int BITS>
+constexpr int sk_ks()
+{
+    return kLoads * 4 * sk_kpl<BITS>();  // K per split: 256 bytes of a row
+}
+
+constexpr uint32_t kOut = 0x7ffffff0u;  // a buffer offset past every buffer's end
+
+struct SkArgs {
+    uint32_t xbytes, wbytes, sbytes, cbbytes;  // extents of x, packed, scale, cb
+    const void *x;
+    int64_t ldx;
+    int M;
+    const uint8_t *packed;
+    uint32_t row_bytes;
+    const void *scale;
+    int scale_dtype;
+    int64_t lds;
+    const void *cb;
+    int cb_dtype;
+    int levels;
+    int N;
+    int K;
+    int group;
+    int tiles;   // row tiles, ceil(N / 128)
+    int gtiles;  // workgroups along the row tiles (gridDim.x)
+    void *y;
+    int y_dtype;
+    int64_t ldy;
+    int accumulate;
+    float *part;  // [S][M][N] partials (null: results go straight to y)
+};
+
+// Buffer resource of `bytes` bytes at p (raw, no stride; loads past the end
+// return 0).  p and bytes are kernel arguments, i.e. already uniform.
+EP_DEV __amdgpu_buffer_rsrc_t sk_rsrc(const void *p, uint32_t bytes)
+{
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
+                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+template <int BITS, int MT, int XDT>
+__global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
+{
+    constexpr int KPL = sk_kpl<BITS>();
+    constexpr int KS = sk_ks<BITS>();
+    constexpr int SUB = KPL / 8;          // MFMA sub-steps per load
+    constexpr int MR = 16 * MT;           // staged activation rows
+    constexpr int XLD = KS + 8;           // halfs per staged row (padding: conflict-free reads)
+    constexpr int TPR = kSkThreads / MR;  // staging threads per row
+    constexpr int VPT = KS / TPR;         // values per staging thread
+    constexpr int XE = XDT == EP_F32 ? 4 : 2;
+    constexpr int XP = VPT * XE / 16;     // 16-byte activation pieces per thread
+    static_assert(VPT % 8 == 0, "staging in 8-value pieces");
+
+    __shared__ __align__(16) uint32_t tab[kTabDwords];
+    __shared__ __align__(16) f16_t xs[MR * XLD];
+    __shared__ float s_pw[MR];
+    __shared__ uint32_t s_cbraw[kSkThreads];
+    __shared__ uint16_t s_cb[256];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, q = lane >> 4;
+    const int split = blockIdx.y;
+    const int ka = split * KS;
+    const uint32_t kbyte = BITS == 4 ? (uint32_t)ka / 2 : (uint32_t)ka;
+    const auto rx = sk_rsrc(a.x, a.xbytes), rw = sk_rsrc(a.packed, a.wbytes);
+    const auto rs = sk_rsrc(a.scale, a.sbytes), rcb = sk_rsrc(a.cb, a.cbbytes);
+
+    // ---- loads, in the order they are needed: vector-memory results return
+    // in order, so a wait for the activations must not also wait for the
+    // weights.  Every load is a buffer load; a masked lane gets an offset past
+    // the buffer's end and reads 0 (no select on a loaded value, which the
+    // compiler would turn into a load at the point of use).
+    const uint32_t cbraw = __builtin_amdgcn_raw_buffer_load_b32(rcb, tid < 256 ? tid * 4 : kOut, 0, 0);
+    const int xr = tid / TPR, xk0 = (tid % TPR) * VPT;
+    u32x4_t xv[XP];
+#pragma unroll
+    for (int p = 0; p < XP; ++p) {
+        const int k = ka + xk0 + p * (16 / XE);
+        const bool ok = xr < a.M && k < a.K;  // K % 16 == 0: pieces are whole
+        const uint32_t off = ok ? (uint32_t)(((int64_t)xr * a.ldx + k) * XE) : kOut;
+        xv[p] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+    }
+    u32x4_t w[kTpw][kLoads];
+    uint32_t sraw[kTpw][kLoads];  // fp16 scale bits; 0 where the chunk is masked
+#pragma unroll
+    for (int t = 0; t < kTpw; ++t) {
+        const int tile = (int)blockIdx.x + t * a.gtiles;
+        const int n = tile * kSkRows + wave * 16 + j;
+        const bool live = tile < a.tiles && n < a.N;
+#pragma unroll
+        for (int l = 0; l < kLoads; ++l) {
+            const int kc = ka + KPL * (4 * l + q);  // first k of the lane's chunk
+            const bool ok = live && kc < a.K;
+            const uint32_t off = (uint32_t)n * a.row_bytes + kbyte + (uint32_t)(16 * (4 * l + q));
+            w[t][l] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (int)off : (int)kOut, 0, 2);
+            const uint32_t soff = (uint32_t)(((int64_t)n * a.lds + kc / a.group) * 2);
+            sraw[t][l] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (int)soff : (int)kOut, 0, 0);
+        }
+    }
+    // keep every load above ahead of the staging below (which waits for the
+    // activations, i.e. for every load issued before it)
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- codebook -> fp16 bits; activations of the split -> LDS as fp16
+    // after the row's exact power-of-two rescale
+    s_cbraw[tid] = cbraw;  // unconditional: a conditional use would sink the load
+    {
+        float v[VPT];
+#pragma unroll
+        for (int p = 0; p < XP; ++p) {
+            if constexpr (XDT == EP_F32) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    v[4 * p + t] = __uint_as_float(xv[p][t]);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    unpack_pair<XDT>(xv[p][t], v[8 * p + 2 * t], v[8 * p + 2 * t + 1]);
+            }
+        }
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i)
+            am = fmaxf(am, fabsf(v[i]));
+#pragma unroll
+        for (int o = 1; o < TPR; o <<= 1)
+            am = fmaxf(am, __shfl_xor(am, o, 64));
+        const int e = row_exponent(am);
+        const float pw = ldexpf(1.0f, -e);
+        f16_t *dst = xs + xr * XLD + xk0;
+#pragma unroll
+        for (int p = 0; p < VPT; p += 8) {
+            f16x8_t h;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                h[t] = (f16_t)(v[p + t] * pw);
+            *(f16x8_t *)(dst + p) = h;
+        }
+        if (tid % TPR == 0)
+            s_pw[xr] = ldexpf(1.0f, e);
+    }
+    __syncthreads();
+    if (tid < 256) {
+        float c = 0.0f;
+        if (tid < a.levels) {
+            if (a.cb_dtype == EP_F32) {
+                c = __uint_as_float(s_cbraw[tid]);
+            } else {
+                const uint16_t h = (uint16_t)(s_cbraw[tid >> 1] >> (16 * (tid & 1)));
+                c = a.cb_dtype == EP_F16 ? (float)f16_from_bits(h) : bf16_to_f32(h);
+            }
+        }
+        s_cb[tid] = f16_bits((f16_t)c);
+    }
+    __syncthreads();
+    build_table<BITS>(tab, s_cb);
+    __syncthreads();
+
+    const uint32_t lane4 = (uint32_t)lane << 2;
+#pragma unroll
+    for (int t = 0; t < kTpw; ++t) {
+        const int tile = (int)blockIdx.x + t * a.gtiles;
+        if (tile >= a.tiles)
+            break;
+        f32x4_t acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            acc[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int l = 0; l < kLoads; ++l) {
+            const f16_t s16 = f16_from_bits((uint16_t)sraw[t][l]);
+            const f16x2_t s2 = (f16x2_t){s16, s16};
+            f16x2_t pr[KPL / 2];
+            if constexpr (BITS == 4) {
+#pragma unroll
+                for (int wd = 0; wd < 4; ++wd)
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        pr[wd * 4 + b] =
+                            as_f16x2(lds_read_u32(tab, __builtin_amdgcn_perm(w[t][l][wd], lane4, kSelByte[b]))) * s2;
+            } else {
+#pragma unroll
+                for (int wd = 0; wd < 4; ++wd)
+#pragma unroll
+                    for (int b = 0; b < 4; b += 2) {
+                        const uint32_t t0 = lds_read_u32(tab, __builtin_amdgcn_perm(w[t][l][wd], lane4, kSelByte[b]));
+                        const uint32_t t1 =
+                            lds_read_u32(tab, __builtin_amdgcn_perm(w[t][l][wd], lane4, kSelByte[b + 1]));
+                        pr[wd * 2 + b / 2] = as_f16x2(__builtin_amdgcn_perm(t1, t0, 0x05040100u)) * s2;
+                    }
+            }
+#pragma unroll
+            for (int s = 0; s < SUB; ++s) {
+                const f16x8_t bv = {pr[4 * s][0], pr[4 * s][1], pr[4 * s + 1][0], pr[4 * s + 1][1],
+                                    pr[4 * s + 2][0], pr[4 * s + 2][1], pr[4 * s + 3][0], pr[4 * s + 3][1]};
+                const int kx = KPL * (4 * l + q) + 8 * s;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const f16x8_t av = *(const f16x8_t *)(xs + (16 * mt + j) * XLD + kx);
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[mt], 0, 0, 0);
+                }
+            }
+        }
+        // D[row][col] of a 16x16 tile: lane col + 16 * (row / 4), register
+        // row % 4.  Stores only (y is never read here: accumulation goes
+        // through the reduction).
+        const int n = tile * kSkRows + wave * 16 + j;
+        if (n < a.N) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = 16 * mt + 4 * q + r;
+                    if (m < a.M) {
+                        const float v = acc[mt][r] * s_pw[m];
+                        if (a.part) {
+                            *(__attribute__((address_space(1))) float *)(a.part + ((int64_t)split * a.M + m) * a.N + n) = v;
+                        } else {
+                            const int64_t off = (int64_t)m * a.ldy + n;
+                            if (a.y_dtype == EP_F32)
+                                *(__attribute__((address_space(1))) float *)((float *)a.y + off) = v;
+                            else if (a.y_dtype == EP_F16)
+                                *(__attribute__((address_space(1))) uint16_t *)((uint16_t *)a.y + off) = f16_bits((f16_t)v);
+                            else
+                                *(__attribute__((address_space(1))) uint16_t *)((uint16_t *)a.y + off) = f32_to_bf16(v);
+                        }
+                    }
+                }
+        }
+    }
+}
+
+// y[m, n] (=|+=) sum over splits s = 0 .. S-1 of part[s][m][n], in that
+// order.  Four consecutive outputs per thread (N % 4 == 0: 16-byte loads),
+// the loads of eight splits in flight at a time.
+template <bool VEC>
+__global__ void __launch_bounds__(256)
+    sk_reduce_kernel(const float *part, int S, int M, int N, void *y, int y_dtype, int64_t ldy,
+                     int accumulate)
+{
+    constexpr int V = VEC ? 4 : 1;
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+    const int64_t total = (int64_t)M * N;
+    if (i >= total)
+        return;
+    float v[V];
+#pragma unroll
+    for (int t = 0; t < V; ++t)
+        v[t] = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += 8) {
+        float p[8][V];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int s = s0 + u < S ? s0 + u : s0;  // in range; weighted out below
+            const float *src = part + (int64_t)s * total + i;
+            if constexpr (VEC) {
+                const f32x4_t q = *(const f32x4_t *)src;
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    p[u][t] = q[t];
+            } else {
+                p[u][0] = *src;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (s0 + u < S) {
+#pragma unroll
+                for (int t = 0; t < V; ++t)
+                    v[t] += p[u][t];
+            }
+    }
+    const int m = (int)(i / N), n = (int)(i % N);
+#pragma unroll
+    for (int t = 0; t < V; ++t) {
+        const int64_t off = (int64_t)m * ldy + n + t;
+        float r = v[t];
+        if (accumulate)
+            r += load_as_f32(y, y_dtype, off);
+        store_from_f32(y, y_dtype, off, r);
+    }
+}
+
+int sk_splits(int bits, int64_t K) { return (int)((K + (bits == 4 ? sk_ks<4>() : sk_ks<8>()) - 1) / (bits == 4 ? sk_ks<4>() : sk_ks<8>())); }
+
+template <int BITS, int MT>
+int sk_launch_x(const SkArgs &a, int S, int xdt, hipStream_t s)
+{
+    const dim3 grid((unsigned)a.gtiles, (unsigned)S);
+    switch (xdt) {
+    case EP_BF16:
+        hipLaunchKernelGGL((sk_kernel<BITS, MT, EP_BF16>), grid, dim3(kSkThreads), 0, s, a);
+        break;
+    case EP_F16:
+        hipLaunchKernelGGL((sk_kernel<BITS, MT, EP_F16>), grid, dim3(kSkThreads), 0, s, a);
+        break;
+    default:
+        hipLaunchKernelGGL((sk_kernel<BITS, MT, EP_F32>), grid, dim3(kSkThreads), 0, s, a);
+        break;
+    }
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+template <int BITS>
+int sk_launch_bits(const SkArgs &a, int S, int xdt, hipStream_t s)
+{
+    if (a.M <= 16)
+        return sk_launch_x<BITS, 1>(a, S, xdt, s);
+    if (a.M <= 32)
+        return sk_launch_x<BITS, 2>(a, S, xdt, s);
+    return sk_launch_x<BITS, 4>(a, S, xdt, s);
+}
+
+}  // namespace
+
+bool skinny_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
+{
+    const int bits = w.bits();
+    const int kpl = bits == 4 ? sk_kpl<4>() : sk_kpl<8>();
+    if (M < 2 || M > 64 || w.N < 1 || w.K < kpl || w.K % kpl != 0 || w.group % kpl != 0)
+        return false;
+    if (w.scale_dtype != EP_F16)
+        return false;  // fp16 group scales (the container's); f32 after make_trainable goes to the tiles
+    // every buffer extent fits the 32-bit offsets of the buffer loads, below
+    // the offset that masked lanes use
+    const int esz = x.dtype == EP_F32 ? 4 : 2;
+    const int64_t rb = bits == 4 ? w.K / 2 : w.K;
+    const int64_t G = (w.K + w.group - 1) / w.group;
+    if (w.N * rb > kOut || ((M - 1) * x.ld + w.K) * esz > kOut || ((w.N - 1) * w.ld_scale + G) * 2 > kOut)
+        return false;
+    if (((uintptr_t)w.packed & 15) != 0 || ((uintptr_t)x.ptr & 15) != 0)
+        return false;
+    return (x.ld * esz) % 16 == 0;
+}
+
+size_t skinny_workspace(int64_t M, int64_t N, int64_t K, int levels)
+{
+    // partial sums of every split (also with one split when accumulating)
+    return (size_t)sk_splits(levels <= 16 ? 4 : 8, K) * (size_t)M * (size_t)N * sizeof(float);
+}
+
+int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y, void *ws,
+                  size_t ws_bytes, hipStream_t stream)
+{
+    if (!skinny_serves(w, x, M))
+        return EP_DECLINE_SHAPE;
+    const int bits = w.bits();
+    const int S = sk_splits(bits, w.K);
+    const bool partials = S > 1 || y.accumulate;
+    const size_t need = partials ? skinny_workspace(M, w.N, w.K, w.levels) : 0;
+    if (need > 0 && (!ws || ws_bytes < need))
+        return set_error(EP_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws_bytes);
+    SkArgs a{};
+    const int esz = x.dtype == EP_F32 ? 4 : 2;
+    a.xbytes = (uint32_t)(((M - 1) * x.ld + w.K) * esz);
+    a.wbytes = (uint32_t)(w.N * (bits == 4 ? w.K / 2 : w.K));
+    a.sbytes = (uint32_t)(((w.N - 1) * w.ld_scale + (w.K + w.group - 1) / w.group) * 2);
+    a.cbbytes = (uint32_t)(w.levels * (w.cb_dtype == EP_F32 ? 4 : 2));
+    a.x = x.ptr;
+    a.ldx = x.ld;
+    a.M = (int)M;
+    a.packed = w.packed;
+    a.row_bytes = (uint32_t)(bits == 4 ? w.K / 2 : w.K);
+    a.scale = w.scale;
+    a.scale_dtype = w.scale_dtype;
+    a.lds = w.ld_scale;
+    a.cb = w.cb;
+    a.cb_dtype = w.cb_dtype;
+    a.levels = w.levels;
+    a.N = (int)w.N;
+    a.K = (int)w.K;
+    a.group = w.group;
+    a.tiles = (int)((w.N + kSkRows - 1) / kSkRows);
+    // one resident workgroup per CU: enough row-tile groups that S of them
+    // fill the device, at most kTpw tiles per workgroup
+    const int cus = device_cus();
+    int g = (cus + S - 1) / S;
+    const int gmin = (a.tiles + kTpw - 1) / kTpw;
+    if (g < gmin)
+        g = gmin;
+    if (g > a.tiles)
+        g = a.tiles;
+    a.gtiles = g;
+    a.y = y.ptr;
+    a.y_dtype = y.dtype;
+    a.ldy = y.ld;
+    a.accumulate = y.accumulate;
+    a.part = partials ? (float *)ws : nullptr;
+    const int rc = bits == 4 ? sk_launch_bits<4>(a, S, x.dtype, stream) : sk_launch_bits<8>(a, S, x.dtype, stream);
+    if (rc != EP_OK || !partials)
+        return rc;
+    const int64_t total = M * w.N;
+    if (w.N % 4 == 0)
+        hipLaunchKernelGGL(sk_reduce_kernel<true>, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0,
+                           stream, (const float *)ws, S, (int)M, (int)w.N, y.ptr, y.dtype, y.ld, y.accumulate);
+    else
+        hipLaunchKernelGGL(sk_reduce_kernel<false>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                           stream, (const float *)ws, S, (int)M, (int)w.N, y.ptr, y.dtype, y.ld, y.accumulate);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+}  // namespace ep
