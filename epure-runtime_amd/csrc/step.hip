@@ -114,9 +114,10 @@ struct Model {
 };
 
 // Llama-3-8B and Qwen3-1.7B shapes; shares
-// at 256 workgroups: q|k|v 6 / 4 quads, o 4 / 2, gate|up 14 / 6, down 4 / 2.
-using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 4, 14, 4, 0, 0, 0, 2>;
-using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 2, 6, 2>;
+// at 256 workgroups: q|k|v 6 / 4 quads, o 8 / 4 (on at least half the grid),
+// gate|up 14 / 6, down 4 / 2.
+using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 8, 14, 4, 0, 0, 0, 2>;
+using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 4, 6, 2>;
 
 // Where a phase of contraction length K keeps its activations, factors and
 // accumulator inside the region.
@@ -1173,7 +1174,9 @@ EP_DEV Segs segs_qkv(LayerC &L, const StepArgs &a, const Shape &sh)
     return s;
 }
 
-EP_DEV Segs segs_one(LayerC &L, int li, int N, int ldsb, const Shape &sh)
+// One weight's row quads over workgroups skip .. G - 1 (workgroups below
+// `skip` get an empty share).
+EP_DEV Segs segs_one(LayerC &L, int li, int N, int ldsb, const Shape &sh, int skip = 0)
 {
     Segs s;
     s.pk0 = s.pk1 = s.pk2 = L.packed[li];
@@ -1183,7 +1186,13 @@ EP_DEV Segs segs_one(LayerC &L, int li, int N, int ldsb, const Shape &sh)
     s.q1 = s.q2 = 0x7fffffff;
     s.nq = N / 4;
     s.ldsb = ldsb;
-    share(s, sh.b, sh.G, false);
+    if (sh.b < skip) {
+        s.qa = s.qb = 0;
+        s.sfirst = 0;
+        s.ntab = 1;
+    } else {
+        share(s, sh.b - skip, sh.G - skip, false);
+    }
     return s;
 }
 
@@ -1242,6 +1251,10 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
 
     const int nchunk = pos / kChunk + 1;
     const int nitems = a.Hkv * nchunk;
+    // workgroups that run an attention item first hold no o rows (up to
+    // half the grid): the o phase then never waits for its slowest members,
+    // the combining attention workgroups
+    const int xo = nitems < G / 2 ? nitems : G / 2;
 
     typename PQ::Blk qb[PQ::NBUF];
     typename PO::Blk ob[PO::NBUF];
@@ -1257,7 +1270,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         __builtin_amdgcn_sched_barrier(0);
         PQ::prefetch(qb, sq, a.group);
         build_tables(tab, cb16, cbv, sq.ntab);
-        const Segs so = segs_one(layers[0], 3, M::H, sh.ldsb_o, sh);
+        const Segs so = segs_one(layers[0], 3, M::H, sh.ldsb_o, sh, xo);
         cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
     }
 
@@ -1290,7 +1303,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // would delay it: results return in order) and the o table is built
         // after the attention.  The other workgroups prefetch o and build
         // its table now.
-        const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
+        const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh, xo);
         if (b < nitems) {
             AttnRegs ar;
             attn_load(ar, L.kcache, L.vcache, b % a.Hkv, b / a.Hkv, pos, a.max_pos);
@@ -1308,7 +1321,8 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
                                  [] {});
                 lds_sync();
             }
-            build_tables(tab, cb16, cbv, so.ntab);
+            if (so.qb > so.qa)
+                build_tables(tab, cb16, cbv, so.ntab);
         } else {
             PO::prefetch(ob, so, a.group);
             build_tables(tab, cb16, cbv, so.ntab);
@@ -1319,15 +1333,18 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             cbv = load_cb(sg, sg.ntab, a.levels, a.cb_dtype);
         }
         stamp(a, l, 2);
-        // ---- o (+= residual)
+        // ---- o (+= residual); attention workgroups below xo hold no o rows
+        // and go straight on to gate|up (no wait for the attention output)
         {
-            const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
-            const float hv = residual_rows(so, a, h_prev, tag_of(seq, l - 1, PH_DOWN));
-            stage<XS_BF16, M::HQD>(at_l, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf, part8,
-                                   err);
-            stamp(a, l, 3);
-            PO::template run<MODE_ACC>(ob, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
-                                       1.0f, h_o, a.h0, false, nullptr, tag_of(seq, l, PH_O));
+            const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh, xo);
+            if (so.qb > so.qa) {
+                const float hv = residual_rows(so, a, h_prev, tag_of(seq, l - 1, PH_DOWN));
+                stage<XS_BF16, M::HQD>(at_l, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf,
+                                       part8, err);
+                stamp(a, l, 3);
+                PO::template run<MODE_ACC>(ob, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
+                                           1.0f, h_o, a.h0, false, nullptr, tag_of(seq, l, PH_O));
+            }
         }
         stamp(a, l, 4);
         {
@@ -1374,7 +1391,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             const Segs sq = segs_qkv(layers[l + 1], a, sh);
             PQ::prefetch(qb, sq, a.group);
             build_tables(tab, cb16, cbv, sq.ntab);
-            const Segs so = segs_one(layers[l + 1], 3, M::H, sh.ldsb_o, sh);
+            const Segs so = segs_one(layers[l + 1], 3, M::H, sh.ldsb_o, sh, xo);
             cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
         }
     }
@@ -1407,7 +1424,8 @@ int launch_model(const StepArgs &a, hipStream_t stream)
     // every share must fit its LDS accumulator (and an accumulating share
     // the 64 residual slots)
     auto quads = [&](int rows) { return (rows / 4 + grid - 1) / grid; };
-    if (quads(M::HQD + 2 * Nkv) > M::MQ_QKV || quads(M::H) > M::MQ_O ||
+    const int ogrid = grid - grid / 2;  // workgroups left for o when attention takes half
+    if (quads(M::HQD + 2 * Nkv) > M::MQ_QKV || (M::H / 4 + ogrid - 1) / ogrid > M::MQ_O ||
         quads(M::I) > M::MQ_GU || quads(M::H) > M::MQ_D || quads(M::H) * 4 > 64)
         return set_error(EP_DECLINE_SHAPE, "decode step: %d workgroups too few for the shape",
                          grid);
