@@ -103,9 +103,11 @@ size_t ep_dequant_matmul_workspace(int64_t M, int64_t N, int64_t K, int levels, 
     // Any M may land on the MFMA path (shapes the GEMV does not serve), so
     // the per-row exponent buffer is always requested; 2..64 rows may take
     // the split-K path and its partial sums.
-    const size_t a = mfma_workspace(M);
+    size_t need = mfma_workspace(M);
     const size_t b = (M >= 2 && M <= 64) ? skinny_workspace(M, N, K, levels) : 0;
-    return a > b ? a : b;
+    const size_t c = M > 64 ? prefill_workspace(M, N, K, levels) : 0;
+    need = need > b ? need : b;
+    return need > c ? need : c;
 }
 
 int ep_dequant_matmul(const void *x, int x_dtype, int64_t ldx, const uint8_t *packed,
@@ -138,6 +140,8 @@ int ep_dequant_matmul(const void *x, int x_dtype, int64_t ldx, const uint8_t *pa
         return launch_gemv(w, xa, M, ya, s);
     if (skinny_serves(w, xa, M))
         return launch_skinny(w, xa, M, ya, workspace, workspace_bytes, s);
+    if (M > 64 && prefill_serves(w, xa, M))
+        return launch_prefill(w, xa, M, ya, workspace, workspace_bytes, s);
     if (mfma_serves(w, xa, M))
         return launch_mfma(w, xa, M, ya, workspace, workspace_bytes, s);
     if (M <= 64)

@@ -140,6 +140,15 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
                   size_t ws_bytes, hipStream_t stream);
 bool skinny_serves(const PackedDesc &w, const ActDesc &x, int64_t M);
 size_t skinny_workspace(int64_t M, int64_t N, int64_t K, int levels);
+// y (=|+=) sum over s < S of part[s][M][N], in split order (skinny.hip).
+int launch_split_reduce(const float *part, int S, int64_t M, int64_t N, const OutDesc &y,
+                        hipStream_t stream);
+
+// Prefill (more than 64 rows) dequant-matmul on 32x32x16 MFMA (prefill.hip).
+int launch_prefill(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y, void *ws,
+                   size_t ws_bytes, hipStream_t stream);
+bool prefill_serves(const PackedDesc &w, const ActDesc &x, int64_t M);
+size_t prefill_workspace(int64_t M, int64_t N, int64_t K, int levels);
 
 int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, int64_t M,
                     const OutDesc &gx, float *grad_cb, float *grad_scale, int64_t ld_gscale,

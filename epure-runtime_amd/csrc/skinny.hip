@@ -445,13 +445,18 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     const int rc = bits == 4 ? sk_launch_bits<4>(a, S, x.dtype, stream) : sk_launch_bits<8>(a, S, x.dtype, stream);
     if (rc != EP_OK || !partials)
         return rc;
-    const int64_t total = M * w.N;
-    if (w.N % 4 == 0)
+    return launch_split_reduce((const float *)ws, S, M, w.N, y, stream);
+}
+
+int launch_split_reduce(const float *part, int S, int64_t M, int64_t N, const OutDesc &y, hipStream_t stream)
+{
+    const int64_t total = M * N;
+    if (N % 4 == 0)
         hipLaunchKernelGGL(sk_reduce_kernel<true>, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0,
-                           stream, (const float *)ws, S, (int)M, (int)w.N, y.ptr, y.dtype, y.ld, y.accumulate);
+                           stream, part, S, (int)M, (int)N, y.ptr, y.dtype, y.ld, y.accumulate);
     else
         hipLaunchKernelGGL(sk_reduce_kernel<false>, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                           stream, (const float *)ws, S, (int)M, (int)w.N, y.ptr, y.dtype, y.ld, y.accumulate);
+                           stream, part, S, (int)M, (int)N, y.ptr, y.dtype, y.ld, y.accumulate);
     EP_HIP_CHECK(hipGetLastError());
     return EP_OK;
 }
