@@ -7,13 +7,16 @@
 //   grad_cb[l]       = sum_{idx[n,k] == l} G[n, k] * scale[n, g(k)]
 //   with G = gy^T . x, which is never written to memory  (dw kernel)
 //
-// dx: MFMA over 128x128 (m, k) tiles, contraction over n in steps of 32.
-//     gy enters as fp16 after the exact per-row power-of-two rescale (as in
-//     the forward); each W tile is read once from the packed bytes,
-//     expanded to fp16(cb * scale) and written transposed into LDS.
+// dx: MFMA over 128x128 (m, k) tiles, contraction over n in steps of 128
+//     (split in up to 8 parts, summed in split order, when the tiles alone
+//     cannot fill the device).  gy enters as fp16 after the exact per-row
+//     power-of-two rescale (as in the forward); W is dequantized per 8x8
+//     block to fp16(cb) * fp16(scale) and transposed in registers, so the
+//     W^T tile goes to LDS as 16-byte rows.
 // dw: MFMA (bf16 operands: gy and x are bf16, products exact in fp32) over
 //     128x128 (k, n) tiles of G, contraction over the token dimension m in
-//     steps of 32.  The epilogue never stores G: each value is multiplied by
+//     steps of 64 (x and gy transposed per 8x8 block in registers, LDS
+//     double-buffered).  The epilogue never stores G: each value is multiplied by
 //     cb[idx] and summed over its group (grad_scale is complete inside the
 //     tile, one plain store per (n, g)), and multiplied by its scale and
 //     added into a per-thread private LDS histogram over the 16 codebook
@@ -28,9 +31,11 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int T = 128;   // output tile (both dims)
-constexpr int KS = 32;   // contraction step
-constexpr int LD = KS + 8;  // LDS row length (elements), padded
+constexpr int T = 128;        // output tile (both dims)
+constexpr int CS = 64;        // dx: contraction step over n
+constexpr int MS = 64;        // dw: contraction step over m
+constexpr int LDX = CS + 8;   // dx LDS row length (halfs), padded
+constexpr int LDW = MS + 8;   // dw LDS row length (halfs), padded
 
 struct BwdArgs {
     const void *gy;
@@ -53,56 +58,115 @@ struct BwdArgs {
     float *gscale;
     int64_t ldgs;
     const int *rexp;     // [M] per-row exponents of gy
+    const f16_t *gy16;   // [M][N] fp16(gy * 2^-rexp), written by gy_prep_kernel
     float *gc_part;      // [num dw workgroups][16]
+    int dx_steps;        // contraction steps per dx split
+    float *dx_part;      // [splits][M][K] f32 partials (null: one split, results go to gx)
 };
 
-__global__ void __launch_bounds__(256)
-    row_exp_gy_kernel(const void *gy, int dt, int64_t ld, int M, int N, int *rexp)
+EP_DEV uint32_t bits_of(f16x2_t v)
 {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= M)
-        return;
-    float amax = 0.0f;
-    for (int64_t n = lane; n < N; n += 64)
-        amax = fmaxf(amax, fabsf(load_as_f32(gy, dt, row * ld + n)));
-    amax = wave_max_bfly(amax);
-    if (lane == 0)
-        rexp[row] = row_exponent(amax);
+    uint32_t u;
+    __builtin_memcpy(&u, &v, 4);
+    return u;
 }
 
-// grad_x[m, k] = sum_n gy[m, n] W[n, k]
-template <int BITS>
-__global__ void __launch_bounds__(256) dx_kernel(BwdArgs a)
+// 8x8 transpose of 16-bit elements: r[i] is row i (dword d holds elements
+// 2d and 2d + 1), c[j] becomes column j (dword d holds rows 2d and 2d + 1).
+// 32 byte permutes; lets a thread write whole 16-byte rows of a transposed
+// LDS tile instead of 64 two-byte stores.
+EP_DEV void tr8x8(const u32x4_t (&r)[8], u32x4_t (&c)[8])
 {
-    __shared__ __align__(16) f16_t As[T * LD];  // gy tile [m][n]
-    __shared__ __align__(16) f16_t Bs[T * LD];  // W^T tile [k][n]
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            c[j][d] = __builtin_amdgcn_perm(r[2 * d + 1][j >> 1], r[2 * d][j >> 1],
+                                            (j & 1) ? 0x07060302u : 0x05040100u);
+}
+
+// Per-row exponent of the largest |gy| (row_exponent) and the rescaled
+// fp16 copy of the row, converted once here instead of once per k tile of
+// the dx kernel: one wave per row of bf16 values, 16-byte loads, four in
+// flight per lane (rows are 16-byte aligned and N % 16 == 0); the second
+// pass re-reads the row from the caches.
+__global__ void __launch_bounds__(256)
+    gy_prep_kernel(const uint16_t *gy, int64_t ld, int M, int N, int *rexp, f16_t *gy16)
+{
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M)
+        return;
+    const u32x4_t *p = (const u32x4_t *)(gy + (int64_t)row * ld);
+    const int pieces = N / 8;
+    float amax = 0.0f;
+    for (int i0 = lane; i0 < pieces; i0 += 256) {
+        u32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            v[u] = i0 + 64 * u < pieces ? p[i0 + 64 * u] : (u32x4_t){0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                amax = fmaxf(amax, fmaxf(fabsf(__uint_as_float(v[u][t] << 16)),
+                                         fabsf(__uint_as_float(v[u][t] & 0xffff0000u))));
+    }
+    amax = wave_max(amax);
+    const int e = row_exponent(amax);
+    if (lane == 0)
+        rexp[row] = e;
+    const float pw = ldexpf(1.0f, -e);
+    f16x8_t *q = (f16x8_t *)(gy16 + (int64_t)row * N);
+    for (int i0 = lane; i0 < pieces; i0 += 256) {
+        u32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            v[u] = i0 + 64 * u < pieces ? p[i0 + 64 * u] : (u32x4_t){0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            f16x8_t h;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                h[2 * t] = (f16_t)(__uint_as_float(v[u][t] << 16) * pw);
+                h[2 * t + 1] = (f16_t)(__uint_as_float(v[u][t] & 0xffff0000u) * pw);
+            }
+            if (i0 + 64 * u < pieces)
+                q[i0 + 64 * u] = h;
+        }
+    }
+}
+
+// grad_x[m, k] = sum_n gy[m, n] W[n, k] over a 128 x 128 (m, k) tile,
+// contraction over n in steps of CS (blockIdx.z: the split of the steps).
+// Staging per step: gy rows (already fp16, rescaled by 2^-e per row) go to
+// LDS as they are ([m][n]); W is dequantized by 8 x 8 blocks (8 rows n x 8
+// columns k: one packed dword per row, fp16(cb) pairs from the LDS table
+// times the fp16 scale, i.e. materialize(float16)), transposed in registers
+// and written as W^T rows ([k][n]), so both MFMA operands are 16-byte LDS
+// reads.  The next step's global loads are in flight during the MFMAs.
+__global__ void __launch_bounds__(256, 3) dx_kernel(BwdArgs a)
+{
+    __shared__ __align__(16) f16_t Gs[T * LDX];  // gy tile [m][n]
+    __shared__ __align__(16) f16_t Ws[T * LDX];  // W^T tile [k][n]
     __shared__ uint32_t tab[256];
-    __shared__ float s_pw[T];
     __shared__ int s_e[T];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wk = wave & 1;
     const int m0 = blockIdx.y * T, k0 = blockIdx.x * T;
+    const int nsteps = (a.N + CS - 1) / CS;
+    const int st0 = blockIdx.z * a.dx_steps;
+    const int st1 = st0 + a.dx_steps < nsteps ? st0 + a.dx_steps : nsteps;
     {
-        const int b = tid;
-        uint32_t v;
-        if constexpr (BITS == 4) {
-            const int lo = b & 15, hi = b >> 4;
-            const float clo = lo < a.levels ? load_as_f32(a.cb, a.cb_dtype, lo) : 0.0f;
-            const float chi = hi < a.levels ? load_as_f32(a.cb, a.cb_dtype, hi) : 0.0f;
-            v = (uint32_t)f16_bits((f16_t)clo) | ((uint32_t)f16_bits((f16_t)chi) << 16);
-        } else {
-            const float c = b < a.levels ? load_as_f32(a.cb, a.cb_dtype, b) : 0.0f;
-            v = f16_bits((f16_t)c);
-        }
-        tab[b] = v;
+        const int lo = tid & 15, hi = tid >> 4;
+        const float clo = lo < a.levels ? load_as_f32(a.cb, a.cb_dtype, lo) : 0.0f;
+        const float chi = hi < a.levels ? load_as_f32(a.cb, a.cb_dtype, hi) : 0.0f;
+        tab[tid] = (uint32_t)f16_bits((f16_t)clo) | ((uint32_t)f16_bits((f16_t)chi) << 16);
     }
     if (tid < T) {
         const int m = m0 + tid;
-        const int e = m < a.M ? a.rexp[m] : 0;
-        s_e[tid] = e;
-        s_pw[tid] = ldexpf(1.0f, -e);
+        s_e[tid] = m < a.M ? a.rexp[m] : 0;
     }
 
     f32x16_t acc[2][2];
@@ -114,98 +178,73 @@ __global__ void __launch_bounds__(256) dx_kernel(BwdArgs a)
             for (int r = 0; r < 16; ++r)
                 acc[i][j][r] = 0.0f;
 
-    // staging registers for one contraction step
-    float gv[16];          // gy: 128 rows x 32 n = 16 values per thread
-    u32x4_t wr;            // W: 32 rows x 128 k; 4-bit: 16 bytes/thread (128 threads)
-    float wsc = 0.0f;      //    8-bit: 16 bytes/thread (256 threads)
-    constexpr int WTHREADS = BITS == 4 ? 128 : 256;
-    constexpr int KPC = BITS == 4 ? 32 : 16;   // k per 16-byte chunk
-
+    // gy: rows 32 p + (tid >> 3), columns 8 (tid & 7) .. + 7 (p = 0..3);
+    // W (threads below 128, waves 0-1): the 8 x 8 block of rows nb * 8 ..,
+    // columns kb * 8 ..
+    const int gr0 = tid >> 3, gc = 8 * (tid & 7);
+    const bool wthr = tid < 128;  // wave-uniform
+    const int nb = tid & 7, kb = (tid >> 3) & 15;
+    const int64_t rowb = a.K / 2;
+    u32x4_t gv[4];
+    uint32_t wv[8];
+    float wsc[8];
     auto load = [&](int n0) {
-        // gy: thread -> row tid/2, 16 consecutive n
-        const int r = tid >> 1, c0 = (tid & 1) * 16;
-        const int m = m0 + r;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int n = n0 + c0 + e;
-            gv[e] = (m < a.M && n < a.N) ? load_as_f32(a.gy, a.gy_dtype, (int64_t)m * a.ldgy + n)
-                                         : 0.0f;
+        for (int p = 0; p < 4; ++p) {
+            const int m = m0 + 32 * p + gr0, n = n0 + gc;
+            gv[p] = (m < a.M && n < a.N) ? *(const u32x4_t *)(a.gy16 + (int64_t)m * a.N + n)
+                                         : (u32x4_t){0u, 0u, 0u, 0u};
         }
-        if (tid < WTHREADS) {
-            const int per_row = T / KPC;             // chunks per W row in the tile
-            const int wrow = tid / per_row, part = tid % per_row;
-            const int n = n0 + wrow;
-            const int64_t kk = (int64_t)k0 + part * KPC;
-            const int64_t byte0 = BITS == 4 ? kk / 2 : kk;
-            if (n < a.N) {
-                wr = *(const u32x4_t *)(a.packed + (int64_t)n * (BITS == 4 ? a.K / 2 : a.K) + byte0);
-                wsc = load_as_f32(a.scale, a.scale_dtype, (int64_t)n * a.lds + kk / a.group);
-            } else {
-                wr = (u32x4_t){0, 0, 0, 0};
-                wsc = 0.0f;
+        if (wthr) {
+            const int k = k0 + kb * 8;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int n = n0 + nb * 8 + i;
+                const bool ok = n < a.N;
+                wv[i] = ok ? *(const uint32_t *)(a.packed + (int64_t)n * rowb + k / 2) : 0u;
+                wsc[i] = ok ? load_as_f32(a.scale, a.scale_dtype, (int64_t)n * a.lds + k / a.group) : 0.0f;
             }
         }
     };
     auto store = [&]() {
-        {
-            const int r = tid >> 1, c0 = (tid & 1) * 16;
-            const float pw = s_pw[r];
-            f16x8_t h0, h1;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                h0[e] = (f16_t)(gv[e] * pw);
-                h1[e] = (f16_t)(gv[8 + e] * pw);
+        for (int p = 0; p < 4; ++p)
+            *(u32x4_t *)&Gs[(32 * p + gr0) * LDX + gc] = gv[p];
+        if (wthr) {
+            u32x4_t rw[8], cw[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const f16_t sh = (f16_t)wsc[i];
+                const f16x2_t s2 = (f16x2_t){sh, sh};
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+                    rw[i][d] = bits_of(as_f16x2(tab[(wv[i] >> (8 * d)) & 0xffu]) * s2);
             }
-            *(f16x8_t *)&As[r * LD + c0] = h0;
-            *(f16x8_t *)&As[r * LD + c0 + 8] = h1;
-        }
-        if (tid < WTHREADS) {
-            const int per_row = T / KPC;
-            const int wrow = tid / per_row, part = tid % per_row;
-            const f16_t sh = (f16_t)wsc;
-            const f16x2_t s2 = (f16x2_t){sh, sh};
+            tr8x8(rw, cw);
 #pragma unroll
-            for (int wd = 0; wd < 4; ++wd) {
-                const uint32_t w = wr[wd];
-                if constexpr (BITS == 4) {
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const f16x2_t v =
-                            as_f16x2(tab[(w >> (8 * b)) & 0xffu]) * s2;
-                        const int kl = part * KPC + (wd * 4 + b) * 2;
-                        Bs[kl * LD + wrow] = v[0];
-                        Bs[(kl + 1) * LD + wrow] = v[1];
-                    }
-                } else {
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const f16x2_t v = as_f16x2(tab[(w >> (8 * b)) & 0xffu] & 0xffffu) * s2;
-                        const int kl = part * KPC + wd * 4 + b;
-                        Bs[kl * LD + wrow] = v[0];
-                    }
-                }
-            }
+            for (int j = 0; j < 8; ++j)
+                *(u32x4_t *)&Ws[(kb * 8 + j) * LDX + nb * 8] = cw[j];
         }
     };
 
-    const int steps = (a.N + KS - 1) / KS;
     __syncthreads();
-    load(0);
-    for (int st = 0; st < steps; ++st) {
+    if (st0 < st1)
+        load(st0 * CS);
+    for (int st = st0; st < st1; ++st) {
         store();
         __syncthreads();
-        if (st + 1 < steps)
-            load((st + 1) * KS);
+        if (st + 1 < st1)
+            load((st + 1) * CS);
 #pragma unroll
-        for (int kk = 0; kk < KS / 16; ++kk) {
+        for (int kk = 0; kk < CS / 16; ++kk) {
             f16x8_t af[2], bf[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                af[i] = *(const f16x8_t *)&As[(wm * 64 + i * 32 + (lane & 31)) * LD + kk * 16 +
+                af[i] = *(const f16x8_t *)&Gs[(wm * 64 + i * 32 + (lane & 31)) * LDX + kk * 16 +
                                                (lane >> 5) * 8];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                bf[j] = *(const f16x8_t *)&Bs[(wk * 64 + j * 32 + (lane & 31)) * LD + kk * 16 +
+                bf[j] = *(const f16x8_t *)&Ws[(wk * 64 + j * 32 + (lane & 31)) * LDX + kk * 16 +
                                                (lane >> 5) * 8];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -216,6 +255,8 @@ __global__ void __launch_bounds__(256) dx_kernel(BwdArgs a)
         __syncthreads();
     }
 
+    // D[row][col] of a 32x32 tile: lane col + 32 * ((row / 4) % 2),
+    // register (row % 4) + 4 * (row / 8); rows m, columns k
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -225,48 +266,39 @@ __global__ void __launch_bounds__(256) dx_kernel(BwdArgs a)
                 const int row = wm * 64 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
                 const int col = wk * 64 + j * 32 + (lane & 31);
                 const int m = m0 + row, k = k0 + col;
-                if (m < a.M && k < a.K)
-                    store_from_f32(a.gx, a.gx_dtype, (int64_t)m * a.ldgx + k,
-                                   ldexpf(acc[i][j][r], s_e[row]));
+                if (m >= a.M)
+                    continue;
+                const float v = ldexpf(acc[i][j][r], s_e[row]);
+                if (a.dx_part)
+                    a.dx_part[((int64_t)blockIdx.z * a.M + m) * a.K + k] = v;
+                else
+                    store_from_f32(a.gx, a.gx_dtype, (int64_t)m * a.ldgx + k, v);
             }
 }
 
 // G tile (k x n) = x^T . gy, reduced into grad_scale and per-workgroup
 // codebook-gradient partials.  4-bit indices (levels <= 16), bf16 gy / x.
-__global__ void __launch_bounds__(256) dw_kernel(BwdArgs a)
+// Staging per step of MS rows m: waves 0-1 take x, waves 2-3 gy, each
+// thread one 8 x 8 block (8 rows m x 8 columns), transposed in registers
+// and written as 16-byte rows of x^T [k][m] / gy^T [n][m]; the next step's
+// loads are in flight during the MFMAs.  Single-buffered (37 KB of LDS):
+// three workgroups per CU.  The epilogue reuses the staging space.
+constexpr int kDwStage = 2 * T * LDW * 2;  // [x^T | gy^T] bf16
+__global__ void __launch_bounds__(256, 3) dw_kernel(BwdArgs a)
 {
-    __shared__ __align__(16) __bf16 Xs[T * LD];   // x^T  [k][m]
-    __shared__ __align__(16) __bf16 Gs[T * LD];   // gy^T [n][m]
-    __shared__ uint8_t Ps[T * (T / 2)];           // packed bytes of the tile [n][k/2]
-    __shared__ float Ss[T * 4];                   // scale[n][g] for the tile's groups
-    __shared__ float cbf[16];
-    __shared__ float hist[16 * 256];              // private per-thread level histograms
-    __shared__ float gsp[2][T * 4];               // grad_scale partials per k-wave
+    __shared__ __align__(16) char smem[kDwStage];
+    // epilogue views of the same space
+    uint8_t *Ps = (uint8_t *)smem;                    // packed bytes of the tile [n][k/2]
+    float *Ss = (float *)(smem + T * (T / 2));        // scale[n][g] for the tile's groups
+    float *cbf = Ss + T * 4;                          // [16]
+    float *hist = cbf + 16;                           // [16][256] private per-thread histograms
+    float *gsp = hist + 16 * 256;                     // [2][T * 4] grad_scale partials per k-wave
+    static_assert(T * (T / 2) + (T * 4 + 16 + 16 * 256 + 2 * T * 4) * 4 <= kDwStage, "epilogue fits");
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wk = wave >> 1, wn = wave & 1;
     const int k0 = blockIdx.x * T, n0 = blockIdx.y * T;
     const int gpt = T / a.group;  // groups per tile (1, 2 or 4)
-
-    if (tid < 16)
-        cbf[tid] = tid < a.levels ? load_as_f32(a.cb, a.cb_dtype, tid) : 0.0f;
-    for (int i = tid; i < 16 * 256; i += 256)
-        hist[i] = 0.0f;
-    for (int i = tid; i < T * gpt; i += 256) {
-        const int nl = i / gpt, gi = i % gpt;
-        const int n = n0 + nl;
-        Ss[nl * 4 + gi] =
-            n < a.N ? load_as_f32(a.scale, a.scale_dtype, (int64_t)n * a.lds + k0 / a.group + gi)
-                    : 0.0f;
-    }
-    for (int i = tid; i < T * (T / 2) / 16; i += 256) {
-        const int nl = i / (T / 32), part = i % (T / 32);
-        const int n = n0 + nl;
-        u32x4_t v = (u32x4_t){0, 0, 0, 0};
-        if (n < a.N)
-            v = *(const u32x4_t *)(a.packed + (int64_t)n * (a.K / 2) + k0 / 2 + part * 16);
-        *(u32x4_t *)&Ps[nl * (T / 2) + part * 16] = v;
-    }
 
     f32x16_t acc[2][2];
 #pragma unroll
@@ -277,54 +309,51 @@ __global__ void __launch_bounds__(256) dw_kernel(BwdArgs a)
             for (int r = 0; r < 16; ++r)
                 acc[i][j][r] = 0.0f;
 
-    // staging: x tile [32 m x 128 k] and gy tile [32 m x 128 n], bf16;
-    // thread -> row m = tid / 8, 16 consecutive columns (two 16-byte loads)
-    u32x4_t xr[2], gr[2];
+    // this thread's 8 x 8 staging block: rows (blk >> 4) * 8 .. of the
+    // step, columns (blk & 15) * 8 .. of the tile
+    const bool isx = tid < 128;  // wave-uniform
+    const int blk = tid & 127;
+    const int br = (blk >> 4) * 8, bc = (blk & 15) * 8;
+    const uint16_t *src = isx ? (const uint16_t *)a.x + k0 + bc : (const uint16_t *)a.gy + n0 + bc;
+    const int64_t ld = isx ? a.ldx : a.ldgy;
+    const bool colok = isx ? true : n0 + bc < a.N;
+    u32x4_t rr[8];
     auto load = [&](int mb) {
-        const int r = tid >> 3, c0 = (tid & 7) * 16;
-        const int m = mb + r;
-        const bool ok = m < a.M;
-        const uint16_t *xp = (const uint16_t *)a.x + (int64_t)m * a.ldx + k0 + c0;
-        const uint16_t *gp = (const uint16_t *)a.gy + (int64_t)m * a.ldgy + n0 + c0;
-        xr[0] = ok ? *(const u32x4_t *)xp : (u32x4_t){0, 0, 0, 0};
-        xr[1] = ok ? *(const u32x4_t *)(xp + 8) : (u32x4_t){0, 0, 0, 0};
-        const bool okn = ok && n0 + c0 < a.N;
-        gr[0] = okn ? *(const u32x4_t *)gp : (u32x4_t){0, 0, 0, 0};
-        gr[1] = okn ? *(const u32x4_t *)(gp + 8) : (u32x4_t){0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int m = mb + br + i;
+            rr[i] = (colok && m < a.M) ? *(const u32x4_t *)(src + (int64_t)m * ld)
+                                       : (u32x4_t){0u, 0u, 0u, 0u};
+        }
     };
-    auto store = [&]() {
-        const int r = tid >> 3, c0 = (tid & 7) * 16;
-        uint16_t *xs = (uint16_t *)Xs, *gs = (uint16_t *)Gs;
+    auto store = [&](int buf) {
+        u32x4_t cc[8];
+        tr8x8(rr, cc);
+        __bf16 *dst = (__bf16 *)smem + (buf * 2 + (isx ? 0 : 1)) * T * LDW;  // buf is 0
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int c = c0 + h * 8 + 2 * e;
-                xs[c * LD + r] = (uint16_t)(xr[h][e] & 0xffffu);
-                xs[(c + 1) * LD + r] = (uint16_t)(xr[h][e] >> 16);
-                gs[c * LD + r] = (uint16_t)(gr[h][e] & 0xffffu);
-                gs[(c + 1) * LD + r] = (uint16_t)(gr[h][e] >> 16);
-            }
+        for (int j = 0; j < 8; ++j)
+            *(u32x4_t *)&dst[(bc + j) * LDW + br] = cc[j];
     };
 
-    const int steps = (a.M + KS - 1) / KS;
-    __syncthreads();
+    const int steps = (a.M + MS - 1) / MS;
+    const __bf16 *Xs = (const __bf16 *)smem;
+    const __bf16 *Gs = Xs + T * LDW;
     load(0);
     for (int st = 0; st < steps; ++st) {
-        store();
+        store(0);
         __syncthreads();
         if (st + 1 < steps)
-            load((st + 1) * KS);
+            load((st + 1) * MS);
 #pragma unroll
-        for (int kk = 0; kk < KS / 16; ++kk) {
+        for (int kk = 0; kk < MS / 16; ++kk) {
             bf16x8_t af[2], bf[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
-                af[i] = *(const bf16x8_t *)&Xs[(wk * 64 + i * 32 + (lane & 31)) * LD + kk * 16 +
+                af[i] = *(const bf16x8_t *)&Xs[(wk * 64 + i * 32 + (lane & 31)) * LDW + kk * 16 +
                                                 (lane >> 5) * 8];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                bf[j] = *(const bf16x8_t *)&Gs[(wn * 64 + j * 32 + (lane & 31)) * LD + kk * 16 +
+                bf[j] = *(const bf16x8_t *)&Gs[(wn * 64 + j * 32 + (lane & 31)) * LDW + kk * 16 +
                                                 (lane >> 5) * 8];
 #pragma unroll
             for (int i = 0; i < 2; ++i)
@@ -337,6 +366,34 @@ __global__ void __launch_bounds__(256) dw_kernel(BwdArgs a)
     }
 
     // ---- epilogue: G[k][n] -> grad_scale partials and level histograms ----
+    // the tile's packed bytes, scales and the codebook (loaded only now:
+    // registers held across the main loop would spill)
+    u32x4_t pk[2];
+    float sv[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int c = tid + 256 * q;  // 16-byte piece: row c >> 2, part c & 3
+        const int n = n0 + (c >> 2);
+        pk[q] = n < a.N ? *(const u32x4_t *)(a.packed + (int64_t)n * (a.K / 2) + k0 / 2 + (c & 3) * 16)
+                        : (u32x4_t){0u, 0u, 0u, 0u};
+        const int nl = c / gpt, gi = c % gpt;
+        sv[q] = (c < T * gpt && n0 + nl < a.N)
+                    ? load_as_f32(a.scale, a.scale_dtype, (int64_t)(n0 + nl) * a.lds + k0 / a.group + gi)
+                    : 0.0f;
+    }
+    const float cbv = tid < a.levels ? load_as_f32(a.cb, a.cb_dtype, tid) : 0.0f;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int c = tid + 256 * q;
+        *(u32x4_t *)&Ps[(c >> 2) * (T / 2) + (c & 3) * 16] = pk[q];
+        if (c < T * gpt)
+            Ss[(c / gpt) * 4 + c % gpt] = sv[q];
+    }
+    if (tid < 16)
+        cbf[tid] = cbv;
+    for (int i = tid; i < 16 * 256; i += 256)
+        hist[i] = 0.0f;
+    __syncthreads();
     // D[row][col] of a 32x32 tile sits in lane col + 32 * ((row / 4) % 2),
     // register (row % 4) + 4 * (row / 8); rows are k, cols are n.
     float *my_hist = hist + tid;  // slot [level * 256 + tid]
@@ -363,15 +420,14 @@ __global__ void __launch_bounds__(256) dw_kernel(BwdArgs a)
         if (lane < 32)
 #pragma unroll
             for (int gi = 0; gi < 4; ++gi)
-                gsp[wk][nl * 4 + gi] = gs_acc[gi];
+                gsp[wk * T * 4 + nl * 4 + gi] = gs_acc[gi];
     }
     __syncthreads();
     for (int i = tid; i < T * gpt; i += 256) {
         const int nl = i / gpt, gi = i % gpt;
         const int n = n0 + nl;
         if (n < a.N)
-            a.gscale[(int64_t)n * a.ldgs + k0 / a.group + gi] =
-                gsp[0][nl * 4 + gi] + gsp[1][nl * 4 + gi];
+            a.gscale[(int64_t)n * a.ldgs + k0 / a.group + gi] = gsp[nl * 4 + gi] + gsp[T * 4 + nl * 4 + gi];
     }
     if (tid < 16) {
         float s = 0.0f;
@@ -403,12 +459,31 @@ __global__ void __launch_bounds__(256) gc_final_kernel(const float *part, int nw
 
 }  // namespace
 
+// Splits of the dx contraction: enough work items for the three resident
+// workgroups per CU where the (m, k) tiles alone cannot provide them, at
+// least 4 steps per split.
+static int dx_splits(int64_t M, int64_t N, int64_t K)
+{
+    const int64_t tiles = ((K + T - 1) / T) * ((M + T - 1) / T);
+    const int64_t nsteps = (N + CS - 1) / CS;
+    const int64_t slots = 3 * (int64_t)device_cus();
+    int64_t S = (slots + tiles - 1) / tiles;
+    if (S > 8)
+        S = 8;
+    while (S > 1 && nsteps / S < 4)
+        --S;
+    return (int)S;
+}
+
 size_t backward_workspace(int64_t M, int64_t N, int64_t K, int levels, int group)
 {
     (void)levels;
     (void)group;
     const int64_t nwg = ((K + T - 1) / T) * ((N + T - 1) / T);
-    return (size_t)((M * 4 + 255) / 256 * 256) + (size_t)nwg * 16 * sizeof(float);
+    const int S = dx_splits(M, N, K);
+    return (size_t)((M * 4 + 255) / 256 * 256) + (size_t)nwg * 16 * sizeof(float) +
+           (size_t)((M * N * 2 + 255) / 256 * 256) +
+           (S > 1 ? (size_t)S * (size_t)M * (size_t)K * sizeof(float) : 0);
 }
 
 bool backward_serves(const PackedDesc &w, int gy_dtype, int x_dtype)
@@ -461,18 +536,29 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
     a.rexp = (const int *)ws;
     a.gc_part = (float *)((char *)ws + (M * 4 + 255) / 256 * 256);
     if (gx.ptr) {
-        hipLaunchKernelGGL(row_exp_gy_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream,
-                           gy.ptr, gy.dtype, gy.ld, (int)M, (int)w.N, (int *)ws);
+        const size_t nwg_bytes = (size_t)((w.K + T - 1) / T) * ((w.N + T - 1) / T) * 16 * sizeof(float);
+        f16_t *gy16 = (f16_t *)((char *)a.gc_part + nwg_bytes);
+        a.gy16 = gy16;
+        hipLaunchKernelGGL(gy_prep_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream,
+                           (const uint16_t *)gy.ptr, gy.ld, (int)M, (int)w.N, (int *)ws, gy16);
         EP_HIP_CHECK(hipGetLastError());
-        hipLaunchKernelGGL(dx_kernel<4>, dim3((unsigned)((w.K + T - 1) / T), (unsigned)((M + T - 1) / T)),
+        const int S = dx_splits(M, w.N, w.K);
+        const int nsteps = (int)((w.N + CS - 1) / CS);
+        a.dx_steps = (nsteps + S - 1) / S;
+        const int Sused = (nsteps + a.dx_steps - 1) / a.dx_steps;
+        a.dx_part = Sused > 1 ? (float *)((char *)gy16 + (size_t)((M * w.N * 2 + 255) / 256 * 256)) : nullptr;
+        hipLaunchKernelGGL(dx_kernel, dim3((unsigned)((w.K + T - 1) / T), (unsigned)((M + T - 1) / T), (unsigned)Sused),
                            dim3(256), 0, stream, a);
         EP_HIP_CHECK(hipGetLastError());
+        if (Sused > 1) {
+            const int rc = launch_split_reduce(a.dx_part, Sused, M, w.K, OutDesc{gx.ptr, gx.dtype, gx.ld, 0}, stream);
+            if (rc != EP_OK)
+                return rc;
+        }
     }
     if (grad_cb || grad_scale) {
-        float *gs_dummy = nullptr;
         if (!grad_scale)
             return set_error(EP_ERR_ARG, "grad_cb without grad_scale is not served");
-        (void)gs_dummy;
         const dim3 grid((unsigned)(w.K / T), (unsigned)((w.N + T - 1) / T));
         hipLaunchKernelGGL(dw_kernel, grid, dim3(256), 0, stream, a);
         EP_HIP_CHECK(hipGetLastError());
