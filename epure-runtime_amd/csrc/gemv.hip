@@ -14,9 +14,10 @@
 //    so one ds_read_b32 + one v_dot2_f32_f16 consumes two weights.  8-bit
 //    indices use the same table shape holding one fp16 per byte value and
 //    two reads per v_dot2.
-//  * The table is replicated 64x with lane l reading slot l, so each of the
-//    64 lanes of a ds_read_b32 hits its own bank: no bank conflicts despite
-//    random byte values.  Address = (byte << 8) | (lane << 2), one v_perm.
+//  * The table is replicated 32x with lane l reading copy l & 31, so the
+//    32 lanes a ds_read_b32 serves per cycle hit 32 banks: no bank conflicts
+//    despite random byte values.  Address = (byte << 8) | ((lane & 31) << 2),
+//    one v_perm.
 //  * 16 lanes cover 256 contiguous bytes of a row with 16-byte loads (fully
 //    coalesced); a wave covers 4 rows x 256 bytes per load instruction and
 //    the waves of a workgroup split the row's bytes into 256-byte slabs, so
@@ -327,7 +328,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     }
     __syncthreads();
 
-    const uint32_t lane4 = (uint32_t)lane << 2;
+    const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
 
     for (; blk < nblk; blk += nwg) {
         const int nxt = blk + nwg;

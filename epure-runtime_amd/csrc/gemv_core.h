@@ -3,29 +3,33 @@
 //
 // Dequantization is an LDS "pair table": byte value b -> half2(cb[b & 15],
 // cb[b >> 4]) for 4-bit indices (low nibble = even k, epure/runtime.py:45),
-// or the single fp16 cb[b] duplicated for 8-bit indices.  The table is
-// replicated once per lane (64 x 256 dwords = 64 KiB) and lane l reads
-// replica l, so a ds_read_b32 with random byte values never has two lanes
-// on one bank.  The byte address of a lookup is (b << 8) | (lane << 2),
-// formed by one v_perm from the packed word.
+// or the single fp16 cb[b] duplicated for 8-bit indices.  Entry b holds 32
+// copies at bytes (b << 8) + 4 c (the upper half of each 256-byte entry is
+// unused) and lane l reads copy l & 31, so a ds_read_b32 with random byte
+// values never has two lanes of one 32-lane half on one bank.  The byte
+// address of a lookup is (b << 8) | ((lane & 31) << 2), formed by one
+// v_perm from the packed word.
 #pragma once
 
 #include "ep_common.h"
 
 namespace ep {
 
-constexpr int kRepl = 64;                // table replicas (one per lane)
-constexpr int kTabDwords = 256 * kRepl;  // 64 KiB per table
+constexpr int kTabDwords = 256 * 64;     // 64 KiB per table (32 copies per 256-byte entry used)
 constexpr int kTabBytes = kTabDwords * 4;
+constexpr int kTabCopies = 32;
 constexpr int kSlabBytes = 256;          // bytes of a row covered by 16 lanes x 16 B
 
 // Fills one pair table from the codebook's fp16 bits (cb16[l] = 0 for
-// l >= levels, as the Rust LUT's zeros, kernel/src/lib.rs:58-59).
+// l >= levels, as the Rust LUT's zeros, kernel/src/lib.rs:58-59): 2048
+// 16-byte stores per workgroup, the codebook reads of four at a time issued
+// together.
 template <int BITS>
 EP_DEV void build_table(uint32_t *tab, const uint16_t *cb16)
 {
-    for (int e4 = threadIdx.x; e4 < kTabDwords / 4; e4 += blockDim.x) {
-        const int b = (e4 * 4) / kRepl;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < 256 * kTabCopies / 4; i += blockDim.x) {
+        const int b = i >> 3;  // entry; (i & 7) = its 16-byte piece
         uint32_t v;
         if constexpr (BITS == 4) {
             v = (uint32_t)cb16[b & 15] | ((uint32_t)cb16[b >> 4] << 16);
@@ -33,7 +37,7 @@ EP_DEV void build_table(uint32_t *tab, const uint16_t *cb16)
             const uint32_t h = cb16[b];
             v = h | (h << 16);
         }
-        ((u32x4_t *)tab)[e4] = (u32x4_t){v, v, v, v};
+        ((u32x4_t *)tab)[b * 16 + (i & 7)] = (u32x4_t){v, v, v, v};
     }
 }
 

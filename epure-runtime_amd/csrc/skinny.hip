@@ -211,7 +211,7 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
     build_table<BITS>(tab, s_cb);
     __syncthreads();
 
-    const uint32_t lane4 = (uint32_t)lane << 2;
+    const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
 #pragma unroll
     for (int t = 0; t < kTpw; ++t) {
         const int tile = (int)blockIdx.x + t * a.gtiles;
