@@ -98,6 +98,12 @@ EP_DEV int row_exponent(float amax)
     return s;
 }
 
+// Workgroup barrier ordering LDS only: waits for this wave's LDS (and
+// scalar) operations, then s_barrier.  __syncthreads() also waits for every
+// global load and store of the wave still in flight (vmcnt), which would
+// serialize a prologue with the weight loads it is meant to overlap.
+EP_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Cross-workgroup hand-off without device-scope fences.  On gfx950 a
 // device-scope fence writes back and invalidates the whole L2 of the XCD;
 // instead, values another workgroup will read are stored and loaded as

@@ -196,12 +196,72 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
 
     u32x4_t wqA[SPW][RQ], wqB[SPW][RQ];
     float scA[SPW][RQ], scB[SPW][RQ];
-    if (blk < nblk)
-        load_block(blk, wqA, scA);  // in flight while the table and x are staged
-    // the codebook load goes out now too (its own round trip otherwise)
+    // FAST (one plain activation row, one slab per wave, one block per
+    // workgroup -- the batch-1 decode shape): every load is issued at entry,
+    // this thread's chunk of x and its codebook entry first, then the
+    // weights and their raw scale halves, all unconditionally from clamped
+    // addresses and in the global address space, so the compiler's waits
+    // count them exactly;
+    // staging and the table build then overlap the weight round trip and
+    // the scales are converted only at use (a conversion right after the
+    // load would wait for every load in flight).  Other variants hold too
+    // many registers for this and keep the plain order.
+    constexpr bool FAST = XS == XS_PLAIN && MT == 1 && SPW == 1 && !DB;
+    constexpr int XPC = (XDT == EP_F32 ? 4 : 2) * KPC / 16;  // 16-byte pieces per chunk
+    uint32_t scR[FAST ? SPW : 1][FAST ? RQ : 1][2];
+    u32x4_t xraw[FAST ? XPC : 1];
+    uint32_t cb_lo = 0, cb_hi = 0;
+    const bool sc_f32 = a.scale_dtype == EP_F32;
+    auto load_fast = [&](int b) {
+        const int row0 = b * ROWS;
+        const auto *sp = (const __attribute__((address_space(1))) uint16_t *)scale;
+#pragma unroll
+        for (int q = 0; q < RQ; ++q) {
+            const int row = row0 + 4 * q + rq;
+            const uint32_t rs = row < N ? (uint32_t)row : 0u;
+            const auto *wp = (const __attribute__((address_space(1))) u32x4_t *)(
+                packed + (rs * (uint32_t)a.row_bytes + cbyte[0]));
+#if EP_GEMV_NT_LOADS
+            wqA[0][q] = __builtin_nontemporal_load(wp);
+#else
+            wqA[0][q] = *wp;
+#endif
+        }
+        // both halves of an f32 scale, the one half (twice) of a 16-bit one:
+        // the same two loads on every path
+#pragma unroll
+        for (int q = 0; q < RQ; ++q) {
+            const int row = row0 + 4 * q + rq;
+            const uint32_t rs = row < N ? (uint32_t)row : 0u;
+            const uint32_t e = rs * (uint32_t)a.lds + (uint32_t)gidx[0];
+            scR[0][q][0] = sp[sc_f32 ? 2 * e : e];
+            scR[0][q][1] = sp[sc_f32 ? 2 * e + 1 : e];
+        }
+    };
     float cbv = 0.0f;
-    if (tid < a.levels)
-        cbv = load_as_f32(cbp, a.cb_dtype, tid);
+    if constexpr (FAST) {
+        const int xc = tid < (int)(a.K / KPC) ? tid : 0;
+        const auto *xp = (const __attribute__((address_space(1))) u32x4_t *)(
+            (const char *)a.x + (int64_t)xc * KPC * (XDT == EP_F32 ? 4 : 2));
+#pragma unroll
+        for (int p = 0; p < XPC; ++p)
+            xraw[p] = xp[p];
+        const bool cb32 = a.cb_dtype == EP_F32;
+        const uint32_t ci = (uint32_t)(tid < a.levels ? tid : a.levels - 1);
+        const auto *cp = (const __attribute__((address_space(1))) uint16_t *)cbp;
+        cb_lo = cp[cb32 ? 2 * ci : ci];
+        cb_hi = cp[cb32 ? 2 * ci + 1 : ci];
+        // the weights last: results return in order, so a load issued after
+        // them could not be used before they have all arrived
+        load_fast(blk < nblk ? blk : 0);  // a workgroup past the last block never uses it
+        __builtin_amdgcn_sched_barrier(0);  // every load goes out before any use
+    } else {
+        if (blk < nblk)
+            load_block(blk, wqA, scA);  // in flight while the table and x are staged
+        // the codebook load goes out now too (its own round trip otherwise)
+        if (tid < a.levels)
+            cbv = load_as_f32(cbp, a.cb_dtype, tid);
+    }
 
     // ---- stage activations ----------------------------------------------
     // The workgroup converts the activation row(s) once, cooperatively: one
@@ -213,10 +273,49 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     constexpr int NCH = 2 * XCAP / KPC;  // chunk slots per activation row
     const int nchunk = (int)(a.K / KPC);
     float ssq = 0.0f;
+    if constexpr (FAST) {
+        // straight-line code after the loads, run and stored by every thread
+        // (a thread past the last chunk loaded chunk 0 and writes exactly
+        // chunk 0's values again): no branch the compiler could sink the x
+        // loads into, behind the weight loads.  One chunk per thread covers
+        // the row (blockDim = 64 x slabs >= K / KPC).
+        float v[KPC];
+        if constexpr (XDT == EP_F32) {
+#pragma unroll
+            for (int p = 0; p < XPC; ++p)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    v[4 * p + t] = __uint_as_float(xraw[p][t]);
+        } else {
+#pragma unroll
+            for (int p = 0; p < XPC; ++p)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    unpack_pair<XDT>(xraw[p][t], v[8 * p + 2 * t], v[8 * p + 2 * t + 1]);
+        }
+        const int cc = tid < nchunk ? tid : 0;
+        float am = 0.0f;
+#pragma unroll
+        for (int t = 0; t < KPC; ++t)
+            am = fmaxf(am, fabsf(v[t]));
+        const int e = row_exponent(am);
+        const float pw = ldexpf(1.0f, -e);
+        uint32_t *dst = xs + cc * PAIRS;
+#pragma unroll
+        for (int p = 0; p < PAIRS; p += 4) {
+            u32x4_t q4;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                q4[t] = (uint32_t)f16_bits((f16_t)(v[2 * (p + t)] * pw)) |
+                        ((uint32_t)f16_bits((f16_t)(v[2 * (p + t) + 1] * pw)) << 16);
+            *(u32x4_t *)(dst + p) = q4;
+        }
+        xf[cc] = ldexpf(1.0f, e);
+    }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         const bool live_m = m < a.M;
-        for (int cc = tid; cc < nchunk; cc += blockDim.x) {
+        for (int cc = tid + (FAST ? (int)blockDim.x : 0); cc < nchunk; cc += blockDim.x) {
             const int64_t k0 = (int64_t)cc * KPC;
             float v[KPC];
             if constexpr (XS == XS_RMSNORM) {
@@ -289,15 +388,28 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     }
 
     // codebook -> fp16 bits in LDS, then the pair table
-    for (int i = tid; i < 256; i += blockDim.x)
-        s_cb[i] = i < a.levels ? f16_bits((f16_t)(i == tid ? cbv : load_as_f32(cbp, a.cb_dtype, i)))
-                               : 0;
+    if constexpr (FAST) {
+        cbv = a.cb_dtype == EP_F32 ? __uint_as_float(cb_lo | (cb_hi << 16))
+              : (a.cb_dtype == EP_F16 ? (float)f16_from_bits((uint16_t)cb_lo) : bf16_to_f32((uint16_t)cb_lo));
+        if (tid < 256)
+            s_cb[tid] = tid < a.levels ? f16_bits((f16_t)cbv) : 0;
+        if (blockDim.x < 256) {
+            // small workgroups load the remaining entries (the waits for
+            // these loads stay inside this branch)
+            for (int i = tid + (int)blockDim.x; i < 256; i += blockDim.x)
+                s_cb[i] = i < a.levels ? f16_bits((f16_t)load_as_f32(cbp, a.cb_dtype, i)) : 0;
+        }
+    } else {
+        for (int i = tid; i < 256; i += blockDim.x)
+            s_cb[i] = i < a.levels ? f16_bits((f16_t)(i == tid ? cbv : load_as_f32(cbp, a.cb_dtype, i)))
+                                   : 0;
+    }
     if constexpr (XS == XS_RMSNORM) {
         const float v = wave_sum_bfly(ssq);
         if (lane == 0)
             s_part[wave] = v;
     }
-    __syncthreads();
+    lds_barrier();
     build_table<BITS>(tab, s_cb);
     if constexpr (XS == XS_RMSNORM) {
         if (tid == 0) {
@@ -326,9 +438,21 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
             fexp[j][m] = act[j] ? xf[m * NCH + cc] : 0.0f;
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
+    // scale of (slab j, quad q) of the current block (0 past the row end)
+    auto scale_at = [&](int j, int q) {
+        if constexpr (FAST) {
+            const uint32_t raw = scR[0][q][0] | (scR[0][q][1] << 16);
+            const float v = sc_f32 ? __uint_as_float(raw)
+                                   : (a.scale_dtype == EP_F16 ? (float)f16_from_bits((uint16_t)raw)
+                                                              : bf16_to_f32((uint16_t)raw));
+            return (act[0] && blk * ROWS + 4 * q + rq < N) ? v : 0.0f;
+        } else {
+            return scA[j][q];
+        }
+    };
 
     for (; blk < nblk; blk += nwg) {
         const int nxt = blk + nwg;
@@ -384,7 +508,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                 }
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
-                    acc[q][m] = fmaf(part[m], scA[j][q] * fexp[j][m], acc[q][m]);
+                    acc[q][m] = fmaf(part[m], scale_at(j, q) * fexp[j][m], acc[q][m]);
             }
 
         const int row0 = blk * ROWS;
@@ -396,7 +520,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                 if (c == 0)
                     red[(wave * ROWS + 4 * q + rq) * MT + m] = v;
             }
-        __syncthreads();
+        lds_barrier();
         for (int t = tid; t < ROWS * MT; t += blockDim.x) {
             const int r = t / MT, m = t % MT;
             const int row = row0 + r;
@@ -412,7 +536,8 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                 store_from_f32(yseg, a.y_dtype, off, v);
             }
         }
-        __syncthreads();
+        if (nxt < nblk)
+            lds_barrier();  // red is reused (the last block leaves at once)
 
         if (nxt < nblk) {
             if constexpr (DB) {
@@ -423,6 +548,8 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                         wqA[j][q] = wqB[j][q];
                         scA[j][q] = scB[j][q];
                     }
+            } else if constexpr (FAST) {
+                load_fast(nxt);
             } else {
                 load_block(nxt, wqA, scA);
             }

@@ -220,7 +220,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
     s_cbraw[tid] = cbraw;
     if (tid < BM)
         s_e[tid] = 0;
-    __syncthreads();
+    lds_barrier();
     {
         float c = 0.0f;
         if (tid < a.levels) {
@@ -233,7 +233,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
         }
         // fp16 bits of the entries (past levels: 0, the Rust LUT's zeros)
         s_cb16[tid] = tid < a.levels ? f16_bits((f16_t)c) : (uint16_t)0;
-        __syncthreads();
+        lds_barrier();
         // entry t: (cb[t & 15], cb[t >> 4]) at 4 bits, cb[t] twice at 8 bits
         const uint32_t v = BITS == 4 ? ((uint32_t)s_cb16[tid & 15] | ((uint32_t)s_cb16[tid >> 4] << 16))
                                      : ((uint32_t)s_cb16[tid] | ((uint32_t)s_cb16[tid] << 16));
@@ -245,7 +245,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
     if (tid % TPR == 0 && xm < a.M)
         s_e[xr] = ex;
     store_x(xv[0], xs[0] + xr * XLD + xq * VPT);
-    __syncthreads();
+    lds_barrier();
 
     f32x16_t acc[MT][2];
 #pragma unroll

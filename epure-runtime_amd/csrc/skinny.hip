@@ -194,7 +194,7 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
         if (tid % TPR == 0)
             s_pw[xr] = ldexpf(1.0f, e);
     }
-    __syncthreads();
+    lds_barrier();
     if (tid < 256) {
         float c = 0.0f;
         if (tid < a.levels) {
@@ -207,9 +207,9 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
         }
         s_cb[tid] = f16_bits((f16_t)c);
     }
-    __syncthreads();
+    lds_barrier();
     build_table<BITS>(tab, s_cb);
-    __syncthreads();
+    lds_barrier();
 
     const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
 #pragma unroll
