@@ -208,6 +208,23 @@ int ep_dequant_tile(const uint8_t *packed, const void *scale, int scale_dtype, i
     return launch_dequant_tile(w, out, out_dtype, ldo, (hipStream_t)stream);
 }
 
+int ep_embedding_rows(const uint8_t *packed, const void *scale, int scale_dtype, int64_t ld_scale,
+                      const void *cb, int cb_dtype, int levels, int group, int64_t N, int64_t K,
+                      const int64_t *ids, int64_t n_ids, void *out, int out_dtype, int64_t ldo,
+                      void *stream)
+{
+    g_err[0] = 0;
+    PackedDesc w{packed, scale, scale_dtype, ld_scale, cb, cb_dtype, levels, group, N, K};
+    int rc = check_weight(w);
+    if (rc != EP_OK)
+        return rc;
+    if (!valid_dtype(out_dtype))
+        return set_error(EP_DECLINE_DTYPE, "out dtype %d not served", out_dtype);
+    if (n_ids < 0 || (n_ids > 0 && K > 0 && (!ids || !out || ldo < K)))
+        return set_error(EP_ERR_ARG, "bad embedding arguments");
+    return launch_embedding_rows(w, ids, n_ids, out, out_dtype, ldo, (hipStream_t)stream);
+}
+
 int ep_fused_gemv(int xsrc, const void *x, int x_dtype, const void *x_aux, float eps, int64_t K,
                   int group, int levels, int scale_dtype, int cb_dtype, int nseg,
                   const uint8_t *const *packed, const void *const *scale, const void *const *cb,

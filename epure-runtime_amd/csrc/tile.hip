@@ -8,7 +8,8 @@
 //            f16/bf16:  dtype(dtype(cb) * dtype(scale))
 //          The exact product of two fp16 (or two bf16) values fits in fp32,
 //          so computing it in fp32 and rounding once is the torch result.
-// Both read indices through the same flat-stream addressing as the GEMV
+// embedding rows: the dequant of selected rows (PackedEmbedding).
+// All read indices through the same flat-stream addressing as the GEMV
 // fallback, so odd K with 4-bit packing is covered.
 #include "ep_common.h"
 #include "ep_internal.h"
@@ -67,20 +68,39 @@ struct TileArgs {
     int64_t ldo;
 };
 
+// Element (n, k) of the dequantized weight in out_dtype's rounding.
+__device__ __forceinline__ float dequant_elem(const TileArgs &a, int64_t n, int64_t k)
+{
+    const bool four = a.levels <= 16;
+    const int64_t p = n * a.K + k;
+    const uint8_t byte = a.packed[four ? (p >> 1) : p];
+    const int idx = four ? ((p & 1) ? (byte >> 4) : (byte & 15)) : byte;
+    const float c = idx < a.levels ? load_as_f32(a.cb, a.cb_dtype, idx) : 0.0f;
+    const float s = load_as_f32(a.scale, a.scale_dtype, n * a.lds + k / a.group);
+    return round_to(a.out_dtype, c) * round_to(a.out_dtype, s);
+}
+
 __global__ void __launch_bounds__(256) dequant_tile_kernel(TileArgs a)
 {
     const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (k >= a.K)
         return;
-    const bool four = a.levels <= 16;
-    for (int64_t n = blockIdx.y; n < a.N; n += gridDim.y) {
-        const int64_t p = n * a.K + k;
-        const uint8_t byte = a.packed[four ? (p >> 1) : p];
-        const int idx = four ? ((p & 1) ? (byte >> 4) : (byte & 15)) : byte;
-        const float c = idx < a.levels ? load_as_f32(a.cb, a.cb_dtype, idx) : 0.0f;
-        const float s = load_as_f32(a.scale, a.scale_dtype, n * a.lds + k / a.group);
-        const float w = round_to(a.out_dtype, c) * round_to(a.out_dtype, s);
-        store_from_f32(a.out, a.out_dtype, n * a.ldo + k, w);
+    for (int64_t n = blockIdx.y; n < a.N; n += gridDim.y)
+        store_from_f32(a.out, a.out_dtype, n * a.ldo + k, dequant_elem(a, n, k));
+}
+
+// out[i, :] = dequantized row ids[i] (epure/runtime.py:139-156
+// PackedEmbedding.forward: only the rows a batch asks for are expanded);
+// an id outside [0, N) gives a row of zeros.
+__global__ void __launch_bounds__(256) embedding_rows_kernel(TileArgs a, const int64_t *ids, int64_t n_ids)
+{
+    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= a.K)
+        return;
+    for (int64_t i = blockIdx.y; i < n_ids; i += gridDim.y) {
+        const int64_t n = ids[i];
+        const float w = (n >= 0 && n < a.N) ? dequant_elem(a, n, k) : 0.0f;
+        store_from_f32(a.out, a.out_dtype, i * a.ldo + k, w);
     }
 }
 
@@ -107,6 +127,19 @@ int launch_dequant_tile(const PackedDesc &w, void *out, int out_dtype, int64_t l
                w.group, w.N, w.K, out, out_dtype, ldo};
     dim3 grid((unsigned)((w.K + 255) / 256), (unsigned)(w.N < 65535 ? w.N : 65535));
     hipLaunchKernelGGL(dequant_tile_kernel, grid, dim3(256), 0, stream, a);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+int launch_embedding_rows(const PackedDesc &w, const int64_t *ids, int64_t n_ids, void *out,
+                          int out_dtype, int64_t ldo, hipStream_t stream)
+{
+    if (n_ids <= 0 || w.K <= 0)
+        return EP_OK;
+    TileArgs a{w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
+               w.group, w.N, w.K, out, out_dtype, ldo};
+    dim3 grid((unsigned)((w.K + 255) / 256), (unsigned)(n_ids < 65535 ? n_ids : 65535));
+    hipLaunchKernelGGL(embedding_rows_kernel, grid, dim3(256), 0, stream, a, ids, n_ids);
     EP_HIP_CHECK(hipGetLastError());
     return EP_OK;
 }

@@ -2,7 +2,7 @@
 packed linear, on hand-written gfx950 HIP kernels.
 
 Public names follow the reference package (epure/__init__.py:31-37) for the
-parts this build covers: the packed store and linear, the fine-tuning
+parts this build covers: the packed store, linear and embedding, the fine-tuning
 helpers, and the ``epure.kernels`` backend contract.
 """
 from .finetune import (
@@ -13,12 +13,12 @@ from .finetune import (
     trainable_forward,
     verify_frozen,
 )
-from .runtime import PackedLinear, PackedWeight, apply_packed
+from .runtime import PackedEmbedding, PackedLinear, PackedWeight, apply_packed, tie_packed_lm_head
 
 __version__ = "0.2.4+mi355x"
 
 __all__ = [
-    "PackedWeight", "PackedLinear", "apply_packed",
+    "PackedWeight", "PackedLinear", "PackedEmbedding", "apply_packed", "tie_packed_lm_head",
     "make_trainable", "packed_weights", "snapshot_indices", "verify_frozen",
     "trainable_forward", "ScaleTuner",
     "__version__",

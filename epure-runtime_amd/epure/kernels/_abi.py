@@ -48,6 +48,9 @@ _SIGS = {
     "ep_dequant_tile": (_c_int, [
         _p, _p, _c_int, _c_i64, _p, _c_int, _c_int, _c_int, _c_i64, _c_i64,
         _p, _c_int, _c_i64, _p]),
+    "ep_embedding_rows": (_c_int, [
+        _p, _p, _c_int, _c_i64, _p, _c_int, _c_int, _c_int, _c_i64, _c_i64,
+        _p, _c_i64, _p, _c_int, _c_i64, _p]),
     # include/epure_decode.h
     "ep_fused_gemv": (_c_int, [
         _c_int, _p, _c_int, _p, ctypes.c_float,  # xsrc, x, x_dtype, x_aux, eps

@@ -1,11 +1,12 @@
 """Packed store and packed linear -- the caller side of the fused kernels.
 
 Mirrors the reference's resident representation and dispatch
-(epure/runtime.py:34-126): ``PackedWeight`` owns ``packed`` / ``scale`` /
+(epure/runtime.py:34-160): ``PackedWeight`` owns ``packed`` / ``scale`` /
 ``cb`` buffers, ``PackedLinear.forward`` hands the call to a backend and
-materializes when the backend declines.  Only what the packed-linear path
-needs is here; the ``.ebin`` loader, embeddings and MoE holders are outside
-this build.
+materializes when the backend declines, ``PackedEmbedding`` expands only the
+rows a batch asks for, and ``tie_packed_lm_head`` runs a tied lm_head through
+the packed linear (runtime.py:289-300).  The ``.ebin`` loader and MoE holders
+are outside this build.
 """
 import os
 
@@ -134,6 +135,84 @@ class PackedLinear(nn.Module):
         out = F.linear(x, w, self.bias)
         del w
         return out
+
+
+class PackedEmbedding(nn.Module):
+    """Embedding over a ``PackedWeight``: expands only the requested rows
+    (runtime.py:129-160).
+
+    ``forward(ids)`` returns ``[*ids.shape, in_features]`` in ``dtype`` with
+    the reference's rounding, ``dtype(cb[idx]) * dtype(scale)`` per group --
+    the rows of ``materialize(dtype)``.  On a gfx950 device the rows are
+    expanded by the library's ``ep_embedding_rows`` kernel; CPU tensors take
+    the reference's torch expression.  Ids outside ``[0, num_embeddings)``
+    raise ``IndexError`` (checked on the host outside graph capture; a
+    captured call writes zero rows for them).
+    """
+
+    def __init__(self, store, dtype=torch.float16):
+        super().__init__()
+        self.store = store
+        self.dtype = dtype
+        self.num_embeddings = store.out_features
+        self.embedding_dim = store.in_features
+
+    def forward(self, ids):
+        s = self.store
+        flat = ids.reshape(-1)
+        n_in = s.in_features
+        if (flat.is_cuda and s.packed.is_cuda and cuda_kernel.available()
+                and self.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+            h = cuda_kernel._hot(s)
+            if not h.usable():
+                raise RuntimeError("PackedEmbedding: store buffers are not contiguous")
+            flat = flat.to(torch.int64).contiguous()
+            if flat.numel() and not torch.cuda.is_current_stream_capturing():
+                lo, hi = int(flat.min()), int(flat.max())
+                if lo < 0 or hi >= self.num_embeddings:
+                    raise IndexError(f"embedding id out of range [0, {self.num_embeddings}): "
+                                     f"{lo if lo < 0 else hi}")
+            out = torch.empty((flat.numel(), n_in), dtype=self.dtype, device=flat.device)
+            rc = _abi.lib.ep_embedding_rows(
+                h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+                h.cb.data_ptr(), h.cb_dt, h.levels, h.group, h.N, h.K,
+                flat.data_ptr(), flat.numel(), out.data_ptr(), _abi.dtype_code(self.dtype),
+                out.stride(0), _abi.stream_handle(flat.device))
+            _abi.check(rc, "ep_embedding_rows")
+            return out.view(*ids.shape, n_in)
+        if flat.numel() and (int(flat.min()) < 0 or int(flat.max()) >= self.num_embeddings):
+            raise IndexError(f"embedding id out of range [0, {self.num_embeddings})")
+        if s.levels > 16:
+            idx = s.packed.view(self.num_embeddings, n_in)[flat].to(torch.long)
+        else:
+            rows = s.packed.view(self.num_embeddings, n_in // 2)[flat]
+            lo, hi = (rows & 0x0F).to(torch.long), (rows >> 4).to(torch.long)
+            idx = torch.empty(flat.numel(), n_in, dtype=torch.long, device=lo.device)
+            idx[:, 0::2], idx[:, 1::2] = lo, hi
+        cbt = torch.zeros(256, dtype=s.cb.dtype, device=s.cb.device)
+        cbt[:s.cb.numel()] = s.cb.reshape(-1)  # indices >= levels read 0 (lib.rs:58-59)
+        w = cbt[idx].to(self.dtype)
+        sc = s.scale[flat].to(self.dtype)
+        for gi, start in enumerate(range(0, n_in, s.group)):
+            end = min(start + s.group, n_in)
+            w[:, start:end] *= sc[:, gi:gi + 1]
+        return w.view(*ids.shape, n_in)
+
+    @property
+    def weight(self):
+        return self.store.materialize(self.dtype)
+
+
+def tie_packed_lm_head(model, embed_store):
+    """Run a tied lm_head through the packed embedding store
+    (runtime.py:289-300): ``model.lm_head = PackedLinear(embed_store)`` and
+    the config's ``tie_word_embeddings`` cleared, so a later
+    ``tie_weights()`` does not look for a dense embedding Parameter."""
+    model.lm_head = PackedLinear(embed_store)
+    cfg = getattr(model, "config", None)
+    if cfg is not None and getattr(cfg, "tie_word_embeddings", False):
+        cfg.tie_word_embeddings = False
+    return model
 
 
 def apply_packed(model, stores):

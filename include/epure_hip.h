@@ -131,6 +131,19 @@ int ep_dequant_tile(const uint8_t *packed, const void *scale, int scale_dtype,
                     int group, int64_t N, int64_t K, void *out, int out_dtype,
                     int64_t ldo, void *stream);
 
+/*
+ * out[i, 0..K) = row ids[i] of the dequantized weight (same rounding as
+ * ep_dequant_tile), for i < n_ids: the packed embedding lookup that expands
+ * only the rows a batch asks for (epure/runtime.py:129-156,
+ * PackedEmbedding.forward; the reference gathers, unpacks and multiplies
+ * with torch ops).  An id outside [0, N) gives a row of zeros (the caller
+ * checks ranges where it can raise, as torch indexing does).
+ */
+int ep_embedding_rows(const uint8_t *packed, const void *scale, int scale_dtype,
+                      int64_t ld_scale, const void *cb, int cb_dtype, int levels,
+                      int group, int64_t N, int64_t K, const int64_t *ids, int64_t n_ids,
+                      void *out, int out_dtype, int64_t ldo, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

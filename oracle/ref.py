@@ -14,6 +14,8 @@ packed_2d                  epure/runtime.py:73-76                shape/stride id
 dequant_tile_f32           epure/container.py:70-88,             pure-Python double product rounded once
                            lib.rs:36-40 (LUT), runtime.py:78-89  to f32 (exact for fp16-valued inputs)
 materialize                epure/runtime.py:78-89                torch CPU of the same expression
+embedding_rows             epure/runtime.py:139-156              == materialize(dtype)[ids] (a second route),
+                                                                 pure-Python brute force on a tiny store
 rust_dequant_matmul        kernel/src/lib.rs:36-151              bit-exact vs oracle/rowdot.c, fp64 bound,
                                                                  single-term and power-of-two closed forms
 linear_f64                 (mathematics)                         itself the brute force
@@ -132,6 +134,37 @@ def materialize(packed, scale, cb, out_features, in_features, group, levels, dty
         w = dequant_tile_f32(idx, s, c, group)
         return round_bf16(w)
     raise ValueError(dtype)
+
+
+def embedding_rows(packed, scale, cb, out_features, in_features, group, levels, ids,
+                   dtype="f16"):
+    """runtime.py:139-156 PackedEmbedding.forward: for each id, that row's
+    indices (positions id * K .. id * K + K - 1 of the flat stream), the
+    codebook entries and the row's group scales each rounded to ``dtype``,
+    their product rounded to ``dtype`` (an index >= levels reads 0, as the
+    Rust LUT).  Only the requested rows are unpacked.  Returns float32
+    values [len(ids), K]."""
+    k = in_features
+    packed = np.ascontiguousarray(packed, dtype=np.uint8).ravel()
+    cbf = np.zeros(256, np.float32)
+    cbv = np.asarray(cb, np.float32).ravel()
+    cbf[:cbv.size] = cbv
+    sc = np.asarray(scale, np.float32).reshape(out_features, -1)
+    rnd = {"f32": lambda a: a.astype(np.float32),
+           "f16": lambda a: a.astype(np.float16).astype(np.float32),
+           "bf16": round_bf16}[dtype]
+    out = np.empty((len(ids), k), np.float32)
+    pos = np.arange(k, dtype=np.int64)
+    for i, r in enumerate(np.asarray(ids, np.int64).ravel()):
+        p = int(r) * k + pos
+        if levels > 16:
+            idx = packed[p]
+        else:
+            b = packed[p >> 1]
+            idx = np.where(p & 1, b >> 4, b & 0x0F)
+        w = rnd(cbf[idx]) * rnd(sc[int(r), pos // group])
+        out[i] = rnd(w)
+    return out
 
 
 # ---------------------------------------------------------------- forward

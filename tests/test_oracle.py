@@ -83,6 +83,37 @@ def test_materialize_matches_torch_expression(dtype):
     assert np.array_equal(got, w.float().numpy())
 
 
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("levels,k", [(16, 256), (16, 37), (256, 96), (12, 64)])
+def test_embedding_rows_are_materialize_rows(dtype, levels, k):
+    # PackedEmbedding (runtime.py:139-156) and materialize (runtime.py:78-89)
+    # apply the same per-element rounding; the oracle computes them by two
+    # routes (row gather of the flat stream vs whole-matrix unpack)
+    n = 50
+    idx = rng(20).integers(0, 16 if levels == 12 else levels, (n, k)).astype(np.uint8)
+    packed = ref.pack4(idx.ravel(), levels)
+    cb = rng(21).standard_normal(levels).astype(np.float32)
+    scale = (np.abs(rng(22).standard_normal((n, -(-k // 32)))) * 0.02 + 1e-3).astype(np.float32)
+    ids = np.array([0, 49, 7, 7, 23, 1], np.int64)
+    got = ref.embedding_rows(packed, scale, cb, n, k, 32, levels, ids, dtype)
+    full = ref.materialize(packed, scale, cb, n, k, 32, levels, dtype)
+    assert np.array_equal(got, full[ids])
+
+
+def test_embedding_rows_brute_force():
+    n, k, levels, group = 6, 10, 16, 4
+    idx = rng(23).integers(0, 16, (n, k)).astype(np.uint8)
+    packed = ref.pack4(idx.ravel(), levels)
+    cb = rng(24).standard_normal(levels).astype(np.float32)
+    scale = rng(25).uniform(0.5, 2.0, (n, 3)).astype(np.float32)
+    got = ref.embedding_rows(packed, scale, cb, n, k, group, levels, [5, 2], "f16")
+    for i, r in enumerate([5, 2]):
+        for c in range(k):
+            a = np.float16(cb[idx[r, c]])
+            b = np.float16(scale[r, c // group])
+            assert got[i, c] == np.float32(np.float16(np.float32(a) * np.float32(b)))
+
+
 def test_bf16_rounding_matches_torch():
     x = rng(6).standard_normal(10000).astype(np.float32) * 1000
     x[:4] = [np.inf, -np.inf, 0.0, -0.0]

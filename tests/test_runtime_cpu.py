@@ -71,3 +71,38 @@ def test_finetune_index_freeze_cycle():
 def test_make_trainable_rejects_mode():
     with pytest.raises(ValueError):
         make_trainable(torch.nn.Sequential(), "nope")
+
+
+@pytest.mark.parametrize("dtype,name", [(torch.float32, "f32"), (torch.float16, "f16"),
+                                        (torch.bfloat16, "bf16")])
+@pytest.mark.parametrize("levels", [16, 256])
+def test_packed_embedding_cpu_matches_oracle(dtype, name, levels):
+    # the reference's torch expression (runtime.py:139-156) on CPU tensors
+    idx, packed, scale, cb = ref.synth_linear(40, 128, levels, 32, seed=levels)
+    s = PackedWeight((40, 128), packed, scale, cb.astype(np.float32), 32, levels)
+    ids = torch.tensor([[3, 39], [0, 3]])
+    out = runtime.PackedEmbedding(s, dtype)(ids)
+    assert out.shape == (2, 2, 128) and out.dtype == dtype
+    want = ref.embedding_rows(packed, scale.astype(np.float32), cb, 40, 128, 32, levels,
+                              ids.numpy().ravel(), name)
+    assert np.array_equal(out.float().numpy().reshape(-1, 128), want)
+
+
+def test_packed_embedding_cpu_rejects_out_of_range():
+    _, s = store(n=8, k=64)
+    with pytest.raises(IndexError):
+        runtime.PackedEmbedding(s)(torch.tensor([8]))
+
+
+def test_tie_packed_lm_head_replaces_module_and_clears_flag():
+    _, s = store(n=32, k=64)
+
+    class M(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.config = type("C", (), {"tie_word_embeddings": True})()
+            self.lm_head = torch.nn.Linear(64, 32, bias=False)
+
+    m = runtime.tie_packed_lm_head(M(), s)
+    assert isinstance(m.lm_head, PackedLinear) and m.lm_head.store is s
+    assert m.config.tie_word_embeddings is False
