@@ -20,9 +20,10 @@
 //  * dequantization is one LDS lookup per packed byte in a 256-entry table
 //    replicated 32 times (lane & 31 reads its own copy: no bank conflicts),
 //    then the group scale is applied in fp16 (v_pk_mul_f16);
-//  * activations are converted to fp16 after the exact per-row power-of-two
-//    rescale of a pre-kernel (pf_rowexp_kernel) and staged in LDS, double
-//    buffered: step k + 1 is stored while step k is multiplied;
+//  * activations are converted once to fp16 after the exact per-row
+//    power-of-two rescale by a pre-kernel (pf_prep_kernel, into the
+//    workspace) and staged in LDS as they are, double buffered: step k + 1
+//    is stored while step k is multiplied;
 //  * weight loads run PD steps ahead in registers (buffer loads: a row past
 //    N or a step past K reads zeros without touching memory);
 //  * when the grid of (N / 256) x (M / BM) workgroups cannot fill the device,
@@ -76,10 +77,13 @@ EP_DEV __amdgpu_buffer_rsrc_t pf_rsrc(const void *p, uint32_t bytes)
                                              (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 
-// Per-row exponent of the largest |x| (row_exponent): one wave per row,
-// 16-byte loads, four in flight per lane.
+// Per-row exponent of the largest |x| (row_exponent), then the row rescaled
+// by 2^-e and rounded to fp16 into xh [M][K] (one wave per row, 16-byte
+// loads, four in flight per lane; the second pass re-reads the row from the
+// caches).  Converting once here saves the main kernel a conversion per
+// N tile.
 __global__ void __launch_bounds__(256)
-    pf_rowexp_kernel(const void *x, int xdt, int64_t ldx, int M, int K, int *rexp)
+    pf_prep_kernel(const void *x, int xdt, int64_t ldx, int M, int K, int *rexp, f16_t *xh)
 {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -115,18 +119,48 @@ __global__ void __launch_bounds__(256)
             }
     }
     amax = wave_max(amax);
+    const int e = row_exponent(amax);
     if (lane == 0)
-        rexp[row] = row_exponent(amax);
+        rexp[row] = e;
+    const float pw = ldexpf(1.0f, -e);
+    // output pieces of 8 values: 16 input bytes (2-byte types) or 32 (f32)
+    f16x8_t *dst = (f16x8_t *)(xh + (int64_t)row * K);
+    for (int q = lane; q < K / 8; q += 64) {
+        float v[8];
+        if (xdt == EP_F32) {
+            const u32x4_t a0 = *(const __attribute__((address_space(1))) u32x4_t *)(base + (int64_t)q * 32);
+            const u32x4_t a1 = *(const __attribute__((address_space(1))) u32x4_t *)(base + (int64_t)q * 32 + 16);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                v[t] = __uint_as_float(a0[t]);
+                v[4 + t] = __uint_as_float(a1[t]);
+            }
+        } else {
+            const u32x4_t a0 = *(const __attribute__((address_space(1))) u32x4_t *)(base + (int64_t)q * 16);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                if (xdt == EP_BF16)
+                    unpack_pair<EP_BF16>(a0[t], v[2 * t], v[2 * t + 1]);
+                else
+                    unpack_pair<EP_F16>(a0[t], v[2 * t], v[2 * t + 1]);
+            }
+        }
+        f16x8_t h;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            h[t] = (f16_t)(v[t] * pw);
+        dst[q] = h;
+    }
 }
 
-template <int BITS, int BM, int XDT, int PD>
+template <int BITS, int BM, int PD>
 __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
 {
     constexpr int MT = BM / 32;                  // 32-row M tiles per wave
     constexpr int XLD = kPfBK + 8;               // halfs per staged activation row
     constexpr int TPR = kPfThreads / BM;         // staging threads per activation row
     constexpr int VPT = kPfBK / TPR;             // values per staging thread and step
-    constexpr int XE = XDT == EP_F32 ? 4 : 2;
+    constexpr int XE = 2;  // activations: fp16, pre-scaled per row (pf_prep_kernel)
     constexpr int XP = VPT * XE / 16;            // 16-byte pieces per staging thread
     constexpr int WL = BITS == 4 ? 1 : 2;        // 16-byte weight loads per lane, N tile and step
     constexpr int NB = (PD > 2 ? PD : 2) + 1;    // register sets (weights PD, activations 2 steps ahead)
@@ -192,28 +226,10 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
         issue_w(kt0 + d, wb[d], sb[d]);
     __builtin_amdgcn_sched_barrier(0);
 
-    const float pw = ldexpf(1.0f, -ex);
     auto store_x = [&](const u32x4_t (&v4)[XP], f16_t *dst) {
 #pragma unroll
-        for (int p = 0; p < VPT / 8; ++p) {
-            f16x8_t hv;
-            if constexpr (XDT == EP_F32) {
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    hv[t] = (f16_t)(__uint_as_float(v4[2 * p][t]) * pw);
-                    hv[4 + t] = (f16_t)(__uint_as_float(v4[2 * p + 1][t]) * pw);
-                }
-            } else {
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float lo, hi;
-                    unpack_pair<XDT>(v4[p][t], lo, hi);
-                    hv[2 * t] = (f16_t)(lo * pw);
-                    hv[2 * t + 1] = (f16_t)(hi * pw);
-                }
-            }
-            *(f16x8_t *)(dst + 8 * p) = hv;
-        }
+        for (int p = 0; p < XP; ++p)
+            *(u32x4_t *)(dst + 8 * p) = v4[p];
     };
 
     // codebook -> fp16 -> the replicated table; step 0's activations -> LDS
@@ -381,20 +397,10 @@ PfPlan pf_plan(int bits, int64_t M, int64_t N, int64_t K)
 }
 
 template <int BITS, int BM, int PD>
-int pf_launch_x(const PfArgs &a, const PfPlan &p, int xdt, hipStream_t s)
+int pf_launch(const PfArgs &a, const PfPlan &p, hipStream_t s)
 {
     const dim3 grid((unsigned)((a.N + kPfBN - 1) / kPfBN), (unsigned)((a.M + BM - 1) / BM), (unsigned)p.S);
-    switch (xdt) {
-    case EP_BF16:
-        hipLaunchKernelGGL((pf_kernel<BITS, BM, EP_BF16, PD>), grid, dim3(kPfThreads), 0, s, a);
-        break;
-    case EP_F16:
-        hipLaunchKernelGGL((pf_kernel<BITS, BM, EP_F16, PD>), grid, dim3(kPfThreads), 0, s, a);
-        break;
-    default:
-        hipLaunchKernelGGL((pf_kernel<BITS, BM, EP_F32, PD>), grid, dim3(kPfThreads), 0, s, a);
-        break;
-    }
+    hipLaunchKernelGGL((pf_kernel<BITS, BM, PD>), grid, dim3(kPfThreads), 0, s, a);
     EP_HIP_CHECK(hipGetLastError());
     return EP_OK;
 }
@@ -418,11 +424,13 @@ bool prefill_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
     return (x.ld * esz) % 16 == 0;
 }
 
+// Workspace: row exponents, the fp16 activations, then the split partials.
 size_t prefill_workspace(int64_t M, int64_t N, int64_t K, int levels)
 {
     const PfPlan p = pf_plan(levels <= 16 ? 4 : 8, M, N, K);
     const size_t ex = (size_t)((M * 4 + 255) / 256 * 256);
-    return ex + (p.S > 1 ? (size_t)p.S * (size_t)M * (size_t)N * sizeof(float) : 0);
+    const size_t xh = (size_t)((M * K * 2 + 255) / 256 * 256);
+    return ex + xh + (p.S > 1 ? (size_t)p.S * (size_t)M * (size_t)N * sizeof(float) : 0);
 }
 
 int launch_prefill(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y, void *ws,
@@ -434,21 +442,22 @@ int launch_prefill(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDe
     const PfPlan p = pf_plan(bits, M, w.N, w.K);
     const bool partials = p.S > 1;
     const size_t ex = (size_t)((M * 4 + 255) / 256 * 256);
-    const size_t need = ex + (partials ? (size_t)p.S * (size_t)M * (size_t)w.N * sizeof(float) : 0);
+    const size_t xhb = (size_t)((M * w.K * 2 + 255) / 256 * 256);
+    const size_t need = ex + xhb + (partials ? (size_t)p.S * (size_t)M * (size_t)w.N * sizeof(float) : 0);
     if (!ws || ws_bytes < need)
         return set_error(EP_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws_bytes);
     int *rexp = (int *)ws;
-    hipLaunchKernelGGL(pf_rowexp_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream, x.ptr, x.dtype,
-                       x.ld, (int)M, (int)w.K, rexp);
+    f16_t *xh = (f16_t *)((char *)ws + ex);
+    hipLaunchKernelGGL(pf_prep_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream, x.ptr, x.dtype,
+                       x.ld, (int)M, (int)w.K, rexp, xh);
     EP_HIP_CHECK(hipGetLastError());
     PfArgs a{};
-    const int esz = x.dtype == EP_F32 ? 4 : 2;
-    a.xbytes = (uint32_t)(((M - 1) * x.ld + w.K) * esz);
+    a.xbytes = (uint32_t)(M * w.K * 2);
     a.wbytes = (uint32_t)(w.N * (bits == 4 ? w.K / 2 : w.K));
     a.sbytes = (uint32_t)(((w.N - 1) * w.ld_scale + (w.K + w.group - 1) / w.group) * 2);
     a.cbbytes = (uint32_t)(w.levels * (w.cb_dtype == EP_F32 ? 4 : 2));
-    a.x = x.ptr;
-    a.ldx = x.ld;
+    a.x = xh;
+    a.ldx = w.K;
     a.M = (int)M;
     a.packed = w.packed;
     a.row_bytes = (uint32_t)(bits == 4 ? w.K / 2 : w.K);
@@ -466,12 +475,12 @@ int launch_prefill(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDe
     a.y_dtype = y.dtype;
     a.ldy = y.ld;
     a.accumulate = y.accumulate;
-    a.part = partials ? (float *)((char *)ws + ex) : nullptr;
+    a.part = partials ? (float *)((char *)ws + ex + xhb) : nullptr;
     int rc;
     if (bits == 4)
-        rc = p.bm == 128 ? pf_launch_x<4, 128, 2>(a, p, x.dtype, stream) : pf_launch_x<4, 64, 4>(a, p, x.dtype, stream);
+        rc = p.bm == 128 ? pf_launch<4, 128, 2>(a, p, stream) : pf_launch<4, 64, 4>(a, p, stream);
     else
-        rc = pf_launch_x<8, 64, 3>(a, p, x.dtype, stream);
+        rc = pf_launch<8, 64, 3>(a, p, stream);
     if (rc != EP_OK || !partials)
         return rc;
     return launch_split_reduce(a.part, p.S, M, w.N, y, stream);
