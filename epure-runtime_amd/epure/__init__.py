@@ -13,12 +13,21 @@ from .finetune import (
     trainable_forward,
     verify_frozen,
 )
-from .runtime import PackedEmbedding, PackedLinear, PackedWeight, apply_packed, tie_packed_lm_head
+from .runtime import (
+    ExpertHolder,
+    PackedEmbedding,
+    PackedExperts,
+    PackedLinear,
+    PackedWeight,
+    apply_packed,
+    tie_packed_lm_head,
+)
 
 __version__ = "0.2.4+mi355x"
 
 __all__ = [
-    "PackedWeight", "PackedLinear", "PackedEmbedding", "apply_packed", "tie_packed_lm_head",
+    "PackedWeight", "PackedLinear", "PackedEmbedding", "PackedExperts", "ExpertHolder",
+    "apply_packed", "tie_packed_lm_head",
     "make_trainable", "packed_weights", "snapshot_indices", "verify_frozen",
     "trainable_forward", "ScaleTuner",
     "__version__",

@@ -4,9 +4,11 @@ Mirrors the reference's resident representation and dispatch
 (epure/runtime.py:34-160): ``PackedWeight`` owns ``packed`` / ``scale`` /
 ``cb`` buffers, ``PackedLinear.forward`` hands the call to a backend and
 materializes when the backend declines, ``PackedEmbedding`` expands only the
-rows a batch asks for, and ``tie_packed_lm_head`` runs a tied lm_head through
-the packed linear (runtime.py:289-300).  The ``.ebin`` loader and MoE holders
-are outside this build.
+rows a batch asks for, ``tie_packed_lm_head`` runs a tied lm_head through
+the packed linear (runtime.py:289-300), ``ExpertHolder`` keeps a stacked
+expert slab packed between calls (runtime.py:163-186) and ``PackedExperts``
+runs expert-indexed linears without expanding the slab.  The ``.ebin``
+loader is outside this build.
 """
 import os
 
@@ -201,6 +203,93 @@ class PackedEmbedding(nn.Module):
     @property
     def weight(self):
         return self.store.materialize(self.dtype)
+
+
+class ExpertHolder:
+    """Keeps a stacked expert slab packed except while its module runs
+    (runtime.py:163-186): a forward pre-hook attaches ``materialize(dtype)``
+    as ``mod.<attr>`` (on a gfx950 device the library's dequant kernel), a
+    forward hook drops it again."""
+
+    def __init__(self, mod, attr, store, dtype=torch.float16):
+        self.mod, self.attr, self.store = mod, attr, store
+        self.dtype = dtype
+        if attr in mod._parameters:
+            del mod._parameters[attr]
+        mod.register_forward_pre_hook(self._attach)
+        mod.register_forward_hook(self._release)
+        setattr(mod, attr, None)
+
+    def _attach(self, mod, _a):
+        setattr(mod, self.attr, self.store.materialize(self.dtype))
+
+    def _release(self, mod, _a, _o):
+        setattr(mod, self.attr, None)
+
+
+class PackedExperts(nn.Module):
+    """Expert-indexed linear over a stacked ``(E, N, K)`` store, kept packed.
+
+    ``forward(x, expert_ids)`` returns ``y[t] = x[t] @ W[expert_ids[t]]^T``
+    (``[T, N]`` in ``x.dtype``): the rows of one expert are a contiguous row
+    range of the folded store (``out_features = E * N``, runtime.py:64-68),
+    so each expert's tokens run the packed linear on that range -- the
+    batch-1 GEMV, the small-M or the MFMA path by their count -- without
+    expanding any expert (the reference's holder materializes the whole
+    slab per call, runtime.py:163-186).  GPU tensors only.
+    """
+
+    def __init__(self, store):
+        super().__init__()
+        if len(store.shape) != 3:
+            raise ValueError(f"expert store must be (E, N, K), got {store.shape}")
+        self.store = store
+        self.num_experts, self.out_features, self.in_features = store.shape
+
+    def forward(self, x, expert_ids):
+        s = self.store
+        K, N = self.in_features, self.out_features
+        x2 = x.reshape(-1, K)
+        ids = expert_ids.reshape(-1).to(torch.int64)
+        if ids.numel() != x2.shape[0]:
+            raise ValueError("one expert id per row of x")
+        if not (x2.is_cuda and cuda_kernel.available()):
+            raise RuntimeError("PackedExperts runs on the gfx950 backend only")
+        out = torch.empty((x2.shape[0], N), dtype=x2.dtype, device=x2.device)
+        if ids.numel() == 0:
+            return out
+        order = torch.argsort(ids, stable=True)
+        experts, counts = torch.unique_consecutive(ids[order], return_counts=True)
+        experts, counts = experts.tolist(), counts.tolist()
+        if experts[0] < 0 or experts[-1] >= self.num_experts:
+            raise IndexError(f"expert id out of range [0, {self.num_experts})")
+        h = cuda_kernel._hot(s)
+        if not h.usable():
+            raise RuntimeError("PackedExperts: store buffers are not contiguous")
+        row_bytes = K if s.levels > 16 else K // 2
+        if s.levels <= 16 and K % 2:
+            raise ValueError("4-bit expert rows need an even K")
+        esz = h.scale.element_size()
+        start = 0
+        for e, c in zip(experts, counts):
+            rows = order[start:start + c]
+            start += c
+            xe = x2.index_select(0, rows).contiguous()
+            ye = torch.empty((c, N), dtype=x2.dtype, device=x2.device)
+            ws_bytes = _abi.lib.ep_dequant_matmul_workspace(c, N, K, h.levels, h.group)
+            ws = torch.empty(ws_bytes, device=x2.device, dtype=torch.uint8) if ws_bytes else None
+            rc = _abi.lib.ep_dequant_matmul(
+                xe.data_ptr(), _abi.dtype_code(xe.dtype), xe.stride(0),
+                h.packed.data_ptr() + e * N * row_bytes,
+                h.scale.data_ptr() + e * N * h.ld_scale * esz, h.scale_dt, h.ld_scale,
+                h.cb.data_ptr(), h.cb_dt, h.levels, h.group,
+                c, N, K, ye.data_ptr(), _abi.dtype_code(ye.dtype), ye.stride(0), 0,
+                ws.data_ptr() if ws is not None else None, ws_bytes,
+                _abi.stream_handle(x2.device))
+            if not _abi.check(rc, "ep_dequant_matmul"):
+                raise RuntimeError(f"PackedExperts: shape declined: {_abi.last_error()}")
+            out.index_copy_(0, rows, ye)
+        return out
 
 
 def tie_packed_lm_head(model, embed_store):

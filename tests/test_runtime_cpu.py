@@ -106,3 +106,28 @@ def test_tie_packed_lm_head_replaces_module_and_clears_flag():
     m = runtime.tie_packed_lm_head(M(), s)
     assert isinstance(m.lm_head, PackedLinear) and m.lm_head.store is s
     assert m.config.tie_word_embeddings is False
+
+
+def test_expert_holder_cpu_and_packed_experts_shape_checks():
+    idx, packed, scale, cb = ref.synth_linear(3 * 8, 64, 16, 32, seed=9)
+    s = PackedWeight((3, 8, 64), packed, scale, cb.astype(np.float32), 32, 16)
+
+    class Moe(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.w = torch.nn.Parameter(torch.zeros(3, 8, 64))
+
+        def forward(self, x):
+            return self.w.sum() + x
+
+    m = Moe()
+    runtime.ExpertHolder(m, "w", s, torch.float32)
+    assert m.w is None
+    out = m(torch.zeros(1))
+    want = ref.materialize(packed, scale, cb, 24, 64, 32, 16, "f32").sum()
+    assert abs(float(out) - float(want)) < 1e-3 * max(1.0, abs(float(want)))
+    assert m.w is None
+    with pytest.raises(ValueError):
+        runtime.PackedExperts(PackedWeight((24, 64), packed, scale, cb, 32, 16))
+    with pytest.raises(RuntimeError):
+        runtime.PackedExperts(s)(torch.zeros(2, 64), torch.tensor([0, 1]))
