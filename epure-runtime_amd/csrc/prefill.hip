@@ -7,11 +7,14 @@
 // (runtime.py:78-89): the weight enters the product as fp16(fp16(cb) * fp16(scale)).
 //
 // Layout of the work (v_mfma_f32_32x32x16_f16):
-//  * a workgroup is 4 waves and covers 256 weight rows x BM activation rows;
-//    each wave owns 64 weight rows (two 32-row N tiles) and all BM rows, so
-//    every weight is dequantized exactly once per workgroup, in registers,
-//    straight into the B operand -- the dense weight never reaches LDS or
-//    global memory;
+//  * a workgroup is 4 waves and covers 4 x 32 NT weight rows x BM activation
+//    rows; each wave owns NT 32-row N tiles and all BM rows, so every weight
+//    is dequantized exactly once per workgroup, in registers, straight into
+//    the B operand -- the dense weight never reaches LDS or global memory.
+//    Dequantization is the VALU-heavy part, so the MFMAs per dequantized
+//    weight (BM / 32) set the pace: 8-bit at M >= 256 runs BM = 128 with one
+//    N tile per wave (64 accumulators; two N tiles would not fit 256 VGPRs),
+//    ~1.25x the 64 x 2-tile layout;
 //  * lane (j = lane & 31, h = lane >> 5) of a wave holds, per 64-k step and
 //    N tile, 32 consecutive weights of row j (k = 32 h .. 32 h + 31 of the
 //    step: one 16-byte load at 4 bits, two at 8 bits); MFMA sub-step s takes
@@ -39,7 +42,7 @@ namespace ep {
 namespace {
 
 constexpr int kPfThreads = 256;        // 4 waves
-constexpr int kPfBN = 256;             // weight rows per workgroup (64 per wave)
+constexpr int kPfWaves = 4;            // waves per workgroup, 32 * NT weight rows each
 constexpr int kPfBK = 64;              // k per step
 constexpr int kPfCopies = 32;          // LDS table replicas
 constexpr uint32_t kPfOut = 0x7ffffff0u;  // a buffer offset past every buffer's end
@@ -153,7 +156,7 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-template <int BITS, int BM, int PD>
+template <int BITS, int BM, int PD, int NT>
 __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
 {
     constexpr int MT = BM / 32;                  // 32-row M tiles per wave
@@ -176,7 +179,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, h = lane >> 5;
-    const int nw = blockIdx.x * kPfBN + wave * 64;  // the wave's first weight row
+    const int nw = blockIdx.x * (kPfWaves * 32 * NT) + wave * (32 * NT);  // the wave's first weight row
     const int m0 = blockIdx.y * BM;
     const int kt0 = blockIdx.z * a.ksteps;
     const int nk = a.K / kPfBK;
@@ -197,10 +200,10 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
         for (int p = 0; p < XP; ++p)
             xv[p] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (int)(off + 16 * p) : (int)kPfOut, 0, 0);
     };
-    auto issue_w = [&](int kt, u32x4_t (&w)[2][WL], uint32_t (&sr)[2][WL]) {
+    auto issue_w = [&](int kt, u32x4_t (&w)[NT][WL], uint32_t (&sr)[NT][WL]) {
         const bool kok = kt < nk && kt < kt0 + a.ksteps;
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
             const int n = nw + nt * 32 + j;
             const bool ok = kok && n < a.N;
 #pragma unroll
@@ -217,8 +220,8 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
     // NB register sets, rotated with static indices: weights run PD steps
     // ahead, activations two steps ahead (stored to LDS one step ahead)
     u32x4_t xv[NB][XP];
-    u32x4_t wb[NB][2][WL];
-    uint32_t sb[NB][2][WL];
+    u32x4_t wb[NB][NT][WL];
+    uint32_t sb[NB][NT][WL];
     issue_x(kt0, xv[0]);
     issue_x(kt0 + 1, xv[1]);
 #pragma unroll
@@ -263,11 +266,11 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
     store_x(xv[0], xs[0] + xr * XLD + xq * VPT);
     lds_barrier();
 
-    f32x16_t acc[MT][2];
+    f32x16_t acc[MT][NT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int r = 0; r < 16; ++r)
                 acc[mt][nt][r] = 0.0f;
@@ -284,11 +287,11 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
         // would otherwise sink them next to their use)
         __builtin_amdgcn_sched_barrier(0);
         const f16_t *xa = xs[(kt - kt0) & 1];
-        u32x4_t (&wc)[2][WL] = wb[r];
-        uint32_t (&sc)[2][WL] = sb[r];
-        f16x2_t pr[2][16];
+        u32x4_t (&wc)[NT][WL] = wb[r];
+        uint32_t (&sc)[NT][WL] = sb[r];
+        f16x2_t pr[NT][16];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
             for (int l = 0; l < WL; ++l) {
                 const f16_t s16 = f16_from_bits((uint16_t)sc[nt][l]);
@@ -319,7 +322,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
             for (int mt = 0; mt < MT; ++mt)
                 av[mt] = *(const f16x8_t *)(xa + (mt * 32 + j) * XLD + 32 * h + 8 * s);
 #pragma unroll
-            for (int nt = 0; nt < 2; ++nt) {
+            for (int nt = 0; nt < NT; ++nt) {
                 const f16x8_t bv = {pr[nt][4 * s][0],     pr[nt][4 * s][1],     pr[nt][4 * s + 1][0],
                                     pr[nt][4 * s + 1][1], pr[nt][4 * s + 2][0], pr[nt][4 * s + 2][1],
                                     pr[nt][4 * s + 3][0], pr[nt][4 * s + 3][1]};
@@ -351,7 +354,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
+        for (int nt = 0; nt < NT; ++nt) {
             const int n = nw + nt * 32 + j;
             if (n >= a.N)
                 continue;
@@ -373,17 +376,36 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
 }
 
 // Tile rows, weight prefetch depth and K split for a shape.
+// 8-bit tiling knobs (measured: weight prefetch depth 2-4 within 1%)
+#ifndef EP_PF_BIG8_M
+#define EP_PF_BIG8_M 256  // M from which 8-bit runs BM = 128, one N tile per wave
+#endif
+#ifndef EP_PF_PD8
+#define EP_PF_PD8 3
+#endif
 struct PfPlan {
-    int bm, pd, S, ksteps;
+    int bm, pd, nt, S, ksteps;
 };
 
 PfPlan pf_plan(int bits, int64_t M, int64_t N, int64_t K)
 {
     PfPlan p;
-    p.bm = (bits == 4 && M >= 1024) ? 128 : 64;  // 8-bit x 128 rows needs more than 256 VGPRs
-    p.pd = bits == 8 ? 3 : (p.bm == 128 ? 2 : 4);
+    if (bits == 4) {
+        p.bm = M >= 1024 ? 128 : 64;
+        p.pd = p.bm == 128 ? 2 : 4;
+        p.nt = 2;
+    } else if (M >= EP_PF_BIG8_M) {
+        p.bm = 128;
+        p.pd = EP_PF_PD8;
+        p.nt = 1;
+    } else {
+        p.bm = 64;
+        p.pd = 3;
+        p.nt = 2;
+    }
     const int nb = (p.pd > 2 ? p.pd : 2) + 1;
-    const int64_t tiles = ((N + kPfBN - 1) / kPfBN) * ((M + p.bm - 1) / p.bm);
+    const int bn = kPfWaves * 32 * p.nt;
+    const int64_t tiles = ((N + bn - 1) / bn) * ((M + p.bm - 1) / p.bm);
     const int nk = (int)(K / kPfBK);
     const int target = 2 * device_cus();  // two resident workgroups per CU
     int S = 1;
@@ -396,11 +418,12 @@ PfPlan pf_plan(int bits, int64_t M, int64_t N, int64_t K)
     return p;
 }
 
-template <int BITS, int BM, int PD>
+template <int BITS, int BM, int PD, int NT>
 int pf_launch(const PfArgs &a, const PfPlan &p, hipStream_t s)
 {
-    const dim3 grid((unsigned)((a.N + kPfBN - 1) / kPfBN), (unsigned)((a.M + BM - 1) / BM), (unsigned)p.S);
-    hipLaunchKernelGGL((pf_kernel<BITS, BM, PD>), grid, dim3(kPfThreads), 0, s, a);
+    constexpr int BN = kPfWaves * 32 * NT;
+    const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM), (unsigned)p.S);
+    hipLaunchKernelGGL((pf_kernel<BITS, BM, PD, NT>), grid, dim3(kPfThreads), 0, s, a);
     EP_HIP_CHECK(hipGetLastError());
     return EP_OK;
 }
@@ -478,9 +501,9 @@ int launch_prefill(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDe
     a.part = partials ? (float *)((char *)ws + ex + xhb) : nullptr;
     int rc;
     if (bits == 4)
-        rc = p.bm == 128 ? pf_launch<4, 128, 2>(a, p, stream) : pf_launch<4, 64, 4>(a, p, stream);
+        rc = p.bm == 128 ? pf_launch<4, 128, 2, 2>(a, p, stream) : pf_launch<4, 64, 4, 2>(a, p, stream);
     else
-        rc = pf_launch<8, 64, 3>(a, p, stream);
+        rc = p.nt == 1 ? pf_launch<8, 128, EP_PF_PD8, 1>(a, p, stream) : pf_launch<8, 64, 3, 2>(a, p, stream);
     if (rc != EP_OK || !partials)
         return rc;
     return launch_split_reduce(a.part, p.S, M, w.N, y, stream);

@@ -186,7 +186,7 @@ class Decoder:
         self.attn_part = torch.zeros(ws // 4 + 1, device=dev, dtype=f32)
         self.attn_ctr = torch.zeros(cfg.n_heads, device=dev, dtype=i32)
         props = torch.cuda.get_device_properties(dev)
-        self.head_grid = head_grid or 4 * props.multi_processor_count
+        self.head_grid = head_grid or props.multi_processor_count
         self.head_val = torch.zeros(self.head_grid, device=dev, dtype=f32)
         self.head_idx = torch.zeros(self.head_grid, device=dev, dtype=i32)
         self.head_ctr = torch.zeros(1, device=dev, dtype=i32)

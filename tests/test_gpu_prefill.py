@@ -122,9 +122,12 @@ def test_prefill_x_dtypes(xdt):
     assert_close(run(s, x).cpu().numpy(), f64_ref(x, s))
 
 
+@pytest.mark.parametrize("m", [80, 300])
 @pytest.mark.parametrize("group,levels", [(32, 16), (64, 16), (16, 256), (256, 256)])
-def test_prefill_groups(group, levels):
-    n, k, m = 300, 1024, 80
+def test_prefill_groups(group, levels, m):
+    """Both tilings: 64 activation rows x 64 weight rows per wave, and (8-bit,
+    M >= 256) 128 activation rows x 32 weight rows per wave."""
+    n, k = 300, 1024
     _, packed, scale, cb, s = make(n, k, levels, group=group, seed=group)
     x32, x = x_bf16(m, k, group)
     assert_close(run(s, x).cpu().numpy(), rust_ref(x32, packed, scale, cb, n, k, levels, group))
