@@ -14,7 +14,8 @@
 //    Dequantization is the VALU-heavy part, so the MFMAs per dequantized
 //    weight (BM / 32) set the pace: 8-bit at M >= 256 runs BM = 128 with one
 //    N tile per wave (64 accumulators; two N tiles would not fit 256 VGPRs),
-//    ~1.25x the 64 x 2-tile layout;
+//    ~1.25x the 64 x 2-tile layout; 4-bit runs 128 x 1 at M = 256..1023 and
+//    128 x 2 from 1024;
 //  * lane (j = lane & 31, h = lane >> 5) of a wave holds, per 64-k step and
 //    N tile, 32 consecutive weights of row j (k = 32 h .. 32 h + 31 of the
 //    step: one 16-byte load at 4 bits, two at 8 bits); MFMA sub-step s takes
@@ -391,9 +392,10 @@ PfPlan pf_plan(int bits, int64_t M, int64_t N, int64_t K)
 {
     PfPlan p;
     if (bits == 4) {
-        p.bm = M >= 1024 ? 128 : 64;
-        p.pd = p.bm == 128 ? 2 : 4;
-        p.nt = 2;
+        // measured: 128 x 2 tiles lead from M = 1024, 128 x 1 at 256..1023
+        p.bm = M >= 256 ? 128 : 64;
+        p.nt = M >= 256 && M < 1024 ? 1 : 2;
+        p.pd = p.bm == 128 && p.nt == 2 ? 2 : 4;
     } else if (M >= EP_PF_BIG8_M) {
         p.bm = 128;
         p.pd = EP_PF_PD8;
@@ -501,7 +503,8 @@ int launch_prefill(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDe
     a.part = partials ? (float *)((char *)ws + ex + xhb) : nullptr;
     int rc;
     if (bits == 4)
-        rc = p.bm == 128 ? pf_launch<4, 128, 2, 2>(a, p, stream) : pf_launch<4, 64, 4, 2>(a, p, stream);
+        rc = p.nt == 1 ? pf_launch<4, 128, 4, 1>(a, p, stream)
+             : p.bm == 128 ? pf_launch<4, 128, 2, 2>(a, p, stream) : pf_launch<4, 64, 4, 2>(a, p, stream);
     else
         rc = p.nt == 1 ? pf_launch<8, 128, EP_PF_PD8, 1>(a, p, stream) : pf_launch<8, 64, 3, 2>(a, p, stream);
     if (rc != EP_OK || !partials)
