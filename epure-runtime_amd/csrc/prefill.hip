@@ -7,15 +7,18 @@
 // (runtime.py:78-89): the weight enters the product as fp16(fp16(cb) * fp16(scale)).
 //
 // Layout of the work (v_mfma_f32_32x32x16_f16):
-//  * a workgroup is 4 waves and covers 4 x 32 NT weight rows x BM activation
-//    rows; each wave owns NT 32-row N tiles and all BM rows, so every weight
-//    is dequantized exactly once per workgroup, in registers, straight into
-//    the B operand -- the dense weight never reaches LDS or global memory.
-//    Dequantization is the VALU-heavy part, so the MFMAs per dequantized
-//    weight (BM / 32) set the pace: 8-bit at M >= 256 runs BM = 128 with one
-//    N tile per wave (64 accumulators; two N tiles would not fit 256 VGPRs),
-//    ~1.25x the 64 x 2-tile layout; 4-bit runs 128 x 1 at M = 256..1023 and
-//    128 x 2 from 1024;
+//  * a workgroup is WAVES waves and covers WAVES x 32 NT weight rows x BM
+//    activation rows; each wave owns NT 32-row N tiles and all BM rows, so
+//    every weight is dequantized exactly once per workgroup, in registers,
+//    straight into the B operand -- the dense weight never reaches LDS or
+//    global memory.  At M >= 256: 8 waves x BM = 128 (8-bit: one N tile per
+//    wave, as two would not fit 256 VGPRs; 4-bit: one tile at M < 1024, two
+//    from 1024), one workgroup per CU.  What bounds these tilings is the
+//    bytes a CU pulls from L2 per k step (weights + the activation tile: a
+//    CU keeps ~32 KiB of loads in flight), so wider workgroups -- more weight
+//    rows per staged activation tile -- measured faster than 4-wave ones
+//    (8-bit 1.1-1.15x) and than two weight tiles at 64 activation rows
+//    (8-bit 1.25x); M < 256 runs 4 waves x BM = 64 x two tiles;
 //  * lane (j = lane & 31, h = lane >> 5) of a wave holds, per 64-k step and
 //    N tile, 32 consecutive weights of row j (k = 32 h .. 32 h + 31 of the
 //    step: one 16-byte load at 4 bits, two at 8 bits); MFMA sub-step s takes
@@ -23,14 +26,15 @@
 //    activation operand is read from LDS with the same k mapping;
 //  * dequantization is one LDS lookup per packed byte in a 256-entry table
 //    replicated 32 times (lane & 31 reads its own copy: no bank conflicts),
-//    then the group scale is applied in fp16 (v_pk_mul_f16);
+//    addressed by one v_perm of the packed word, then the group scale is
+//    applied in fp16 (v_pk_mul_f16);
 //  * activations are converted once to fp16 after the exact per-row
 //    power-of-two rescale by a pre-kernel (pf_prep_kernel, into the
 //    workspace) and staged in LDS as they are, double buffered: step k + 1
 //    is stored while step k is multiplied;
 //  * weight loads run PD steps ahead in registers (buffer loads: a row past
 //    N or a step past K reads zeros without touching memory);
-//  * when the grid of (N / 256) x (M / BM) workgroups cannot fill the device,
+//  * when the grid of (N / (32 WAVES NT)) x (M / BM) workgroups cannot fill the device,
 //    K is split and the f32 partials are summed in split order by the
 //    reduction shared with the small-M path (deterministic).
 #include "ep_common.h"
@@ -42,11 +46,12 @@
 namespace ep {
 namespace {
 
-constexpr int kPfThreads = 256;        // 4 waves
-constexpr int kPfWaves = 4;            // waves per workgroup, 32 * NT weight rows each
+// A workgroup is WAVES waves (4 or 8), 32 * NT weight rows each.
 constexpr int kPfBK = 64;              // k per step
 constexpr int kPfCopies = 32;          // LDS table replicas
-constexpr uint32_t kPfOut = 0x7ffffff0u;  // a buffer offset past every buffer's end
+// A buffer offset past every buffer's end (buffers are at most this long);
+// sums of two such parts plus a piece offset stay below 2^32.
+constexpr uint32_t kPfOut = 0x7fffff00u;
 
 struct PfArgs {
     const void *x;
@@ -62,6 +67,7 @@ struct PfArgs {
     int N;
     int K;
     int group;
+    int gk_mul, gk_shift;  // k step kt starts in group (kt * gk_mul) >> gk_shift
     int ksteps;   // k steps per split (a multiple of the unroll)
     const int *rexp;
     uint32_t xbytes, wbytes, sbytes, cbbytes;
@@ -157,30 +163,36 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-template <int BITS, int BM, int PD, int NT>
-__global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
+template <int BITS, int BM, int PD, int NT, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64, 8 / WAVES) pf_kernel(PfArgs a)
 {
     constexpr int MT = BM / 32;                  // 32-row M tiles per wave
-    constexpr int XLD = kPfBK + 8;               // halfs per staged activation row
-    constexpr int TPR = kPfThreads / BM;         // staging threads per activation row
+    constexpr int THREADS = WAVES * 64;
+    constexpr int TPR = THREADS / BM;            // staging threads per activation row
     constexpr int VPT = kPfBK / TPR;             // values per staging thread and step
     constexpr int XE = 2;  // activations: fp16, pre-scaled per row (pf_prep_kernel)
     constexpr int XP = VPT * XE / 16;            // 16-byte pieces per staging thread
     constexpr int WL = BITS == 4 ? 1 : 2;        // 16-byte weight loads per lane, N tile and step
     constexpr int NB = (PD > 2 ? PD : 2) + 1;    // register sets (weights PD, activations 2 steps ahead)
     static_assert(VPT % 8 == 0, "staging in 8-value pieces");
-    static_assert(kPfThreads == 256, "one table entry per thread");
+    static_assert(THREADS >= 256, "one table entry per thread");
+    static_assert(BM <= 128, "two activation buffers in the table's gaps");
 
-    __shared__ __align__(16) uint32_t tab[256 * kPfCopies];
-    __shared__ __align__(16) f16_t xs[2][BM * XLD];
-    __shared__ uint32_t s_cbraw[kPfThreads];
+    // 256-byte table entries: the lower 128 bytes hold entry b's 32 copies
+    // (copy c at byte (b << 8) | (c << 2), the address one v_perm builds from
+    // the packed byte); the upper 128 bytes of entry q * 128 + r hold row r
+    // of activation buffer q (64 fp16 values), 16-byte piece p at position
+    // p ^ (r & 7) so a 32-row operand read and the staging stores are free
+    // of bank conflicts.
+    __shared__ __align__(16) uint32_t tab[256 * 64];
+    __shared__ uint32_t s_cbraw[256];
     __shared__ uint16_t s_cb16[256];
     __shared__ int s_e[BM];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, h = lane >> 5;
-    const int nw = blockIdx.x * (kPfWaves * 32 * NT) + wave * (32 * NT);  // the wave's first weight row
+    const int nw = blockIdx.x * (WAVES * 32 * NT) + wave * (32 * NT);  // the wave's first weight row
     const int m0 = blockIdx.y * BM;
     const int kt0 = blockIdx.z * a.ksteps;
     const int nk = a.K / kPfBK;
@@ -193,29 +205,43 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
     const int xm = m0 + xr;
     const int ex = *(const __attribute__((address_space(1))) int *)(a.rexp + (xm < a.M ? xm : 0));
 
+    // Load offsets = a per-lane part fixed for the whole loop (kPfOut for a
+    // row past M or N) + a per-step part that is uniform (kPfOut for a step
+    // past K or the split): one add per load.  Both parts stay below 2^31,
+    // so a sum with either at kPfOut is past the buffer and reads zeros
+    // (the bounds check covers the per-lane offset, which holds the sum).
+    const uint32_t xlo = xm < a.M ? (uint32_t)(((int64_t)xm * a.ldx + xq * VPT) * XE) : kPfOut;
+    uint32_t wlo[NT][WL], slo[NT][WL];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int n = nw + nt * 32 + j;
+#pragma unroll
+        for (int l = 0; l < WL; ++l) {
+            const int kl = 32 * h + 16 * l;  // first k of the piece within the step
+            wlo[nt][l] = n < a.N ? (uint32_t)n * a.row_bytes + (uint32_t)(BITS == 4 ? kl / 2 : kl) : kPfOut;
+            // the group divides 64 or is 64 * 2^i: the piece's group is the
+            // step's (kt * gk_mul) >> gk_shift plus kl / group
+            slo[nt][l] = n < a.N ? (uint32_t)(((int64_t)n * a.lds + kl / a.group) * 2) : kPfOut;
+        }
+    }
+    auto kstep_ok = [&](int kt) { return kt < nk && kt < kt0 + a.ksteps; };
     auto issue_x = [&](int kt, u32x4_t (&xv)[XP]) {
-        const int k = kt * kPfBK + xq * VPT;
-        const bool ok = xm < a.M && kt < nk && kt < kt0 + a.ksteps;
-        const uint32_t off = (uint32_t)(((int64_t)xm * a.ldx + k) * XE);
+        const uint32_t ks = kstep_ok(kt) ? (uint32_t)(kt * kPfBK * XE) : kPfOut;
 #pragma unroll
         for (int p = 0; p < XP; ++p)
-            xv[p] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? (int)(off + 16 * p) : (int)kPfOut, 0, 0);
+            xv[p] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(xlo + ks + 16 * p), 0, 0);
     };
     auto issue_w = [&](int kt, u32x4_t (&w)[NT][WL], uint32_t (&sr)[NT][WL]) {
-        const bool kok = kt < nk && kt < kt0 + a.ksteps;
+        const bool kok = kstep_ok(kt);
+        const uint32_t kw = kok ? (uint32_t)(kt * (BITS == 4 ? kPfBK / 2 : kPfBK)) : kPfOut;
+        const uint32_t kg = kok ? (uint32_t)(((kt * a.gk_mul) >> a.gk_shift) * 2) : kPfOut;
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const int n = nw + nt * 32 + j;
-            const bool ok = kok && n < a.N;
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int l = 0; l < WL; ++l) {
-                const int k = kt * kPfBK + 32 * h + 16 * l;  // first k of the 16-byte piece (8-bit) / 32 (4-bit)
-                const uint32_t off = (uint32_t)n * a.row_bytes + (uint32_t)(BITS == 4 ? k / 2 : k);
-                w[nt][l] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (int)off : (int)kPfOut, 0, 0);
-                const uint32_t soff = (uint32_t)(((int64_t)n * a.lds + k / a.group) * 2);
-                sr[nt][l] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (int)soff : (int)kPfOut, 0, 0);
+                w[nt][l] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(wlo[nt][l] + kw), 0, 0);
+                sr[nt][l] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)(slo[nt][l] + kg), 0, 0);
             }
-        }
     };
 
     // NB register sets, rotated with static indices: weights run PD steps
@@ -230,14 +256,19 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
         issue_w(kt0 + d, wb[d], sb[d]);
     __builtin_amdgcn_sched_barrier(0);
 
-    auto store_x = [&](const u32x4_t (&v4)[XP], f16_t *dst) {
+    // staged activation row r, buffer q, 16-byte piece p (see the layout above)
+    auto xs_off = [](int q, int r, int p) -> uint32_t {
+        return ((uint32_t)(q * 128 + r) << 8) + 128u + ((uint32_t)(p ^ (r & 7)) << 4);
+    };
+    auto store_x = [&](const u32x4_t (&v4)[XP], int q) {
 #pragma unroll
         for (int p = 0; p < XP; ++p)
-            *(u32x4_t *)(dst + 8 * p) = v4[p];
+            *(u32x4_t *)((char *)tab + xs_off(q, xr, xq * XP + p)) = v4[p];
     };
 
     // codebook -> fp16 -> the replicated table; step 0's activations -> LDS
-    s_cbraw[tid] = cbraw;
+    if (tid < 256)
+        s_cbraw[tid] = cbraw;
     if (tid < BM)
         s_e[tid] = 0;
     lds_barrier();
@@ -252,19 +283,22 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
             }
         }
         // fp16 bits of the entries (past levels: 0, the Rust LUT's zeros)
-        s_cb16[tid] = tid < a.levels ? f16_bits((f16_t)c) : (uint16_t)0;
+        if (tid < 256)
+            s_cb16[tid] = tid < a.levels ? f16_bits((f16_t)c) : (uint16_t)0;
         lds_barrier();
         // entry t: (cb[t & 15], cb[t >> 4]) at 4 bits, cb[t] twice at 8 bits
-        const uint32_t v = BITS == 4 ? ((uint32_t)s_cb16[tid & 15] | ((uint32_t)s_cb16[tid >> 4] << 16))
-                                     : ((uint32_t)s_cb16[tid] | ((uint32_t)s_cb16[tid] << 16));
-        u32x4_t *row = (u32x4_t *)(tab + tid * kPfCopies);
+        if (tid < 256) {
+            const uint32_t v = BITS == 4 ? ((uint32_t)s_cb16[tid & 15] | ((uint32_t)s_cb16[tid >> 4] << 16))
+                                         : ((uint32_t)s_cb16[tid] | ((uint32_t)s_cb16[tid] << 16));
+            u32x4_t *row = (u32x4_t *)(tab + tid * 64);
 #pragma unroll
-        for (int i = 0; i < kPfCopies / 4; ++i)
-            row[i] = (u32x4_t){v, v, v, v};
+            for (int i = 0; i < kPfCopies / 4; ++i)
+                row[i] = (u32x4_t){v, v, v, v};
+        }
     }
     if (tid % TPR == 0 && xm < a.M)
         s_e[xr] = ex;
-    store_x(xv[0], xs[0] + xr * XLD + xq * VPT);
+    store_x(xv[0], 0);
     lds_barrier();
 
     f32x16_t acc[MT][NT];
@@ -276,7 +310,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
             for (int r = 0; r < 16; ++r)
                 acc[mt][nt][r] = 0.0f;
 
-    const uint32_t c8 = (uint32_t)(lane & 31) << 3;  // (copy << 2) << 1: the address is halved below
+    const uint32_t c4 = (uint32_t)(lane & 31) << 2;  // the lane's table copy
     // One step (register set r = (kt - kt0) % NB): issue step kt + 2's
     // activations and step kt + PD's weights, multiply step kt, store step
     // kt + 1's activations.
@@ -287,7 +321,8 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
         // the loads above stay here, ahead of the work below (the scheduler
         // would otherwise sink them next to their use)
         __builtin_amdgcn_sched_barrier(0);
-        const f16_t *xa = xs[(kt - kt0) & 1];
+        // activation buffer of step kt: static when the unroll is even
+        const int q = NB % 2 == 0 ? (r & 1) : ((kt - kt0) & 1);
         u32x4_t (&wc)[NT][WL] = wb[r];
         uint32_t (&sc)[NT][WL] = sb[r];
         f16x2_t pr[NT][16];
@@ -304,12 +339,12 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
 #pragma unroll
                         for (int b = 0; b < 4; ++b)
                             pr[nt][wd * 4 + b] =
-                                as_f16x2(lds_read_u32(tab, __builtin_amdgcn_perm(word, c8, kSelByte[b]) >> 1)) * s2;
+                                as_f16x2(lds_read_u32(tab, __builtin_amdgcn_perm(word, c4, kSelByte[b]))) * s2;
                     } else {
-                        const uint32_t t0 = lds_read_u32(tab, __builtin_amdgcn_perm(word, c8, kSelByte[0]) >> 1);
-                        const uint32_t t1 = lds_read_u32(tab, __builtin_amdgcn_perm(word, c8, kSelByte[1]) >> 1);
-                        const uint32_t t2 = lds_read_u32(tab, __builtin_amdgcn_perm(word, c8, kSelByte[2]) >> 1);
-                        const uint32_t t3 = lds_read_u32(tab, __builtin_amdgcn_perm(word, c8, kSelByte[3]) >> 1);
+                        const uint32_t t0 = lds_read_u32(tab, __builtin_amdgcn_perm(word, c4, kSelByte[0]));
+                        const uint32_t t1 = lds_read_u32(tab, __builtin_amdgcn_perm(word, c4, kSelByte[1]));
+                        const uint32_t t2 = lds_read_u32(tab, __builtin_amdgcn_perm(word, c4, kSelByte[2]));
+                        const uint32_t t3 = lds_read_u32(tab, __builtin_amdgcn_perm(word, c4, kSelByte[3]));
                         pr[nt][l * 8 + wd * 2] = as_f16x2(__builtin_amdgcn_perm(t1, t0, 0x05040100u)) * s2;
                         pr[nt][l * 8 + wd * 2 + 1] = as_f16x2(__builtin_amdgcn_perm(t3, t2, 0x05040100u)) * s2;
                     }
@@ -321,7 +356,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
             f16x8_t av[MT];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
-                av[mt] = *(const f16x8_t *)(xa + (mt * 32 + j) * XLD + 32 * h + 8 * s);
+                av[mt] = *(const f16x8_t *)((const char *)tab + xs_off(q, mt * 32 + j, 4 * h + s));
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt) {
                 const f16x8_t bv = {pr[nt][4 * s][0],     pr[nt][4 * s][1],     pr[nt][4 * s + 1][0],
@@ -333,7 +368,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        store_x(xv[(r + 1) % NB], xs[(kt + 1 - kt0) & 1] + xr * XLD + xq * VPT);
+        store_x(xv[(r + 1) % NB], q ^ 1);
         // LDS-only barrier: __syncthreads() would also wait for the loads
         // in flight
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -385,7 +420,7 @@ __global__ void __launch_bounds__(kPfThreads, 2) pf_kernel(PfArgs a)
 #define EP_PF_PD8 3
 #endif
 struct PfPlan {
-    int bm, pd, nt, S, ksteps;
+    int bm, pd, nt, waves, S, ksteps;
 };
 
 PfPlan pf_plan(int bits, int64_t M, int64_t N, int64_t K)
@@ -396,20 +431,23 @@ PfPlan pf_plan(int bits, int64_t M, int64_t N, int64_t K)
         p.bm = M >= 256 ? 128 : 64;
         p.nt = M >= 256 && M < 1024 ? 1 : 2;
         p.pd = p.bm == 128 && p.nt == 2 ? 2 : 4;
+        p.waves = M >= 256 ? 8 : 4;
     } else if (M >= EP_PF_BIG8_M) {
         p.bm = 128;
         p.pd = EP_PF_PD8;
         p.nt = 1;
+        p.waves = 8;
     } else {
         p.bm = 64;
         p.pd = 3;
         p.nt = 2;
+        p.waves = 4;
     }
     const int nb = (p.pd > 2 ? p.pd : 2) + 1;
-    const int bn = kPfWaves * 32 * p.nt;
+    const int bn = p.waves * 32 * p.nt;
     const int64_t tiles = ((N + bn - 1) / bn) * ((M + p.bm - 1) / p.bm);
     const int nk = (int)(K / kPfBK);
-    const int target = 2 * device_cus();  // two resident workgroups per CU
+    const int target = 8 / p.waves * device_cus();  // 8 resident waves per CU
     int S = 1;
     while (tiles * S < target && S < 8 && nk / (S * 2) >= 8)
         S *= 2;
@@ -420,12 +458,12 @@ PfPlan pf_plan(int bits, int64_t M, int64_t N, int64_t K)
     return p;
 }
 
-template <int BITS, int BM, int PD, int NT>
+template <int BITS, int BM, int PD, int NT, int WAVES>
 int pf_launch(const PfArgs &a, const PfPlan &p, hipStream_t s)
 {
-    constexpr int BN = kPfWaves * 32 * NT;
+    constexpr int BN = WAVES * 32 * NT;
     const dim3 grid((unsigned)((a.N + BN - 1) / BN), (unsigned)((a.M + BM - 1) / BM), (unsigned)p.S);
-    hipLaunchKernelGGL((pf_kernel<BITS, BM, PD, NT>), grid, dim3(kPfThreads), 0, s, a);
+    hipLaunchKernelGGL((pf_kernel<BITS, BM, PD, NT, WAVES>), grid, dim3(WAVES * 64), 0, s, a);
     EP_HIP_CHECK(hipGetLastError());
     return EP_OK;
 }
@@ -438,6 +476,10 @@ bool prefill_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
     if (M < 1 || M > ((int64_t)1 << 24) || w.N < 1 || w.K < kPfBK || w.K % kPfBK != 0)
         return false;
     if (w.scale_dtype != EP_F16 || w.group % (bits == 4 ? 32 : 16) != 0)
+        return false;
+    // groups that divide the 64-wide k step or are 64 * 2^i (others: the
+    // generic MFMA path)
+    if (64 % w.group != 0 && (w.group % 64 != 0 || ((w.group / 64) & (w.group / 64 - 1)) != 0))
         return false;
     const int esz = x.dtype == EP_F32 ? 4 : 2;
     const int64_t rb = bits == 4 ? w.K / 2 : w.K;
@@ -494,6 +536,10 @@ int launch_prefill(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDe
     a.N = (int)w.N;
     a.K = (int)w.K;
     a.group = w.group;
+    a.gk_mul = w.group <= kPfBK ? kPfBK / w.group : 1;
+    a.gk_shift = 0;
+    while (w.group > kPfBK && (kPfBK << a.gk_shift) < w.group)
+        ++a.gk_shift;
     a.ksteps = p.ksteps;
     a.rexp = rexp;
     a.y = y.ptr;
@@ -503,10 +549,12 @@ int launch_prefill(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDe
     a.part = partials ? (float *)((char *)ws + ex + xhb) : nullptr;
     int rc;
     if (bits == 4)
-        rc = p.nt == 1 ? pf_launch<4, 128, 4, 1>(a, p, stream)
-             : p.bm == 128 ? pf_launch<4, 128, 2, 2>(a, p, stream) : pf_launch<4, 64, 4, 2>(a, p, stream);
+        rc = p.nt == 1 ? pf_launch<4, 128, 4, 1, 8>(a, p, stream)
+             : p.bm == 128 ? pf_launch<4, 128, 2, 2, 8>(a, p, stream)
+                           : pf_launch<4, 64, 4, 2, 4>(a, p, stream);
     else
-        rc = p.nt == 1 ? pf_launch<8, 128, EP_PF_PD8, 1>(a, p, stream) : pf_launch<8, 64, 3, 2>(a, p, stream);
+        rc = p.nt == 1 ? pf_launch<8, 128, EP_PF_PD8, 1, 8>(a, p, stream)
+                       : pf_launch<8, 64, 3, 2, 4>(a, p, stream);
     if (rc != EP_OK || !partials)
         return rc;
     return launch_split_reduce(a.part, p.S, M, w.N, y, stream);

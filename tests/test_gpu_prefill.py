@@ -123,11 +123,13 @@ def test_prefill_x_dtypes(xdt):
 
 
 @pytest.mark.parametrize("m", [80, 300])
-@pytest.mark.parametrize("group,levels", [(32, 16), (64, 16), (16, 256), (256, 256)])
+@pytest.mark.parametrize("group,levels", [(32, 16), (64, 16), (16, 256), (256, 256), (96, 16), (48, 256)])
 def test_prefill_groups(group, levels, m):
-    """Both tilings: 64 activation rows x 64 weight rows per wave, and (8-bit,
-    M >= 256) 128 activation rows x 32 weight rows per wave."""
-    n, k = 300, 1024
+    """Both tilings: 64 activation rows x 64 weight rows per wave, and 128
+    activation rows x 32 weight rows per wave (M >= 256).  Groups that
+    neither divide the 64-wide k step nor are 64 * 2^i (96, 48) are served by
+    the generic MFMA path."""
+    n, k = 300, 1024 if 1024 % group == 0 else 1152
     _, packed, scale, cb, s = make(n, k, levels, group=group, seed=group)
     x32, x = x_bf16(m, k, group)
     assert_close(run(s, x).cpu().numpy(), rust_ref(x32, packed, scale, cb, n, k, levels, group))
