@@ -216,7 +216,7 @@ def prefill_sweep(seed=0, replays=10):
                          "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
                          "kernel": ("gemv_lut_kernel" if m == 1 else
                                     "sk_kernel + sk_reduce_kernel" if m <= 64 else
-                                    "pf_rowexp_kernel + pf_kernel (+ sk_reduce_kernel when K is split)")})
+                                    "pf_prep_kernel + pf_kernel (+ sk_reduce_kernel when K is split)")})
             del lins, x
         del stores
         torch.cuda.empty_cache()
