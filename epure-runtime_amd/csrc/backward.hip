@@ -64,6 +64,18 @@ struct BwdArgs {
     float *dx_part;      // [splits][M][K] f32 partials (null: one split, results go to gx)
 };
 
+// Buffer descriptor over `bytes` bytes at p: loads at offsets past the end
+// read zeros.  kBwOut is past the end of every descriptor.
+constexpr uint32_t kBwOut = 0x7fffff00u;
+EP_DEV __amdgpu_buffer_rsrc_t bw_rsrc(const void *p, uint32_t bytes)
+{
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
+                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
 EP_DEV uint32_t bits_of(f16x2_t v)
 {
     uint32_t u;
@@ -145,7 +157,8 @@ __global__ void __launch_bounds__(256)
 // times the fp16 scale, i.e. materialize(float16)), transposed in registers
 // and written as W^T rows ([k][n]), so both MFMA operands are 16-byte LDS
 // reads.  The next step's global loads are in flight during the MFMAs.
-__global__ void __launch_bounds__(256, 3) dx_kernel(BwdArgs a)
+template <int SDT>  // scale dtype
+__global__ void __launch_bounds__(256, 2) dx_kernel(BwdArgs a)
 {
     __shared__ __align__(16) f16_t Gs[T * LDX];  // gy tile [m][n]
     __shared__ __align__(16) f16_t Ws[T * LDX];  // W^T tile [k][n]
@@ -181,60 +194,78 @@ __global__ void __launch_bounds__(256, 3) dx_kernel(BwdArgs a)
     // gy: rows 32 p + (tid >> 3), columns 8 (tid & 7) .. + 7 (p = 0..3);
     // W (threads below 128, waves 0-1): the 8 x 8 block of rows nb * 8 ..,
     // columns kb * 8 ..
+    // Loads never branch: buffer descriptors over the tile's gy rows (rows
+    // past M read zeros), the packed weights and the scales; an element past
+    // N, or any element of a step past this split's end, gets an offset
+    // past every buffer.
     const int gr0 = tid >> 3, gc = 8 * (tid & 7);
     const bool wthr = tid < 128;  // wave-uniform
     const int nb = tid & 7, kb = (tid >> 3) & 15;
-    const int64_t rowb = a.K / 2;
-    u32x4_t gv[4];
-    uint32_t wv[8];
-    float wsc[8];
-    auto load = [&](int n0) {
+    const uint32_t rowb = (uint32_t)(a.K / 2);
+    constexpr int SE = SDT == EP_F32 ? 4 : 2;
+    const int64_t gleft = (int64_t)(a.M - m0) * a.N * 2;
+    const auto rg = bw_rsrc(a.gy16 + (int64_t)m0 * a.N, gleft < kBwOut ? (uint32_t)gleft : kBwOut);
+    const auto rw = bw_rsrc(a.packed, (uint32_t)((int64_t)a.N * rowb));
+    const auto rs = bw_rsrc(a.scale, (uint32_t)(((int64_t)(a.N - 1) * a.lds + a.K / a.group) * SE));
+    const uint32_t kbyte = (uint32_t)((k0 + kb * 8) / 2);
+    const int kgrp = (k0 + kb * 8) / a.group;
+    u32x4_t gva[4], gvb[4];
+    uint32_t wva[8], wvb[8], sca[8], scb[8];
+    auto load = [&](int st, u32x4_t (&gv)[4], uint32_t (&wv)[8], uint32_t (&sc)[8]) {
+        const bool kok = st < st1;  // uniform
+        const int n0 = st * CS;
+        {
+            const int n = n0 + gc;
+            const bool ok = kok && n < a.N;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const int m = m0 + 32 * p + gr0, n = n0 + gc;
-            gv[p] = (m < a.M && n < a.N) ? *(const u32x4_t *)(a.gy16 + (int64_t)m * a.N + n)
-                                         : (u32x4_t){0u, 0u, 0u, 0u};
+            for (int p = 0; p < 4; ++p)
+                gv[p] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rg, ok ? (int)(((32 * p + gr0) * a.N + n) * 2) : (int)kBwOut, 0, 0);
         }
-        if (wthr) {
-            const int k = k0 + kb * 8;
+        // every wave issues them (waves 2-3 out of range: no memory traffic),
+        // so no load sits in a branch and the waits stay exact
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int n = n0 + nb * 8 + i;
-                const bool ok = n < a.N;
-                wv[i] = ok ? *(const uint32_t *)(a.packed + (int64_t)n * rowb + k / 2) : 0u;
-                wsc[i] = ok ? load_as_f32(a.scale, a.scale_dtype, (int64_t)n * a.lds + k / a.group) : 0.0f;
-            }
+        for (int i = 0; i < 8; ++i) {
+            const int n = n0 + nb * 8 + i;
+            const bool ok = wthr && kok && n < a.N;
+            wv[i] = __builtin_amdgcn_raw_buffer_load_b32(rw, ok ? (int)((uint32_t)n * rowb + kbyte) : (int)kBwOut,
+                                                        0, 0);
+            const int so = (int)(((int64_t)n * a.lds + kgrp) * SE);
+            if constexpr (SE == 4)
+                sc[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, ok ? so : (int)kBwOut, 0, 0);
+            else
+                sc[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? so : (int)kBwOut, 0, 0);
         }
     };
-    auto store = [&]() {
+    auto store = [&](const u32x4_t (&gv)[4], const uint32_t (&wv)[8], const uint32_t (&sc)[8]) {
 #pragma unroll
         for (int p = 0; p < 4; ++p)
             *(u32x4_t *)&Gs[(32 * p + gr0) * LDX + gc] = gv[p];
         if (wthr) {
-            u32x4_t rw[8], cw[8];
+            u32x4_t rw8[8], cw[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const f16_t sh = (f16_t)wsc[i];
+                const float sf = SDT == EP_F32 ? __uint_as_float(sc[i])
+                                 : SDT == EP_BF16 ? bf16_to_f32((uint16_t)sc[i])
+                                                  : (float)f16_from_bits((uint16_t)sc[i]);
+                const f16_t sh = (f16_t)sf;
                 const f16x2_t s2 = (f16x2_t){sh, sh};
 #pragma unroll
                 for (int d = 0; d < 4; ++d)
-                    rw[i][d] = bits_of(as_f16x2(tab[(wv[i] >> (8 * d)) & 0xffu]) * s2);
+                    rw8[i][d] = bits_of(as_f16x2(tab[(wv[i] >> (8 * d)) & 0xffu]) * s2);
             }
-            tr8x8(rw, cw);
+            tr8x8(rw8, cw);
 #pragma unroll
             for (int j = 0; j < 8; ++j)
                 *(u32x4_t *)&Ws[(kb * 8 + j) * LDX + nb * 8] = cw[j];
         }
     };
-
-    __syncthreads();
-    if (st0 < st1)
-        load(st0 * CS);
-    for (int st = st0; st < st1; ++st) {
-        store();
-        __syncthreads();
-        if (st + 1 < st1)
-            load((st + 1) * CS);
+    auto step = [&](int st, u32x4_t (&gv)[4], uint32_t (&wv)[8], uint32_t (&sc)[8]) {
+        store(gv, wv, sc);
+        lds_barrier();
+        load(st + 2, gv, wv, sc);
+        // keep the loads here and the next step's staging out of this one
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < CS / 16; ++kk) {
             f16x8_t af[2], bf[2];
@@ -252,7 +283,22 @@ __global__ void __launch_bounds__(256, 3) dx_kernel(BwdArgs a)
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        __syncthreads();
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    lds_barrier();  // tab, s_e
+    // two register sets, loads two steps ahead; the step count is rounded up
+    // to even (a padding step reads zeros) so the sets rotate with static
+    // indices and every wait counts exactly the younger set's loads
+    load(st0, gva, wva, sca);
+    __builtin_amdgcn_sched_barrier(0);
+    load(st0 + 1, gvb, wvb, scb);
+    __builtin_amdgcn_sched_barrier(0);
+    const int stend = st0 + ((st1 - st0 + 1) & ~1);
+    for (int st = st0; st < stend; st += 2) {
+        step(st, gva, wva, sca);
+        step(st + 1, gvb, wvb, scb);
     }
 
     // D[row][col] of a 32x32 tile: lane col + 32 * ((row / 4) % 2),
@@ -284,7 +330,7 @@ __global__ void __launch_bounds__(256, 3) dx_kernel(BwdArgs a)
 // loads are in flight during the MFMAs.  Single-buffered (37 KB of LDS):
 // three workgroups per CU.  The epilogue reuses the staging space.
 constexpr int kDwStage = 2 * T * LDW * 2;  // [x^T | gy^T] bf16
-__global__ void __launch_bounds__(256, 3) dw_kernel(BwdArgs a)
+__global__ void __launch_bounds__(256, 2) dw_kernel(BwdArgs a)
 {
     __shared__ __align__(16) char smem[kDwStage];
     // epilogue views of the same space
@@ -314,19 +360,25 @@ __global__ void __launch_bounds__(256, 3) dw_kernel(BwdArgs a)
     const bool isx = tid < 128;  // wave-uniform
     const int blk = tid & 127;
     const int br = (blk >> 4) * 8, bc = (blk & 15) * 8;
-    const uint16_t *src = isx ? (const uint16_t *)a.x + k0 + bc : (const uint16_t *)a.gy + n0 + bc;
-    const int64_t ld = isx ? a.ldx : a.ldgy;
+    // Loads never branch: each step reads through a buffer descriptor based
+    // at the step's first row and sized to the bytes left from there, so rows
+    // past M (and a step past the end) read zeros; a column past N is sent
+    // out of range by its per-lane offset.
+    const char *base = isx ? (const char *)a.x : (const char *)a.gy;  // wave-uniform
+    const int64_t rowb = (isx ? a.ldx : a.ldgy) * 2;
+    const int64_t total = ((int64_t)(a.M - 1) * (isx ? a.ldx : a.ldgy) + (isx ? a.K : a.N)) * 2;
     const bool colok = isx ? true : n0 + bc < a.N;
-    u32x4_t rr[8];
-    auto load = [&](int mb) {
+    const uint32_t off0 = colok ? (uint32_t)(br * rowb + (int64_t)((isx ? k0 : n0) + bc) * 2) : kBwOut;
+    const uint32_t offr = (uint32_t)rowb;
+    auto load = [&](int mb, u32x4_t (&rr)[8]) {
+        const int64_t left = total - (int64_t)mb * rowb;
+        const auto rsrc = bw_rsrc(base + (left > 0 ? (int64_t)mb * rowb : 0),
+                                  left > 0 ? (left < kBwOut ? (uint32_t)left : kBwOut) : 0u);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int m = mb + br + i;
-            rr[i] = (colok && m < a.M) ? *(const u32x4_t *)(src + (int64_t)m * ld)
-                                       : (u32x4_t){0u, 0u, 0u, 0u};
-        }
+        for (int i = 0; i < 8; ++i)
+            rr[i] = __builtin_amdgcn_raw_buffer_load_b128(rsrc, colok ? (int)(off0 + i * offr) : (int)kBwOut, 0, 0);
     };
-    auto store = [&](int buf) {
+    auto store = [&](const u32x4_t (&rr)[8], int buf) {
         u32x4_t cc[8];
         tr8x8(rr, cc);
         __bf16 *dst = (__bf16 *)smem + (buf * 2 + (isx ? 0 : 1)) * T * LDW;  // buf is 0
@@ -335,15 +387,25 @@ __global__ void __launch_bounds__(256, 3) dw_kernel(BwdArgs a)
             *(u32x4_t *)&dst[(bc + j) * LDW + br] = cc[j];
     };
 
+    // Two register sets, loads two steps ahead; the step count is rounded up
+    // to even (a padding step reads zeros) so the sets rotate with static
+    // indices and every wait counts exactly the younger set's loads.
     const int steps = (a.M + MS - 1) / MS;
+    const int steps2 = (steps + 1) & ~1;
     const __bf16 *Xs = (const __bf16 *)smem;
     const __bf16 *Gs = Xs + T * LDW;
-    load(0);
-    for (int st = 0; st < steps; ++st) {
-        store(0);
-        __syncthreads();
-        if (st + 1 < steps)
-            load((st + 1) * MS);
+    u32x4_t rra[8], rrb[8];
+    load(0, rra);
+    __builtin_amdgcn_sched_barrier(0);  // in issue order: the first set is the older
+    load(MS, rrb);
+    __builtin_amdgcn_sched_barrier(0);
+    auto step = [&](int st, u32x4_t (&rr)[8]) {
+        store(rr, 0);
+        lds_barrier();
+        load((st + 2) * MS, rr);
+        // keep the loads here and the next step's transpose out of this one
+        // (either move makes a wait cover the younger register set)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int kk = 0; kk < MS / 16; ++kk) {
             bf16x8_t af[2], bf[2];
@@ -362,7 +424,12 @@ __global__ void __launch_bounds__(256, 3) dw_kernel(BwdArgs a)
                     acc[i][j] =
                         __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        __syncthreads();
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int st = 0; st < steps2; st += 2) {
+        step(st, rra);
+        step(st + 1, rrb);
     }
 
     // ---- epilogue: G[k][n] -> grad_scale partials and level histograms ----
@@ -489,9 +556,11 @@ size_t backward_workspace(int64_t M, int64_t N, int64_t K, int levels, int group
 bool backward_serves(const PackedDesc &w, int gy_dtype, int x_dtype)
 {
     // gy is staged in 16-column chunks, so N % 16 == 0 keeps every load in its row.
+    // buffer offsets stay below kBwOut: packed bytes, scales, 128 gy rows
+    const int64_t sbytes = ((w.N - 1) * w.ld_scale + w.K / w.group) * (w.scale_dtype == EP_F32 ? 4 : 2);
     return w.levels <= 16 && w.K % T == 0 && T % w.group == 0 && T / w.group <= 4 &&
            w.N % 16 == 0 && gy_dtype == EP_BF16 && x_dtype == EP_BF16 && w.N <= INT32_MAX &&
-           w.K <= INT32_MAX;
+           w.K <= INT32_MAX && w.N * (w.K / 2) < kBwOut && sbytes < kBwOut && w.N * T * 2 < kBwOut;
 }
 
 int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, int64_t M,
@@ -511,6 +580,8 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
     if (((uintptr_t)gy.ptr & 15) || ((uintptr_t)x.ptr & 15) || (gy.ld % 8) || (x.ld % 8) ||
         ((uintptr_t)w.packed & 15))
         return set_error(EP_DECLINE_SHAPE, "fused backward needs 16-byte aligned rows");
+    if (64 * gy.ld * 2 >= kBwOut || 64 * x.ld * 2 >= kBwOut)
+        return set_error(EP_DECLINE_SHAPE, "fused backward: row strides of gy and x below 16M elements");
     BwdArgs a{};
     a.gy = gy.ptr;
     a.gy_dtype = gy.dtype;
@@ -547,8 +618,13 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         a.dx_steps = (nsteps + S - 1) / S;
         const int Sused = (nsteps + a.dx_steps - 1) / a.dx_steps;
         a.dx_part = Sused > 1 ? (float *)((char *)gy16 + (size_t)((M * w.N * 2 + 255) / 256 * 256)) : nullptr;
-        hipLaunchKernelGGL(dx_kernel, dim3((unsigned)((w.K + T - 1) / T), (unsigned)((M + T - 1) / T), (unsigned)Sused),
-                           dim3(256), 0, stream, a);
+        const dim3 grid((unsigned)((w.K + T - 1) / T), (unsigned)((M + T - 1) / T), (unsigned)Sused);
+        if (w.scale_dtype == EP_F32)
+            hipLaunchKernelGGL(dx_kernel<EP_F32>, grid, dim3(256), 0, stream, a);
+        else if (w.scale_dtype == EP_BF16)
+            hipLaunchKernelGGL(dx_kernel<EP_BF16>, grid, dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL(dx_kernel<EP_F16>, grid, dim3(256), 0, stream, a);
         EP_HIP_CHECK(hipGetLastError());
         if (Sused > 1) {
             const int rc = launch_split_reduce(a.dx_part, Sused, M, w.K, OutDesc{gx.ptr, gx.dtype, gx.ld, 0}, stream);
