@@ -330,7 +330,7 @@ __global__ void __launch_bounds__(256, 2) dx_kernel(BwdArgs a)
 // loads are in flight during the MFMAs.  Single-buffered (37 KB of LDS):
 // three workgroups per CU.  The epilogue reuses the staging space.
 constexpr int kDwStage = 2 * T * LDW * 2;  // [x^T | gy^T] bf16
-__global__ void __launch_bounds__(256, 2) dw_kernel(BwdArgs a)
+__global__ void __launch_bounds__(256, 3) dw_kernel(BwdArgs a)
 {
     __shared__ __align__(16) char smem[kDwStage];
     // epilogue views of the same space
@@ -387,22 +387,19 @@ __global__ void __launch_bounds__(256, 2) dw_kernel(BwdArgs a)
             *(u32x4_t *)&dst[(bc + j) * LDW + br] = cc[j];
     };
 
-    // Two register sets, loads two steps ahead; the step count is rounded up
-    // to even (a padding step reads zeros) so the sets rotate with static
-    // indices and every wait counts exactly the younger set's loads.
+    // One register set (a second one costs the third resident workgroup,
+    // measured slower): the next step's loads are issued right after the
+    // set is staged and waited for only at the next staging, so they overlap
+    // this step's MFMAs (the barriers wait for LDS operations only).
     const int steps = (a.M + MS - 1) / MS;
-    const int steps2 = (steps + 1) & ~1;
     const __bf16 *Xs = (const __bf16 *)smem;
     const __bf16 *Gs = Xs + T * LDW;
-    u32x4_t rra[8], rrb[8];
+    u32x4_t rra[8];
     load(0, rra);
-    __builtin_amdgcn_sched_barrier(0);  // in issue order: the first set is the older
-    load(MS, rrb);
-    __builtin_amdgcn_sched_barrier(0);
     auto step = [&](int st, u32x4_t (&rr)[8]) {
         store(rr, 0);
         lds_barrier();
-        load((st + 2) * MS, rr);
+        load((st + 1) * MS, rr);
         // keep the loads here and the next step's transpose out of this one
         // (either move makes a wait cover the younger register set)
         __builtin_amdgcn_sched_barrier(0);
@@ -427,10 +424,8 @@ __global__ void __launch_bounds__(256, 2) dw_kernel(BwdArgs a)
         lds_barrier();
         __builtin_amdgcn_sched_barrier(0);
     };
-    for (int st = 0; st < steps2; st += 2) {
+    for (int st = 0; st < steps; ++st)
         step(st, rra);
-        step(st + 1, rrb);
-    }
 
     // ---- epilogue: G[k][n] -> grad_scale partials and level histograms ----
     // the tile's packed bytes, scales and the codebook (loaded only now:

@@ -61,7 +61,8 @@ def run_bwd(s, gy, x, gx_dtype=torch.float32):
 
 
 @pytest.mark.parametrize("n,k,m,group", [(256, 512, 64, 128), (384, 1024, 100, 64),
-                                         (208, 256, 33, 32), (128, 128, 1, 128)])
+                                         (208, 256, 33, 32), (128, 128, 1, 128),
+                                         (320, 640, 130, 128)])
 def test_backward_small_vs_closed_forms(n, k, m, group):
     idx, packed, scale, cb, s = make(n, k, group, seed=n + k)
     x, gy = bf16((m, k), 1), bf16((m, n), 2, 1e-2)
