@@ -11,14 +11,14 @@
 //    activation rows; each wave owns NT 32-row N tiles and all BM rows, so
 //    every weight is dequantized exactly once per workgroup, in registers,
 //    straight into the B operand -- the dense weight never reaches LDS or
-//    global memory.  At M >= 256: 8 waves x BM = 128 (8-bit: one N tile per
-//    wave, as two would not fit 256 VGPRs; 4-bit: one tile at M < 1024, two
-//    from 1024), one workgroup per CU.  What bounds these tilings is the
+//    global memory.  From M = 128 (8-bit) or 160 (4-bit): 8 waves x BM = 128
+//    (8-bit: one N tile per wave, as two would not fit 256 VGPRs; 4-bit: one
+//    tile at M < 1024, two from 1024), one workgroup per CU.  What bounds these tilings is the
 //    bytes a CU pulls from L2 per k step (weights + the activation tile: a
 //    CU keeps ~32 KiB of loads in flight), so wider workgroups -- more weight
 //    rows per staged activation tile -- measured faster than 4-wave ones
 //    (8-bit 1.1-1.15x) and than two weight tiles at 64 activation rows
-//    (8-bit 1.25x); M < 256 runs 4 waves x BM = 64 x two tiles;
+//    (8-bit 1.25x); smaller M runs 4 waves x BM = 64 x two tiles;
 //  * lane (j = lane & 31, h = lane >> 5) of a wave holds, per 64-k step and
 //    N tile, 32 consecutive weights of row j (k = 32 h .. 32 h + 31 of the
 //    step: one 16-byte load at 4 bits, two at 8 bits); MFMA sub-step s takes
@@ -413,8 +413,13 @@ __global__ void __launch_bounds__(WAVES * 64, 8 / WAVES) pf_kernel(PfArgs a)
 
 // Tile rows, weight prefetch depth and K split for a shape.
 // 8-bit tiling knobs (measured: weight prefetch depth 2-4 within 1%)
+// M from which the 8-wave 128-row tilings run (measured: 8-bit gains from
+// M = 128, 4-bit only above it)
+#ifndef EP_PF_BIG4_M
+#define EP_PF_BIG4_M 160
+#endif
 #ifndef EP_PF_BIG8_M
-#define EP_PF_BIG8_M 256  // M from which 8-bit runs BM = 128, one N tile per wave
+#define EP_PF_BIG8_M 128
 #endif
 #ifndef EP_PF_PD8
 #define EP_PF_PD8 3
@@ -428,10 +433,10 @@ PfPlan pf_plan(int bits, int64_t M, int64_t N, int64_t K)
     PfPlan p;
     if (bits == 4) {
         // measured: 128 x 2 tiles lead from M = 1024, 128 x 1 at 256..1023
-        p.bm = M >= 256 ? 128 : 64;
-        p.nt = M >= 256 && M < 1024 ? 1 : 2;
+        p.bm = M >= EP_PF_BIG4_M ? 128 : 64;
+        p.nt = M >= EP_PF_BIG4_M && M < 1024 ? 1 : 2;
         p.pd = p.bm == 128 && p.nt == 2 ? 2 : 4;
-        p.waves = M >= 256 ? 8 : 4;
+        p.waves = M >= EP_PF_BIG4_M ? 8 : 4;
     } else if (M >= EP_PF_BIG8_M) {
         p.bm = 128;
         p.pd = EP_PF_PD8;
