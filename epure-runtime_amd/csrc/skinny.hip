@@ -9,9 +9,9 @@
 //
 // At these M the contraction is HBM-bound: the packed bytes must stream at
 // full rate while the MFMA units and LDS are mostly idle.  So:
-//  * a workgroup (8 waves) owns one K split of KS values and up to kTpw row
+//  * a workgroup (8 waves) owns one K split of KS values and up to TPW row
 //    tiles of 128 rows (16 per wave); every one of its weight loads (16
-//    bytes per lane, kLoads per tile) is issued at kernel entry, before the
+//    bytes per lane, LD per tile, 16 in all) is issued at kernel entry, before the
 //    activation staging and the table build, so HBM streams from the first
 //    cycle;
 //  * weights are dequantized in registers straight into the B operand of
@@ -39,18 +39,26 @@ namespace {
 constexpr int kSkThreads = 512;
 constexpr int kSkWaves = kSkThreads / 64;
 constexpr int kSkRows = 16 * kSkWaves;  // rows of a row tile
-constexpr int kLoads = 4;               // 16-byte weight loads per lane and tile
-constexpr int kTpw = 4;                 // most row tiles one workgroup covers
+// 16-byte weight loads per lane and row tile (LD: 4, 8 or 16) and row
+// tiles per workgroup (16 / LD: 16 loads per lane in flight).  A longer K
+// split means fewer f32 partials [S][M][N] and fewer rounds of loads in the
+// ordered reduction; the launch takes the longest split whose grid still
+// fills every CU.  The staged activation tile (16 MT rows x K split, fp16)
+// stays within ~66 KiB next to the 64 KiB table: sk_ld_max.
+constexpr int sk_ld_max(int bits, int mt)
+{
+    return bits == 8 ? (mt <= 2 ? 16 : 8) : (mt == 1 ? 16 : (mt == 2 ? 8 : 4));
+}
 
 template <int BITS>
 constexpr int sk_kpl()
 {
     return BITS == 4 ? 32 : 16;  // weights per 16-byte load
 }
-template <int BITS>
+template <int BITS, int LD>
 constexpr int sk_ks()
 {
-    return kLoads * 4 * sk_kpl<BITS>();  // K per split: 256 bytes of a row
+    return LD * 4 * sk_kpl<BITS>();  // K per split: LD x 64 bytes of a row
 }
 
 constexpr uint32_t kOut = 0x7ffffff0u;  // a buffer offset past every buffer's end
@@ -91,11 +99,13 @@ EP_DEV __amdgpu_buffer_rsrc_t sk_rsrc(const void *p, uint32_t bytes)
                                              (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 
-template <int BITS, int MT, int XDT>
+template <int BITS, int MT, int XDT, int LD>
 __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
 {
     constexpr int KPL = sk_kpl<BITS>();
-    constexpr int KS = sk_ks<BITS>();
+    static_assert(LD <= sk_ld_max(BITS, MT), "activation tile within LDS");
+    constexpr int TPW = 16 / LD;
+    constexpr int KS = sk_ks<BITS, LD>();
     constexpr int SUB = KPL / 8;          // MFMA sub-steps per load
     constexpr int MR = 16 * MT;           // staged activation rows
     constexpr int XLD = KS + 8;           // halfs per staged row (padding: conflict-free reads)
@@ -135,15 +145,15 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
         const uint32_t off = ok ? (uint32_t)(((int64_t)xr * a.ldx + k) * XE) : kOut;
         xv[p] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
     }
-    u32x4_t w[kTpw][kLoads];
-    uint32_t sraw[kTpw][kLoads];  // fp16 scale bits; 0 where the chunk is masked
+    u32x4_t w[TPW][LD];
+    uint32_t sraw[TPW][LD];  // fp16 scale bits; 0 where the chunk is masked
 #pragma unroll
-    for (int t = 0; t < kTpw; ++t) {
+    for (int t = 0; t < TPW; ++t) {
         const int tile = (int)blockIdx.x + t * a.gtiles;
         const int n = tile * kSkRows + wave * 16 + j;
         const bool live = tile < a.tiles && n < a.N;
 #pragma unroll
-        for (int l = 0; l < kLoads; ++l) {
+        for (int l = 0; l < LD; ++l) {
             const int kc = ka + KPL * (4 * l + q);  // first k of the lane's chunk
             const bool ok = live && kc < a.K;
             const uint32_t off = (uint32_t)n * a.row_bytes + kbyte + (uint32_t)(16 * (4 * l + q));
@@ -213,7 +223,7 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
 
     const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
 #pragma unroll
-    for (int t = 0; t < kTpw; ++t) {
+    for (int t = 0; t < TPW; ++t) {
         const int tile = (int)blockIdx.x + t * a.gtiles;
         if (tile >= a.tiles)
             break;
@@ -222,7 +232,7 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
         for (int mt = 0; mt < MT; ++mt)
             acc[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int l = 0; l < kLoads; ++l) {
+        for (int l = 0; l < LD; ++l) {
             const f16_t s16 = f16_from_bits((uint16_t)sraw[t][l]);
             const f16x2_t s2 = (f16x2_t){s16, s16};
             f16x2_t pr[KPL / 2];
@@ -336,35 +346,60 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-int sk_splits(int bits, int64_t K) { return (int)((K + (bits == 4 ? sk_ks<4>() : sk_ks<8>()) - 1) / (bits == 4 ? sk_ks<4>() : sk_ks<8>())); }
+int sk_mt(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+int sk_split_k(int bits, int ld) { return ld * 4 * (bits == 4 ? sk_kpl<4>() : sk_kpl<8>()); }
+int sk_splits_ld(int bits, int ld, int64_t K) { return (int)((K + sk_split_k(bits, ld) - 1) / sk_split_k(bits, ld)); }
+// The longest split (most loads per tile) whose workgroups, one row tile
+// each at most, still fill the CUs; 4 when none does.
+int sk_choose_ld(int bits, int64_t M, int64_t N, int64_t K)
+{
+    const int64_t tiles = (N + kSkRows - 1) / kSkRows;
+    for (int ld = sk_ld_max(bits, sk_mt(M)); ld > 4; ld /= 2)
+        if (tiles * sk_splits_ld(bits, ld, K) >= device_cus())
+            return ld;
+    return 4;
+}
+int sk_splits(int bits, int64_t M, int64_t N, int64_t K) { return sk_splits_ld(bits, sk_choose_ld(bits, M, N, K), K); }
 
-template <int BITS, int MT>
+template <int BITS, int MT, int LD>
 int sk_launch_x(const SkArgs &a, int S, int xdt, hipStream_t s)
 {
     const dim3 grid((unsigned)a.gtiles, (unsigned)S);
     switch (xdt) {
     case EP_BF16:
-        hipLaunchKernelGGL((sk_kernel<BITS, MT, EP_BF16>), grid, dim3(kSkThreads), 0, s, a);
+        hipLaunchKernelGGL((sk_kernel<BITS, MT, EP_BF16, LD>), grid, dim3(kSkThreads), 0, s, a);
         break;
     case EP_F16:
-        hipLaunchKernelGGL((sk_kernel<BITS, MT, EP_F16>), grid, dim3(kSkThreads), 0, s, a);
+        hipLaunchKernelGGL((sk_kernel<BITS, MT, EP_F16, LD>), grid, dim3(kSkThreads), 0, s, a);
         break;
     default:
-        hipLaunchKernelGGL((sk_kernel<BITS, MT, EP_F32>), grid, dim3(kSkThreads), 0, s, a);
+        hipLaunchKernelGGL((sk_kernel<BITS, MT, EP_F32, LD>), grid, dim3(kSkThreads), 0, s, a);
         break;
     }
     EP_HIP_CHECK(hipGetLastError());
     return EP_OK;
 }
 
+template <int BITS, int MT>
+int sk_launch_ld(const SkArgs &a, int S, int ld, int xdt, hipStream_t s)
+{
+    if constexpr (sk_ld_max(BITS, MT) >= 16)
+        if (ld == 16)
+            return sk_launch_x<BITS, MT, 16>(a, S, xdt, s);
+    if constexpr (sk_ld_max(BITS, MT) >= 8)
+        if (ld == 8)
+            return sk_launch_x<BITS, MT, 8>(a, S, xdt, s);
+    return sk_launch_x<BITS, MT, 4>(a, S, xdt, s);
+}
+
 template <int BITS>
-int sk_launch_bits(const SkArgs &a, int S, int xdt, hipStream_t s)
+int sk_launch_bits(const SkArgs &a, int S, int ld, int xdt, hipStream_t s)
 {
     if (a.M <= 16)
-        return sk_launch_x<BITS, 1>(a, S, xdt, s);
+        return sk_launch_ld<BITS, 1>(a, S, ld, xdt, s);
     if (a.M <= 32)
-        return sk_launch_x<BITS, 2>(a, S, xdt, s);
-    return sk_launch_x<BITS, 4>(a, S, xdt, s);
+        return sk_launch_ld<BITS, 2>(a, S, ld, xdt, s);
+    return sk_launch_ld<BITS, 4>(a, S, ld, xdt, s);
 }
 
 }  // namespace
@@ -392,7 +427,7 @@ bool skinny_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
 size_t skinny_workspace(int64_t M, int64_t N, int64_t K, int levels)
 {
     // partial sums of every split (also with one split when accumulating)
-    return (size_t)sk_splits(levels <= 16 ? 4 : 8, K) * (size_t)M * (size_t)N * sizeof(float);
+    return (size_t)sk_splits(levels <= 16 ? 4 : 8, M, N, K) * (size_t)M * (size_t)N * sizeof(float);
 }
 
 int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y, void *ws,
@@ -401,7 +436,8 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     if (!skinny_serves(w, x, M))
         return EP_DECLINE_SHAPE;
     const int bits = w.bits();
-    const int S = sk_splits(bits, w.K);
+    const int ld = sk_choose_ld(bits, M, w.N, w.K);
+    const int S = sk_splits_ld(bits, ld, w.K);
     const bool partials = S > 1 || y.accumulate;
     const size_t need = partials ? skinny_workspace(M, w.N, w.K, w.levels) : 0;
     if (need > 0 && (!ws || ws_bytes < need))
@@ -428,10 +464,11 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     a.group = w.group;
     a.tiles = (int)((w.N + kSkRows - 1) / kSkRows);
     // one resident workgroup per CU: enough row-tile groups that S of them
-    // fill the device, at most kTpw tiles per workgroup
+    // fill the device, at most sk_tpw tiles per workgroup
     const int cus = device_cus();
+    const int tpw = 16 / ld;
     int g = (cus + S - 1) / S;
-    const int gmin = (a.tiles + kTpw - 1) / kTpw;
+    const int gmin = (a.tiles + tpw - 1) / tpw;
     if (g < gmin)
         g = gmin;
     if (g > a.tiles)
@@ -442,7 +479,7 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     a.ldy = y.ld;
     a.accumulate = y.accumulate;
     a.part = partials ? (float *)ws : nullptr;
-    const int rc = bits == 4 ? sk_launch_bits<4>(a, S, x.dtype, stream) : sk_launch_bits<8>(a, S, x.dtype, stream);
+    const int rc = bits == 4 ? sk_launch_bits<4>(a, S, ld, x.dtype, stream) : sk_launch_bits<8>(a, S, ld, x.dtype, stream);
     if (rc != EP_OK || !partials)
         return rc;
     return launch_split_reduce((const float *)ws, S, M, w.N, y, stream);

@@ -161,10 +161,28 @@ def test_skinny_deterministic():
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-def test_skinny_workspace_covers_partials():
+# Loads per lane and row tile of the small-M path, at most (the staged
+# activation rows x K split fit the LDS); a split is 64 bytes of a row per
+# load, and the launch takes the longest split whose grid (one 128-row tile
+# per workgroup at most) still fills the CUs.
+LD_MAX = {(16, 16): 16, (16, 32): 8, (16, 64): 4, (256, 16): 16, (256, 32): 16, (256, 64): 8}
+
+
+def skinny_splits(m, n, k, levels):
+    mb = 16 if m <= 16 else (32 if m <= 32 else 64)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    per_load = 128 if levels <= 16 else 64  # k values per load's 64 bytes
+    tiles = -(-n // 128)
+    ld = LD_MAX[(levels, mb)]
+    while ld > 4 and tiles * -(-k // (ld * per_load)) < cus:
+        ld //= 2
+    return -(-k // (ld * per_load))
+
+
+@pytest.mark.parametrize("m", [2, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("levels", [16, 256])
+@pytest.mark.parametrize("n,k", [(14336, 4096 + 64), (4096, 4096), (4096, 14336)])
+def test_skinny_workspace_covers_partials(m, levels, n, k):
     """The workspace query covers every split's partial sums."""
-    m, n, k = 64, 14336, 4096
-    need = _abi.lib.ep_dequant_matmul_workspace(m, n, k, 16, 128)
-    assert need >= (k // 512) * m * n * 4
-    need8 = _abi.lib.ep_dequant_matmul_workspace(m, n, k, 256, 128)
-    assert need8 >= (k // 256) * m * n * 4
+    need = _abi.lib.ep_dequant_matmul_workspace(m, n, k, levels, 128)
+    assert need >= skinny_splits(m, n, k, levels) * m * n * 4
