@@ -64,17 +64,9 @@ struct BwdArgs {
     float *dx_part;      // [splits][M][K] f32 partials (null: one split, results go to gx)
 };
 
-// Buffer descriptor over `bytes` bytes at p: loads at offsets past the end
-// read zeros.  kBwOut is past the end of every descriptor.
+// A buffer offset past the end of every descriptor (buffer_rsrc: loads
+// there read zeros); sums of two such parts stay below 2^32.
 constexpr uint32_t kBwOut = 0x7fffff00u;
-EP_DEV __amdgpu_buffer_rsrc_t bw_rsrc(const void *p, uint32_t bytes)
-{
-    const uint64_t v = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
-                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
-}
 
 EP_DEV uint32_t bits_of(f16x2_t v)
 {
@@ -204,9 +196,9 @@ __global__ void __launch_bounds__(256, 2) dx_kernel(BwdArgs a)
     const uint32_t rowb = (uint32_t)(a.K / 2);
     constexpr int SE = SDT == EP_F32 ? 4 : 2;
     const int64_t gleft = (int64_t)(a.M - m0) * a.N * 2;
-    const auto rg = bw_rsrc(a.gy16 + (int64_t)m0 * a.N, gleft < kBwOut ? (uint32_t)gleft : kBwOut);
-    const auto rw = bw_rsrc(a.packed, (uint32_t)((int64_t)a.N * rowb));
-    const auto rs = bw_rsrc(a.scale, (uint32_t)(((int64_t)(a.N - 1) * a.lds + a.K / a.group) * SE));
+    const auto rg = buffer_rsrc(a.gy16 + (int64_t)m0 * a.N, gleft < kBwOut ? (uint32_t)gleft : kBwOut);
+    const auto rw = buffer_rsrc(a.packed, (uint32_t)((int64_t)a.N * rowb));
+    const auto rs = buffer_rsrc(a.scale, (uint32_t)(((int64_t)(a.N - 1) * a.lds + a.K / a.group) * SE));
     const uint32_t kbyte = (uint32_t)((k0 + kb * 8) / 2);
     const int kgrp = (k0 + kb * 8) / a.group;
     u32x4_t gva[4], gvb[4];
@@ -372,7 +364,7 @@ __global__ void __launch_bounds__(256, 3) dw_kernel(BwdArgs a)
     const uint32_t offr = (uint32_t)rowb;
     auto load = [&](int mb, u32x4_t (&rr)[8]) {
         const int64_t left = total - (int64_t)mb * rowb;
-        const auto rsrc = bw_rsrc(base + (left > 0 ? (int64_t)mb * rowb : 0),
+        const auto rsrc = buffer_rsrc(base + (left > 0 ? (int64_t)mb * rowb : 0),
                                   left > 0 ? (left < kBwOut ? (uint32_t)left : kBwOut) : 0u);
 #pragma unroll
         for (int i = 0; i < 8; ++i)

@@ -104,6 +104,20 @@ EP_DEV int row_exponent(float amax)
 // serialize a prologue with the weight loads it is meant to overlap.
 EP_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Raw buffer descriptor over `bytes` bytes at a wave-uniform base p: a load
+// at an offset past the end reads zeros.  Base and size go through
+// readfirstlane so the descriptor is known to live in scalar registers (one
+// the compiler cannot prove uniform turns every load into a per-lane
+// waterfall loop).
+EP_DEV __amdgpu_buffer_rsrc_t buffer_rsrc(const void *p, uint32_t bytes = 0x7fffffffu)
+{
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
+                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
 // Cross-workgroup hand-off without device-scope fences.  On gfx950 a
 // device-scope fence writes back and invalidates the whole L2 of the XCD;
 // instead, values another workgroup will read are stored and loaded as

@@ -78,15 +78,6 @@ struct PfArgs {
     float *part;     // [S][M][N] partials (null: results go straight to y)
 };
 
-EP_DEV __amdgpu_buffer_rsrc_t pf_rsrc(const void *p, uint32_t bytes)
-{
-    const uint64_t v = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
-                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
-}
-
 // Per-row exponent of the largest |x| (row_exponent), then the row rescaled
 // by 2^-e and rounded to fp16 into xh [M][K] (one wave per row, 16-byte
 // loads, four in flight per lane; the second pass re-reads the row from the
@@ -196,8 +187,8 @@ __global__ void __launch_bounds__(WAVES * 64, 8 / WAVES) pf_kernel(PfArgs a)
     const int m0 = blockIdx.y * BM;
     const int kt0 = blockIdx.z * a.ksteps;
     const int nk = a.K / kPfBK;
-    const auto rx = pf_rsrc(a.x, a.xbytes), rw = pf_rsrc(a.packed, a.wbytes);
-    const auto rs = pf_rsrc(a.scale, a.sbytes), rcb = pf_rsrc(a.cb, a.cbbytes);
+    const auto rx = buffer_rsrc(a.x, a.xbytes), rw = buffer_rsrc(a.packed, a.wbytes);
+    const auto rs = buffer_rsrc(a.scale, a.sbytes), rcb = buffer_rsrc(a.cb, a.cbbytes);
 
     // ---- first loads: codebook, row exponents, step 0's activations
     const uint32_t cbraw = __builtin_amdgcn_raw_buffer_load_b32(rcb, tid * 4, 0, 0);

@@ -88,17 +88,6 @@ struct SkArgs {
     float *part;  // [S][M][N] partials (null: results go straight to y)
 };
 
-// Buffer resource of `bytes` bytes at p (raw, no stride; loads past the end
-// return 0).  p and bytes are kernel arguments, i.e. already uniform.
-EP_DEV __amdgpu_buffer_rsrc_t sk_rsrc(const void *p, uint32_t bytes)
-{
-    const uint64_t v = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
-                                             (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
-}
-
 template <int BITS, int MT, int XDT, int LD>
 __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
 {
@@ -127,8 +116,8 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
     const int split = blockIdx.y;
     const int ka = split * KS;
     const uint32_t kbyte = BITS == 4 ? (uint32_t)ka / 2 : (uint32_t)ka;
-    const auto rx = sk_rsrc(a.x, a.xbytes), rw = sk_rsrc(a.packed, a.wbytes);
-    const auto rs = sk_rsrc(a.scale, a.sbytes), rcb = sk_rsrc(a.cb, a.cbbytes);
+    const auto rx = buffer_rsrc(a.x, a.xbytes), rw = buffer_rsrc(a.packed, a.wbytes);
+    const auto rs = buffer_rsrc(a.scale, a.sbytes), rcb = buffer_rsrc(a.cb, a.cbbytes);
 
     // ---- loads, in the order they are needed: vector-memory results return
     // in order, so a wait for the activations must not also wait for the

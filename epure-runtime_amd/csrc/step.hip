@@ -168,19 +168,6 @@ EP_DEV float ldg_as_f32(const void *p, int dt, int64_t i)
     return bf16_to_f32(ldg((const uint16_t *)p + i));
 }
 
-// Buffer descriptor of a wave-uniform base pointer.  The base goes through
-// readfirstlane so the descriptor is known to live in scalar registers (a
-// descriptor the compiler cannot prove uniform turns every load into a
-// per-lane waterfall loop).
-EP_DEV __amdgpu_buffer_rsrc_t rsrc(const void *p, uint32_t bytes = 0x7fffffffu)
-{
-    const uint64_t v = (uint64_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return __builtin_amdgcn_make_buffer_rsrc((void *)(((uint64_t)hi << 32) | lo), 0,
-                                             (int)__builtin_amdgcn_readfirstlane(bytes),
-                                             0x00020000);
-}
 // 16-byte load with sc1 (coherent at agent scope: sees other XCDs' sc1 stores).
 EP_DEV u32x4_t ldc16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off)
 {
@@ -444,7 +431,7 @@ struct Gemv {
             const bool ok = live && vq < sg.qb;
             const int s = seg_of(sg, ok ? vq : sg.qa, i);
             const int quad = ok ? vq - first_quad(sg, s) : 0;
-            const auto rp = rsrc(sel3(s, sg.pk0, sg.pk1, sg.pk2), live ? 0x7fffffffu : 0u);
+            const auto rp = buffer_rsrc(sel3(s, sg.pk0, sg.pk1, sg.pk2), live ? 0x7fffffffu : 0u);
             bk.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)(rq * RB + chunk_byte(j, wv)),
                                                             quad * 4 * RB, kAuxStream);
         }
@@ -720,7 +707,7 @@ template <int XS, int K>
 EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, uint32_t *xs,
                    uint32_t *xl, float *xf, float *part8, int *err)
 {
-    const auto rs = rsrc(x);
+    const auto rs = buffer_rsrc(x);
     float ssq = 0.0f;
     for (int e = tid_fresh(); e < K / 8; e += kThreads) {
         float v[8];
@@ -852,8 +839,8 @@ EP_DEV void attn_load(AttnRegs &r, const uint16_t *kc, const uint16_t *vc, int j
     const int pw0 = c * kChunk + wave * kRowsPerWave;
     const uint32_t bytes = pw0 <= pos ? kRowsPerWave * kD * 2u : 0u;
     const int64_t row0 = pw0 <= pos ? (int64_t)j * max_pos + pw0 : 0;
-    const auto rk = rsrc(kc + row0 * kD, bytes);
-    const auto rv = rsrc(vc + row0 * kD, bytes);
+    const auto rk = buffer_rsrc(kc + row0 * kD, bytes);
+    const auto rv = buffer_rsrc(vc + row0 * kD, bytes);
     const uint32_t off = (uint32_t)lane * 16;  // row lane >> 4, dims 8 (lane & 15)
 #pragma unroll
     for (int k = 0; k < kLoadsPerWave; ++k)
