@@ -275,9 +275,21 @@ def traffic_from_profile():
     return None
 
 
+def cpu_model():
+    """The host CPU's model name (Linux /proc/cpuinfo)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(cfg, threads):
     """Reference Rust kernel semantics (C port) on one layer's 7 packed
-    linears; tok/s ceiling = 1 / (time per layer * layers)."""
+    linears; tok/s ceiling = 1 / (time per layer * layers), on all host
+    threads and on one."""
     import numpy as np
     from oracle import ref, rowdot
     shapes = cfg.packed_linear_shapes()
@@ -290,22 +302,28 @@ def cpu_baseline(cfg, threads):
                      cb.astype(np.float32)))
     nt = threads or rowdot.threads()
 
-    def layer():
-        for x, p, s, c in data:
-            rowdot.dequant_matmul(x, p, s, c, cfg.group, True, nthreads=nt)
-    layer()                                       # warm-up
-    times = []
-    t_end = time.perf_counter() + 10.0
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
-        t0 = time.perf_counter()
-        layer()
-        times.append(time.perf_counter() - t0)
-    t_layer = float(np.median(times))
+    def timed(threads_used, budget_s):
+        def layer():
+            for x, p, s, c in data:
+                rowdot.dequant_matmul(x, p, s, c, cfg.group, True, nthreads=threads_used)
+        layer()                                   # warm-up
+        times = []
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+            t0 = time.perf_counter()
+            layer()
+            times.append(time.perf_counter() - t0)
+        return float(np.median(times)), len(times)
+
+    t_layer, runs = timed(nt, 10.0)
+    t_one, runs_one = timed(1, 8.0)
     return {"value": round(1.0 / (t_layer * cfg.layers), 4), "unit": "tok/s", "cores": nt,
-            "kind": "port",
+            "kind": "port", "cpu_model": cpu_model(),
+            "value_1_thread": round(1.0 / (t_one * cfg.layers), 4),
             "sample": f"C port of kernel/src/lib.rs on one layer's 7 packed linears "
                       f"({sum(n * k for _, n, k in shapes) / 1e6:.0f}M weights, f32 x), median of "
-                      f"{len(times)} runs = {t_layer * 1e3:.1f} ms, scaled x{cfg.layers} layers "
+                      f"{runs} runs = {t_layer * 1e3:.1f} ms on {nt} threads ({runs_one} runs = "
+                      f"{t_one * 1e3:.1f} ms on 1 thread), scaled x{cfg.layers} layers "
                       f"(linears only, lm_head excluded)"}
 
 
@@ -335,6 +353,7 @@ def cpu_gemv_baseline(n, k, levels, ms, threads):
     wb = _weight_bytes(n, k, levels)
     m, t, runs = out[0]
     return {"value": round(wb / t / 1e9, 3), "unit": "GB/s", "cores": nt, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"C port of kernel/src/lib.rs, {n}x{k} {'4' if levels <= 16 else '8'}-bit "
                       f"linear, f32 x; " + "; ".join(
                           f"M={m_}: {t_ * 1e3:.2f} ms (median of {r_})" for m_, t_, r_ in out)}
@@ -462,12 +481,17 @@ def main():
     packed = w.packed_bytes()
     norm_bytes = sum(t.numel() * 2 for L in w.layers
                      for t in (L.attn_norm, L.mlp_norm, L.q_norm, L.k_norm) if t is not None)
-    kv_bytes = 2 * cfg.layers * cfg.n_kv * pos * cfg.head_dim * 2
+    # the replayed step reads KV rows 0..pos-1 from the f32 cache
+    kv_bytes = 2 * cfg.layers * cfg.n_kv * pos * cfg.head_dim * 4
     alg = packed + norm_bytes + kv_bytes
     kern_gbs = alg / (kern_ms * 1e-3) / 1e9
-    resident = w.resident_bytes()
     step_ms = dt / args.steps * 1e3
-
+    # whole-model bytes a token must read: the packed linears, the bf16
+    # lm_head (the tied embedding when tied), the norm weights and ONE
+    # embedding row (the step gathers a single row of the table)
+    lm_bytes = w.lm_head.numel() * 2
+    model_bytes = packed + lm_bytes + norm_bytes + w.final_norm.numel() * 2 + cfg.hidden * 2
+    first_pos = n_prompt - 1 + args.warmup
     out = {
         "metric": METRIC,
         "value": round(tok_s, 2),
@@ -487,10 +511,11 @@ def main():
                         f"prompt {n_prompt}",
             "layers": cfg.layers, "hidden": cfg.hidden, "intermediate": cfg.intermediate,
             "vocab": cfg.vocab, "prompt": n_prompt, "decoded": args.warmup + args.steps,
-            "packed_linear_bytes": packed, "resident_weight_bytes": resident,
-            "step_hbm_gbs_resident": round(resident / (step_ms * 1e-3) / 1e9, 1),
-            "step_frac_resident": round(resident / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "packed_linear_bytes": packed, "model_bytes_per_token": model_bytes,
+            "step_gbs_model": round(model_bytes / (step_ms * 1e-3) / 1e9, 1),
+            "step_frac_model": round(model_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "step_frac_packed": round(packed / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "timed_kv_positions": [first_pos, first_pos + args.steps - 1],
             "layers_path": "per-layer launches" if args.per_layer else "one-launch step kernel",
             "layers_ms_per_step": round(kern_ms, 4),
             "layers_alg_bytes": alg,
@@ -505,6 +530,10 @@ def main():
             "unit": "GB/s",
             "frac": round(kern_gbs / HBM_PEAK_GBS, 4),
             "traffic": None if args.per_layer else traffic_from_profile(),
+            "traffic_source": None if args.per_layer else
+            "profiles/decode_step_llama3_8b_traffic.md: rocprofv3 FETCH_SIZE and WRITE_SIZE passes "
+            "over this command's roofline replays (its final KV position is stated there), "
+            "calibrated by bench.py --copy-probe; not measured in this run",
         },
     }
     if not args.no_gemv:

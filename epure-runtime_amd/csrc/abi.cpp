@@ -172,7 +172,8 @@ int ep_dequant_matmul_bwd(const void *gy, int gy_dtype, int64_t ldgy, const void
         return set_error(EP_DECLINE_DTYPE, "gy/x/grad_x dtype not served");
     if (M < 0)
         return set_error(EP_ERR_ARG, "negative M");
-    if (ldgy < N || ldx < K || (grad_x && ldgx < K) ||
+    // activation strides only matter where there are rows to read
+    if ((M > 0 && (ldgy < N || ldx < K || (grad_x && ldgx < K))) ||
         (grad_scale && ld_gscale < (K + group - 1) / group))
         return set_error(EP_ERR_ARG, "leading dimension smaller than the row length");
     ActDesc gya{gy, gy_dtype, ldgy};
@@ -269,9 +270,9 @@ size_t ep_attention_workspace(int Hq, int D, int max_pos)
 }
 
 int ep_decode_attention(const float *q, const float *k, const float *v, const uint16_t *qn_w,
-                        const uint16_t *kn_w, float qk_eps, uint16_t *kcache, uint16_t *vcache,
+                        const uint16_t *kn_w, float qk_eps, float *kcache, float *vcache,
                         const float *cos_t, const float *sin_t, const int *state, float *part,
-                        int *counters, uint16_t *out, int Hq, int Hkv, int D, int max_pos,
+                        int *counters, float *out, int Hq, int Hkv, int D, int max_pos,
                         float scale, void *stream)
 {
     g_err[0] = 0;

@@ -511,6 +511,16 @@ __global__ void __launch_bounds__(256) gc_final_kernel(const float *part, int nw
         gcb[lev] = red[0];
 }
 
+// rows x cols f32 zeros (row stride ld): 4 rows per workgroup of 256
+__global__ void __launch_bounds__(256) zero_rows_kernel(float *p, int rows, int cols, int64_t ld)
+{
+    const int r = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (r >= rows)
+        return;
+    for (int c = (int)(threadIdx.x & 63); c < cols; c += 64)
+        p[(int64_t)r * ld + c] = 0.0f;
+}
+
 }  // namespace
 
 // Splits of the dx contraction: enough work items for the three resident
@@ -519,6 +529,8 @@ __global__ void __launch_bounds__(256) gc_final_kernel(const float *part, int nw
 static int dx_splits(int64_t M, int64_t N, int64_t K)
 {
     const int64_t tiles = ((K + T - 1) / T) * ((M + T - 1) / T);
+    if (tiles <= 0)
+        return 1;
     const int64_t nsteps = (N + CS - 1) / CS;
     const int64_t slots = 3 * (int64_t)device_cus();
     int64_t S = (slots + tiles - 1) / tiles;
@@ -533,6 +545,8 @@ size_t backward_workspace(int64_t M, int64_t N, int64_t K, int levels, int group
 {
     (void)levels;
     (void)group;
+    if (M <= 0 || N <= 0 || K <= 0)
+        return 0;
     const int64_t nwg = ((K + T - 1) / T) * ((N + T - 1) / T);
     const int S = dx_splits(M, N, K);
     return (size_t)((M * 4 + 255) / 256 * 256) + (size_t)nwg * 16 * sizeof(float) +
@@ -558,8 +572,19 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         return set_error(EP_DECLINE_SHAPE,
                          "fused backward serves levels <= 16, K %% 128 == 0, N %% 16 == 0, group "
                          "in {32, 64, 128}, bf16 gy and x");
-    if (M <= 0 || w.N <= 0)
+    if (M <= 0 || w.N <= 0) {
+        // no tokens: grad_x is empty, grad_cb and grad_scale are sums over
+        // nothing (zeros, written by a kernel so the call stays capturable)
+        const int G = (int)((w.K + w.group - 1) / w.group);
+        if (grad_scale && w.N > 0 && G > 0)
+            hipLaunchKernelGGL(zero_rows_kernel, dim3((unsigned)((w.N + 3) / 4)), dim3(256), 0,
+                               stream, grad_scale, (int)w.N, G, ld_gscale);
+        if (grad_cb)
+            hipLaunchKernelGGL(zero_rows_kernel, dim3(1), dim3(256), 0, stream, grad_cb, 1,
+                               w.levels, (int64_t)w.levels);
+        EP_HIP_CHECK(hipGetLastError());
         return EP_OK;
+    }
     const size_t need = backward_workspace(M, w.N, w.K, w.levels, w.group);
     if (!ws || ws_bytes < need)
         return set_error(EP_ERR_WORKSPACE, "backward workspace of %zu bytes needed, %zu given",

@@ -24,7 +24,6 @@ namespace {
 constexpr int kChunk = 64;  // KV positions per attention workgroup
 constexpr int kMaxD = 128;  // head_dim served
 
-EP_DEV float bf16_round(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 // Sum of a value held by every thread of a 256-thread workgroup.
 EP_DEV float block_sum256(float v, float *scratch)
@@ -73,14 +72,14 @@ struct AttnArgs {
     const uint16_t *qn_w;  // [D] bf16 q RMSNorm weight, or null
     const uint16_t *kn_w;  // [D] bf16 k RMSNorm weight, or null
     float qk_eps;
-    uint16_t *kcache;      // [Hkv][max_pos][D] bf16
-    uint16_t *vcache;      // [Hkv][max_pos][D] bf16
+    float *kcache;         // [Hkv][max_pos][D] f32
+    float *vcache;         // [Hkv][max_pos][D] f32
     const float *cos_t;    // [max_pos][D / 2]
     const float *sin_t;
     const int *state;      // state[0] = position of this step's token
     float *part;           // [Hq][max_chunks][D + 2]
     int *counters;         // [Hq], zero between launches
-    uint16_t *out;         // [Hq * D] bf16
+    float *out;            // [Hq * D] f32
     int Hq, Hkv, D, max_pos;
     float scale;
 };
@@ -89,7 +88,9 @@ struct AttnArgs {
 // head h over positions [c * 64, c * 64 + 64) ∩ [0, pos]; the last chunk
 // also holds this step's key/value, which the first query head of the
 // group writes to the cache.  Other workgroups never read cache row `pos`,
-// so there is no write/read race on it.
+// so there is no write/read race on it.  Cache rows, scores, softmax and
+// the output are float32 (the precision of the reference model's float32
+// forward, runtime.py:_runtime_dtype on CPU).
 __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
 {
     __shared__ float qs[kMaxD], kn[kMaxD], vn[kMaxD];
@@ -111,31 +112,32 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
     const int t1 = min(t0 + kChunk, pos + 1);
     const float *cs = a.cos_t + (int64_t)pos * (D / 2);
     const float *sn = a.sin_t + (int64_t)pos * (D / 2);
-    const uint16_t *kbase = a.kcache + (int64_t)kvh * a.max_pos * D;
-    const uint16_t *vbase = a.vcache + (int64_t)kvh * a.max_pos * D;
+    const float *kbase = a.kcache + (int64_t)kvh * a.max_pos * D;
+    const float *vbase = a.vcache + (int64_t)kvh * a.max_pos * D;
 
     // K and V tiles go out first: they depend only on the position.
-    // K: thread -> (position t/4, D/4-dim quarter t%4); V: thread ->
-    // (8-dim slice t%16, positions t/16 + 16 i).  Cache row `pos` is not read
-    // (this step's k/v come from the projections below).
+    // K: thread -> (position t/4, D/4-dim quarter t%4, 4 dims per load);
+    // V: thread -> (8-dim slice t%16, positions t/16 + 16 i).  Cache row
+    // `pos` is not read (this step's k/v come from the projections below).
     const int ktl = t >> 2, kq = t & 3, kdn = D / 4;
     const bool kok = t0 + ktl < t1 && t0 + ktl != pos;
-    u32x4_t kr[4];
+    f32x4_t kr[kMaxD / 16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int d = kq * kdn + i * 8;
-        kr[i] = (kok && d < (kq + 1) * kdn)
-                    ? *(const u32x4_t *)(kbase + (int64_t)(t0 + ktl) * D + d)
-                    : (u32x4_t){0, 0, 0, 0};
+    for (int i = 0; i < kMaxD / 16; ++i) {
+        const int d = kq * kdn + i * 4;
+        kr[i] = (kok && i * 4 < kdn) ? *(const f32x4_t *)(kbase + (int64_t)(t0 + ktl) * D + d)
+                                     : (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
     }
     const int vdc = t & 15, vpg = t >> 4;
-    u32x4_t vr[4];
+    f32x4_t vr[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int tl = vpg + 16 * i;
         const bool ok = t0 + tl < t1 && t0 + tl != pos && vdc * 8 < D;
-        vr[i] = ok ? *(const u32x4_t *)(vbase + (int64_t)(t0 + tl) * D + vdc * 8)
-                   : (u32x4_t){0, 0, 0, 0};
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+            vr[i][hh] = ok ? *(const f32x4_t *)(vbase + (int64_t)(t0 + tl) * D + vdc * 8 + 4 * hh)
+                           : (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
     }
 
     if (t < D)
@@ -143,19 +145,15 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
     const bool has_new = (c == nact - 1);
     if (has_new && t < D) {
         kn[t] = a.k[kvh * D + t];
-        vn[t] = bf16_round(a.v[kvh * D + t]);
+        vn[t] = a.v[kvh * D + t];
     }
     norm_rope(qs, a.qn_w, a.qk_eps, cs, sn, D, scratch);
     if (has_new) {
         norm_rope(kn, a.kn_w, a.qk_eps, cs, sn, D, scratch);
-        if (t < D) {
-            const float kr16 = bf16_round(kn[t]);
-            kn[t] = kr16;
-            if (h % group == 0) {
-                const int64_t row = ((int64_t)kvh * a.max_pos + pos) * D + t;
-                a.kcache[row] = f32_to_bf16(kr16);
-                a.vcache[row] = f32_to_bf16(vn[t]);
-            }
+        if (t < D && h % group == 0) {
+            const int64_t row = ((int64_t)kvh * a.max_pos + pos) * D + t;
+            a.kcache[row] = kn[t];
+            a.vcache[row] = vn[t];
         }
         __syncthreads();
     }
@@ -171,14 +169,11 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
                     s = fmaf(qs[d], kn[d], s);
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    if (i * 8 < kdn) {
+                for (int i = 0; i < kMaxD / 16; ++i)
+                    if (i * 4 < kdn) {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int d = d0 + i * 8 + 2 * e;
-                            s = fmaf(qs[d], __uint_as_float(kr[i][e] << 16), s);
-                            s = fmaf(qs[d + 1], __uint_as_float(kr[i][e] & 0xffff0000u), s);
-                        }
+                        for (int e = 0; e < 4; ++e)
+                            s = fmaf(qs[d0 + i * 4 + e], kr[i][e], s);
                     }
             }
         }
@@ -211,17 +206,9 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
             const int tp = t0 + tl;
             if (tp < t1) {
                 const float p = sc[tl];
-                if (tp == pos) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        o[e] = fmaf(p, vn[vdc * 8 + e], o[e]);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        o[2 * e] = fmaf(p, __uint_as_float(vr[i][e] << 16), o[2 * e]);
-                        o[2 * e + 1] = fmaf(p, __uint_as_float(vr[i][e] & 0xffff0000u), o[2 * e + 1]);
-                    }
-                }
+                for (int e = 0; e < 8; ++e)
+                    o[e] = fmaf(p, tp == pos ? vn[vdc * 8 + e] : vr[i][e >> 2][e & 3], o[e]);
             }
         }
 #pragma unroll
@@ -264,7 +251,7 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a)
             o = fmaf(ld_agent(pj + 2 + t), w, o);
     }
     if (t < D)
-        a.out[h * D + t] = f32_to_bf16(o / L);
+        a.out[h * D + t] = o / L;
     if (t == 0)
         st_agent(&a.counters[h], 0);
 }
@@ -288,7 +275,7 @@ struct HeadArgs {
     int max_pos;
 };
 
-constexpr int kHeadPerLane = 64;  // bf16 activations per lane: H <= 4096
+constexpr int kHeadPerLane = 64;  // activations per lane: H <= 4096
 
 template <int CTRL>
 EP_DEV float dpp_f(float v)
@@ -307,17 +294,18 @@ EP_DEV float row16_sum_dpp(float v)
 }
 
 // lm_head GEMV with the final RMSNorm fused in front and greedy selection
-// behind.  The workgroup normalizes the residual once into LDS (bf16, as the
-// reference's bf16 model feeds its lm_head); each wave keeps its 64 values
-// in registers and streams whole rows with 16-byte loads, two rows in
-// flight; row sums use DPP within 16-lane rows and readlane across them.
+// behind.  The workgroup normalizes the residual once into LDS (float32: the
+// reference model's float32 forward); each wave keeps its 64 values in
+// registers and streams whole bf16 rows with 16-byte loads, two rows in
+// flight, every product an exact f32 FMA of the widened bf16 weight; row
+// sums use DPP within 16-lane rows and readlane across them.
 __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
 {
     __shared__ float wv[4];
     __shared__ int wi[4];
     __shared__ float ssq_s[4];
     __shared__ int s_last;
-    __shared__ __align__(16) uint16_t xs[64 * kHeadPerLane];
+    __shared__ __align__(16) float xs[64 * kHeadPerLane];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = a.H;
     const int nld = H / 512;  // 16-byte loads per lane per row
@@ -351,17 +339,22 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
     __syncthreads();
     const float rinv = rsqrtf((ssq_s[0] + ssq_s[1] + ssq_s[2] + ssq_s[3]) / (float)H + a.eps);
     for (int k = threadIdx.x; k < H; k += 256)
-        xs[k] = f32_to_bf16(bf16_round(a.h[k] * rinv) * bf16_to_f32(a.norm_w[k]));
+        xs[k] = a.h[k] * rinv * bf16_to_f32(a.norm_w[k]);
     __syncthreads();
-    bf16x2_t x[kHeadPerLane / 2];
+    // lane's values: dims (lane + 64 i) * 8 .. + 7 of load i
+    float x[kHeadPerLane];
 #pragma unroll
     for (int i = 0; i < kHeadPerLane / 8; ++i) {
-        u32x4_t q4 = (u32x4_t){0, 0, 0, 0};
-        if (i < nld)
-            q4 = *(const u32x4_t *)(xs + (lane + 64 * i) * 8);
+        f32x4_t a0 = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f}, a1 = a0;
+        if (i < nld) {
+            a0 = *(const f32x4_t *)(xs + (lane + 64 * i) * 8);
+            a1 = *(const f32x4_t *)(xs + (lane + 64 * i) * 8 + 4);
+        }
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            x[4 * i + e] = as_bf16x2(q4[e]);
+        for (int e = 0; e < 4; ++e) {
+            x[8 * i + e] = a0[e];
+            x[8 * i + 4 + e] = a1[e];
+        }
     }
 
     float best = -INFINITY;
@@ -374,9 +367,12 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
             for (int i = 0; i < kHeadPerLane / 8; ++i)
                 if (i < nld) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        sacc[q] = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(w[q][i][e]),
-                                                                  x[4 * i + e], sacc[q], false);
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t wp = w[q][i][e];
+                        sacc[q] = fmaf(__uint_as_float(wp << 16), x[8 * i + 2 * e], sacc[q]);
+                        sacc[q] = fmaf(__uint_as_float(wp & 0xffff0000u), x[8 * i + 2 * e + 1],
+                                       sacc[q]);
+                    }
                 }
         if (rb + 2 * nw < a.V)
             load_rows(rb + 2 * nw);  // next rows in flight during the reduction

@@ -70,17 +70,17 @@ struct FusedGemv {
 };
 int launch_gemv_fused(const FusedGemv &f, hipStream_t stream);
 
-// Decode attention over a bf16 KV cache (decode.hip).
+// Decode attention over an f32 KV cache (decode.hip).
 struct AttnDesc {
     const float *q, *k, *v;
     const uint16_t *qn_w, *kn_w;
     float qk_eps;
-    uint16_t *kcache, *vcache;
+    float *kcache, *vcache;  // [Hkv][max_pos][D]
     const float *cos_t, *sin_t;
     const int *state;
     float *part;
     int *counters;
-    uint16_t *out;
+    float *out;  // [Hq * D]
     int Hq, Hkv, D, max_pos;
     float scale;
 };

@@ -91,6 +91,28 @@ struct GemvArgs {
     Seg seg[kMaxSeg];
 };
 
+// Writes one chunk of 2 * PAIRS activations (already multiplied by the
+// chunk's power of two pw) as fp16 pairs, and with HL their lo terms.
+template <bool HL, int PAIRS>
+EP_DEV void stage_chunk(const float *v, float pw, uint32_t *hi, uint32_t *lo)
+{
+#pragma unroll
+    for (int p = 0; p < PAIRS; p += 4) {
+        u32x4_t q4, l4;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float a0 = v[2 * (p + t)] * pw, a1 = v[2 * (p + t) + 1] * pw;
+            const f16_t h0 = (f16_t)a0, h1 = (f16_t)a1;
+            q4[t] = (uint32_t)f16_bits(h0) | ((uint32_t)f16_bits(h1) << 16);
+            l4[t] = (uint32_t)f16_bits((f16_t)(a0 - (float)h0)) |
+                    ((uint32_t)f16_bits((f16_t)(a1 - (float)h1)) << 16);
+        }
+        *(u32x4_t *)(hi + p) = q4;
+        if constexpr (HL)
+            *(u32x4_t *)(lo + p) = l4;
+    }
+}
+
 template <int BITS, int MT, int RQ, int SPW, int XDT, int XS, bool DB, int XCAP>
 __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
 {
@@ -106,7 +128,13 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     __shared__ float s_part[kMaxWaves];            // sum-of-squares partials
     __shared__ uint16_t s_cb[256];                 // codebook as fp16 bits
     __shared__ float s_rinv;
+    // f32 activations are carried as two fp16 terms, hi = fp16(x) and
+    // lo = fp16(x - hi) (~22 significant bits together, after the chunk's
+    // power-of-two factor): every table lookup feeds two dot products, so
+    // an f32 row is not narrowed to fp16.  16-bit rows are exact in hi.
+    constexpr bool HL = XDT == EP_F32;
     __shared__ __align__(16) uint32_t xs[XCAP * MT];      // staged activations, fp16 pairs
+    __shared__ __align__(16) uint32_t xl[HL ? XCAP * MT : 4];  // their lo terms
     __shared__ float xf[(2 * XCAP / (BITS == 4 ? 32 : 16)) * MT];  // 2^e per chunk
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -300,16 +328,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
             am = fmaxf(am, fabsf(v[t]));
         const int e = row_exponent(am);
         const float pw = ldexpf(1.0f, -e);
-        uint32_t *dst = xs + cc * PAIRS;
-#pragma unroll
-        for (int p = 0; p < PAIRS; p += 4) {
-            u32x4_t q4;
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-                q4[t] = (uint32_t)f16_bits((f16_t)(v[2 * (p + t)] * pw)) |
-                        ((uint32_t)f16_bits((f16_t)(v[2 * (p + t) + 1] * pw)) << 16);
-            *(u32x4_t *)(dst + p) = q4;
-        }
+        stage_chunk<HL, PAIRS>(v, pw, xs + cc * PAIRS, xl + cc * PAIRS);
         xf[cc] = ldexpf(1.0f, e);
     }
 #pragma unroll
@@ -373,16 +392,8 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                 am = fmaxf(am, fabsf(v[t]));
             const int e = row_exponent(am);
             const float pw = ldexpf(1.0f, -e);
-            uint32_t *dst = xs + m * XCAP + cc * PAIRS;
-#pragma unroll
-            for (int p = 0; p < PAIRS; p += 4) {
-                u32x4_t q4;
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    q4[t] = (uint32_t)f16_bits((f16_t)(v[2 * (p + t)] * pw)) |
-                            ((uint32_t)f16_bits((f16_t)(v[2 * (p + t) + 1] * pw)) << 16);
-                *(u32x4_t *)(dst + p) = q4;
-            }
+            stage_chunk<HL, PAIRS>(v, pw, xs + m * XCAP + cc * PAIRS,
+                                   xl + (HL ? m * XCAP + cc * PAIRS : 0));
             xf[m * NCH + cc] = ldexpf(1.0f, e);
         }
     }
@@ -421,6 +432,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     }
     // this lane's activation chunks, from LDS into registers
     f16x2_t xh[SPW][MT][PAIRS];
+    f16x2_t xlo[HL ? SPW : 1][HL ? MT : 1][HL ? PAIRS : 1];
     float fexp[SPW][MT];
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
@@ -434,6 +446,12 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
                     xh[j][m][p + t] = as_f16x2(q4[t]);
+                if constexpr (HL) {
+                    const u32x4_t l4 = *(const u32x4_t *)(xl + m * XCAP + cc * PAIRS + p);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        xlo[j][m][p + t] = as_f16x2(l4[t]);
+                }
             }
             fexp[j][m] = act[j] ? xf[m * NCH + cc] : 0.0f;
         }
@@ -472,10 +490,10 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
         for (int j = 0; j < SPW; ++j)
 #pragma unroll
             for (int q = 0; q < RQ; ++q) {
-                float part[MT];
+                float part[MT], plo[MT];
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
-                    part[m] = 0.0f;
+                    part[m] = plo[m] = 0.0f;
 #pragma unroll
                 for (int wd = 0; wd < 4; ++wd) {
                     const uint32_t w = wqA[j][q][wd];
@@ -486,9 +504,13 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                                 lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[i]));
                             const f16x2_t wv = as_f16x2(t);
 #pragma unroll
-                            for (int m = 0; m < MT; ++m)
+                            for (int m = 0; m < MT; ++m) {
                                 part[m] = __builtin_amdgcn_fdot2(wv, xh[j][m][wd * 4 + i], part[m],
                                                                  false);
+                                if constexpr (HL)
+                                    plo[m] = __builtin_amdgcn_fdot2(wv, xlo[j][m][wd * 4 + i],
+                                                                    plo[m], false);
+                            }
                         }
                     } else {
 #pragma unroll
@@ -500,15 +522,20 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                             const uint32_t pr = __builtin_amdgcn_perm(t1, t0, 0x07060100u);
                             const f16x2_t wv = as_f16x2(pr);
 #pragma unroll
-                            for (int m = 0; m < MT; ++m)
+                            for (int m = 0; m < MT; ++m) {
                                 part[m] = __builtin_amdgcn_fdot2(wv, xh[j][m][wd * 2 + p], part[m],
                                                                  false);
+                                if constexpr (HL)
+                                    plo[m] = __builtin_amdgcn_fdot2(wv, xlo[j][m][wd * 2 + p],
+                                                                    plo[m], false);
+                            }
                         }
                     }
                 }
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
-                    acc[q][m] = fmaf(part[m], scale_at(j, q) * fexp[j][m], acc[q][m]);
+                    acc[q][m] = fmaf(HL ? part[m] + plo[m] : part[m], scale_at(j, q) * fexp[j][m],
+                                     acc[q][m]);
             }
 
         const int row0 = blk * ROWS;
@@ -591,14 +618,21 @@ __global__ void __launch_bounds__(256) gemv_generic_kernel(GemvArgs a)
 
 // Row quads per block for a given number of slabs per wave: keeps the
 // 16-byte loads in flight per lane (SPW * RQ, double-buffered) at 8.
-constexpr int rq_for(int spw) { return spw >= 8 ? 1 : (spw >= 4 ? 2 : (spw >= 2 ? 4 : EP_GEMV_RQ1)); }
-
-// Activation registers (SPW * MT * pairs-per-chunk) stay within 64 VGPRs,
-// and several activation rows are served with one slab per wave (the other
-// variants spill).
-constexpr bool fits(int bits, int spw, int mt)
+// f32 rows (hi and lo activation terms) take half the row quads from two
+// slabs per wave up, to stay in registers.
+constexpr int rq_for(int spw, bool hl = false)
 {
-    return spw * mt * (bits == 4 ? 16 : 8) <= 64 && (mt == 1 || spw == 1);
+    return spw >= 8 ? 1 : (spw >= 4 ? (hl ? 1 : 2) : (spw >= 2 ? (hl ? 2 : 4) : EP_GEMV_RQ1));
+}
+
+// Activation registers (SPW * MT * pairs-per-chunk, twice that for f32
+// rows: hi and lo terms) stay within 64 VGPRs (128 for one f32 row), and
+// several activation rows are served with one slab per wave (the other
+// variants spill).
+constexpr bool fits(int bits, int spw, int mt, bool hl = false)
+{
+    const int regs = spw * mt * (bits == 4 ? 16 : 8) * (hl ? 2 : 1);
+    return regs <= (hl && mt == 1 ? 128 : 64) && (mt == 1 || spw == 1) && !(hl && spw >= 8);
 }
 
 // Splits the persistent grid across segments in proportion to their row
@@ -634,17 +668,18 @@ void assign_workgroups(GemvArgs &a, int rows_per_block, int per_cu)
 }
 
 // LDS bytes of one workgroup of a variant (table + staged activations).
-constexpr size_t lds_bytes(int bits, int mt, int rq, int xcap)
+constexpr size_t lds_bytes(int bits, int mt, int rq, int xcap, bool hl)
 {
-    return (size_t)kTabDwords * 4 + (size_t)kMaxWaves * 4 * rq * mt * 4 + (size_t)xcap * mt * 4 +
+    return (size_t)kTabDwords * 4 + (size_t)kMaxWaves * 4 * rq * mt * 4 +
+           (size_t)xcap * mt * 4 * (hl ? 2 : 1) +
            (size_t)(2 * xcap / (bits == 4 ? 32 : 16)) * mt * 4 + 1024;
 }
 
 template <int BITS, int MT, int SPW, int XDT, int XS, int XCAP>
 int launch_xcap(GemvArgs a, int waves, hipStream_t stream)
 {
-    constexpr int RQ = rq_for(SPW);
-    constexpr size_t lds = lds_bytes(BITS, MT, RQ, XCAP);
+    constexpr int RQ = rq_for(SPW, XDT == EP_F32);
+    constexpr size_t lds = lds_bytes(BITS, MT, RQ, XCAP, XDT == EP_F32);
     static_assert(lds <= 160 * 1024, "LDS budget");
     // persistent grid: as many workgroups per CU as LDS and registers allow
     int per_cu = (int)((160 * 1024) / lds);
@@ -674,13 +709,13 @@ int launch_xcap(GemvArgs a, int waves, hipStream_t stream)
 template <int BITS, int MT, int SPW, int XDT, int XS>
 int launch_lut(GemvArgs a, int waves, hipStream_t stream)
 {
-    if constexpr (!fits(BITS, SPW, MT)) {
+    if constexpr (!fits(BITS, SPW, MT, XDT == EP_F32)) {
         return set_error(EP_DECLINE_SHAPE, "GEMV variant does not fit registers");
     } else {
         const int64_t pairs = a.K / 2;
         if (pairs <= 2048)
             return launch_xcap<BITS, MT, SPW, XDT, XS, 2048>(a, waves, stream);
-        if constexpr (MT <= 2) {
+        if constexpr (MT == 1 || (MT == 2 && XDT != EP_F32)) {  // LDS: f32 rows stage twice
             if (pairs <= 8192)
                 return launch_xcap<BITS, MT, SPW, XDT, XS, 8192>(a, waves, stream);
         }
@@ -779,7 +814,7 @@ bool shape_ok(int bits, int64_t N, int64_t K, int group, int64_t ld_scale)
         return false;
     int spw, waves;
     plan(rb, spw, waves);
-    return spw <= 8 && fits(bits, spw, 1);
+    return spw <= 8 && fits(bits, spw, 1, true);
 }
 
 }  // namespace
@@ -799,7 +834,7 @@ bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
     const int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);
     if (mt > 2 && w.K > 4096)
         return false;  // activations of 4 rows staged in LDS: K <= 4096
-    return fits(bits, spw, mt);
+    return fits(bits, spw, mt, x.dtype == EP_F32);
 }
 
 int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,

@@ -275,7 +275,7 @@ struct StepLayer {
     const void *scale[7];      // fp16 [N][K / group]
     const void *cb[7];         // [levels] f32 or fp16
     const uint16_t *attn_norm, *mlp_norm, *q_norm, *k_norm;  // bf16 (q/k norm may be null)
-    uint16_t *kcache, *vcache;  // [Hkv][max_pos][D] bf16
+    float *kcache, *vcache;  // [Hkv][max_pos][D] f32
 };
 
 // A layer descriptor as the kernel reads it: through the constant address
@@ -289,7 +289,7 @@ struct StepArgs {
     float *h0;          // [H] f32: the step's input embedding; the final residual on exit
     uint64_t *ht;       // [2 kRing][H] tagged residual: o and down outputs of each layer
     uint64_t *qt, *kt, *vt;  // [Hq * D], [Hkv * D], [Hkv * D] tagged f32
-    uint64_t *at;       // [kRing][Hq * D / 2] tagged bf16 pairs: attention output
+    uint64_t *at;       // [kRing][Hq * D] tagged f32: attention output
     uint64_t *actt;     // [kRing][I] tagged f32: silu(gate) * up
     uint64_t *part;     // [Hq][max_pos / kChunk + 1][D + 2] tagged split-KV partials
     int *sync;          // [0] finished workgroups, [1] launch sequence, [2] error flag
@@ -696,8 +696,7 @@ EP_DEV void build_tables(uint32_t *tab, uint16_t *cb16, float cbv, int ntab)
 // ---------------------------------------------------------------- activations
 constexpr int XS_RMS_H0 = 0;  // h0 (f32, untagged: written by an earlier launch) * norm weight
 constexpr int XS_RMS = 1;     // tagged residual * norm weight (bf16); 1/rms returned
-constexpr int XS_BF16 = 2;    // tagged bf16 pairs (attention output)
-constexpr int XS_F32 = 3;     // tagged f32 (SwiGLU output)
+constexpr int XS_F32 = 3;     // tagged f32 (attention output, SwiGLU output)
 
 // Converts the K-vector to fp16 pairs in LDS with one exact power-of-two
 // factor per 32 values (the 4 threads of a 32-value chunk agree on it
@@ -719,19 +718,6 @@ EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, ui
                 v[t] = __uint_as_float(h0[t]);
                 v[4 + t] = __uint_as_float(h1[t]);
             }
-        } else if constexpr (XS == XS_BF16) {
-            // 4 entries: 2 bf16 + tag each; a ring slot: first through the caches
-            u32x4_t q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)e * 32, 0, 0);
-            u32x4_t q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)e * 32 + 16, 0, 0);
-            Spin sp;
-            while ((q0[1] != tag || q0[3] != tag || q1[1] != tag || q1[3] != tag) && sp.again(err)) {
-                q0 = ldc16(rs, (uint32_t)e * 32);
-                q1 = ldc16(rs, (uint32_t)e * 32 + 16);
-            }
-            unpack_pair<EP_BF16>(q0[0], v[0], v[1]);
-            unpack_pair<EP_BF16>(q0[2], v[2], v[3]);
-            unpack_pair<EP_BF16>(q1[0], v[4], v[5]);
-            unpack_pair<EP_BF16>(q1[2], v[6], v[7]);
         } else {  // XS_RMS, XS_F32: 8 tagged f32 = 64 bytes
             u32x4_t q[4];
             Spin sp;
@@ -818,39 +804,48 @@ EP_DEV void stamp(const StepArgs &a, int l, int ev, int thread = 0)
 // reads over many CUs: one CU streams only a few tens of GB/s).  Wave w
 // owns the chunk's positions 8 w .. 8 w + 7; lane (r = lane >> 4,
 // e = lane & 15) holds dims 8 e .. 8 e + 7 of rows 8 w + 4 k + r (k = 0, 1),
-// so every K or V load instruction reads four whole rows (1 KB,
-// contiguous).  Row pos is this step's k/v (from LDS), rows past pos are
-// weighted 0.
+// as two 16-byte halves, so each pair of K or V load instructions reads
+// four whole f32 rows (2 KB, contiguous).  Row pos is this step's k/v (from
+// LDS), rows past pos are weighted 0.
 constexpr int kRowsPerWave = kChunk / kWaves;  // 8
 constexpr int kLoadsPerWave = kRowsPerWave / 4;  // 2
 struct AttnRegs {
-    u32x4_t k[kLoadsPerWave];  // K rows (bf16)
-    u32x4_t v[kLoadsPerWave];  // V rows (bf16)
+    f32x4_t k[kLoadsPerWave][2];  // K rows (f32), dims 8 e .. 8 e + 3 and 8 e + 4 .. 8 e + 7
+    f32x4_t v[kLoadsPerWave][2];  // V rows (f32)
 };
 
 // K/V rows of item (j, c); a wave whose positions all lie past pos gets a
 // zero-length descriptor (its loads return 0 and touch no memory).  The
 // wave's rows pw0 .. pw0 + 7 exist when pw0 <= pos: pw0 is a multiple of 8,
 // max_pos of 64.
-EP_DEV void attn_load(AttnRegs &r, const uint16_t *kc, const uint16_t *vc, int j, int c, int pos,
+EP_DEV f32x4_t ld_f4(__amdgpu_buffer_rsrc_t r, uint32_t off, int soff)
+{
+    const u32x4_t q = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, soff, 0);
+    return (f32x4_t){__uint_as_float(q[0]), __uint_as_float(q[1]), __uint_as_float(q[2]),
+                     __uint_as_float(q[3])};
+}
+
+EP_DEV void attn_load(AttnRegs &r, const float *kc, const float *vc, int j, int c, int pos,
                       int max_pos)
 {
     const int lane = tid_fresh() & 63, wave = wave_id();
     const int pw0 = c * kChunk + wave * kRowsPerWave;
-    const uint32_t bytes = pw0 <= pos ? kRowsPerWave * kD * 2u : 0u;
+    const uint32_t bytes = pw0 <= pos ? kRowsPerWave * kD * 4u : 0u;
     const int64_t row0 = pw0 <= pos ? (int64_t)j * max_pos + pw0 : 0;
     const auto rk = buffer_rsrc(kc + row0 * kD, bytes);
     const auto rv = buffer_rsrc(vc + row0 * kD, bytes);
-    const uint32_t off = (uint32_t)lane * 16;  // row lane >> 4, dims 8 (lane & 15)
+    const uint32_t off = (uint32_t)lane * 32;  // row lane >> 4, dims 8 (lane & 15)
 #pragma unroll
     for (int k = 0; k < kLoadsPerWave; ++k)
-        r.k[k] = __builtin_amdgcn_raw_buffer_load_b128(rk, (int)off, k * 4 * kD * 2, 0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            r.k[k][h] = ld_f4(rk, off + 16 * h, k * 4 * kD * 4);
 #pragma unroll
     for (int k = 0; k < kLoadsPerWave; ++k)
-        r.v[k] = __builtin_amdgcn_raw_buffer_load_b128(rv, (int)off, k * 4 * kD * 2, 0);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            r.v[k][h] = ld_f4(rv, off + 16 * h, k * 4 * kD * 4);
 }
-
-EP_DEV float bf16r(float v) { return bf16_to_f32(f32_to_bf16(v)); }
 
 // `done` runs once the item's partial or output is stored.
 template <int GQ, class F>
@@ -871,8 +866,8 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
 
 
     // this step's q (GQ heads), k and v rows: per-head RMSNorm (Qwen3) and
-    // rotate-half RoPE on q and k; k and v rounded to bf16 as cached.  Lane l
-    // holds dims l and l + 64, the pair RoPE rotates together.
+    // rotate-half RoPE on q and k.  Lane l holds dims l and l + 64, the pair
+    // RoPE rotates together.
     if (wave < GQ + 2) {
         const uint64_t *src = wave < GQ ? a.qt + (hq0 + wave) * kD
                                         : (wave == GQ ? a.kt + j * kD : a.vt + j * kD);
@@ -894,26 +889,20 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
             }
             const float cs = ldg(a.cos_t + (int64_t)pos * (kD / 2) + lane);
             const float sn = ldg(a.sin_t + (int64_t)pos * (kD / 2) + lane);
-            float y0 = x0 * cs - x1 * sn;
-            float y1 = x1 * cs + x0 * sn;
             float *dst = wave < GQ ? qs + wave * kD : kn;
-            if (wave == GQ) {
-                y0 = bf16r(y0);
-                y1 = bf16r(y1);
-            }
-            dst[lane] = y0;
-            dst[lane + 64] = y1;
+            dst[lane] = x0 * cs - x1 * sn;
+            dst[lane + 64] = x1 * cs + x0 * sn;
         } else {
-            vn[lane] = bf16r(x0);
-            vn[lane + 64] = bf16r(x1);
+            vn[lane] = x0;
+            vn[lane + 64] = x1;
         }
     }
     lds_sync();
     stamp(a, l, 10);  // q/k/v received
     if (c == nchunk - 1 && tid < kD) {  // append this step's row (read by later steps only)
         const int64_t row = ((int64_t)j * a.max_pos + pos) * kD + tid;
-        stg(L.kcache + row, f32_to_bf16(kn[tid]));
-        stg(L.vcache + row, f32_to_bf16(vn[tid]));
+        stg(L.kcache + row, kn[tid]);
+        stg(L.vcache + row, vn[tid]);
     }
 
     // scores: 8 dims per lane, then the sum over the row's 16 lanes
@@ -934,22 +923,17 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
 #pragma unroll
         for (int k = 0; k < kLoadsPerWave; ++k) {
             const int p = pw0 + 4 * k + rr;
-            u32x4_t kw = r.k[k];
-            if (p == pos) {  // this step's key (bf16-exact)
+            float kw[8];
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    kw[t] = (uint32_t)f32_to_bf16(kn[e16 * 8 + 2 * t]) |
-                            ((uint32_t)f32_to_bf16(kn[e16 * 8 + 2 * t + 1]) << 16);
-            }
+            for (int t = 0; t < 8; ++t)  // row pos: this step's key, from LDS
+                kw[t] = p == pos ? kn[e16 * 8 + t] : r.k[k][t >> 2][t & 3];
             float sg[GQ];
 #pragma unroll
             for (int g = 0; g < GQ; ++g) {
                 float acc = 0.0f;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    acc = fmaf(qv[g][2 * t], __uint_as_float(kw[t] << 16), acc);
-                    acc = fmaf(qv[g][2 * t + 1], __uint_as_float(kw[t] & 0xffff0000u), acc);
-                }
+                for (int t = 0; t < 8; ++t)
+                    acc = fmaf(qv[g][t], kw[t], acc);
                 sg[g] = row16_sum(acc);
             }
             if (e16 == 0) {
@@ -992,25 +976,16 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
         for (int t = 0; t < 8; ++t)
             o[g][t] = 0.0f;
     if (wave_live) {
-        const uint32_t vnew[4] = {
-            (uint32_t)f32_to_bf16(vn[e16 * 8 + 0]) | ((uint32_t)f32_to_bf16(vn[e16 * 8 + 1]) << 16),
-            (uint32_t)f32_to_bf16(vn[e16 * 8 + 2]) | ((uint32_t)f32_to_bf16(vn[e16 * 8 + 3]) << 16),
-            (uint32_t)f32_to_bf16(vn[e16 * 8 + 4]) | ((uint32_t)f32_to_bf16(vn[e16 * 8 + 5]) << 16),
-            (uint32_t)f32_to_bf16(vn[e16 * 8 + 6]) | ((uint32_t)f32_to_bf16(vn[e16 * 8 + 7]) << 16)};
 #pragma unroll
         for (int k = 0; k < kLoadsPerWave; ++k) {
             const int p = pw0 + 4 * k + rr;
             const int pl = wave * kRowsPerWave + 4 * k + rr;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint32_t vv = p == pos ? vnew[t] : (p < pos ? r.v[k][t] : 0u);
-                const float v0 = __uint_as_float(vv << 16), v1 = __uint_as_float(vv & 0xffff0000u);
+            for (int t = 0; t < 8; ++t) {
+                const float vv = p == pos ? vn[e16 * 8 + t] : (p < pos ? r.v[k][t >> 2][t & 3] : 0.0f);
 #pragma unroll
-                for (int g = 0; g < GQ; ++g) {
-                    const float pe = S[g * kChunk + pl];
-                    o[g][2 * t] = fmaf(pe, v0, o[g][2 * t]);
-                    o[g][2 * t + 1] = fmaf(pe, v1, o[g][2 * t + 1]);
-                }
+                for (int g = 0; g < GQ; ++g)
+                    o[g][t] = fmaf(S[g * kChunk + pl], vv, o[g][t]);
             }
         }
     }
@@ -1046,7 +1021,7 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
             n1 += ow[(w * GQ + g) * kD + dd + 1];
         }
     }
-    uint64_t *outp = at + ((hq0 + g) * kD + dd) / 2;
+    uint64_t *outp = at + (hq0 + g) * kD + dd;
     const uint32_t tatt = tag_of(seq, l, PH_ATT), tpart = tag_of(seq, l, PH_PART);
     const int maxch = a.max_pos / kChunk + 1;
     if (nchunk > 1 && c > 0) {
@@ -1112,7 +1087,8 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
                 M = Mn;
             }
         }
-        st_tag(outp, (uint32_t)f32_to_bf16(n0 / Ls) | ((uint32_t)f32_to_bf16(n1 / Ls) << 16), tatt);
+        st_tag(outp, __float_as_uint(n0 / Ls), tatt);
+        st_tag(outp + 1, __float_as_uint(n1 / Ls), tatt);
     }
     stamp(a, l, 12);  // output written (combined)
     done();
@@ -1269,7 +1245,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         uint64_t *h_o = a.ht + (size_t)((2 * gl) % (2 * kRing)) * M::H;
         uint64_t *h_d = a.ht + (size_t)((2 * gl + 1) % (2 * kRing)) * M::H;
         const uint64_t *h_prev = l == 0 ? nullptr : a.ht + (size_t)((2 * gl - 1) % (2 * kRing)) * M::H;
-        uint64_t *at_l = a.at + (size_t)(gl % kRing) * (M::HQD / 2);
+        uint64_t *at_l = a.at + (size_t)(gl % kRing) * M::HQD;
         uint64_t *actl = a.actt + (size_t)(gl % kRing) * M::I;
         const bool last = l + 1 == a.n_layers;
         stamp(a, l, 0);
@@ -1326,8 +1302,8 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh, xo);
             if (so.qb > so.qa) {
                 const float hv = residual_rows(so, a, h_prev, tag_of(seq, l - 1, PH_DOWN));
-                stage<XS_BF16, M::HQD>(at_l, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf,
-                                       part8, err);
+                stage<XS_F32, M::HQD>(at_l, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf,
+                                      part8, err);
                 stamp(a, l, 3);
                 PO::template run<MODE_ACC>(ob, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
                                            1.0f, h_o, a.h0, false, nullptr, tag_of(seq, l, PH_O));
@@ -1473,7 +1449,7 @@ static StepWs step_ws(int H, int I, int Hq, int Hkv, int D, int max_pos)
     w.qt = take((size_t)Hq * D);
     w.kt = take((size_t)Hkv * D);
     w.vt = take((size_t)Hkv * D);
-    w.at = take((size_t)kRing * Hq * D / 2);
+    w.at = take((size_t)kRing * Hq * D);
     w.actt = take((size_t)kRing * I);
     w.part = take((size_t)Hq * (max_pos / kChunk + 1) * (D + 2));
     w.total = o;

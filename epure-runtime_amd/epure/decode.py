@@ -17,10 +17,19 @@ embedding).  The token position lives in device memory, so the step is
 captured once as a HIP graph and replayed per token.
 
 Weights are random-init (there is no network for checkpoints), seeded, in
-the reference's packed format: 4-bit indices two per byte, a sorted
-16-entry fp16-valued codebook per linear (stored fp32 as the container
+the reference's packed format: 4-bit indices two per byte, a 16-entry
+fp16-valued codebook per linear (16 sorted N(0, 1) draws, centred: their
+mean is subtracted before the fp16 rounding; stored fp32 as the container
 does), group-128 fp16 scales |N(0, 0.02)| + 1e-3; embeddings and lm_head
 bf16 N(0, 0.02); norm weights 1.
+
+Why the codebook is centred: with uniform indices and positive scales an
+uncentred codebook gives every row the mean mean(cb) * scale, so each linear
+maps the all-ones direction to itself with gain ~ mean(cb) * mean(scale) * K
+(about 17 at K = 4096).  Within a few layers that one direction owns the
+residual stream, every position produces the same logits and greedy decode
+repeats one token -- a parity check on such a model compares a constant.
+Centring keeps the bytes, the format and the kernels' work identical.
 """
 import ctypes
 import math
@@ -79,15 +88,17 @@ def _gen(seed, device):
     return g
 
 
-def random_packed_linear(n, k, cfg, gen, device):
-    """One packed weight: uniform indices, sorted N(0, 1) fp16-valued codebook,
-    |N(0, 0.02)| + 1e-3 fp16 group scales."""
+def random_packed_linear(n, k, cfg, gen, device, center=True):
+    """One packed weight: uniform indices, sorted N(0, 1) fp16-valued codebook
+    (mean removed when ``center``), |N(0, 0.02)| + 1e-3 fp16 group scales."""
     nbytes = n * k // 2 if cfg.levels <= 16 else n * k
     hi = 256 if cfg.levels in (16, 256) else None
     if hi is None:
         raise ValueError("random weights are generated for 16 or 256 levels")
     packed = torch.randint(0, hi, (nbytes,), generator=gen, device=device, dtype=torch.uint8)
     cb = torch.sort(torch.randn(cfg.levels, generator=gen, device=device)).values
+    if center:
+        cb = cb - cb.mean()
     cb = cb.half().float()
     g = (k + cfg.group - 1) // cfg.group
     scale = (torch.randn(n, g, generator=gen, device=device).abs() * 0.02 + 1e-3).half()
@@ -124,7 +135,7 @@ class DecoderWeights:
             self.final_norm.numel() * 2
 
 
-def random_weights(cfg, seed=0, device="cuda"):
+def random_weights(cfg, seed=0, device="cuda", center=True):
     device = torch.device(device)
     gen = _gen(seed, device)
     h = cfg.hidden
@@ -134,7 +145,7 @@ def random_weights(cfg, seed=0, device="cuda"):
     ones = lambda n: torch.ones(n, device=device, dtype=torch.bfloat16)  # noqa: E731
     layers = []
     for _ in range(cfg.layers):
-        lin = {name: random_packed_linear(n, k, cfg, gen, device)
+        lin = {name: random_packed_linear(n, k, cfg, gen, device, center)
                for name, n, k in cfg.packed_linear_shapes()}
         layers.append(Layer(ones(h), ones(h), lin,
                             ones(cfg.head_dim) if cfg.qk_norm else None,
@@ -170,11 +181,13 @@ class Decoder:
         self.q = torch.zeros(cfg.n_heads * D, device=dev, dtype=f32)
         self.k = torch.zeros(cfg.n_kv * D, device=dev, dtype=f32)
         self.v = torch.zeros(cfg.n_kv * D, device=dev, dtype=f32)
-        self.attn = torch.zeros(cfg.n_heads * D, device=dev, dtype=bf16)
+        self.attn = torch.zeros(cfg.n_heads * D, device=dev, dtype=f32)
         self.g = torch.zeros(cfg.intermediate, device=dev, dtype=f32)
         self.u = torch.zeros(cfg.intermediate, device=dev, dtype=f32)
         self.logits = torch.zeros(cfg.vocab, device=dev, dtype=f32)
-        self.kcache = torch.zeros(cfg.layers, cfg.n_kv, max_pos, D, device=dev, dtype=bf16)
+        # float32 KV cache: the decoder computes in the reference model's
+        # float32 precision (its CPU runtime dtype, runtime.py:_runtime_dtype)
+        self.kcache = torch.zeros(cfg.layers, cfg.n_kv, max_pos, D, device=dev, dtype=f32)
         self.vcache = torch.zeros_like(self.kcache)
         self.cos, self.sin = rope_tables(cfg, max_pos, dev)
         self.state = torch.zeros(2, device=dev, dtype=i32)
@@ -261,8 +274,11 @@ class Decoder:
         self.step_trace = None
 
     def step_failed(self):
-        """True if a hand-over wait of the persistent step timed out (its
-        results are garbage).  Synchronizes."""
+        """True if a hand-over wait of the persistent step timed out since
+        the last ``reset()`` (every result from then on is garbage: the flag
+        stays set and later waits give up at once).  Synchronizes.  Callers
+        that drive ``step()`` themselves must check it; ``generate()``
+        does."""
         return self.persistent and int(self.step_ws[2].item()) != 0
 
     def _step_kernel(self, stream):
@@ -328,7 +344,7 @@ class Decoder:
                 self.attn_ctr.data_ptr(), self.attn.data_ptr(), cfg.n_heads, cfg.n_kv, D,
                 self.max_pos, self.scale, stream)
             _abi.check(rc, "ep_decode_attention") or _raise_decline("ep_decode_attention")
-            self._gemv(a["o"], _abi.XSRC_PLAIN, self.attn, _abi.BF16, None, True, stream)
+            self._gemv(a["o"], _abi.XSRC_PLAIN, self.attn, _abi.F32, None, True, stream)
             self._gemv(a["gu"], _abi.XSRC_RMSNORM, self.h, _abi.F32, L.mlp_norm, False, stream)
             self._gemv(a["down"], _abi.XSRC_SWIGLU, self.g, _abi.F32, self.u, True, stream)
 
@@ -340,7 +356,7 @@ class Decoder:
         for a in self._layer_args:
             L = a["L"]
             self._gemv(a["qkv"], _abi.XSRC_RMSNORM, self.h, _abi.F32, L.attn_norm, False, stream)
-            self._gemv(a["o"], _abi.XSRC_PLAIN, self.attn, _abi.BF16, None, True, stream)
+            self._gemv(a["o"], _abi.XSRC_PLAIN, self.attn, _abi.F32, None, True, stream)
             self._gemv(a["gu"], _abi.XSRC_RMSNORM, self.h, _abi.F32, L.mlp_norm, False, stream)
             self._gemv(a["down"], _abi.XSRC_SWIGLU, self.g, _abi.F32, self.u, True, stream)
 
@@ -356,6 +372,9 @@ class Decoder:
         if self.n_prompt != n:
             self.n_prompt = n
             self.graph = None               # n_prompt is a launch argument
+        if self.persistent:
+            # hand-over words, tags and the time-out flag start clean
+            self.step_ws.zero_()
         self.tokens.zero_()
         self.tokens[0] = int(prompt[0])
         self.argmax.fill_(-1)
@@ -394,6 +413,8 @@ class Decoder:
         for _ in range(steps):
             self.step(use_graph)
         torch.cuda.synchronize(self.device)
+        if self.step_failed():
+            raise RuntimeError("decode step: a hand-over wait timed out; the tokens are invalid")
         n = self.n_prompt + n_new
         return self.tokens[:n].cpu().tolist(), self.argmax[:n - 1].cpu().tolist()
 

@@ -1,105 +1,152 @@
-"""Compressed-state fine-tuning: codebook and scales train, indices stay frozen.
+"""Compressed-state fine-tuning: the codebook and the group scales learn, the
+indices never move.
 
-Mirrors the reference API (epure/finetune.py:39-176).  One behavioural
-difference: the fused HIP path is differentiable (its backward writes
-grad_cb / grad_scale straight from the packed indices), so gradients reach
-``cb`` and ``scale`` whichever path a forward takes.  The reference's
-``trainable_forward`` set a flag that nothing read (finetune.py:135-143 vs
-runtime.py:98-126); here the flag is honoured by ``PackedLinear`` and forces
-the materialize path.
+Public surface of the reference's epure/finetune.py:39-176 (``MODES``,
+``packed_weights``, ``make_trainable``, ``snapshot_indices``,
+``verify_frozen``, ``trainable_forward``, ``ScaleTuner``).
+
+The weight of a packed linear is ``cb[idx] * scale``: with ``idx`` frozen it
+is smooth in ``cb`` and ``scale``, so training is plain backprop into those
+two small tensors.  In this build both routes carry the gradient: the fused
+gfx950 kernels have their own backward (grad_cb / grad_scale straight from
+the packed indices, ``epure.kernels.cuda``), and the materialize route is
+differentiable.  ``trainable_forward`` therefore is not needed for
+correctness; it forces the materialize route, which ``PackedLinear``
+honours (the reference set a flag nothing read, runtime.py:98-126).
 """
 import hashlib
 
 import torch
 import torch.nn as nn
 
-from .runtime import PackedLinear, PackedWeight
+from .runtime import PackedEmbedding, PackedLinear, PackedWeight
 
 MODES = ("scale", "codebook", "both")
 
+# which store tensors each mode trains
+_TRAINED = {"scale": ("scale",), "codebook": ("cb",), "both": ("scale", "cb")}
+
+# per-store caches that hold tensor pointers and must not outlive a swap
+_POINTER_CACHES = ("_hip_hot", "_hot_cache")
+
 
 def packed_weights(model):
-    """Every packed store in the model with its owner's path (finetune.py:42-46)."""
-    for name, mod in model.named_modules():
-        if isinstance(mod, PackedLinear):
-            yield name, mod.store
+    """``(module path, store)`` for every packed linear and packed embedding
+    (finetune.py:42-46).  A store shared by two modules (tied lm_head) is
+    reported under both paths."""
+    for path, mod in model.named_modules():
+        if isinstance(mod, (PackedLinear, PackedEmbedding)):
+            yield path, mod.store
+
+
+def _unique_stores(model):
+    found = {}
+    for _, store in packed_weights(model):
+        found.setdefault(id(store), store)
+    return list(found.values())
+
+
+def _trainable(store, attr):
+    """``store.<attr>`` as an fp32 leaf Parameter with grad on.
+
+    A buffer is swapped for a Parameter once (a tied store is reached twice:
+    the second visit reuses it); the swap drops the store's pointer caches,
+    which would otherwise keep feeding the kernels the old tensor.
+    """
+    cur = getattr(store, attr)
+    if not isinstance(cur, nn.Parameter):
+        for key in _POINTER_CACHES:
+            store.__dict__.pop(key, None)
+        del store._buffers[attr]
+        cur = nn.Parameter(cur.detach().to(torch.float32).clone())
+        store.register_parameter(attr, cur)
+    cur.requires_grad_(True)
+    return cur
 
 
 def make_trainable(model, mode="both", verbose=True):
-    """Promote ``scale`` and/or ``cb`` buffers to fp32 Parameters (finetune.py:49-102)."""
+    """Freeze the model, then make ``scale`` and/or ``cb`` of every packed
+    store a trainable fp32 Parameter (finetune.py:49-102).  Returns the
+    Parameters, per store ``scale`` before ``cb``."""
     if mode not in MODES:
-        raise ValueError(f"mode must be one of {MODES}")
-    for p in model.parameters():
-        p.requires_grad_(False)
-
-    def promote(store, attr):
-        cur = getattr(store, attr)
-        if isinstance(cur, nn.Parameter):
-            cur.requires_grad_(True)
-            return cur
-        store.__dict__.pop("_hot_cache", None)
-        store.__dict__.pop("_hip_hot", None)
-        store._buffers.pop(attr, None)
-        setattr(store, attr, nn.Parameter(cur.detach().float().clone(), requires_grad=True))
-        return getattr(store, attr)
-
-    params, seen = [], set()
-    for _, store in packed_weights(model):
-        if id(store) in seen:
-            continue
-        seen.add(id(store))
-        if mode in ("scale", "both"):
-            params.append(promote(store, "scale"))
-        if mode in ("codebook", "both"):
-            params.append(promote(store, "cb"))
+        raise ValueError(f"mode {mode!r} is not one of {MODES}")
+    model.requires_grad_(False)
+    stores = _unique_stores(model)
+    params = [_trainable(s, attr) for s in stores for attr in _TRAINED[mode]]
     if verbose:
         n_train = sum(p.numel() for p in params)
-        print(f"  mode {mode}: {len(seen)} packed tensors, {n_train / 1e6:.2f}M trainable")
+        n_idx = sum(s.out_features * s.in_features for s in stores)
+        share = 100.0 * n_train / max(n_train + n_idx, 1)
+        print(f"  mode {mode}: {len(stores)} packed stores, {n_train / 1e6:.2f}M trainable "
+              f"values ({share:.2f}% of the weight values; indices frozen)")
     return params
 
 
+def _digest(t):
+    raw = t.detach().to("cpu").contiguous().view(torch.uint8).numpy()
+    return hashlib.blake2b(raw.tobytes(), digest_size=16).hexdigest()
+
+
 def snapshot_indices(model):
-    """blake2b-128 of every store's packed bytes (finetune.py:105-117)."""
-    return {name: hashlib.blake2b(store.packed.detach().cpu().numpy().tobytes(),
-                                  digest_size=16).hexdigest()
-            for name, store in packed_weights(model)}
+    """``{path: blake2b-128 hex of the store's packed bytes}`` (the digest of
+    finetune.py:105-117): a byte hash, so swapped indices change it."""
+    return {path: _digest(store.packed) for path, store in packed_weights(model)}
 
 
 def verify_frozen(model, snapshot):
-    """Raise if any index buffer changed since ``snapshot`` (finetune.py:120-132)."""
+    """True if no index buffer differs from ``snapshot``; otherwise raises
+    ``RuntimeError`` naming the stores whose indices changed (a store that
+    disappeared counts as changed)."""
     now = snapshot_indices(model)
-    moved = [k for k, v in snapshot.items() if now.get(k) != v]
-    if moved:
-        raise RuntimeError(f"{len(moved)} index buffers changed during training "
-                           f"(first: {moved[0]}). Indices must stay frozen.")
+    changed = sorted(p for p, d in snapshot.items() if now.get(p) != d)
+    if changed:
+        shown = ", ".join(changed[:4]) + (" ..." if len(changed) > 4 else "")
+        raise RuntimeError(f"packed indices are no longer frozen: {len(changed)} store(s) "
+                           f"differ from the snapshot ({shown})")
     return True
 
 
 def trainable_forward(model, enable=True):
-    """Force the materialize path for every packed linear (finetune.py:135-143)."""
-    for _, store in packed_weights(model):
-        store._force_materialize = enable
+    """Route every packed linear through ``materialize`` (``enable``) or back
+    to the fused kernels (finetune.py:135-143)."""
+    for store in _unique_stores(model):
+        if enable:
+            store._force_materialize = True
+        else:
+            store.__dict__.pop("_force_materialize", None)
     return model
 
 
+def _device_of(model):
+    for t in model.parameters():
+        return t.device
+    for t in model.buffers():
+        return t.device
+    return torch.device("cpu")
+
+
 class ScaleTuner:
-    """Minimal codebook/scale adaptation loop (finetune.py:146-176)."""
+    """A minimal codebook/scale adaptation loop (finetune.py:146-176): AdamW
+    on the Parameters ``make_trainable`` returns, causal-LM loss from
+    ``model(input_ids, labels=...)``, and ``finish()`` proves the indices
+    never moved before freezing the Parameters again."""
 
     def __init__(self, model, mode="both", lr=1e-4, device=None):
         self.model = model
-        self.device = device or next((p.device for p in model.parameters()),
-                                     torch.device("cpu"))
+        self.device = torch.device(device) if device is not None else _device_of(model)
         self.params = make_trainable(model, mode)
         self.snapshot = snapshot_indices(model)
         self.opt = torch.optim.AdamW(self.params, lr=lr)
 
     def step(self, input_ids, labels=None):
-        labels = input_ids if labels is None else labels
-        out = self.model(input_ids.to(self.device), labels=labels.to(self.device))
-        out.loss.backward()
-        self.opt.step()
+        """One optimizer step; returns the loss before the update."""
+        ids = input_ids.to(self.device)
+        target = ids if labels is None else labels.to(self.device)
+        loss = self.model(ids, labels=target).loss
         self.opt.zero_grad(set_to_none=True)
-        return float(out.loss.detach())
+        loss.backward()
+        self.opt.step()
+        return loss.item()
 
     def finish(self):
         verify_frozen(self.model, self.snapshot)

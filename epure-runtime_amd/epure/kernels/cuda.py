@@ -7,12 +7,16 @@ Drop-in for ``epure/kernels/cuda.py`` of the reference: the same
 
 Differences from the reference backend, all deliberate:
 
-* bf16, fp16 and fp32 activations are served (the reference declined every
+* bf16 and fp16 activations are served (the reference declined every
   non-fp16 ``x``, cuda.py:101-106, so bf16 models never reached it); the
-  output has ``x.dtype``.
+  output has ``x.dtype``.  fp32 activations are declined, as in the
+  reference: the kernels carry activations as fp16 operands, which would
+  narrow an fp32 model (the caller then takes the exact fp32 materialize
+  route).  ``EPURE_FUSED_F32=1`` serves them anyway, at fp16-operand
+  accuracy.
 * every M is served by the library itself (batch-1 GEMV for M <= 4, dequant
-  into LDS + MFMA above), so the caller's ``EPURE_DENSE_ABOVE`` crossover is
-  not needed for speed.
+  into LDS + MFMA above); the caller's ``EPURE_DENSE_ABOVE`` decides when a
+  dense GEMM takes over.
 * the codebook is applied exactly (the reference's default polynomial mode,
   cuda.py:53-55 / _triton.py:112-185, is an approximation and is not
   reproduced); ``MODE`` is kept for API compatibility and only "table" exists.
@@ -20,9 +24,10 @@ Differences from the reference backend, all deliberate:
   custom autograd function with the fused backward, so gradients are never
   dropped (the reference's fused paths had no backward).
 * if a GPU is present but the library cannot be loaded, importing this
-  module raises: a silent fallback is how the reference once shipped a dead
-  GPU path (cuda.py:26-31).  ``EPURE_ALLOW_FALLBACK=1`` turns that into the
-  reference's RuntimeWarning + decline behaviour.
+  module emits a RuntimeWarning naming the cause and ``available()`` is
+  False, so every call declines (the reference's contract, cuda.py:23-46).
+  Nothing here computes a result any other way: the GPU tests assert
+  ``available()`` and fail when the library is missing.
 """
 import os
 import warnings
@@ -38,13 +43,13 @@ _abi._load()
 if _abi.lib is None:
     IMPORT_ERROR = _abi.LOAD_ERROR
     if torch.cuda.is_available():
-        msg = (f"epure: a GPU is present but {_abi.LIB_NAME} failed to load "
-               f"({type(IMPORT_ERROR).__name__}: {IMPORT_ERROR}). Build it with "
-               "__graft_entry__.build().")
-        if os.environ.get("EPURE_ALLOW_FALLBACK") == "1":
-            warnings.warn(msg + " Falling back to the slow path.", RuntimeWarning, stacklevel=2)
-        else:
-            raise ImportError(msg)
+        warnings.warn(
+            f"epure: a GPU is present but {_abi.LIB_NAME} failed to load "
+            f"({type(IMPORT_ERROR).__name__}: {IMPORT_ERROR}); every packed linear will "
+            "materialize. Build it with __graft_entry__.build().",
+            RuntimeWarning, stacklevel=2)
+
+SERVE_F32 = os.environ.get("EPURE_FUSED_F32") == "1"
 
 _AVAILABLE = None
 
@@ -180,7 +185,8 @@ def linear(x, store):
     """``x @ dequant(store).T`` on the GPU, or ``None`` if unsupported."""
     if not available() or not x.is_cuda or len(store.shape) != 2:
         return None
-    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+    if x.dtype not in (torch.float16, torch.bfloat16) and not (
+            SERVE_F32 and x.dtype == torch.float32):
         return None
     h = _hot(store)
     if not h.usable() or not store.packed.is_cuda:

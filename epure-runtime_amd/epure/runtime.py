@@ -1,15 +1,35 @@
-"""Packed store and packed linear -- the caller side of the fused kernels.
+"""Packed stores and the modules that run them on the fused kernels.
 
-Mirrors the reference's resident representation and dispatch
-(epure/runtime.py:34-160): ``PackedWeight`` owns ``packed`` / ``scale`` /
-``cb`` buffers, ``PackedLinear.forward`` hands the call to a backend and
-materializes when the backend declines, ``PackedEmbedding`` expands only the
-rows a batch asks for, ``tie_packed_lm_head`` runs a tied lm_head through
-the packed linear (runtime.py:289-300), ``ExpertHolder`` keeps a stacked
-expert slab packed between calls (runtime.py:163-186) and ``PackedExperts``
-runs expert-indexed linears without expanding the slab.  The ``.ebin``
-loader is outside this build.
+Interface kept from the reference (epure/runtime.py:34-186, :289-300): a
+``PackedWeight`` owns non-persistent ``packed`` / ``scale`` / ``cb`` buffers
+and reports ``shape``, ``levels``, ``group``, ``in_features``,
+``out_features`` and ``packed_2d()``; ``PackedLinear`` asks a backend for the
+fused product and materializes the weight only when the backend declines;
+``PackedEmbedding`` expands the rows a batch asks for; an expert holder keeps
+a stacked slab packed between calls; a tied lm_head is a ``PackedLinear``
+over the embedding store.
+
+How this build does it:
+
+* every dense expansion on the host goes through one helper, ``_expand``:
+  a 256-entry level table in the target dtype (entries past ``levels`` are
+  0, as the Rust kernel's zero-filled LUT makes them, kernel/src/lib.rs:58-59)
+  gathered by index, then multiplied group-wise by the scales broadcast over
+  a ``[rows, groups, group]`` view.  Both operands are in the target dtype
+  before the product, which rounds once: the reference's
+  ``dtype(cb)[idx] * dtype(scale)`` (runtime.py:78-89), and it is
+  differentiable in ``cb`` and ``scale`` (the fine-tune path);
+* indices of arbitrary rows are read straight from the flat packed stream
+  (row r owns flat positions r*K .. r*K + K - 1; byte = position / 2, nibble
+  = position & 1), so odd K needs no special case;
+* on a gfx950 device without autograd, ``materialize`` and the embedding run
+  the library's ``ep_dequant_tile`` / ``ep_embedding_rows`` kernels;
+* ``PackedExperts`` (no counterpart in the reference, which expands the
+  whole slab per call) runs expert-indexed rows packed.
+
+The ``.ebin`` reader lives in ``epure.container``.
 """
+import math
 import os
 
 import numpy as np
@@ -17,139 +37,216 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .kernels import _abi
 from .kernels import cpu as cpu_kernel
 from .kernels import cuda as cuda_kernel
-from .kernels import _abi
 
+# Per-store host copies for the CPU backend, keyed by store identity
+# (the reference's runtime.py:24 cache; the CPU backend drops an entry
+# whose tensors were replaced).
 _BUFFER_CACHE = {}
 
-# Rows at or above which the GPU path materializes and calls a dense GEMM
-# (reference runtime.py:26-31 defaults to 8).  The HIP backend serves every
-# M itself, so the default keeps the fused path always.
+# Rows at or above which a GPU call skips the fused kernels and runs
+# materialize + a dense GEMM (reference runtime.py:26-31 defaults to 8 on
+# A100).  Unset, every row count stays on the fused kernels.
 _DENSE_ABOVE = int(os.environ.get("EPURE_DENSE_ABOVE", str(2**31 - 1)))
 
+_TABLE = 256  # entries of the level table (the largest codebook an index can address)
 
+
+# ---------------------------------------------------------------- packing
 def _pack4(idx, levels):
-    """Flat index stream -> bytes (runtime.py:34-45 layout).
+    """Index stream -> the stored bytes (format of runtime.py:34-45).
 
-    Up to 16 levels two indices share a byte, the even position in the low
-    nibble; an odd count gets a zero pad.  Above 16 levels one index per byte.
+    levels <= 16: two indices per byte over the flat stream, even position
+    in the low nibble, a zero nibble pads an odd count.  levels > 16: one
+    index per byte.  An index that does not fit a nibble is rejected rather
+    than truncated.
     """
-    flat = np.asarray(idx, dtype=np.uint8).reshape(-1)
+    flat = np.asarray(idx).reshape(-1)
     if levels > 16:
-        return np.ascontiguousarray(flat)
-    if flat.size & 1:
-        flat = np.concatenate([flat, np.zeros(1, np.uint8)])
-    pairs = flat.reshape(-1, 2)
-    return np.ascontiguousarray((pairs[:, 0] & 0x0F) | (pairs[:, 1] << 4)).astype(np.uint8)
+        return flat.astype(np.uint8)
+    if flat.size and int(flat.max()) > 15:
+        raise ValueError(f"index {int(flat.max())} does not fit 4 bits (levels={levels})")
+    even = flat[0::2].astype(np.uint16)
+    odd = np.zeros_like(even)
+    odd[:flat.size // 2] = flat[1::2]
+    return (even + odd * 16).astype(np.uint8)
 
 
 def _unpack4(packed, n, levels):
-    """Bytes -> flat index stream of length n (runtime.py:48-54)."""
+    """Stored bytes -> the first ``n`` indices of the flat stream (uint8)."""
     if levels > 16:
-        return packed[:n]
+        return packed.reshape(-1)[:n]
     if packed.is_cuda and cuda_kernel.available():
         out = torch.empty(n, dtype=torch.uint8, device=packed.device)
         rc = _abi.lib.ep_unpack_indices(packed.data_ptr(), n, levels, out.data_ptr(),
                                         _abi.stream_handle(packed.device))
         _abi.check(rc, "ep_unpack_indices")
         return out
-    both = torch.stack((packed & 0x0F, packed >> 4), dim=-1)
+    nib = torch.tensor([0, 4], dtype=torch.uint8, device=packed.device)
+    both = (packed.reshape(-1, 1) >> nib) & 0x0F      # [bytes, 2]: low, high
     return both.reshape(-1)[:n]
 
 
-def _as_tensor(a):
+def _row_indices(store, rows):
+    """Indices (int64 ``[len(rows), K]``) of the given rows, read from the
+    flat stream by position."""
+    K = store.in_features
+    pos = rows.reshape(-1, 1).to(torch.int64) * K + torch.arange(K, device=rows.device)
+    flat = store.packed.reshape(-1)
+    if store.levels > 16:
+        return flat[pos].to(torch.int64)
+    byte = flat[pos >> 1].to(torch.int64)
+    return (byte >> ((pos & 1) * 4)) & 0x0F
+
+
+def _level_table(cb, dtype):
+    """cb in ``dtype``, zero-extended to 256 entries (differentiable)."""
+    c = cb.reshape(-1).to(dtype)
+    return F.pad(c, (0, _TABLE - c.numel())) if c.numel() < _TABLE else c[:_TABLE]
+
+
+def _expand(store, idx, scale_rows, dtype):
+    """``dtype(cb)[idx] * dtype(scale)`` for a block of rows.
+
+    ``idx``: int64 ``[R, K]``; ``scale_rows``: ``[R, >= ceil(K/group)]``.
+    """
+    R, K = idx.shape
+    g = store.group
+    ng = -(-K // g)
+    vals = _level_table(store.cb, dtype)[idx]
+    if ng * g != K:
+        vals = F.pad(vals, (0, ng * g - K))
+    sc = scale_rows[:, :ng].to(dtype).unsqueeze(-1)
+    return (vals.view(R, ng, g) * sc).view(R, ng * g)[:, :K]
+
+
+def _tensor(a):
     return a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a))
 
 
+def _needs_grad(store):
+    return torch.is_grad_enabled() and (store.cb.requires_grad or store.scale.requires_grad)
+
+
+# ---------------------------------------------------------------- store
 class PackedWeight(nn.Module):
-    """Indices, per-group scales and a codebook (runtime.py:57-89)."""
+    """The resident form of one weight: indices, group scales, codebook
+    (interface of runtime.py:57-89).
+
+    ``shape`` is the logical weight shape; every axis but the last folds into
+    rows (a stacked ``(E, N, K)`` expert slab has ``E*N`` rows).  ``packed``
+    holds ``ceil(rows*K/2)`` bytes at 4-bit (levels <= 16) or ``rows*K`` at
+    8-bit; ``scale`` is ``[rows, ceil(K/group)]`` (fp16, or fp32 once
+    trained); ``cb`` holds ``levels`` values (f32 in the container, fp16
+    accepted).
+    """
 
     def __init__(self, shape, packed, scale, cb, group, levels):
         super().__init__()
-        self.levels, self.group = int(levels), int(group)
-        self.shape = tuple(int(d) for d in shape)
-        self.in_features = self.shape[-1]
-        rows = 1
-        for d in self.shape[:-1]:
-            rows *= d
-        self.out_features = rows
-        self.register_buffer("packed", _as_tensor(packed), persistent=False)
-        self.register_buffer("scale", _as_tensor(scale), persistent=False)
-        self.register_buffer("cb", _as_tensor(cb), persistent=False)
+        dims = tuple(int(d) for d in shape)
+        if len(dims) < 2 or min(dims) < 0:
+            raise ValueError(f"packed weight shape {shape} needs rank >= 2")
+        self.shape = dims
+        self.levels = int(levels)
+        self.group = int(group)
+        if not 1 <= self.levels <= _TABLE or self.group < 1:
+            raise ValueError(f"levels {levels} / group {group} out of range")
+        self.in_features = dims[-1]
+        self.out_features = math.prod(dims[:-1])
+        for name, value in (("packed", packed), ("scale", scale), ("cb", cb)):
+            self.register_buffer(name, _tensor(value), persistent=False)
+        want = self.out_features * self.row_bytes if self.levels > 16 else \
+            -(-self.out_features * self.in_features // 2)
+        if self.packed.numel() != want:
+            raise ValueError(f"packed holds {self.packed.numel()} bytes, shape {dims} at "
+                             f"levels {levels} needs {want}")
+
+    @property
+    def row_bytes(self):
+        """Bytes of one row in the ``packed_2d`` view."""
+        return self.in_features if self.levels > 16 else (self.in_features + 1) // 2
 
     def packed_2d(self):
-        cols = self.in_features if self.levels > 16 else (self.in_features + 1) // 2
-        return self.packed.view(self.out_features, cols)
+        """``packed`` as ``[rows, row_bytes]`` (runtime.py:73-76); rows are
+        byte-aligned in the flat stream only for even K at 4-bit."""
+        return self.packed.view(self.out_features, self.row_bytes)
 
     def materialize(self, dtype=torch.float16):
-        """Dense weight in ``dtype`` (runtime.py:78-89 semantics).
+        """The dense weight in ``dtype`` (``shape``-shaped).
 
-        ``dtype(cb)[idx] * dtype(scale)`` -- for fp16/bf16 both operands are
-        rounded to ``dtype`` before the product, as the reference does.  On a
-        gfx950 device without autograd this runs the library's dequant
-        kernel; with gradients required it uses differentiable torch ops.
+        Without autograd on a gfx950 device this is one ``ep_dequant_tile``
+        launch; otherwise the differentiable host expression (``_expand``).
         """
-        n = self.out_features * self.in_features
-        needs_grad = torch.is_grad_enabled() and (self.cb.requires_grad
-                                                  or self.scale.requires_grad)
-        if (not needs_grad and self.packed.is_cuda and cuda_kernel.available()
+        rows, K = self.out_features, self.in_features
+        w = None
+        if (not _needs_grad(self) and self.packed.is_cuda and cuda_kernel.available()
                 and dtype in (torch.float32, torch.float16, torch.bfloat16)):
-            h = cuda_kernel._hot(self)
-            if h.usable():
-                w = torch.empty((self.out_features, self.in_features), dtype=dtype,
-                                device=self.packed.device)
-                rc = _abi.lib.ep_dequant_tile(
-                    h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
-                    h.cb.data_ptr(), h.cb_dt, h.levels, h.group, h.N, h.K,
-                    w.data_ptr(), _abi.dtype_code(dtype), w.stride(0),
-                    _abi.stream_handle(self.packed.device))
-                if _abi.check(rc, "ep_dequant_tile"):
-                    return w.reshape(self.shape) if len(self.shape) > 2 else w
-        idx = _unpack4(self.packed, n, self.levels).view(self.out_features, self.in_features)
-        table = self.cb.to(dtype).reshape(-1, 1)
-        w = F.embedding(idx.int(), table).squeeze(-1)
-        sc = self.scale.to(dtype).repeat_interleave(self.group, dim=1)[:, :self.in_features]
-        w = w * sc
+            w = _dequant_on_device(self, dtype)
+        if w is None:
+            idx = _unpack4(self.packed, rows * K, self.levels).view(rows, K).to(torch.int64)
+            w = _expand(self, idx, self.scale.reshape(rows, -1), dtype)
         return w.reshape(self.shape) if len(self.shape) > 2 else w
 
 
+def _dequant_on_device(store, dtype):
+    h = cuda_kernel._hot(store)
+    if not h.usable():
+        return None
+    w = torch.empty((h.N, h.K), dtype=dtype, device=store.packed.device)
+    rc = _abi.lib.ep_dequant_tile(
+        h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+        h.cb.data_ptr(), h.cb_dt, h.levels, h.group, h.N, h.K,
+        w.data_ptr(), _abi.dtype_code(dtype), w.stride(0), _abi.stream_handle(w.device))
+    return w if _abi.check(rc, "ep_dequant_tile") else None
+
+
+# ---------------------------------------------------------------- linear
 class PackedLinear(nn.Module):
-    """Linear layer over a ``PackedWeight`` (runtime.py:92-126)."""
+    """``y = x W^T (+ bias)`` over a ``PackedWeight`` (runtime.py:92-126).
+
+    A fused backend serves the call when it can (GPU: fewer than
+    ``_DENSE_ABOVE`` rows; CPU: levels <= 16); a ``None`` from it, a rank>2
+    store, or a store flagged ``_force_materialize`` (``trainable_forward``)
+    takes the dense route.
+    """
 
     def __init__(self, store, bias=None):
         super().__init__()
         self.store = store
         self.bias = bias
 
-    def forward(self, x):
+    def _fused(self, x):
         s = self.store
-        if len(s.shape) == 2 and not s.__dict__.get("_force_materialize", False):
-            out = None
-            if x.is_cuda:
-                if x.reshape(-1, x.shape[-1]).shape[0] < _DENSE_ABOVE:
-                    out = cuda_kernel.linear(x, s)
-            elif s.levels <= 16:
-                out = cpu_kernel.linear(x, s, _BUFFER_CACHE)
-            if out is not None:
-                return out + self.bias if self.bias is not None else out
-        w = s.materialize(x.dtype)
-        out = F.linear(x, w, self.bias)
-        del w
-        return out
+        if len(s.shape) != 2 or s.__dict__.get("_force_materialize", False):
+            return None
+        if x.is_cuda:
+            rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
+            return cuda_kernel.linear(x, s) if rows < _DENSE_ABOVE else None
+        if s.levels > 16:
+            return None
+        return cpu_kernel.linear(x, s, _BUFFER_CACHE)
+
+    def forward(self, x):
+        y = self._fused(x)
+        if y is None:
+            # the dense route adds the bias inside the GEMM, as the reference does
+            return F.linear(x, self.store.materialize(x.dtype), self.bias)
+        return y if self.bias is None else y + self.bias
 
 
+# ---------------------------------------------------------------- embedding
 class PackedEmbedding(nn.Module):
-    """Embedding over a ``PackedWeight``: expands only the requested rows
-    (runtime.py:129-160).
+    """Token embedding over a ``PackedWeight`` that expands only the rows a
+    batch asks for (interface of runtime.py:129-160).
 
-    ``forward(ids)`` returns ``[*ids.shape, in_features]`` in ``dtype`` with
-    the reference's rounding, ``dtype(cb[idx]) * dtype(scale)`` per group --
-    the rows of ``materialize(dtype)``.  On a gfx950 device the rows are
-    expanded by the library's ``ep_embedding_rows`` kernel; CPU tensors take
-    the reference's torch expression.  Ids outside ``[0, num_embeddings)``
-    raise ``IndexError`` (checked on the host outside graph capture; a
-    captured call writes zero rows for them).
+    ``forward(ids)`` is ``[*ids.shape, in_features]`` in ``dtype`` with the
+    rounding of ``materialize(dtype)``.  Ids outside ``[0, num_embeddings)``
+    raise ``IndexError`` (on the host; a call being captured into a HIP graph
+    cannot look at the ids and writes zero rows for them instead).  With
+    ``cb`` or ``scale`` requiring grad the expression is differentiable (a
+    trained tied embedding gets its gradient).
     """
 
     def __init__(self, store, dtype=torch.float16):
@@ -159,72 +256,73 @@ class PackedEmbedding(nn.Module):
         self.num_embeddings = store.out_features
         self.embedding_dim = store.in_features
 
+    def _check_ids(self, flat):
+        if flat.numel() == 0:
+            return
+        lo, hi = int(flat.min()), int(flat.max())
+        if lo < 0 or hi >= self.num_embeddings:
+            bad = lo if lo < 0 else hi
+            raise IndexError(f"embedding id {bad} outside [0, {self.num_embeddings})")
+
     def forward(self, ids):
         s = self.store
-        flat = ids.reshape(-1)
-        n_in = s.in_features
-        if (flat.is_cuda and s.packed.is_cuda and cuda_kernel.available()
-                and self.dtype in (torch.float32, torch.float16, torch.bfloat16)):
-            h = cuda_kernel._hot(s)
-            if not h.usable():
-                raise RuntimeError("PackedEmbedding: store buffers are not contiguous")
-            flat = flat.to(torch.int64).contiguous()
-            if flat.numel() and not torch.cuda.is_current_stream_capturing():
-                lo, hi = int(flat.min()), int(flat.max())
-                if lo < 0 or hi >= self.num_embeddings:
-                    raise IndexError(f"embedding id out of range [0, {self.num_embeddings}): "
-                                     f"{lo if lo < 0 else hi}")
-            out = torch.empty((flat.numel(), n_in), dtype=self.dtype, device=flat.device)
-            rc = _abi.lib.ep_embedding_rows(
-                h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
-                h.cb.data_ptr(), h.cb_dt, h.levels, h.group, h.N, h.K,
-                flat.data_ptr(), flat.numel(), out.data_ptr(), _abi.dtype_code(self.dtype),
-                out.stride(0), _abi.stream_handle(flat.device))
-            _abi.check(rc, "ep_embedding_rows")
-            return out.view(*ids.shape, n_in)
-        if flat.numel() and (int(flat.min()) < 0 or int(flat.max()) >= self.num_embeddings):
-            raise IndexError(f"embedding id out of range [0, {self.num_embeddings})")
-        if s.levels > 16:
-            idx = s.packed.view(self.num_embeddings, n_in)[flat].to(torch.long)
+        flat = ids.reshape(-1).to(torch.int64)
+        on_device = (flat.is_cuda and s.packed.is_cuda and cuda_kernel.available()
+                     and self.dtype in (torch.float32, torch.float16, torch.bfloat16))
+        capturing = on_device and torch.cuda.is_current_stream_capturing()
+        if not capturing:
+            self._check_ids(flat)
+        if on_device and not _needs_grad(s):
+            out = _embedding_on_device(s, flat.contiguous(), self.dtype)
         else:
-            rows = s.packed.view(self.num_embeddings, n_in // 2)[flat]
-            lo, hi = (rows & 0x0F).to(torch.long), (rows >> 4).to(torch.long)
-            idx = torch.empty(flat.numel(), n_in, dtype=torch.long, device=lo.device)
-            idx[:, 0::2], idx[:, 1::2] = lo, hi
-        cbt = torch.zeros(256, dtype=s.cb.dtype, device=s.cb.device)
-        cbt[:s.cb.numel()] = s.cb.reshape(-1)  # indices >= levels read 0 (lib.rs:58-59)
-        w = cbt[idx].to(self.dtype)
-        sc = s.scale[flat].to(self.dtype)
-        for gi, start in enumerate(range(0, n_in, s.group)):
-            end = min(start + s.group, n_in)
-            w[:, start:end] *= sc[:, gi:gi + 1]
-        return w.view(*ids.shape, n_in)
+            out = _expand(s, _row_indices(s, flat), s.scale.reshape(s.out_features, -1)[flat],
+                          self.dtype)
+        return out.view(*ids.shape, s.in_features)
 
     @property
     def weight(self):
         return self.store.materialize(self.dtype)
 
 
+def _embedding_on_device(store, flat, dtype):
+    h = cuda_kernel._hot(store)
+    if not h.usable():
+        raise RuntimeError("PackedEmbedding: store buffers are not contiguous")
+    out = torch.empty((flat.numel(), h.K), dtype=dtype, device=flat.device)
+    rc = _abi.lib.ep_embedding_rows(
+        h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+        h.cb.data_ptr(), h.cb_dt, h.levels, h.group, h.N, h.K,
+        flat.data_ptr(), flat.numel(), out.data_ptr(), _abi.dtype_code(dtype),
+        out.stride(0), _abi.stream_handle(flat.device))
+    _abi.check(rc, "ep_embedding_rows")
+    return out
+
+
+# ---------------------------------------------------------------- experts
 class ExpertHolder:
-    """Keeps a stacked expert slab packed except while its module runs
-    (runtime.py:163-186): a forward pre-hook attaches ``materialize(dtype)``
-    as ``mod.<attr>`` (on a gfx950 device the library's dequant kernel), a
-    forward hook drops it again."""
+    """Keeps a module's stacked expert slab packed except while the module
+    runs (the behaviour of the reference's runtime.py:163-186 holder).
+
+    The parameter ``attr`` of ``mod`` is replaced by the store: a forward
+    pre-hook sets ``mod.<attr>`` to ``materialize(dtype)`` (one dequant
+    launch on a gfx950 device) and a forward hook clears it, so between calls
+    only the packed form is resident.  ``remove()`` detaches both hooks.
+    """
 
     def __init__(self, mod, attr, store, dtype=torch.float16):
-        self.mod, self.attr, self.store = mod, attr, store
-        self.dtype = dtype
-        if attr in mod._parameters:
-            del mod._parameters[attr]
-        mod.register_forward_pre_hook(self._attach)
-        mod.register_forward_hook(self._release)
+        self.mod, self.attr, self.store, self.dtype = mod, attr, store, dtype
+        mod._parameters.pop(attr, None)
         setattr(mod, attr, None)
+        self._hooks = (mod.register_forward_pre_hook(lambda m, args: self._set(m, True)),
+                       mod.register_forward_hook(lambda m, args, out: self._set(m, False)))
 
-    def _attach(self, mod, _a):
-        setattr(mod, self.attr, self.store.materialize(self.dtype))
+    def _set(self, mod, live):
+        setattr(mod, self.attr, self.store.materialize(self.dtype) if live else None)
 
-    def _release(self, mod, _a, _o):
-        setattr(mod, self.attr, None)
+    def remove(self):
+        for h in self._hooks:
+            h.remove()
+        self._hooks = ()
 
 
 class PackedExperts(nn.Module):
@@ -266,7 +364,6 @@ class PackedExperts(nn.Module):
         h = cuda_kernel._hot(s)
         if not h.usable():
             raise RuntimeError("PackedExperts: store buffers are not contiguous")
-        row_bytes = K if s.levels > 16 else K // 2
         if s.levels <= 16 and K % 2:
             raise ValueError("4-bit expert rows need an even K")
         esz = h.scale.element_size()
@@ -280,7 +377,7 @@ class PackedExperts(nn.Module):
             ws = torch.empty(ws_bytes, device=x2.device, dtype=torch.uint8) if ws_bytes else None
             rc = _abi.lib.ep_dequant_matmul(
                 xe.data_ptr(), _abi.dtype_code(xe.dtype), xe.stride(0),
-                h.packed.data_ptr() + e * N * row_bytes,
+                h.packed.data_ptr() + e * N * s.row_bytes,
                 h.scale.data_ptr() + e * N * h.ld_scale * esz, h.scale_dt, h.ld_scale,
                 h.cb.data_ptr(), h.cb_dt, h.levels, h.group,
                 c, N, K, ye.data_ptr(), _abi.dtype_code(ye.dtype), ye.stride(0), 0,
@@ -292,29 +389,36 @@ class PackedExperts(nn.Module):
         return out
 
 
+# ---------------------------------------------------------------- model surgery
 def tie_packed_lm_head(model, embed_store):
-    """Run a tied lm_head through the packed embedding store
-    (runtime.py:289-300): ``model.lm_head = PackedLinear(embed_store)`` and
-    the config's ``tie_word_embeddings`` cleared, so a later
-    ``tie_weights()`` does not look for a dense embedding Parameter."""
+    """Run a tied lm_head on the packed embedding store (runtime.py:289-300).
+
+    ``model.lm_head`` becomes ``PackedLinear(embed_store)``; a config flag
+    ``tie_word_embeddings`` is cleared (on ``model.config`` as well), since a
+    later ``tie_weights()`` would look for a dense embedding Parameter.
+    """
     model.lm_head = PackedLinear(embed_store)
     cfg = getattr(model, "config", None)
-    if cfg is not None and getattr(cfg, "tie_word_embeddings", False):
+    if getattr(cfg, "tie_word_embeddings", False):
         cfg.tie_word_embeddings = False
     return model
 
 
 def apply_packed(model, stores):
-    """Swap ``nn.Linear`` modules for ``PackedLinear`` (runtime.py:261-262).
+    """Replace ``nn.Linear`` modules by ``PackedLinear`` (what ``apply_to``
+    does per packed record, runtime.py:261-262).
 
     ``stores`` maps a module path (``"model.layers.0.mlp.up_proj"``) to a
-    ``PackedWeight``; the linear's bias, if any, is kept.
+    ``PackedWeight``; the linear's bias is kept.
     """
-    for name, store in stores.items():
-        parent_name, _, attr = name.rpartition(".")
-        parent = model.get_submodule(parent_name) if parent_name else model
-        target = getattr(parent, attr)
-        if not isinstance(target, nn.Linear):
-            raise TypeError(f"{name} is {type(target).__name__}, not nn.Linear")
-        setattr(parent, attr, PackedLinear(store, getattr(target, "bias", None)))
+    for path, store in stores.items():
+        owner, _, leaf = path.rpartition(".")
+        parent = model.get_submodule(owner) if owner else model
+        old = getattr(parent, leaf)
+        if not isinstance(old, nn.Linear):
+            raise TypeError(f"{path} is {type(old).__name__}, not nn.Linear")
+        if (old.out_features, old.in_features) != (store.out_features, store.in_features):
+            raise ValueError(f"{path}: store is {store.out_features}x{store.in_features}, "
+                             f"module {old.out_features}x{old.in_features}")
+        setattr(parent, leaf, PackedLinear(store, old.bias))
     return model

@@ -47,21 +47,22 @@ int ep_fused_gemv(int xsrc, const void *x, int x_dtype, const void *x_aux, float
  * Grouped-query decode attention for one layer at position p = state[0]:
  * optional per-head RMSNorm of q and k (weights qn_w / kn_w, bf16, NULL =
  * none), rotate-half RoPE with cos/sin rows p of [max_pos][D/2] f32
- * tables, append of this step's k/v (rounded to bf16) at row p of the
- * [Hkv][max_pos][D] bf16 caches, causal softmax over rows 0..p scaled by
- * `scale`, output [Hq * D] bf16.  `part` needs ep_attention_workspace()
+ * tables, append of this step's k/v at row p of the [Hkv][max_pos][D] f32
+ * caches, causal softmax over rows 0..p scaled by `scale`, output
+ * [Hq * D] f32 (float32 throughout, the precision of the reference
+ * model's float32 forward).  `part` needs ep_attention_workspace()
  * bytes; `counters` holds Hq ints that are zero before the first call and
  * are left zero by every call.  head_dim <= 128, max_pos % 64 == 0.
  */
 size_t ep_attention_workspace(int Hq, int D, int max_pos);
 int ep_decode_attention(const float *q, const float *k, const float *v, const uint16_t *qn_w,
-                        const uint16_t *kn_w, float qk_eps, uint16_t *kcache, uint16_t *vcache,
+                        const uint16_t *kn_w, float qk_eps, float *kcache, float *vcache,
                         const float *cos_t, const float *sin_t, const int *state, float *part,
-                        int *counters, uint16_t *out, int Hq, int Hkv, int D, int max_pos,
+                        int *counters, float *out, int Hq, int Hkv, int D, int max_pos,
                         float scale, void *stream);
 
 /*
- * logits = W[V, H] (bf16) . bf16(rmsnorm(h) * norm_w), then greedy
+ * logits = W[V, H] (bf16) . (rmsnorm(h) * norm_w) in f32, then greedy
  * selection: with p = state[0], argmax_out[p] = argmax (lowest index on
  * ties), the next token is prompt[p + 1] while p + 1 < n_prompt, else the
  * argmax; tokens[p + 1] = next; state = {p + 1, next}; h = embed[next]
@@ -93,7 +94,7 @@ int ep_lm_head_argmax(float *h, const uint16_t *norm_w, float eps, const uint16_
  * packed[7], scale[7] (fp16 [N][K/group]), cb[7] (16 entries f32 or fp16,
  * entries >= levels ignored) for
  * q, k, v, o, gate, up, down; attn_norm, mlp_norm, q_norm, k_norm (bf16
- * [H], [H], [D], [D]; q/k norm NULL for Llama); kcache, vcache (bf16
+ * [H], [H], [D], [D]; q/k norm NULL for Llama); kcache, vcache (f32
  * [Hkv][max_pos][D]).  h [H] f32 holds the step's input embedding and
  * receives the final residual (the lm_head's input).  `workspace`
  * (ep_decode_step_workspace bytes: the tagged hand-over buffers) must be

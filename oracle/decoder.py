@@ -6,11 +6,11 @@ Qwen3ForCausalLM with PackedLinear modules (epure/runtime.py:373-415,
 weights -- the exact f32 tile cb[idx] * scale (container.py:70-88) --
 for the GPU decoder's parity tests.
 
-``bf16_storage=True`` rounds to bf16 at the points where a bf16 model stores
-bf16 values and the GPU decoder does the same (the KV cache rows, the
-attention output fed to o_proj, the normalized lm_head input); all other
-arithmetic stays float32.  ``bf16_storage=False`` is pure float32 and is the
-mode pinned against transformers itself (tests/test_oracle_decoder.py).
+The default is pure float32, the mode pinned against transformers itself
+(tests/test_oracle_decoder.py) and the precision the GPU decoder computes
+in.  ``bf16_storage=True`` additionally rounds to bf16 where a bf16 model
+stores bf16 values (the KV cache rows, the attention output fed to o_proj,
+the normalized lm_head input), for comparisons with a bf16-storage run.
 
 Runs on whatever device its tensors live on (CPU for pinning, the GPU for
 full-size parity runs, where a dense f32 copy of the weights fits).
@@ -63,7 +63,7 @@ class RefDecoder:
     down ([N, K]), attn_norm, mlp_norm, and q_norm / k_norm (or None).
     """
 
-    def __init__(self, cfg, embed, lm_head, final_norm, layers, cos, sin, bf16_storage=True):
+    def __init__(self, cfg, embed, lm_head, final_norm, layers, cos, sin, bf16_storage=False):
         self.cfg, self.embed, self.lm_head, self.final_norm = cfg, embed, lm_head, final_norm
         self.layers, self.cos, self.sin = layers, cos.float(), sin.float()
         self.bf16 = bf16_storage
@@ -74,7 +74,7 @@ class RefDecoder:
         self.vc = [torch.zeros(cfg.n_kv, self.max_pos, D, device=dev) for _ in layers]
 
     @classmethod
-    def from_weights(cls, w, max_pos, bf16_storage=True, device=None):
+    def from_weights(cls, w, max_pos, bf16_storage=False, device=None):
         """Build from epure.decode.DecoderWeights (packed) by dequantizing."""
         cfg = w.cfg
         dev = device or w.embed.device

@@ -144,3 +144,10 @@ def test_decode_step_rejects_bad_arguments_without_launch(lib):
     rc = lib.ep_decode_step(None, 32, None, None, 0, None, None, None, 4096, 14336, 32, 8, 128,
                             448, 16, 128, _abi.F16, _abi.F32, 1e-5, 1e-5, 0.088, None, None)
     assert rc < 0 and "bad arguments" in _abi.last_error()
+
+
+def test_backward_workspace_empty_batch(lib):
+    # no tokens: no workspace, and no division by the zero tile count
+    assert lib.ep_dequant_matmul_bwd_workspace(0, 2048, 6144, 16, 128) == 0
+    assert lib.ep_dequant_matmul_bwd_workspace(4, 0, 6144, 16, 128) == 0
+    assert lib.ep_dequant_matmul_bwd_workspace(64, 256, 512, 16, 128) > 0

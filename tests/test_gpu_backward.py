@@ -129,3 +129,36 @@ def test_backward_declines_unserved():
     gy = torch.randn(4, 128, device=DEV)
     assert cuda.backward(gy, x, h) is None
     assert cuda.linear(x.requires_grad_(True), s) is None   # autograd: falls back to materialize
+
+
+def test_autograd_zero_rows_gives_zero_grads():
+    """An empty batch through a trainable bf16 PackedLinear: grads are the
+    sums over no tokens (zeros), grad_x is empty."""
+    _, _, _, _, s = make(256, 512, seed=31)
+    lin = PackedLinear(s)
+    make_trainable(torch.nn.Sequential(lin), "both", verbose=False)
+    s.cb.grad = torch.full_like(s.cb, 7.0)           # stale values must be replaced,
+    s.scale.grad = None                              # not accumulated into
+    x = torch.zeros((0, 512), device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    y = lin(x)
+    assert y.shape == (0, 256)
+    y.float().sum().backward()
+    torch.cuda.synchronize()
+    assert x.grad.shape == (0, 512)
+    assert torch.all(s.scale.grad == 0)
+    assert torch.all(s.cb.grad == 7.0)               # autograd accumulates a zero grad
+
+
+def test_fp32_activations_take_the_exact_route():
+    """fp32 x is declined by the fused backend (the kernels use fp16
+    operands), so PackedLinear computes it with the fp32 materialized
+    weight: float32 accuracy, not fp16-operand accuracy."""
+    idx, packed, scale, cb, s = make(384, 1024, seed=33)
+    g = torch.Generator(device=DEV).manual_seed(34)
+    x = torch.randn(3, 1024, generator=g, device=DEV)
+    assert cuda.linear(x, s) is None
+    with torch.no_grad():
+        y = PackedLinear(s)(x).double()
+    w = dense_tile(s.packed, s.scale, s.cb, 384, 1024, 128, 16).double()
+    want = x.double() @ w.t()
+    assert rel(y, want) < 1e-5

@@ -1,12 +1,14 @@
 """Greedy-decode parity of the gfx950 decoder against the dense float32
 oracle (oracle/decoder.py, itself pinned against transformers on CPU).
 
-Bar: greedy decode gives identical argmax tokens
-for 64 steps.  The oracle rounds to bf16 where the GPU decoder stores bf16
-(KV rows, attention output, lm_head input); everything else is float32, so
-the remaining differences are the GEMV's fp16 operands and summation order.
-Each test prints the oracle's smallest top-1/top-2 logit margin so a flip
-can be told apart from a near-tie.
+The GPU decoder computes in float32 (f32 KV cache, attention and lm_head
+input; the GEMVs carry f32 activations as hi + lo fp16 terms against the
+exact fp16 codebook entries), the precision of the reference model's float32
+forward, so the remaining differences are f32 rounding and summation
+order.  Bar: greedy decode gives identical argmax tokens for 64 steps at the
+Qwen3-1.7B and Llama-3-8B shapes, on a stream that varies, with every
+oracle top-1/top-2 margin larger than the GPU's logit error at that
+position (so no match is a coin flip).
 """
 import numpy as np
 import pytest
@@ -51,10 +53,8 @@ def test_small_decoder_logits_and_argmax(arch):
     got_arg = dec.argmax[:len(toks) - 1].cpu().tolist()
     print(f"{arch}: worst normwise logit error {worst:.2e}, min margin {min(margins):.3e}")
     assert got_arg == ref_arg
-    # Both sides round the KV rows and the attention output to bf16; a value
-    # that lands on the other side of a bf16 rounding boundary moves by 2^-9
-    # relative, so the logits are compared at 1e-2 (argmax must match).
-    assert worst < 1e-2
+    # float32 on both sides: f32 rounding and summation order only
+    assert worst < 1e-5
 
 
 def test_graph_replay_matches_eager():
@@ -69,19 +69,77 @@ def test_graph_replay_matches_eager():
     assert torch.equal(la, dec.logits)
 
 
+def _teacher_forced(dec, ref, toks):
+    """Both decoders fed ``toks``; per position the GPU's logits against the
+    oracle's: (max abs error, normwise error, oracle top-1 minus top-2
+    margin, oracle argmax, GPU argmax)."""
+    dec.reset(toks)
+    dec.capture()
+    rows = []
+    for pos in range(len(toks) - 1):
+        dec.step()
+        want = ref.step(toks[pos], pos)
+        diff = dec.logits - want
+        err = float(diff.abs().max())
+        top = torch.topk(want, 2)
+        pair = float((diff[top.indices[0]] - diff[top.indices[1]]).abs())
+        rows.append((err, err / float(want.abs().max()), float(top.values[0] - top.values[1]),
+                     int(top.indices[0]), int(dec.logits.argmax()), pair))
+    torch.cuda.synchronize()
+    assert not dec.step_failed(), "a hand-over wait of the one-launch step timed out"
+    return rows
+
+
+FULL = [(QWEN3_1_7B, 32), (LLAMA3_8B, 128)]
+
+
 @pytest.mark.parametrize("persistent", [True, False], ids=["one-launch", "per-layer"])
-@pytest.mark.parametrize("cfg,n_prompt", [(QWEN3_1_7B, 32), (LLAMA3_8B, 128)],
-                         ids=["qwen3-1.7b", "llama3-8b"])
+@pytest.mark.parametrize("cfg,n_prompt", FULL, ids=["qwen3-1.7b", "llama3-8b"])
 def test_greedy_64_steps_identical(cfg, n_prompt, persistent):
+    """Free-running greedy decode, 64 new tokens, full depth: identical to
+    the oracle's.  Not a constant stream (at least 32 distinct tokens), and
+    not luck: at every generated position the oracle's top-1/top-2 margin
+    exceeds the GPU's largest logit error there (measured teacher-forced on
+    the same tokens), so no argmax could have flipped."""
     w = random_weights(cfg, seed=0, device=DEV)
     dec = Decoder(w, n_prompt + 64 + 1, persistent=persistent)
     prompt = prompt_ids(n_prompt, cfg.vocab, 1)
     toks, _ = dec.generate(prompt, 64)
     ref = RefDecoder.from_weights(w, dec.max_pos)
-    want, _, margins = ref.generate(prompt, 64)
-    gen_m = margins[n_prompt - 1:]
-    print(f"{cfg.name}: min oracle margin over the 64 greedy steps {min(gen_m):.3e}")
-    assert not dec.step_failed(), "a grid barrier of the one-launch step timed out"
+    want, _, _ = ref.generate(prompt, 64)
     first = next((i for i, (x, y) in enumerate(zip(toks, want)) if x != y), None)
-    assert first is None, (f"diverged at position {first}: got {toks[first]} want {want[first]}, "
-                           f"oracle margin there {margins[first - 1]:.3e}")
+    assert first is None, f"diverged at position {first}: got {toks[first]} want {want[first]}"
+    gen = want[n_prompt:]
+    rows = _teacher_forced(dec, ref, want)[n_prompt - 1:]
+    slack = min(r[2] - r[0] for r in rows)
+    pslack = min(r[2] - r[5] for r in rows)
+    norm = np.array([r[1] for r in rows])
+    print(f"{cfg.name} {'one-launch' if persistent else 'per-layer'}: {len(set(gen))} distinct of "
+          f"{len(gen)}; min margin {min(r[2] for r in rows):.4e}, max logit error "
+          f"{max(r[0] for r in rows):.4e}, min margin - error {slack:.4e}, min margin - pair error "
+          f"{pslack:.4e}, near-ties {sum(r[2] <= r[0] for r in rows)}, normwise median "
+          f"{np.median(norm):.2e} max {norm.max():.2e}")
+    assert len(set(gen)) >= 32, f"greedy stream nearly constant: {len(set(gen))} distinct"
+    assert slack > 0, "an oracle margin is below the GPU's logit error: a near-tie"
+
+
+@pytest.mark.parametrize("cfg,n_prompt", FULL, ids=["qwen3-1.7b", "llama3-8b"])
+def test_full_depth_teacher_forced_logits(cfg, n_prompt):
+    """Every layer of the full model, one-launch step, random tokens (not
+    self-generated) for n_prompt + 64 positions, against the float32 oracle
+    (the mode pinned against transformers): normwise logit error median
+    < 1e-4 and max < 5e-4, and the argmax equal at every position whose
+    oracle margin exceeds the logit error there."""
+    w = random_weights(cfg, seed=5, device=DEV)
+    toks = prompt_ids(n_prompt + 64, cfg.vocab, 9)
+    dec = Decoder(w, len(toks) + 1, persistent=True)
+    assert dec.persistent
+    ref = RefDecoder.from_weights(w, dec.max_pos)
+    rows = _teacher_forced(dec, ref, toks)
+    norm = np.array([r[1] for r in rows])
+    flips = [i for i, (e, _, m, a, b, _) in enumerate(rows) if a != b and m > e]
+    print(f"{cfg.name} full depth: normwise median {np.median(norm):.2e} max {norm.max():.2e}; "
+          f"argmax agreement {sum(r[3] == r[4] for r in rows)}/{len(rows)}; positions with "
+          f"margin <= error {sum(r[2] <= r[0] for r in rows)}")
+    assert not flips, f"argmax differs beyond the logit error at positions {flips}"
+    assert np.median(norm) < 1e-4 and norm.max() < 5e-4

@@ -54,7 +54,7 @@ def test_fused_rmsnorm_three_segments(K):
     fused(_abi.XSRC_RMSNORM, h, w, segs, ys, K)
     xn = rms(h, w, 1e-5)
     for y, s in zip(ys, segs):
-        assert normwise(y, s[3] @ xn) < 2e-3
+        assert normwise(y, s[3] @ xn) < 2e-5   # f32 activations as hi + lo fp16 terms
 
 
 @pytest.mark.parametrize("K", [1024, 6144, 14336])
@@ -66,7 +66,7 @@ def test_fused_swiglu_accumulate(K):
     y = y0.clone()
     fused(_abi.XSRC_SWIGLU, gt, ut, [seg], [y], K, accumulate=True)
     want = y0 + seg[3] @ (torch.nn.functional.silu(gt) * ut)
-    assert normwise(y, want) < 2e-3
+    assert normwise(y, want) < 2e-5
 
 
 def test_fused_plain_bf16_accumulate():
@@ -88,8 +88,7 @@ def attention_ref(q, k, v, kc, vc, cos, sin, pos, Hq, Hkv, D, qn, kn, eps):
     c = torch.cat((cos[pos], cos[pos]))
     s = torch.cat((sin[pos], sin[pos]))
     q = q * c + rotate_half(q) * s
-    k = (k * c + rotate_half(k) * s).to(torch.bfloat16).float()
-    v = v.to(torch.bfloat16).float()
+    k = k * c + rotate_half(k) * s
     K = kc[:, :pos + 1].float().clone()
     V = vc[:, :pos + 1].float().clone()
     K[:, pos], V[:, pos] = k, v
@@ -109,8 +108,8 @@ def test_decode_attention(qk_norm, Hq, Hkv, D, pos):
     q = torch.randn(Hq * D, generator=g(pos), device=DEV)
     k = torch.randn(Hkv * D, generator=g(pos + 1), device=DEV)
     v = torch.randn(Hkv * D, generator=g(pos + 2), device=DEV)
-    kc = torch.randn(Hkv, max_pos, D, generator=g(3), device=DEV).to(torch.bfloat16)
-    vc = torch.randn(Hkv, max_pos, D, generator=g(4), device=DEV).to(torch.bfloat16)
+    kc = torch.randn(Hkv, max_pos, D, generator=g(3), device=DEV)
+    vc = torch.randn(Hkv, max_pos, D, generator=g(4), device=DEV)
     qn = (1 + 0.1 * torch.randn(D, generator=g(5), device=DEV)).to(torch.bfloat16) \
         if qk_norm else None
     kn = (1 + 0.1 * torch.randn(D, generator=g(6), device=DEV)).to(torch.bfloat16) \
@@ -119,7 +118,7 @@ def test_decode_attention(qk_norm, Hq, Hkv, D, pos):
     state = torch.tensor([pos, 0], dtype=torch.int32, device=DEV)
     part = torch.zeros(_abi.lib.ep_attention_workspace(Hq, D, max_pos) // 4, device=DEV)
     ctr = torch.zeros(Hq, dtype=torch.int32, device=DEV)
-    out = torch.zeros(Hq * D, dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros(Hq * D, dtype=torch.float32, device=DEV)
     for rep in range(2):                                 # second call: counters were reset
         rc = _abi.lib.ep_decode_attention(
             q.data_ptr(), k.data_ptr(), v.data_ptr(), qn.data_ptr() if qk_norm else None,
@@ -129,9 +128,10 @@ def test_decode_attention(qk_norm, Hq, Hkv, D, pos):
         assert rc == 0, _abi.last_error()
         torch.cuda.synchronize()
         assert not ctr.any()
-        assert normwise(out.float(), want) < 1e-2          # bf16 output
-        assert torch.equal(kc[:, pos].float(), kw) or normwise(kc[:, pos].float(), kw) < 1e-2
-        assert torch.equal(vc[:, pos].float(), vw)
+        # float32 throughout: f32 rounding and summation order only
+        assert normwise(out, want) < 2e-6
+        assert normwise(kc[:, pos], kw) < 2e-6
+        assert torch.equal(vc[:, pos], vw)
 
 
 @pytest.mark.parametrize("V,H,n_prompt,pos", [(1000, 512, 1, 0), (128256, 4096, 10, 3),
@@ -141,8 +141,8 @@ def test_lm_head_argmax(V, H, n_prompt, pos):
     emb = (torch.randn(V, H, generator=g(2), device=DEV) * 0.02).to(torch.bfloat16)
     h = torch.randn(H, generator=g(3), device=DEV)
     nw = (1 + 0.1 * torch.randn(H, generator=g(4), device=DEV)).to(torch.bfloat16)
-    xn = (h * torch.rsqrt(h.square().mean() + 1e-5)).to(torch.bfloat16).float() * nw.float()
-    want = W.float() @ xn.to(torch.bfloat16).float()
+    xn = h * torch.rsqrt(h.square().mean() + 1e-5) * nw.float()
+    want = W.float() @ xn
     am = int(want.argmax())
     grid = 1024
     logits = torch.zeros(V, device=DEV)
@@ -159,7 +159,7 @@ def test_lm_head_argmax(V, H, n_prompt, pos):
         tokens.data_ptr(), amax.data_ptr(), emb.data_ptr(), 63, grid, _abi.stream_handle())
     assert rc == 0, _abi.last_error()
     torch.cuda.synchronize()
-    assert normwise(logits, want) < 1e-3
+    assert normwise(logits, want) < 1e-5                   # f32 products, f32 sums
     assert int(amax[pos]) == am, (int(amax[pos]), am, float(torch.topk(want, 2).values.diff()))
     nxt = 100 + pos + 1 if pos + 1 < n_prompt else am
     assert int(tokens[pos + 1]) == nxt and state.tolist() == [pos + 1, nxt]

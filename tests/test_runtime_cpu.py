@@ -131,3 +131,22 @@ def test_expert_holder_cpu_and_packed_experts_shape_checks():
         runtime.PackedExperts(PackedWeight((24, 64), packed, scale, cb, 32, 16))
     with pytest.raises(RuntimeError):
         runtime.PackedExperts(s)(torch.zeros(2, 64), torch.tensor([0, 1]))
+
+
+def test_pack4_rejects_wide_index_and_store_checks_bytes():
+    with pytest.raises(ValueError):
+        runtime._pack4(np.array([3, 16], np.uint8), 16)
+    _, packed, scale, cb = ref.synth_linear(8, 64, 16, 32, seed=1)
+    with pytest.raises(ValueError):
+        PackedWeight((8, 64), packed[:-1], scale, cb, 32, 16)
+
+
+@pytest.mark.parametrize("k", [7, 33])
+def test_packed_embedding_odd_k_reads_flat_stream(k):
+    # 4-bit rows with odd K are not byte-aligned: rows are read by flat position
+    idx, packed, scale, cb = ref.synth_linear(9, k, 16, 4, seed=k)
+    s = PackedWeight((9, k), packed, scale, cb.astype(np.float32), 4, 16)
+    ids = torch.tensor([8, 0, 5, 5])
+    got = runtime.PackedEmbedding(s, torch.float32)(ids)
+    want = ref.dequant_tile_f32(idx.reshape(9, k), scale, cb, 4)[ids.numpy()]
+    assert np.array_equal(got.numpy(), want)
