@@ -34,6 +34,14 @@ _SIGS = {
         _c_i64, _c_i64, _c_i64,                  # M, N, K
         _p, _c_int, _c_i64, _c_int,              # y, y_dtype, ldy, flags
         _p, _sz, _p]),                           # workspace, bytes, stream
+    "ep_noalloc_scratch_bytes": (_sz, []),
+    "ep_dequant_matmul_noalloc": (_c_int, [
+        _p, _c_int, _c_i64,                      # x, x_dtype, ldx
+        _p, _p, _c_int, _c_i64,                  # packed, scale, scale_dtype, ld_scale
+        _p, _c_int, _c_int, _c_int,              # cb, cb_dtype, levels, group
+        _c_i64, _c_i64, _c_i64,                  # M, N, K
+        _p, _c_int, _c_i64, _c_int,              # y, y_dtype, ldy, flags
+        _p]),                                    # stream
     "ep_dequant_matmul_bwd_workspace": (_sz, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "ep_dequant_matmul_bwd": (_c_int, [
         _p, _c_int, _c_i64,                      # gy, gy_dtype, ldgy

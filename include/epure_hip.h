@@ -144,6 +144,25 @@ int ep_embedding_rows(const uint8_t *packed, const void *scale, int scale_dtype,
                       int group, int64_t N, int64_t K, const int64_t *ids, int64_t n_ids,
                       void *out, int out_dtype, int64_t ldo, void *stream);
 
+/*
+ * ep_dequant_matmul without a workspace argument, for callers that cannot
+ * allocate device memory (code being captured into a HIP graph, serving
+ * loops that forbid allocation).  No counterpart in the reference: its
+ * kernels allocate their outputs per call.  Same arguments, semantics and
+ * return codes as ep_dequant_matmul; the workspace is a static device array
+ * of ep_noalloc_scratch_bytes() bytes (32 MiB) per GPU, kept until the
+ * process ends.  Shapes whose ep_dequant_matmul_workspace exceeds it are
+ * rejected with EP_ERR_WORKSPACE before any launch.  Nothing is allocated
+ * and nothing in the scratch must start at zero; calls that overlap on one
+ * GPU (two streams or threads at once) race on the shared scratch.
+ */
+size_t ep_noalloc_scratch_bytes(void);
+int ep_dequant_matmul_noalloc(const void *x, int x_dtype, int64_t ldx,
+                              const uint8_t *packed, const void *scale, int scale_dtype,
+                              int64_t ld_scale, const void *cb, int cb_dtype, int levels,
+                              int group, int64_t M, int64_t N, int64_t K,
+                              void *y, int y_dtype, int64_t ldy, int flags, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

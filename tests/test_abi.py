@@ -113,12 +113,12 @@ def test_decode_step_layer_descriptor_is_27_pointers(lib):
 
 def test_decode_step_workspace_size(lib):
     # 8-byte tagged values, each buffer 256-byte aligned: sync, residual
-    # (2 x 32 ring slots), q, k, v, attention output (bf16 pairs, 32 slots),
+    # (2 x 32 ring slots), q, k, v, attention output (f32, 32 slots),
     # SwiGLU output (32 slots), split-KV partials
     def r(n):
         return (n * 8 + 255) // 256 * 256
     H, I, Hq, Hkv, D, P = 4096, 14336, 32, 8, 128, 448
-    want = r(8) + r(64 * H) + r(Hq * D) + 2 * r(Hkv * D) + r(32 * Hq * D // 2) + r(32 * I) + \
+    want = r(8) + r(64 * H) + r(Hq * D) + 2 * r(Hkv * D) + r(32 * Hq * D) + r(32 * I) + \
         r(Hq * (P // 64 + 1) * (D + 2))
     assert lib.ep_decode_step_workspace(H, I, Hq, Hkv, D, P) == want
     assert lib.ep_decode_step_workspace(H, I, 0, Hkv, D, P) == 0
