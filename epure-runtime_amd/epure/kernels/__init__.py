@@ -6,10 +6,8 @@
 ``None`` means "this backend cannot serve this call" and the caller falls
 back to materializing the weight.
 
-``cuda`` is the gfx950 HIP backend.  ``cpu`` keeps the reference's CPU
-backend interface but always declines: the CPU kernel is outside this
-build's scope (the reference's own CPU path is reproduced only as the test
-oracle), exactly like a reference install without its Rust extension.
+``cuda`` is the gfx950 HIP backend (libepure_hip.so); ``cpu`` is the host
+backend (libepure_cpu.so), bit-identical to the reference's Rust kernel.
 """
 from . import cpu, cuda
 

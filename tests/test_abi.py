@@ -16,13 +16,18 @@ HEADERS = [os.path.join(ROOT, "include", f) for f in os.listdir(os.path.join(ROO
            if f.endswith(".h")]
 
 
+# which library exports the entry points a header declares
+LIBRARY_OF = {"epure_cpu.h": "libepure_cpu.so"}
+
+
 def declared_functions():
     names = set()
     for h in HEADERS:
         text = open(h).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        lib = LIBRARY_OF.get(os.path.basename(h), "libepure_hip.so")
         for m in re.finditer(r"\b(ep_[a-z0-9_]+)\s*\(", text):
-            names.add(m.group(1))
+            names.add((m.group(1), lib))
     return sorted(names)
 
 
@@ -34,16 +39,16 @@ def lib():
 
 
 def test_header_declares_entry_points():
-    names = declared_functions()
+    names = [n for n, _ in declared_functions()]
     for required in ("ep_dequant_matmul", "ep_dequant_matmul_bwd", "ep_unpack_indices",
                      "ep_dequant_tile", "ep_hip_available", "ep_last_error", "ep_abi_version"):
         assert required in names
 
 
-@pytest.mark.parametrize("name", declared_functions())
-def test_library_exports_declared_symbol(lib, name):
-    raw = ctypes.CDLL(_abi.LIB_PATH)
-    assert hasattr(raw, name), f"{name} declared in include/ but not exported"
+@pytest.mark.parametrize("name,libname", declared_functions())
+def test_library_exports_declared_symbol(lib, name, libname):
+    raw = ctypes.CDLL(os.path.join(os.path.dirname(_abi.LIB_PATH), libname))
+    assert hasattr(raw, name), f"{name} declared in include/ but not exported by {libname}"
 
 
 def test_version(lib):

@@ -43,14 +43,15 @@ def test_materialize_cpu_matches_oracle(dtype, name):
     assert np.array_equal(w, want)
 
 
-def test_cpu_backend_declines_and_linear_falls_back():
+def test_cpu_backend_declines_other_dtypes_and_linear_falls_back():
     _, s = store()
-    x = torch.randn(3, 256)
-    assert cpu.available() is False and cpu.linear(x, s) is None
+    x = torch.randn(3, 256).to(torch.bfloat16)
+    assert cpu.available() is True and cpu.linear(x, s) is None   # bf16 x: decline
     assert cuda.linear(x, s) is None                    # CPU tensor: decline
-    lin = PackedLinear(s, bias=torch.ones(16))
+    lin = PackedLinear(s, bias=torch.ones(16, dtype=torch.bfloat16))
     y = lin(x)
-    assert torch.allclose(y, x @ s.materialize(torch.float32).T + 1, rtol=1e-6, atol=1e-6)
+    want = torch.nn.functional.linear(x, s.materialize(torch.bfloat16), lin.bias)
+    assert torch.equal(y, want)
 
 
 def test_finetune_index_freeze_cycle():
