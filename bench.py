@@ -56,7 +56,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--config", default="llama3-8b", choices=["llama3-8b", "qwen3-1.7b"])
+    ap.add_argument("--config", default="llama3-8b",
+                    choices=["llama3-8b", "qwen3-1.7b", "qwen3-8b", "llama3.2-3b"])
     ap.add_argument("--prompt", type=int, default=None)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -189,6 +190,69 @@ def gemv_sweep(seed=0, sets=64, replays=20):
 MFMA_PEAK_TFLOPS = 2500.0
 
 
+def read_probe(replays=10):
+    """The practical read ceiling (ep_read_probe, the dequant kernels' load
+    shape), best over 1-8 resident workgroups per CU: one 1 GiB launch per
+    replay -> GB/s; and a config-0-sized launch (8,650,816 bytes, the
+    4096x4096 4-bit weights) over 64 rotating buffers in one graph ->
+    microseconds per launch."""
+    import torch
+    from epure.kernels import _abi
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    sink = torch.zeros(8 * cus, dtype=torch.int32, device=dev)
+
+    def launch(buf, nbytes, grid):
+        def f(stream):
+            rc = _abi.lib.ep_read_probe(buf.data_ptr(), nbytes, sink.data_ptr(), grid, stream)
+            if rc != 0:
+                raise RuntimeError(f"ep_read_probe: {rc} {_abi.last_error()}")
+        return f
+    grids = [cus, 2 * cus, 4 * cus, 8 * cus]
+    big = torch.ones(1 << 28, dtype=torch.int32, device=dev)          # 1 GiB
+    big_ms = {g: _graph_time([launch(big, big.numel() * 4, g)], replays) for g in grids}
+    del big
+    c0 = _weight_bytes(4096, 4096, 16) // 16 * 16
+    bufs = [torch.ones(c0 // 4, dtype=torch.int32, device=dev) for _ in range(64)]
+    c0_ms = {g: _graph_time([launch(b, c0, g) for b in bufs], replays) / len(bufs) for g in grids}
+    del bufs
+    torch.cuda.empty_cache()
+    gb = min(big_ms, key=big_ms.get)
+    gc = min(c0_ms, key=c0_ms.get)
+    return {"kernel": "read_probe_kernel",
+            "ceiling_gbs": round((1 << 30) / (big_ms[gb] * 1e-3) / 1e9, 1),
+            "ceiling_workgroups_per_cu": gb // cus,
+            "ceiling_gbs_by_wg_per_cu": {g // cus: round((1 << 30) / (ms * 1e-3) / 1e9, 1)
+                                         for g, ms in big_ms.items()},
+            "config0_launch_bytes": c0, "config0_launch_us": round(c0_ms[gc] * 1e3, 3),
+            "config0_launch_workgroups_per_cu": gc // cus,
+            "config0_launch_gbs": round(c0 / (c0_ms[gc] * 1e-3) / 1e9, 1)}
+
+
+def _dense_time(stores, x, replays):
+    """The route the caller takes above EPURE_DENSE_ABOVE (runtime.py:117-126):
+    materialize(bf16) -- one ep_dequant_tile launch into a preallocated
+    [N, K] bf16 tile -- then torch.matmul (hipBLASLt), for each rotating
+    weight set; ms per linear."""
+    import torch
+    from epure.kernels import _abi, cuda
+    hs = [cuda._hot(s) for s in stores]
+    w = torch.empty((hs[0].N, hs[0].K), device=x.device, dtype=torch.bfloat16)
+    y = torch.empty((x.shape[0], hs[0].N), device=x.device, dtype=torch.bfloat16)
+
+    def one(h):
+        def f(stream):
+            rc = _abi.lib.ep_dequant_tile(
+                h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+                h.cb.data_ptr(), h.cb_dt, h.levels, h.group, h.N, h.K, w.data_ptr(),
+                _abi.BF16, w.stride(0), stream)
+            if rc != 0:
+                raise RuntimeError(f"ep_dequant_tile: {_abi.last_error()}")
+            torch.matmul(x, w.t(), out=y)
+        return f
+    return _graph_time([one(h) for h in hs], replays) / len(hs)
+
+
 def prefill_sweep(seed=0, replays=10):
     """Config 3: 8-bit indices (256-entry fp16-valued codebook, group-128 fp16
     scales), (N, K) in {4096x4096, 14336x4096, 4096x14336}, bf16 x with M in
@@ -207,9 +271,11 @@ def prefill_sweep(seed=0, replays=10):
             x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
             lins = [_Linear(s, x) for s in stores]
             ms = _graph_time([L.fwd for L in lins], replays) / sets
+            dense_ms = _dense_time(stores, x, replays)
             byt = wb + m * k * 2 + m * n * 2
             flop = 2.0 * m * n * k
             rows.append({"N": n, "K": k, "M": m, "us": round(ms * 1e3, 2),
+                         "dense_us": round(dense_ms * 1e3, 2),
                          "gbs": round(byt / (ms * 1e-3) / 1e9, 1),
                          "hbm_frac": round(byt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
@@ -370,9 +436,12 @@ def side_workload(args):
                    dtype="f16", **base)
         out["config"] = {"workload": "config 0: one 4096x4096 4-bit packed linear, x bf16 [1,4096], "
                                      f"{g['rotating_sets']} rotating weight sets", **g}
+        probe = read_probe()
         out["roofline"] = {"bound": "hbm", "kernel": g["kernel"], "achieved": g["achieved_gbs"],
                            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": g["frac"],
-                           "traffic": None}
+                           "traffic": None, "probe": probe,
+                           "frac_of_probe_launch": round(probe["config0_launch_us"]
+                                                         / g["us_per_launch"], 4)}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_gemv_baseline(4096, 4096, 16, [1], args.cpu_threads)
     elif args.workload == "prefill":
@@ -381,9 +450,15 @@ def side_workload(args):
         out = dict(metric="8-bit packed linear prefill sweep: TFLOP/s (large M), GB/s (small M)",
                    value=top["tflops"], unit="TFLOP/s", ms_per_step=top["us"] / 1e3,
                    dtype="f16", **base)
+        # the smallest M from which the dense route wins at every shape
+        ms_sorted = sorted({r["M"] for r in rows})
+        cross = next((m for m in ms_sorted
+                      if all(r["dense_us"] < r["us"] for r in rows if r["M"] >= m)), None)
         out["config"] = {"workload": "config 3: 8-bit codebook (256 levels), group 128; "
                                      "(N,K) in {4096x4096, 14336x4096, 4096x14336}, "
-                                     "M in {1,4,16,64,512,2048}", "rows": rows}
+                                     "M in {1,4,16,64,512,2048}", "rows": rows,
+                         "dense_route": "materialize(bf16) via ep_dequant_tile + torch.matmul",
+                         "dense_wins_from_M": cross}
         out["roofline"] = {"bound": "mfma", "kernel": top["kernel"],
                            "achieved": top["tflops"], "peak": MFMA_PEAK_TFLOPS,
                            "unit": "TFLOP/s", "frac": top["mfma_frac"], "traffic": None,
@@ -426,11 +501,10 @@ def main():
         return
 
     import torch
-    from epure.decode import LLAMA3_8B, QWEN3_1_7B, Decoder, random_weights
-    from epure.kernels import _abi
+    from epure.decode import CONFIGS, Decoder, random_weights
 
-    cfg = {"llama3-8b": LLAMA3_8B, "qwen3-1.7b": QWEN3_1_7B}[args.config]
-    n_prompt = args.prompt or (128 if args.config == "llama3-8b" else 32)
+    cfg = CONFIGS[args.config]
+    n_prompt = args.prompt or (32 if args.config == "qwen3-1.7b" else 128)
     dev = torch.device("cuda:0")
     print(f"# building {cfg.name} random weights (seed {args.seed})", file=sys.stderr, flush=True)
     w = random_weights(cfg, seed=args.seed, device=dev)
@@ -536,11 +610,17 @@ def main():
             "calibrated by bench.py --copy-probe; not measured in this run",
         },
     }
+    del dec, w, g
+    torch.cuda.empty_cache()
+    print("# streaming-read probe", file=sys.stderr, flush=True)
+    probe = read_probe()
+    out["roofline"]["probe"] = probe
+    out["roofline"]["frac_of_probe"] = round(kern_gbs / probe["ceiling_gbs"], 4)
     if not args.no_gemv:
-        del dec, w, g
-        torch.cuda.empty_cache()
         print("# config-0 GEMV sweep", file=sys.stderr, flush=True)
         out["gemv"] = gemv_sweep(args.seed)
+        out["gemv"]["frac_of_probe_launch"] = round(probe["config0_launch_us"]
+                                                    / out["gemv"]["us_per_launch"], 4)
     if not args.no_cpu_baseline:
         print("# CPU baseline (reference Rust semantics, C port)", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(cfg, args.cpu_threads)

@@ -156,6 +156,7 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
 size_t backward_workspace(int64_t M, int64_t N, int64_t K, int levels, int group);
 
 int launch_unpack(const uint8_t *packed, int64_t n, int levels, uint8_t *idx, hipStream_t stream);
+int launch_read_probe(const void *buf, int64_t bytes, uint32_t *sink, int grid, hipStream_t stream);
 int launch_embedding_rows(const PackedDesc &w, const int64_t *ids, int64_t n_ids, void *out,
                           int out_dtype, int64_t ldo, hipStream_t stream);
 int launch_dequant_tile(const PackedDesc &w, void *out, int out_dtype, int64_t ldo,

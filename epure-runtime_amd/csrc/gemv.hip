@@ -801,7 +801,8 @@ void plan(int64_t KB, int &spw, int &waves)
         waves = 1;
 }
 
-bool shape_ok(int bits, int64_t N, int64_t K, int group, int64_t ld_scale)
+// hl: the activations are f32 (hi + lo terms, twice the registers).
+bool shape_ok(int bits, int64_t N, int64_t K, int group, int64_t ld_scale, bool hl)
 {
     if (N < 1 || N > INT32_MAX || K < 1)
         return false;
@@ -814,7 +815,7 @@ bool shape_ok(int bits, int64_t N, int64_t K, int group, int64_t ld_scale)
         return false;
     int spw, waves;
     plan(rb, spw, waves);
-    return spw <= 8 && fits(bits, spw, 1, true);
+    return spw <= 8 && fits(bits, spw, 1, hl);
 }
 
 }  // namespace
@@ -822,7 +823,7 @@ bool shape_ok(int bits, int64_t N, int64_t K, int group, int64_t ld_scale)
 bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
 {
     const int bits = w.bits();
-    if (M < 1 || M > 4 || !shape_ok(bits, w.N, w.K, w.group, w.ld_scale))
+    if (M < 1 || M > 4 || !shape_ok(bits, w.N, w.K, w.group, w.ld_scale, x.dtype == EP_F32))
         return false;
     if (((uintptr_t)w.packed & 15) != 0)
         return false;
@@ -900,7 +901,7 @@ int launch_gemv_fused(const FusedGemv &f, hipStream_t stream)
     a.group = f.group;
     a.nseg = f.nseg;
     for (int i = 0; i < f.nseg; ++i) {
-        if (!shape_ok(bits, f.seg[i].N, f.K, f.group, a.lds))
+        if (!shape_ok(bits, f.seg[i].N, f.K, f.group, a.lds, a.x_dtype == EP_F32))
             return set_error(EP_DECLINE_SHAPE, "fused GEMV: segment %d shape not served", i);
         if (((uintptr_t)f.seg[i].packed & 15) != 0)
             return set_error(EP_DECLINE_SHAPE, "fused GEMV: packed not 16-byte aligned");

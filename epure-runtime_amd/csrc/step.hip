@@ -113,11 +113,13 @@ struct Model {
     static_assert(H % 512 == 0 && HQD % 512 == 0 && I % 512 == 0, "rows of whole slabs");
 };
 
-// Llama-3-8B and Qwen3-1.7B shapes; shares
-// at 256 workgroups: q|k|v 6 / 4 quads, o 8 / 4 (on at least half the grid),
-// gate|up 14 / 6, down 4 / 2.
+// Llama-3-8B, Qwen3-1.7B, Qwen3-8B and Llama-3.2-3B shapes; shares at 256
+// workgroups: q|k|v 6 / 4 / 6 / 5 quads, o 8 / 4 / 8 / 6 (on at least half
+// the grid), gate|up 14 / 6 / 12 / 8, down 4 / 2 / 4 / 3.
 using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 8, 14, 4, 0, 0, 0, 2>;
 using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 4, 6, 2>;
+using ModelQ8B = Model<4096, 4096, 12288, 4, 3, 2, 2, 4, 6, 8, 12, 4, 0, 0, 0, 2>;
+using ModelL3B = Model<3072, 3072, 8192, 3, 2, 2, 2, 3, 5, 6, 8, 3>;
 
 // Where a phase of contraction length K keeps its activations, factors and
 // accumulator inside the region.
@@ -1417,12 +1419,17 @@ static int variant_of(const StepDesc &d)
         return 0;
     }
     const int GQ = d.Hq / d.Hkv;
-    if (d.H == ModelL8B::H && d.Hq * d.D == ModelL8B::HQD && d.I == ModelL8B::I &&
-        GQ == ModelL8B::GQ)
+    auto is = [&](int H, int HQD, int I, int gq) {
+        return d.H == H && d.Hq * d.D == HQD && d.I == I && GQ == gq;
+    };
+    if (is(ModelL8B::H, ModelL8B::HQD, ModelL8B::I, ModelL8B::GQ))
         return 1;
-    if (d.H == ModelQ17::H && d.Hq * d.D == ModelQ17::HQD && d.I == ModelQ17::I &&
-        GQ == ModelQ17::GQ)
+    if (is(ModelQ17::H, ModelQ17::HQD, ModelQ17::I, ModelQ17::GQ))
         return 2;
+    if (is(ModelQ8B::H, ModelQ8B::HQD, ModelQ8B::I, ModelQ8B::GQ))
+        return 3;
+    if (is(ModelL3B::H, ModelL3B::HQD, ModelL3B::I, ModelL3B::GQ))
+        return 4;
     set_error(EP_DECLINE_SHAPE,
               "decode step: no persistent variant for hidden %d, heads %d/%d, intermediate %d",
               d.H, d.Hq, d.Hkv, d.I);
@@ -1496,7 +1503,16 @@ int launch_decode_step(const StepDesc &d, hipStream_t stream)
     a.qk_eps = d.qk_eps;
     a.att_scale = d.att_scale;
     a.trace = d.trace;
-    return var == 1 ? launch_model<ModelL8B>(a, stream) : launch_model<ModelQ17>(a, stream);
+    switch (var) {
+    case 1:
+        return launch_model<ModelL8B>(a, stream);
+    case 2:
+        return launch_model<ModelQ17>(a, stream);
+    case 3:
+        return launch_model<ModelQ8B>(a, stream);
+    default:
+        return launch_model<ModelL3B>(a, stream);
+    }
 }
 
 size_t decode_step_layer_bytes() { return sizeof(StepLayer); }

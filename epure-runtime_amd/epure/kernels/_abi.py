@@ -34,6 +34,7 @@ _SIGS = {
         _c_i64, _c_i64, _c_i64,                  # M, N, K
         _p, _c_int, _c_i64, _c_int,              # y, y_dtype, ldy, flags
         _p, _sz, _p]),                           # workspace, bytes, stream
+    "ep_read_probe": (_c_int, [_p, _c_i64, _p, _c_int, _p]),
     "ep_noalloc_scratch_bytes": (_sz, []),
     "ep_dequant_matmul_noalloc": (_c_int, [
         _p, _c_int, _c_i64,                      # x, x_dtype, ldx

@@ -48,7 +48,10 @@ _BUFFER_CACHE = {}
 
 # Rows at or above which a GPU call skips the fused kernels and runs
 # materialize + a dense GEMM (reference runtime.py:26-31 defaults to 8 on
-# A100).  Unset, every row count stays on the fused kernels.
+# A100).  On MI355X the fused kernels win at every measured row count of
+# the 8-bit config-3 sweep (M = 1..2048 at 4096x4096, 14336x4096,
+# 4096x14336) but one near-tie (M = 2048 at 14336x4096: 386 vs 368 us), so
+# unset every row count stays on the fused kernels.
 _DENSE_ABOVE = int(os.environ.get("EPURE_DENSE_ABOVE", str(2**31 - 1)))
 
 _TABLE = 256  # entries of the level table (the largest codebook an index can address)

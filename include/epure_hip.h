@@ -145,6 +145,18 @@ int ep_embedding_rows(const uint8_t *packed, const void *scale, int scale_dtype,
                       void *out, int out_dtype, int64_t ldo, void *stream);
 
 /*
+ * Streaming-read probe: reads bytes (a multiple of 16, 16-byte aligned) of
+ * buf once with the dequant kernels' load shape (16-byte non-temporal loads,
+ * 8 in flight per lane, 512-thread workgroups, `grid` of them) and writes
+ * one XOR word per workgroup to sink[grid] (the XOR of all sink words is the
+ * XOR of the buffer's 32-bit words).  The practical HBM read ceiling the
+ * kernels are measured against; the reference's counterpart is its
+ * same-traffic diagnostic kernel, epure/kernels/_triton.py:188-236
+ * (dequant_nolut).
+ */
+int ep_read_probe(const void *buf, int64_t bytes, uint32_t *sink, int grid, void *stream);
+
+/*
  * ep_dequant_matmul without a workspace argument, for callers that cannot
  * allocate device memory (code being captured into a HIP graph, serving
  * loops that forbid allocation).  No counterpart in the reference: its

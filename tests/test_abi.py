@@ -135,6 +135,15 @@ def test_decode_step_serves_baseline_shapes(lib, shape):
     assert _serves(lib, **shape, cdt=_abi.F16) == 1
 
 
+QWEN8B = dict(H=4096, I=12288, Hq=32, Hkv=8, D=128)
+LLAMA3B = dict(H=3072, I=8192, Hq=24, Hkv=8, D=128)
+
+
+@pytest.mark.parametrize("shape", [QWEN8B, LLAMA3B], ids=["qwen3-8b", "llama3.2-3b"])
+def test_decode_step_serves_more_shapes(lib, shape):
+    assert _serves(lib, **shape) == 1
+
+
 @pytest.mark.parametrize("change", [
     dict(H=1024), dict(I=8192), dict(Hq=16), dict(D=64), dict(levels=256), dict(group=64),
     dict(sdt=_abi.F32), dict(max_pos=100), dict(max_pos=32)])

@@ -167,3 +167,24 @@ def test_prefill_deterministic():
     a = run(s, x).cpu().numpy()
     b = run(s, x).cpu().numpy()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_batch1_8bit_long_k_stays_on_the_gemv():
+    """Batch-1 8-bit at K = 14336 is served by the LUT GEMV (~22 us per
+    4096 x 14336 launch); a shape-check slip once routed it to the MFMA tile
+    path (~450 us).  The bar leaves 2.5x headroom over the GEMV's time."""
+    n, k = 4096, 14336
+    _, packed, scale, cb = ref.synth_linear(n, k, 256, 128, seed=77)
+    s = PackedWeight((n, k), packed, scale, cb.astype(np.float32), 128, 256).to(DEV)
+    x = torch.randn(1, k, device=DEV).to(torch.bfloat16)
+    h = cuda._hot(s)
+    for _ in range(3):
+        cuda.forward(x, h)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(20):
+        cuda.forward(x, h)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / 20 * 1e3
+    assert us < 60.0, f"{us:.1f} us per launch"

@@ -22,7 +22,7 @@ import numpy as np
 import pytest
 import torch
 
-from epure.decode import LLAMA3_8B, QWEN3_1_7B, Decoder, random_weights
+from epure.decode import LLAMA3_8B, LLAMA32_3B, QWEN3_1_7B, QWEN3_8B, Decoder, random_weights
 from oracle.decoder import RefDecoder
 
 pytestmark = pytest.mark.gpu
@@ -129,3 +129,32 @@ def test_persistent_eager_equals_graph(weights):
     assert a == b
     assert torch.equal(la, d.logits)
     assert not d.step_failed()
+
+
+@pytest.mark.parametrize("base", [QWEN3_8B, LLAMA32_3B], ids=["qwen3-8b", "llama3.2-3b"])
+def test_more_shapes_one_launch_against_oracle(base):
+    """The one-launch step at the Qwen3-8B and Llama-3.2-3B shapes (full
+    width, 3 layers: the layer count is a launch argument), teacher-forced
+    over 140 random positions (three 64-position chunks) against the float32
+    oracle, and 24 greedy tokens identical to the oracle's."""
+    cfg = dataclasses.replace(base, layers=3)
+    w = random_weights(cfg, seed=8, device=DEV)
+    toks = _ids(140, cfg.vocab, 9)
+    d = Decoder(w, len(toks) + 1, persistent=True)
+    assert d.persistent
+    ref = RefDecoder.from_weights(w, d.max_pos)
+    d.reset(toks)
+    d.capture()
+    errs = []
+    for pos in range(len(toks) - 1):
+        d.step()
+        want = ref.step(toks[pos], pos)
+        errs.append(float((d.logits - want).abs().max() / want.abs().max()))
+    assert not d.step_failed()
+    errs = np.array(errs)
+    print(f"{cfg.name} x3 layers: normwise median {np.median(errs):.2e} max {errs.max():.2e}")
+    assert np.median(errs) < 1e-5 and errs.max() < 5e-5
+    prompt = _ids(12, cfg.vocab, 10)
+    got, _ = d.generate(prompt, 24)
+    want, _, _ = ref.generate(prompt, 24)
+    assert got == want
