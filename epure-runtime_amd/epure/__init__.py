@@ -5,6 +5,7 @@ Public names follow the reference package (epure/__init__.py:31-37) for the
 parts this build covers: the packed store, linear and embedding, the fine-tuning
 helpers, and the ``epure.kernels`` backend contract.
 """
+from . import container
 from .finetune import (
     ScaleTuner,
     make_trainable,
@@ -29,6 +30,6 @@ __all__ = [
     "PackedWeight", "PackedLinear", "PackedEmbedding", "PackedExperts", "ExpertHolder",
     "apply_packed", "tie_packed_lm_head",
     "make_trainable", "packed_weights", "snapshot_indices", "verify_frozen",
-    "trainable_forward", "ScaleTuner",
+    "trainable_forward", "ScaleTuner", "container",
     "__version__",
 ]

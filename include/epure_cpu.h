@@ -34,6 +34,20 @@ int ep_cpu_dequant_matmul_f32(const float *x, int64_t x_len, const uint8_t *pack
  * replaces kernel/src/lib.rs:155-157 threads(). */
 size_t ep_cpu_threads(void);
 
+/*
+ * Chunked rANS decode of an .ebin index stream, replacing the reference's
+ * epure/container.py:40-51 rans_decode (constriction's stack AnsCoder, one
+ * coder per chunk).  words: the concatenated chunks as 32-bit words (chunk c
+ * holds chunk_words[c] words and decodes to chunk_symbols[c] symbols);
+ * cdf[0..nlevels]: the model's left-sided cumulative table at 24-bit
+ * precision (cdf[0] = 0, cdf[nlevels] = 2^24, strictly increasing).  out
+ * receives the sum of chunk_symbols bytes.  Chunks decode in parallel
+ * (nthreads <= 0: ep_cpu_threads()).  Returns 0, -3 (bad argument), -4 (out
+ * of memory) or -5 (malformed cdf).
+ */
+int ep_rans_decode(const uint32_t *words, const int64_t *chunk_words, const int64_t *chunk_symbols,
+                   int nchunks, const uint32_t *cdf, int nlevels, uint8_t *out, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif
