@@ -449,10 +449,13 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
                 bb = wv[w];
                 bbi = wi[w];
             }
+        // no logit compares (all NaN): argmax -1, and token 0 feeds the next
+        // step so every later access stays inside the tables
+        const bool valid = bbi >= 0 && bbi < a.V;
         const int pos = a.state[0];
-        const int next = pos + 1 < a.n_prompt ? a.prompt[pos + 1] : bbi;
+        const int next = pos + 1 < a.n_prompt ? a.prompt[pos + 1] : (valid ? bbi : 0);
         if (pos < a.max_pos) {
-            a.argmax_out[pos] = bbi;
+            a.argmax_out[pos] = valid ? bbi : -1;
             a.tokens[pos + 1] = next;
         }
         a.state[0] = pos + 1;

@@ -99,9 +99,9 @@ struct Model {
     // their lo terms (same size), one factor per 32 values, then the
     // accumulator [8 waves][rows].
     static constexpr int phase_bytes(int K, int red) { return K * 4 + K / 32 * 4 + red; }
-    // attention scratch: q [GQ][D], k, v [D], S [GQ][256], m, l [GQ], o [8][GQ][D]
-    static constexpr int ATT_BYTES =
-        (GQ * kD + 2 * kD + GQ * kChunk + 2 * GQ + kWaves * GQ * kD) * 4 + 16;
+    // attention scratch: q [GQ][D], k, v [D], per-wave max and sum [8][GQ],
+    // per-wave P.V [8][GQ][D]
+    static constexpr int ATT_BYTES = (GQ * kD + 2 * kD + 2 * kWaves * GQ + kWaves * GQ * kD) * 4;
     static constexpr int REGION =
         imax(imax(imax(phase_bytes(H, kWaves * 4 * MQ_QKV * 4),
                        phase_bytes(HQD, kWaves * 4 * MQ_O * 4)),
@@ -211,16 +211,6 @@ struct Spin {
         return true;
     }
 };
-
-// One tagged f32 value (polled until its tag is current).
-EP_DEV float ld_tag_f32(const uint64_t *p, uint32_t tag, int *err)
-{
-    Spin sp;
-    uint64_t v = ld_tag(p);
-    while ((uint32_t)(v >> 32) != tag && sp.again(err))
-        v = ld_tag(p);
-    return __uint_as_float((uint32_t)v);
-}
 
 // threadIdx.x through an opaque move: values derived from it are recomputed
 // per phase instead of being hoisted out of the layer loop and kept live
@@ -702,94 +692,132 @@ constexpr int XS_F32 = 3;     // tagged f32 (attention output, SwiGLU output)
 
 // Converts the K-vector to fp16 pairs in LDS with one exact power-of-two
 // factor per 32 values (the 4 threads of a 32-value chunk agree on it
-// through a quad max), the same staging as gemv.hip's.  Tagged sources are
-// re-read until every tag is `tag`.
+// through a quad max), the same staging as gemv.hip's.  The loads of a
+// thread's groups (and of the norm weights) are issued together, up to 3
+// groups per batch; tagged groups whose tags are not all `tag` yet are then
+// re-read together, so a stale vector costs one round trip per re-read and
+// batch, not one per group.
 template <int XS, int K>
 EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, uint32_t *xs,
                    uint32_t *xl, float *xf, float *part8, int *err)
 {
-    const auto rs = buffer_rsrc(x);
+    constexpr int NE = K / 8;                            // groups of 8 values
+    constexpr int NIT = (NE + kThreads - 1) / kThreads;  // groups per thread
+    // groups in flight per batch (16 VGPRs each): all of them up to 3
+    constexpr int NB = NIT <= 3 ? NIT : 2;
+    constexpr bool TAGGED = XS != XS_RMS_H0;
+    constexpr bool RMS = XS == XS_RMS_H0 || XS == XS_RMS;
+    // exact extent: a group index past the vector reads zeros (never used)
+    const auto rs = buffer_rsrc(x, TAGGED ? (uint32_t)K * 8u : (uint32_t)K * 4u);
+    const int t0 = tid_fresh();
     float ssq = 0.0f;
-    for (int e = tid_fresh(); e < K / 8; e += kThreads) {
-        float v[8];
-        if constexpr (XS == XS_RMS_H0) {
-            const u32x4_t h0 = ldc16(rs, (uint32_t)e * 32);
-            const u32x4_t h1 = ldc16(rs, (uint32_t)e * 32 + 16);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                v[t] = __uint_as_float(h0[t]);
-                v[4 + t] = __uint_as_float(h1[t]);
+    for (int b0 = 0; b0 < NIT; b0 += NB) {
+        u32x4_t q[NB][4];
+        u32x4_t wv[NB];
+#pragma unroll
+        for (int k = 0; k < NB; ++k) {
+            const uint32_t e = (uint32_t)(t0 + (b0 + k) * kThreads);
+            if constexpr (TAGGED) {
+#pragma unroll
+                for (int h = 0; h < 4; ++h)  // a ring slot: first through the caches
+                    q[k][h] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(e * 64 + 16 * h), 0, 0);
+            } else {
+                q[k][0] = ldc16(rs, e * 32);
+                q[k][1] = ldc16(rs, e * 32 + 16);
             }
-        } else {  // XS_RMS, XS_F32: 8 tagged f32 = 64 bytes
-            u32x4_t q[4];
-            Spin sp;
-            auto ready = [&] {
+            if constexpr (RMS)
+                wv[k] = ldg((const u32x4_t *)(w + (e < (uint32_t)NE ? e : 0u) * 8));
+        }
+        if constexpr (TAGGED) {
+            auto ready = [&](const u32x4_t (&g)[4]) {
                 bool ok = true;
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    ok = ok && q[t][1] == tag && q[t][3] == tag;
+                for (int h = 0; h < 4; ++h)
+                    ok = ok && g[h][1] == tag && g[h][3] == tag;
                 return ok;
             };
+            Spin sp;
+            for (;;) {
+                bool all = true;
 #pragma unroll
-            for (int t = 0; t < 4; ++t)  // a ring slot: first through the caches
-                q[t] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)e * 64 + 16 * t, 0, 0);
-            while (!ready() && sp.again(err)) {
+                for (int k = 0; k < NB; ++k)
+                    all = all && (b0 + k >= NIT || t0 + (b0 + k) * kThreads >= NE || ready(q[k]));
+                if (all || !sp.again(err))
+                    break;
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    q[t] = ldc16(rs, (uint32_t)e * 64 + 16 * t);
-            }
+                for (int k = 0; k < NB; ++k) {
+                    const uint32_t e = (uint32_t)(t0 + (b0 + k) * kThreads);
+                    if (b0 + k < NIT && e < (uint32_t)NE && !ready(q[k])) {
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                v[2 * t] = __uint_as_float(q[t][0]);
-                v[2 * t + 1] = __uint_as_float(q[t][2]);
-            }
-        }
-        if constexpr (XS == XS_RMS_H0 || XS == XS_RMS) {
-            const u32x4_t wv = ldg((const u32x4_t *)(w + e * 8));
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                float w0, w1;
-                unpack_pair<EP_BF16>(wv[t], w0, w1);
-                ssq = fmaf(v[2 * t], v[2 * t], fmaf(v[2 * t + 1], v[2 * t + 1], ssq));
-                v[2 * t] *= w0;
-                v[2 * t + 1] *= w1;
+                        for (int h = 0; h < 4; ++h)
+                            q[k][h] = ldc16(rs, e * 64 + 16 * h);
+                    }
+                }
             }
         }
-        float am = 0.0f;
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-            am = fmaxf(am, fabsf(v[t]));
-        am = fmaxf(am, dpp_mov<0xb1>(am));  // lanes ^ 1
-        am = fmaxf(am, dpp_mov<0x4e>(am));  // lanes ^ 2
-        const int ex = row_exponent(am);
-        const float pw = ldexpf(1.0f, -ex);
-        u32x4_t q4, l4;
+        for (int k = 0; k < NB; ++k) {
+            const int e = t0 + (b0 + k) * kThreads;
+            if (b0 + k >= NIT || e >= NE)
+                break;
+            float v[8];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const float a0 = v[2 * p] * pw, a1 = v[2 * p + 1] * pw;
-            const f16_t h0 = (f16_t)a0, h1 = (f16_t)a1;
-            q4[p] = (uint32_t)f16_bits(h0) | ((uint32_t)f16_bits(h1) << 16);
-            l4[p] = (uint32_t)f16_bits((f16_t)(a0 - (float)h0)) |
-                    ((uint32_t)f16_bits((f16_t)(a1 - (float)h1)) << 16);
+            for (int h = 0; h < 4; ++h) {
+                if constexpr (TAGGED) {
+                    v[2 * h] = __uint_as_float(q[k][h][0]);
+                    v[2 * h + 1] = __uint_as_float(q[k][h][2]);
+                } else {
+                    v[h] = __uint_as_float(q[k][0][h]);
+                    v[4 + h] = __uint_as_float(q[k][1][h]);
+                }
+            }
+            if constexpr (RMS) {
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    float w0, w1;
+                    unpack_pair<EP_BF16>(wv[k][h], w0, w1);
+                    ssq = fmaf(v[2 * h], v[2 * h], fmaf(v[2 * h + 1], v[2 * h + 1], ssq));
+                    v[2 * h] *= w0;
+                    v[2 * h + 1] *= w1;
+                }
+            }
+            float am = 0.0f;
+#pragma unroll
+            for (int h = 0; h < 8; ++h)
+                am = fmaxf(am, fabsf(v[h]));
+            am = fmaxf(am, dpp_mov<0xb1>(am));  // lanes ^ 1
+            am = fmaxf(am, dpp_mov<0x4e>(am));  // lanes ^ 2
+            const int ex = row_exponent(am);
+            const float pw = ldexpf(1.0f, -ex);
+            u32x4_t q4, l4;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const float a0 = v[2 * p] * pw, a1 = v[2 * p + 1] * pw;
+                const f16_t h0 = (f16_t)a0, h1 = (f16_t)a1;
+                q4[p] = (uint32_t)f16_bits(h0) | ((uint32_t)f16_bits(h1) << 16);
+                l4[p] = (uint32_t)f16_bits((f16_t)(a0 - (float)h0)) |
+                        ((uint32_t)f16_bits((f16_t)(a1 - (float)h1)) << 16);
+            }
+            *(u32x4_t *)(xs + e * 4) = q4;
+            *(u32x4_t *)(xl + e * 4) = l4;
+            if ((e & 3) == 0)
+                xf[e >> 2] = ldexpf(1.0f, ex);
         }
-        *(u32x4_t *)(xs + e * 4) = q4;
-        *(u32x4_t *)(xl + e * 4) = l4;
-        if ((e & 3) == 0)
-            xf[e >> 2] = ldexpf(1.0f, ex);
     }
     float rinv = 1.0f;
-    if constexpr (XS == XS_RMS_H0 || XS == XS_RMS) {
+    if constexpr (RMS) {
         const float s = wave_sum(ssq);
         if ((tid_fresh() & 63) == 0)
             part8[tid_fresh() >> 6] = s;
     }
     lds_sync();
-    if constexpr (XS == XS_RMS_H0 || XS == XS_RMS) {
-        float q = 0.0f;
+    if constexpr (RMS) {
+        float q2 = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w)
-            q += part8[w];
-        rinv = rsqrtf(q / (float)K + eps);
+        for (int w2 = 0; w2 < kWaves; ++w2)
+            q2 += part8[w2];
+        rinv = rsqrtf(q2 / (float)K + eps);
     }
     return rinv;
 }
@@ -859,10 +887,9 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
     float *qs = (float *)scratch;        // [GQ][D]
     float *kn = qs + GQ * kD;            // [D]
     float *vn = kn + kD;                 // [D]
-    float *S = vn + kD;                  // [GQ][kChunk] scores, then probabilities
-    float *mw = S + GQ * kChunk;         // [GQ] chunk max
-    float *lw = mw + GQ;                 // [GQ] chunk sum
-    float *ow = lw + GQ;                 // [8][GQ][D]
+    float *mw = vn + kD;                 // [8][GQ] each wave's max score
+    float *lw = mw + kWaves * GQ;        // [8][GQ] each wave's sum of exp(score - max)
+    float *ow = lw + kWaves * GQ;        // [8][GQ][D] each wave's P.V (16-byte aligned)
     const int hq0 = j * GQ;
     int *err = a.sync + 2;
 
@@ -907,9 +934,20 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
         stg(L.vcache + row, vn[tid]);
     }
 
-    // scores: 8 dims per lane, then the sum over the row's 16 lanes
+    // Each wave runs its 8 positions alone (online softmax): scores (8 dims
+    // per lane, summed over the row's 16 lanes), the wave's max and sum of
+    // exponentials over its rows (lanes l, l ^ 16, l ^ 32), its P.V, and one
+    // LDS hand-off of (max, sum, P.V) per wave; the 8 waves are then
+    // combined, rescaled to the item's max.
     const int pw0 = c * kChunk + wave * kRowsPerWave;
-    const bool wave_live = pw0 <= pos;  // wave-uniform
+    const bool wave_live = pw0 <= pos;  // wave-uniform; then row pw0 is live
+    float o[GQ][8];
+#pragma unroll
+    for (int g = 0; g < GQ; ++g)
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            o[g][t] = 0.0f;
+    float mwv[GQ], lwv[GQ];
     if (wave_live) {
         float qv[GQ][8];
 #pragma unroll
@@ -922,6 +960,7 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
                 qv[g][4 + t] = a1[t];
             }
         }
+        float sc[GQ][kLoadsPerWave];
 #pragma unroll
         for (int k = 0; k < kLoadsPerWave; ++k) {
             const int p = pw0 + 4 * k + rr;
@@ -929,76 +968,57 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
 #pragma unroll
             for (int t = 0; t < 8; ++t)  // row pos: this step's key, from LDS
                 kw[t] = p == pos ? kn[e16 * 8 + t] : r.k[k][t >> 2][t & 3];
-            float sg[GQ];
 #pragma unroll
             for (int g = 0; g < GQ; ++g) {
                 float acc = 0.0f;
 #pragma unroll
                 for (int t = 0; t < 8; ++t)
                     acc = fmaf(qv[g][t], kw[t], acc);
-                sg[g] = row16_sum(acc);
-            }
-            if (e16 == 0) {
-#pragma unroll
-                for (int g = 0; g < GQ; ++g)
-                    S[g * kChunk + wave * kRowsPerWave + 4 * k + rr] =
-                        p <= pos ? sg[g] * a.att_scale : -INFINITY;
+                const float sg = row16_sum(acc);
+                sc[g][k] = p <= pos ? sg * a.att_scale : -INFINITY;
             }
         }
-    } else if (e16 == 0) {
+        float pe[GQ][kLoadsPerWave];
 #pragma unroll
-        for (int k = 0; k < kLoadsPerWave; ++k)
+        for (int g = 0; g < GQ; ++g) {
+            float m = sc[g][0];
 #pragma unroll
-            for (int g = 0; g < GQ; ++g)
-                S[g * kChunk + wave * kRowsPerWave + 4 * k + rr] = -INFINITY;
-    }
-    lds_sync();
-    stamp(a, l, 16);  // scores
-    // softmax over the chunk, one wave per head: one score per lane
-    static_assert(kChunk == 64, "one score per lane");
-    if (wave < GQ) {
-        const float sv = S[wave * kChunk + lane];
-        const float m = wave_max(sv);
-        const float pe = sv == -INFINITY ? 0.0f : __expf(sv - m);
-        S[wave * kChunk + lane] = pe;
-        const float lsum = wave_sum(pe);
-        if (lane == 0) {
-            mw[wave] = m;
-            lw[wave] = lsum;
+            for (int k = 1; k < kLoadsPerWave; ++k)
+                m = fmaxf(m, sc[g][k]);
+            m = xor32_max(xor16_max(m));  // finite: row pw0 is live
+            float ls = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kLoadsPerWave; ++k) {
+                pe[g][k] = sc[g][k] == -INFINITY ? 0.0f : __expf(sc[g][k] - m);
+                ls += pe[g][k];
+            }
+            mwv[g] = m;
+            lwv[g] = xor32_sum(xor16_sum(ls));
         }
-    }
-    lds_sync();
-    stamp(a, l, 17);  // softmax
-    // P.V: 8 dims per lane over its 8 rows, then over the wave's 4 row
-    // groups (lanes l, l ^ 16, l ^ 32, l ^ 48), then over the 8 waves
-    float o[GQ][8];
-#pragma unroll
-    for (int g = 0; g < GQ; ++g)
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-            o[g][t] = 0.0f;
-    if (wave_live) {
 #pragma unroll
         for (int k = 0; k < kLoadsPerWave; ++k) {
             const int p = pw0 + 4 * k + rr;
-            const int pl = wave * kRowsPerWave + 4 * k + rr;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
                 const float vv = p == pos ? vn[e16 * 8 + t] : (p < pos ? r.v[k][t >> 2][t & 3] : 0.0f);
 #pragma unroll
                 for (int g = 0; g < GQ; ++g)
-                    o[g][t] = fmaf(S[g * kChunk + pl], vv, o[g][t]);
+                    o[g][t] = fmaf(pe[g][k], vv, o[g][t]);
             }
         }
-    }
 #pragma unroll
-    for (int g = 0; g < GQ; ++g)
+        for (int g = 0; g < GQ; ++g)
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            float x = o[g][t];
-            x = xor32_sum(xor16_sum(x));
-            o[g][t] = x;
+            for (int t = 0; t < 8; ++t)
+                o[g][t] = xor32_sum(xor16_sum(o[g][t]));
+    } else {
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+            mwv[g] = -INFINITY;
+            lwv[g] = 0.0f;
         }
+    }
+    stamp(a, l, 16);  // the wave's scores, softmax and P.V
     if (rr == 0) {
 #pragma unroll
         for (int g = 0; g < GQ; ++g) {
@@ -1008,19 +1028,31 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
                 (f32x4_t){o[g][4], o[g][5], o[g][6], o[g][7]};
         }
     }
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < GQ; ++g) {
+            mw[wave * GQ + g] = mwv[g];
+            lw[wave * GQ + g] = lwv[g];
+        }
+    }
     lds_sync();
     stamp(a, l, 11);  // scores, softmax, P.V done
-    // sum over the 8 waves; thread (g, dims 2dd, 2dd + 1)
+    // the 8 waves rescaled to the item's max; thread (g, dims 2dd, 2dd + 1)
     const bool cth = tid < GQ * 64;
     const int g = tid / 64, dd = 2 * (tid % 64);
     float M = 0.0f, Ls = 0.0f, n0 = 0.0f, n1 = 0.0f;
     if (cth) {
-        M = mw[g];
-        Ls = lw[g];
+        M = mw[g];  // wave 0 always holds a live row
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w)
+            M = fmaxf(M, mw[w * GQ + g]);
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            n0 += ow[(w * GQ + g) * kD + dd];
-            n1 += ow[(w * GQ + g) * kD + dd + 1];
+            const float mwg = mw[w * GQ + g];
+            const float f = mwg == -INFINITY ? 0.0f : __expf(mwg - M);
+            Ls = fmaf(lw[w * GQ + g], f, Ls);
+            n0 = fmaf(ow[(w * GQ + g) * kD + dd], f, n0);
+            n1 = fmaf(ow[(w * GQ + g) * kD + dd + 1], f, n1);
         }
     }
     uint64_t *outp = at + (hq0 + g) * kD + dd;
@@ -1097,16 +1129,30 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
 }
 
 // ---------------------------------------------------------------- kernel
-// The residual rows an accumulating phase owns (one per thread), read with
-// its activation staging: layer 0's o reads the untagged input h0, later
-// phases the tagged residual.
-EP_DEV float residual_rows(const Segs &sg, const StepArgs &a, const uint64_t *hsrc, uint32_t tag)
+// The residual rows an accumulating phase owns (one per thread): the load
+// is issued before the phase's activation staging (residual_issue) and
+// checked after it (residual_take), so both share one round trip.  Layer
+// 0's o reads the untagged input h0, later phases the tagged residual.
+EP_DEV uint64_t residual_issue(const Segs &sg, const StepArgs &a, const uint64_t *hsrc)
+{
+    const int t = tid_fresh();
+    const int n = (sg.qb - sg.qa) * 4;
+    const int row = sg.qa * 4 + (t < n ? t : 0);
+    return hsrc ? ld_tag(hsrc + row) : (uint64_t)__float_as_uint(ldg(a.h0 + row));
+}
+EP_DEV float residual_take(uint64_t v, const Segs &sg, const StepArgs &a, const uint64_t *hsrc,
+                           uint32_t tag)
 {
     const int t = tid_fresh();
     if (t >= (sg.qb - sg.qa) * 4)
         return 0.0f;
-    const int row = sg.qa * 4 + t;
-    return hsrc ? ld_tag_f32(hsrc + row, tag, a.sync + 2) : ldg(a.h0 + row);
+    if (!hsrc)
+        return __uint_as_float((uint32_t)v);
+    const uint64_t *p = hsrc + sg.qa * 4 + t;
+    Spin sp;
+    while ((uint32_t)(v >> 32) != tag && sp.again(a.sync + 2))
+        v = ld_tag(p);
+    return __uint_as_float((uint32_t)v);
 }
 
 
@@ -1303,9 +1349,10 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         {
             const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh, xo);
             if (so.qb > so.qa) {
-                const float hv = residual_rows(so, a, h_prev, tag_of(seq, l - 1, PH_DOWN));
+                const uint64_t hraw = residual_issue(so, a, h_prev);
                 stage<XS_F32, M::HQD>(at_l, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf,
                                       part8, err);
+                const float hv = residual_take(hraw, so, a, h_prev, tag_of(seq, l - 1, PH_DOWN));
                 stamp(a, l, 3);
                 PO::template run<MODE_ACC>(ob, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
                                            1.0f, h_o, a.h0, false, nullptr, tag_of(seq, l, PH_O));
@@ -1344,9 +1391,10 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // ---- down (+= residual)
         {
             const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
-            const float hv = residual_rows(sd, a, h_o, tag_of(seq, l, PH_O));
+            const uint64_t hraw = residual_issue(sd, a, h_o);
             stage<XS_F32, M::I>(actl, nullptr, 0.0f, tag_of(seq, l, PH_ACT), li.xs, li.xl, li.xf, part8,
                                 err);
+            const float hv = residual_take(hraw, sd, a, h_o, tag_of(seq, l, PH_O));
             stamp(a, l, 7);
             PD::template run<MODE_ACC>(db, sd, a.group, tab, li.xs, li.xl, li.xf, li.red, hrow, hv,
                                        1.0f, h_d, a.h0, last, nullptr, tag_of(seq, l, PH_DOWN));

@@ -375,6 +375,8 @@ class Decoder:
         n = int(prompt.numel())
         if n < 1 or n > self.max_pos:
             raise ValueError("prompt length must be 1..max_pos")
+        if int(prompt.min()) < 0 or int(prompt.max()) >= self.cfg.vocab:
+            raise ValueError(f"prompt token ids must lie in [0, {self.cfg.vocab})")
         self.prompt.zero_()
         self.prompt[:n].copy_(prompt.to(self.device))
         if self.n_prompt != n:
@@ -424,7 +426,12 @@ class Decoder:
         if self.step_failed():
             raise RuntimeError("decode step: a hand-over wait timed out; the tokens are invalid")
         n = self.n_prompt + n_new
-        return self.tokens[:n].cpu().tolist(), self.argmax[:n - 1].cpu().tolist()
+        argmax = self.argmax[:n - 1].cpu().tolist()
+        bad = [i for i, t in enumerate(argmax) if t < 0]
+        if bad:
+            raise RuntimeError(f"decode step: no finite logit at position {bad[0]} "
+                               f"({len(bad)} positions); the tokens are invalid")
+        return self.tokens[:n].cpu().tolist(), argmax
 
 
 def _raise_decline(what):

@@ -69,6 +69,31 @@ def test_graph_replay_matches_eager():
     assert torch.equal(la, dec.logits)
 
 
+def test_prompt_token_ids_checked():
+    cfg = SMALL["llama"]
+    dec = Decoder(random_weights(cfg, seed=31, device=DEV), 64)
+    for bad in ([cfg.vocab], [3, -1], [0, 1, cfg.vocab + 7]):
+        with pytest.raises(ValueError, match="token ids"):
+            dec.reset(bad)
+    dec.reset([0, cfg.vocab - 1])  # both ends are valid
+
+
+def test_non_finite_logits_are_reported():
+    """A NaN final-norm weight (forced from the host) makes every logit NaN:
+    the argmax kernel records -1, feeds token 0 so every later access stays
+    in bounds, and generate() raises instead of returning tokens."""
+    cfg = SMALL["llama"]
+    w = random_weights(cfg, seed=32, device=DEV)
+    w.final_norm[5] = float("nan")
+    dec = Decoder(w, 64)
+    with pytest.raises(RuntimeError, match="no finite logit"):
+        dec.generate(prompt_ids(4, cfg.vocab, 33), 6)
+    torch.cuda.synchronize()
+    assert dec.argmax[:9].cpu().tolist() == [-1] * 9   # no position had a finite logit
+    assert dec.tokens[4:10].cpu().tolist() == [0] * 6   # greedy positions fed token 0
+    assert not dec.step_failed()
+
+
 def _teacher_forced(dec, ref, toks):
     """Both decoders fed ``toks``; per position the GPU's logits against the
     oracle's: (max abs error, normwise error, oracle top-1 minus top-2
