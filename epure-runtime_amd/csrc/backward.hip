@@ -347,11 +347,15 @@ __global__ void __launch_bounds__(256, 3) dw_kernel(BwdArgs a)
             for (int r = 0; r < 16; ++r)
                 acc[i][j][r] = 0.0f;
 
-    // this thread's 8 x 8 staging block: rows (blk >> 4) * 8 .. of the
-    // step, columns (blk & 15) * 8 .. of the tile
+    // this thread's 8 x 8 staging block: rows (blk & 7) * 8 .. of the step,
+    // columns (blk >> 3) * 8 .. of the tile.  The step rows vary fastest
+    // over the lanes: a 16-byte LDS store of transposed row bc + j lands at
+    // dword (bc + j) * LDW / 2 + br / 2, i.e. banks 4 j + br / 2 (mod 32),
+    // so the 8 lanes of one store cycle cover 8 distinct bank quads
+    // (columns varying fastest put all 8 on the same banks).
     const bool isx = tid < 128;  // wave-uniform
     const int blk = tid & 127;
-    const int br = (blk >> 4) * 8, bc = (blk & 15) * 8;
+    const int br = (blk & 7) * 8, bc = (blk >> 3) * 8;
     // Loads never branch: each step reads through a buffer descriptor based
     // at the step's first row and sized to the bytes left from there, so rows
     // past M (and a step past the end) read zeros; a column past N is sent
