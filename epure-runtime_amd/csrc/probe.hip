@@ -2,10 +2,12 @@
 // are judged against (the intended analogue of the reference's diagnostic
 // kernel with "the same traffic", epure/kernels/_triton.py:188-236
 // dequant_nolut).  It reads a buffer exactly once with the load shape of
-// the GEMV and the decode step -- 16-byte non-temporal loads, eight per lane
-// in flight, 512 threads per workgroup -- and folds what it read into one
-// XOR word per workgroup, so no load can be dropped and the result is
-// checkable (the XOR of the sink words is the XOR of the buffer's words).
+// the GEMV and the decode step -- each workgroup streams one contiguous
+// slice (as a CU streams its share of rows), 16-byte non-temporal loads,
+// eight per lane in flight, 512 threads per workgroup -- and folds what it
+// read into one XOR word per workgroup, so no load can be dropped and the
+// result is checkable (the XOR of the sink words is the XOR of the
+// buffer's words).
 #include "ep_common.h"
 #include "ep_internal.h"
 
@@ -19,10 +21,15 @@ __global__ void __launch_bounds__(kProbeThreads) read_probe_kernel(const u32x4_t
                                                                    int64_t n16, uint32_t *sink)
 {
     __shared__ uint32_t part[kProbeThreads / 64];
-    const int64_t stride = (int64_t)gridDim.x * kProbeThreads;
-    int64_t i = (int64_t)blockIdx.x * kProbeThreads + threadIdx.x;
+    // slice [beg, end) of the 16-byte elements, whole 512-element rows
+    const int64_t per = (n16 + (int64_t)gridDim.x * kProbeThreads - 1) / ((int64_t)gridDim.x * kProbeThreads) *
+                        kProbeThreads;
+    const int64_t beg = (int64_t)blockIdx.x * per;
+    const int64_t end = beg + per < n16 ? beg + per : n16;
+    constexpr int64_t stride = kProbeThreads;
+    int64_t i = beg + threadIdx.x;
     u32x4_t acc = {0u, 0u, 0u, 0u};
-    for (; i + (kProbeDepth - 1) * stride < n16; i += kProbeDepth * stride) {
+    for (; i + (kProbeDepth - 1) * stride < end; i += kProbeDepth * stride) {
         u32x4_t v[kProbeDepth];
 #pragma unroll
         for (int k = 0; k < kProbeDepth; ++k)
@@ -31,7 +38,7 @@ __global__ void __launch_bounds__(kProbeThreads) read_probe_kernel(const u32x4_t
         for (int k = 0; k < kProbeDepth; ++k)
             acc ^= v[k];
     }
-    for (; i < n16; i += stride)
+    for (; i < end; i += stride)
         acc ^= __builtin_nontemporal_load(buf + i);
     uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 #pragma unroll
