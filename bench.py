@@ -74,6 +74,9 @@ def parse():
                          "(config 3); backward: the compressed-state backward (config 4)")
     ap.add_argument("--no-gemv", action="store_true",
                     help="decode: skip the config-0 GEMV sweep reported beside the step")
+    ap.add_argument("--phases", action="store_true",
+                    help="decode: also replay the step kernel with wall-clock stamps and "
+                         "report where a layer's time goes (per-phase breakdown)")
     return ap.parse_args()
 
 
@@ -339,6 +342,57 @@ def traffic_from_profile():
     except OSError:
         pass
     return None
+
+
+# Wall-clock stamps decode_step_kernel writes when given a trace buffer
+# (csrc/step.hip, stamp(a, layer, id)): [layers][24][workgroups] at 100 MHz.
+_STAMPS = 24
+_PHASE_EVENTS = [(1, "qkv done"), (10, "attention: q/k/v received"),
+                 (11, "attention: item computed"), (12, "attention: output combined"),
+                 (3, "o: activations staged"), (4, "o: done"),
+                 (5, "gate|up: activations staged"), (6, "gate|up: done"),
+                 (7, "down: activations staged"), (8, "down: done")]
+
+
+def phase_breakdown(dec, cfg, replays=4):
+    """One-launch step replayed with stamps at the current position: per
+    event, the median over layers of (median and last workgroup's stamp)
+    minus the layer's start (the last workgroup to begin it), in us; the
+    layer period; and per hand-over, the last producer -> median consumer
+    time and the producer skew (last minus median producer)."""
+    import numpy as np
+    import torch
+    G = torch.cuda.get_device_properties(dec.device).multi_processor_count
+    dec.step_trace = torch.zeros(cfg.layers * _STAMPS * G, dtype=torch.int64, device=dec.device)
+    for _ in range(replays):  # the last replay's stamps are kept
+        dec.step_trace.zero_()
+        dec.layer_launches()
+    torch.cuda.synchronize()
+    tr = dec.step_trace.view(cfg.layers, _STAMPS, G).cpu().numpy().astype(np.float64) * 0.01
+    dec.step_trace = None
+    L = slice(2, cfg.layers - 1)  # steady-state layers
+    start = tr[L, 0, :].max(axis=1, keepdims=True)
+
+    def stat(ev, f):
+        x = np.where(tr[L, ev, :] > 0, tr[L, ev, :] - start, np.nan)
+        return float(np.nanmedian(f(x)))
+    med = lambda x: np.nanmedian(x, axis=1)
+    last = lambda x: np.nanmax(x, axis=1)
+    out = {"position": int(dec.state[0].item()), "layers": [2, cfg.layers - 2],
+           "layer_period_us": round(float(np.median(np.diff(tr[1:, 0, :].max(axis=1)))), 2),
+           "events_us": {n: {"median_wg": round(stat(e, med), 2), "last_wg": round(stat(e, last), 2)}
+                         for e, n in _PHASE_EVENTS}}
+    hops = {}
+    for name, pe, ce in [("q|k|v -> attention", 1, 10), ("attention -> o", 12, 3),
+                         ("o -> gate|up", 4, 5), ("gate|up -> down", 6, 7)]:
+        p = np.where(tr[L, pe, :] > 0, tr[L, pe, :], np.nan)
+        c = np.where(tr[L, ce, :] > 0, tr[L, ce, :], np.nan)
+        lp = np.nanmax(p, axis=1)
+        hops[name] = {"last_producer_to_median_consumer_us": round(float(np.median(np.nanmedian(c, axis=1) - lp)), 2),
+                      "last_producer_to_first_consumer_us": round(float(np.median(np.nanmin(c, axis=1) - lp)), 2),
+                      "producer_skew_us": round(float(np.median(lp - np.nanmedian(p, axis=1))), 2)}
+    out["hand_overs"] = hops
+    return out
 
 
 def cpu_model():
@@ -610,6 +664,9 @@ def main():
             "calibrated by bench.py --copy-probe; not measured in this run",
         },
     }
+    if args.phases and dec.persistent:
+        print("# per-phase breakdown (stamped replays)", file=sys.stderr, flush=True)
+        out["phases"] = phase_breakdown(dec, cfg)
     del dec, w, g
     torch.cuda.empty_cache()
     print("# streaming-read probe", file=sys.stderr, flush=True)
