@@ -441,10 +441,10 @@ def cpu_baseline(cfg, threads):
             "kind": "port", "cpu_model": cpu_model(),
             "value_1_thread": round(1.0 / (t_one * cfg.layers), 4),
             "sample": f"C port of kernel/src/lib.rs on one layer's 7 packed linears "
-                      f"({sum(n * k for _, n, k in shapes) / 1e6:.0f}M weights, f32 x), median of "
-                      f"{runs} runs = {t_layer * 1e3:.1f} ms on {nt} threads ({runs_one} runs = "
-                      f"{t_one * 1e3:.1f} ms on 1 thread), scaled x{cfg.layers} layers "
-                      f"(linears only, lm_head excluded)"}
+                      f"({sum(n * k for _, n, k in shapes) / 1e6:.0f}M weights, f32 x): median "
+                      f"{t_layer * 1e3:.1f} ms over {runs} runs on {nt} threads, median "
+                      f"{t_one * 1e3:.1f} ms over {runs_one} runs on 1 thread; scaled "
+                      f"x{cfg.layers} layers (linears only, lm_head excluded)"}
 
 
 def cpu_gemv_baseline(n, k, levels, ms, threads):
