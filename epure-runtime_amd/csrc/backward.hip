@@ -499,20 +499,60 @@ __global__ void __launch_bounds__(256, 3) dw_kernel(BwdArgs a)
 __global__ void __launch_bounds__(256) gc_final_kernel(const float *part, int nwg, int levels,
                                                        float *gcb)
 {
-    __shared__ float red[256];
-    const int lev = blockIdx.x, t = threadIdx.x;
-    float s = 0.0f;
-    for (int w = t; w < nwg; w += 256)
-        s += part[(int64_t)w * 16 + lev];
-    red[t] = s;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (t < o)
-            red[t] += red[t + o];
-        __syncthreads();
+    // thread t sums the partial rows t, t + 256, ... (16 levels each, four
+    // 16-byte loads per row, four rows in flight); then level l = t / 16 is
+    // summed by 16 threads over 16 slots each and across their lanes.
+    // Fixed order throughout: deterministic.
+    __shared__ float red[16 * 257];
+    const int t = threadIdx.x;
+    const float4 *p4 = reinterpret_cast<const float4 *>(part);
+    float acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        acc[j] = 0.0f;
+    int w = t;
+    for (; w + 3 * 256 < nwg; w += 4 * 256) {
+        float4 v[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                v[r][q] = p4[(int64_t)(w + r * 256) * 4 + q];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc[4 * q] += v[r][q].x;
+                acc[4 * q + 1] += v[r][q].y;
+                acc[4 * q + 2] += v[r][q].z;
+                acc[4 * q + 3] += v[r][q].w;
+            }
     }
-    if (t == 0 && lev < levels)
-        gcb[lev] = red[0];
+    for (; w < nwg; w += 256) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = p4[(int64_t)w * 4 + q];
+            acc[4 * q] += v.x;
+            acc[4 * q + 1] += v.y;
+            acc[4 * q + 2] += v.z;
+            acc[4 * q + 3] += v.w;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        red[j * 257 + t] = acc[j];
+    __syncthreads();
+    const int l = t >> 4, slot = t & 15;
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        s += red[l * 257 + slot * 16 + j];
+    s += dpp_mov<0x128>(s);  // row_ror 8
+    s += dpp_mov<0x124>(s);  // row_ror 4
+    s += dpp_mov<0x4e>(s);   // lanes ^ 2
+    s += dpp_mov<0xb1>(s);   // lanes ^ 1
+    if (slot == 0 && l < levels)
+        gcb[l] = s;
 }
 
 // rows x cols f32 zeros (row stride ld): 4 rows per workgroup of 256
@@ -523,6 +563,129 @@ __global__ void __launch_bounds__(256) zero_rows_kernel(float *p, int rows, int 
         return;
     for (int c = (int)(threadIdx.x & 63); c < cols; c += 64)
         p[(int64_t)r * ld + c] = 0.0f;
+}
+
+// ---- library route (large token counts): gy . W and G = gy^T . x run as
+// hipBLASLt GEMMs (blas.cpp); these kernels finish them.
+
+// grad_x[m, k] = D[m, k] * 2^rexp[m] in gx's dtype, D f32 row-major [M][K]
+// (the GEMM's column-major K x M result).  Four values per thread.
+__global__ void __launch_bounds__(256)
+    dx_finish_kernel(const float *D, const int *rexp, int M, int K, void *gx, int gx_dtype, int64_t ldgx)
+{
+    const int64_t k0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (k0 >= K)
+        return;
+    for (int m = blockIdx.y; m < M; m += gridDim.y) {
+        const int e = rexp[m];
+        const float *src = D + (int64_t)m * K + k0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            if (k0 + t < K)
+                store_from_f32(gx, gx_dtype, (int64_t)m * ldgx + k0 + t, ldexpf(src[t], e));
+    }
+}
+
+// From G [N][K] (f32, row-major): grad_scale[n, g] = sum_{k in g} G[n, k]
+// cb[idx[n, k]] (one plain store per (n, g)) and per-workgroup codebook
+// partials grad_cb[l] = sum_{idx == l} G[n, k] scale[n, g(k)], each thread
+// adding into its own LDS histogram (slot [level][thread]: no two lanes on
+// one bank), summed in thread order at the end; gc_final_kernel sums the
+// workgroups in order.  Deterministic, no atomics.  One row per workgroup:
+// its 4 waves take alternate 256-value steps of the row (many small
+// workgroups per CU hide the histogram's LDS round trips); a lane takes 4
+// consecutive k of a step, with the loads of kEpiU steps in flight; group
+// sums over the lanes of a group through DPP and v_permlane16_swap.
+constexpr int kEpiRows = 1;
+constexpr int kEpiU = 6;
+template <int LPG>  // lanes per group: group / 4 (8, 16 or 32)
+EP_DEV float group_lane_sum(float v)
+{
+    v += dpp_mov<0xb1>(v);  // lanes ^ 1
+    v += dpp_mov<0x4e>(v);  // lanes ^ 2
+    if constexpr (LPG == 8) {
+        v += dpp_mov<0x141>(v);  // row_half_mirror: the other quad of the 8
+    } else {
+        v += dpp_mov<0x124>(v);  // row_ror 4
+        v += dpp_mov<0x128>(v);  // row_ror 8: the 16-lane row
+        if constexpr (LPG == 32)
+            v = xor16_sum(v);
+    }
+    return v;
+}
+
+template <int LPG>
+__global__ void __launch_bounds__(256)
+    gw_epilogue_kernel(const float *G, const uint8_t *packed, const void *scale, int scale_dtype,
+                       int64_t lds, const void *cb, int cb_dtype, int levels, int N, int K,
+                       float *gscale, int64_t ldgs, float *gc_part)
+{
+    __shared__ float hist[16 * 256];
+    __shared__ float cbf[16];
+    constexpr int LG = LPG == 8 ? 5 : (LPG == 16 ? 6 : 7);  // log2(group)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < 16 * 256; i += 256)
+        hist[i] = 0.0f;
+    if (tid < 16)
+        cbf[tid] = tid < levels ? load_as_f32(cb, cb_dtype, tid) : 0.0f;
+    __syncthreads();
+    float *my = hist + tid;
+    {
+        const int n = blockIdx.x;
+        const float *grow = G + (int64_t)n * K;
+        const uint16_t *prow = (const uint16_t *)(packed + (int64_t)n * (K / 2));
+        for (int kb = 256 * wave; kb < K; kb += 256 * 4 * kEpiU) {
+            f32x4_t g4[kEpiU];
+            uint32_t b2[kEpiU];
+            float sc[kEpiU];
+#pragma unroll
+            for (int u = 0; u < kEpiU; ++u) {  // every load first (clamped: a step past K reads k = 0)
+                const int k = kb + 1024 * u + 4 * lane;
+                const int kc = k < K ? k : 0;
+                g4[u] = *(const f32x4_t *)(grow + kc);
+                b2[u] = prow[kc / 4];  // the 2 bytes at byte offset kc / 2 (kc % 4 == 0)
+                sc[u] = load_as_f32(scale, scale_dtype, (int64_t)n * lds + (kc >> LG));
+            }
+#pragma unroll
+            for (int u = 0; u < kEpiU; ++u) {
+                const int k = kb + 1024 * u + 4 * lane;
+                const bool ok = k < K;
+                float gs = 0.0f;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int lev = (b2[u] >> (4 * t)) & 15;
+                    const float g = ok ? g4[u][t] : 0.0f;
+                    gs = fmaf(g, cbf[lev], gs);
+                    if (ok)
+                        my[lev * 256] += g * sc[u];
+                }
+                gs = group_lane_sum<LPG>(gs);  // every lane of the group holds the sum
+                if (ok && (lane & (LPG - 1)) == 0)
+                    gscale[(int64_t)n * ldgs + (k >> LG)] = gs;
+            }
+        }
+    }
+    __syncthreads();
+    // level l = tid / 16: 16 threads sum 16 slots each, then the 16 partial
+    // sums are added across their lanes (DPP, fixed order)
+    {
+        const int l = tid >> 4, part = tid & 15;
+        const float *src = hist + l * 256 + part * 16;
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            v[j] = src[j];
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            s += v[j];
+        s += dpp_mov<0x128>(s);  // row_ror 8
+        s += dpp_mov<0x124>(s);  // row_ror 4
+        s += dpp_mov<0x4e>(s);   // lanes ^ 2
+        s += dpp_mov<0xb1>(s);   // lanes ^ 1
+        if (part == 0)
+            gc_part[(int64_t)blockIdx.x * 16 + l] = s;
+    }
 }
 
 }  // namespace
@@ -545,12 +708,50 @@ static int dx_splits(int64_t M, int64_t N, int64_t K)
     return (int)S;
 }
 
+// Token counts from which grad_x and G run as library GEMMs (hipBLASLt
+// reaches ~2x the fused kernels' MFMA rate on these plain products; below,
+// materializing W costs more than it saves).
+constexpr int64_t kBlasMinM = 512;
+static bool blas_route(int64_t M, int64_t N, int64_t K)
+{
+    return M >= kBlasMinM && N >= 256 && K >= 256;
+}
+static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Library-route workspace: rexp [M] | gc partials [N / kEpiRows][16] | gy16
+// [M][N] | W16 [N][K] | f32 [max(M, N)][K] (grad_x's GEMM result, then G) |
+// hipBLASLt workspace.
+struct BlasWs {
+    size_t rexp, gc, gy16, w16, f32buf, blas, total;
+};
+static BlasWs blas_ws(int64_t M, int64_t N, int64_t K)
+{
+    BlasWs w;
+    size_t o = 0;
+    w.rexp = o;
+    o += al256((size_t)M * 4);
+    w.gc = o;
+    o += al256((size_t)((N + kEpiRows - 1) / kEpiRows) * 16 * 4);
+    w.gy16 = o;
+    o += al256((size_t)M * N * 2);
+    w.w16 = o;
+    o += al256((size_t)N * K * 2);
+    w.f32buf = o;
+    o += al256((size_t)(M > N ? M : N) * K * 4);
+    w.blas = o;
+    o += blas_workspace_bytes();
+    w.total = o;
+    return w;
+}
+
 size_t backward_workspace(int64_t M, int64_t N, int64_t K, int levels, int group)
 {
     (void)levels;
     (void)group;
     if (M <= 0 || N <= 0 || K <= 0)
         return 0;
+    if (blas_route(M, N, K))
+        return blas_ws(M, N, K).total;
     const int64_t nwg = ((K + T - 1) / T) * ((N + T - 1) / T);
     const int S = dx_splits(M, N, K);
     return (size_t)((M * 4 + 255) / 256 * 256) + (size_t)nwg * 16 * sizeof(float) +
@@ -598,6 +799,62 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         return set_error(EP_DECLINE_SHAPE, "fused backward needs 16-byte aligned rows");
     if (64 * gy.ld * 2 >= kBwOut || 64 * x.ld * 2 >= kBwOut)
         return set_error(EP_DECLINE_SHAPE, "fused backward: row strides of gy and x below 16M elements");
+    if (blas_route(M, w.N, w.K)) {
+        // grad_x = (gy16 . W16) * 2^rexp per row; G = gy^T . x -> grad_scale, grad_cb
+        const BlasWs L = blas_ws(M, w.N, w.K);
+        char *base = (char *)ws;
+        int *rexp = (int *)(base + L.rexp);
+        float *gcp = (float *)(base + L.gc);
+        f16_t *gy16 = (f16_t *)(base + L.gy16);
+        f16_t *w16 = (f16_t *)(base + L.w16);
+        float *buf = (float *)(base + L.f32buf);
+        void *bws = base + L.blas;
+        if (gx.ptr) {
+            hipLaunchKernelGGL(gy_prep_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream,
+                               (const uint16_t *)gy.ptr, gy.ld, (int)M, (int)w.N, rexp, gy16);
+            EP_HIP_CHECK(hipGetLastError());
+            int rc = launch_dequant_tile(w, w16, EP_F16, w.K, stream);  // materialize(float16)
+            if (rc != EP_OK)
+                return rc;
+            // column-major: D (K x M) = W16 (K x N) . gy16 (N x M)
+            rc = blas_gemm_f32out(0, 0, w.K, M, w.N, EP_F16, w16, w.K, gy16, w.N, buf, w.K, 1.0f, bws,
+                                  blas_workspace_bytes(), stream);
+            if (rc != EP_OK)
+                return rc;
+            hipLaunchKernelGGL(dx_finish_kernel, dim3((unsigned)((w.K + 1023) / 1024), (unsigned)(M < 65535 ? M : 65535)), dim3(256),
+                               0, stream, buf, rexp, (int)M, (int)w.K, gx.ptr, gx.dtype, gx.ld);
+            EP_HIP_CHECK(hipGetLastError());
+        }
+        if (grad_cb || grad_scale) {
+            if (!grad_scale)
+                return set_error(EP_ERR_ARG, "grad_cb without grad_scale is not served");
+            // column-major: G^T (K x N) = x (K x M) . gy^T (M x N): G row-major [N][K]
+            int rc = blas_gemm_f32out(0, 1, w.K, w.N, M, EP_BF16, x.ptr, x.ld, gy.ptr, gy.ld, buf, w.K, 1.0f,
+                                      bws, blas_workspace_bytes(), stream);
+            if (rc != EP_OK)
+                return rc;
+            const int nwg = (int)((w.N + kEpiRows - 1) / kEpiRows);
+            if (w.group == 32)
+                hipLaunchKernelGGL(gw_epilogue_kernel<8>, dim3((unsigned)nwg), dim3(256), 0, stream, buf,
+                                   w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
+                                   (int)w.N, (int)w.K, grad_scale, ld_gscale, gcp);
+            else if (w.group == 64)
+                hipLaunchKernelGGL(gw_epilogue_kernel<16>, dim3((unsigned)nwg), dim3(256), 0, stream, buf,
+                                   w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
+                                   (int)w.N, (int)w.K, grad_scale, ld_gscale, gcp);
+            else
+                hipLaunchKernelGGL(gw_epilogue_kernel<32>, dim3((unsigned)nwg), dim3(256), 0, stream, buf,
+                                   w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
+                                   (int)w.N, (int)w.K, grad_scale, ld_gscale, gcp);
+            EP_HIP_CHECK(hipGetLastError());
+            if (grad_cb) {
+                hipLaunchKernelGGL(gc_final_kernel, dim3(1), dim3(256), 0, stream, gcp, nwg, w.levels,
+                                   grad_cb);
+                EP_HIP_CHECK(hipGetLastError());
+            }
+        }
+        return EP_OK;
+    }
     BwdArgs a{};
     a.gy = gy.ptr;
     a.gy_dtype = gy.dtype;
@@ -655,7 +912,7 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         hipLaunchKernelGGL(dw_kernel, grid, dim3(256), 0, stream, a);
         EP_HIP_CHECK(hipGetLastError());
         if (grad_cb) {
-            hipLaunchKernelGGL(gc_final_kernel, dim3(16), dim3(256), 0, stream, a.gc_part,
+            hipLaunchKernelGGL(gc_final_kernel, dim3(1), dim3(256), 0, stream, a.gc_part,
                                (int)(grid.x * grid.y), w.levels, grad_cb);
             EP_HIP_CHECK(hipGetLastError());
         }

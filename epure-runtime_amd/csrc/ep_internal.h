@@ -162,6 +162,13 @@ int launch_embedding_rows(const PackedDesc &w, const int64_t *ids, int64_t n_ids
 int launch_dequant_tile(const PackedDesc &w, void *out, int out_dtype, int64_t ldo,
                         hipStream_t stream);
 
+// Library GEMM (blas.cpp, hipBLASLt): D[m x n] (f32, column-major) = alpha *
+// op(A) . op(B), fp16 or bf16 operands, f32 accumulation.
+size_t blas_workspace_bytes();
+int blas_gemm_f32out(int ta, int tb, int64_t m, int64_t n, int64_t k, int ab_dtype, const void *A,
+                     int64_t lda, const void *B, int64_t ldb, float *D, int64_t ldd, float alpha,
+                     void *ws, size_t ws_bytes, hipStream_t stream);
+
 // Checks a HIP call; on failure records the error and returns EP_ERR_HIP.
 #define EP_HIP_CHECK(expr)                                                                 \
     do {                                                                                   \
