@@ -79,6 +79,13 @@ constexpr int geo_wpr(int S)
 constexpr int geo_rg(int S) { return 8 % geo_wpr(S) == 0 ? 8 / geo_wpr(S) : 1; }
 constexpr int geo_spw(int S) { return (S + geo_wpr(S) - 1) / geo_wpr(S); }
 constexpr int imax(int a, int b) { return a > b ? a : b; }
+// First of N2 blocks issued after block bi of a loop of N1 blocks: block k
+// goes out after block floor(k N1 / N2), spreading them evenly.
+template <int N2, int N1>
+EP_DEV constexpr int spread_lo(int bi)
+{
+    return (bi * N2 + N1 - 1) / N1;
+}
 
 // A decoder shape served by the persistent step.  RQ_* = row quads per row
 // group per block of each GEMV phase (blocks are pipelined, the first ones
@@ -87,10 +94,11 @@ constexpr int imax(int a, int b) { return a > b ? a : b; }
 // it; the launch checks it against the grid).
 template <int H_, int HQD_, int I_, int GQ_, int RQ_QKV_, int RQ_O_, int RQ_GU_, int RQ_D_,
           int MQ_QKV_, int MQ_O_, int MQ_GU_, int MQ_D_, int NB_QKV_ = 0, int NB_O_ = 0, int NB_GU_ = 0,
-          int NB_D_ = 0>
+          int NB_D_ = 0, int GU_EARLY_ = 0>
 struct Model {
     // NB_* = block buffers of each phase (0: sized for the loads in flight)
     static constexpr int NB_QKV = NB_QKV_, NB_O = NB_O_, NB_GU = NB_GU_, NB_D = NB_D_;
+    static constexpr int GU_EARLY = GU_EARLY_;
     static constexpr int H = H_, HQD = HQD_, I = I_, GQ = GQ_;
     static constexpr int SH = H / 512, SO = HQD / 512, SI = I / 512;
     static constexpr int RQ_QKV = RQ_QKV_, RQ_O = RQ_O_, RQ_GU = RQ_GU_, RQ_D = RQ_D_;
@@ -116,9 +124,11 @@ struct Model {
 // Llama-3-8B, Qwen3-1.7B, Qwen3-8B and Llama-3.2-3B shapes; shares at 256
 // workgroups: q|k|v 6 / 4 / 6 / 5 quads, o 8 / 4 / 8 / 6 (on at least half
 // the grid), gate|up 14 / 6 / 12 / 8, down 4 / 2 / 4 / 3.
-using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 8, 14, 4, 0, 0, 0, 2>;
+// Llama-3-8B: q|k|v and o whole shares in flight, gate|up 5 of 7 blocks
+// (issued during the attention window), down 3 of 4 (issued during gate|up).
+using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 8, 14, 4, -1, -1, 6, 4, 5>;
 using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 4, 6, 2>;
-using ModelQ8B = Model<4096, 4096, 12288, 4, 3, 2, 2, 4, 6, 8, 12, 4, 0, 0, 0, 2>;
+using ModelQ8B = Model<4096, 4096, 12288, 4, 3, 2, 2, 4, 6, 8, 12, 4, -1, -1, 6, 4, 5>;
 using ModelL3B = Model<3072, 3072, 8192, 3, 2, 2, 2, 3, 5, 6, 8, 3>;
 
 // Where a phase of contraction length K keeps its activations, factors and
@@ -331,7 +341,8 @@ struct Gemv {
     static constexpr int BLOCK_BYTES = RG * WPR * 64 * 16 * NQ;
     static constexpr int NBUF_WANT = 1 + (49152 + BLOCK_BYTES - 1) / BLOCK_BYTES;
     static constexpr int NBUF_AUTO = NBUF_WANT < 2 ? 2 : (NBUF_WANT > MAXB + 1 ? MAXB + 1 : NBUF_WANT);
-    static constexpr int NBUF = NBUF_SET > 0 ? NBUF_SET : NBUF_AUTO;
+    // NBUF_SET < 0: the whole share in flight (every block issued ahead)
+    static constexpr int NBUF = NBUF_SET > 0 ? NBUF_SET : (NBUF_SET < 0 ? MAXB + 1 : NBUF_AUTO);
 
     struct Blk {
         u32x4_t w[NQ];
@@ -451,14 +462,31 @@ struct Gemv {
             issue(bb[k], sg, k, sl);
     }
 
+    // Blocks k0 .. k1 - 1 (below NBUF - 1), issued by every wave (an idle
+    // wave's loads have no records): called from inside another phase's
+    // straight-line block loop, where a load issued by some waves only
+    // would make the compiler's wait counts after the join assume the worst.
+    static EP_DEV void prefetch_range(Blk (&bb)[NBUF], const Segs &sg, int group, int k0, int k1)
+    {
+        const SLane sl = slane(group);
+#pragma unroll
+        for (int k = 0; k + 1 < NBUF; ++k)
+            if (k >= k0 && k < k1)
+                issue(bb[k], sg, k, sl);
+    }
+
     // Runs the share; outputs are tagged (`tag`).  MODE_ACC adds the share's
     // residual rows (hv, one per thread, loaded with the staging) and writes
     // the sum to ht (and to h0 when `last`).
-    template <int MODE>
+    //
+    // `nx(bi)` runs after block bi (every wave, every bi < MAXB, in order;
+    // bi is a constant of the unrolled loop): the next phase's loads go out
+    // there, into the registers the computed blocks left.
+    template <int MODE, class NX>
     static EP_DEV void run(Blk (&bb)[NBUF], const Segs &sg, int group, const uint32_t *tab,
                            const uint32_t *xs, const uint32_t *xlo, const float *xf, float *red,
                            float *hrow, float hv, float rinv, uint64_t *ht, float *h0, bool last,
-                           uint64_t *act, uint32_t tag)
+                           uint64_t *act, uint32_t tag, NX &&nx)
     {
         const int wv = wave_id();
         // residual rows of the share (loaded by the caller with the staging)
@@ -495,7 +523,12 @@ struct Gemv {
                     block(bb[bi % NBUF], sg, qg, sl, xa, fx, tab, acc[qg]);
                 if (j == SPW - 1 && qg < ng)
                     reduce(sg, qg, acc[qg], red);
+                nx(bi);
             }
+        } else {
+#pragma unroll
+            for (int bi = 0; bi < MAXB; ++bi)
+                nx(bi);
         }
         lds_sync();
         // cross-wave sums (fixed order) and outputs, one thread per row
@@ -554,6 +587,13 @@ struct Gemv {
     // (columns = its 4 rows); eight MFMAs take the chunk's 32 weights.  Lane
     // 4 b + r then holds the chunk's hi and lo dot products of row r (D rows
     // 0 and 1), scaled by the row's group scale and the chunk's factor.
+    //
+    // Schedule: the NQ scale shuffles go out first, then the block's 16 NQ
+    // table lookups run as one rolling window of kLookAhead reads in flight
+    // across quad boundaries (two new reads per MFMA), so every wave keeps
+    // the LDS busy instead of draining it twice per quad.  Scheduling
+    // fences hold that order.
+    static constexpr int kLookAhead = 12;  // lgkmcnt counts at most 15
     static EP_DEV void block(const Blk &bk, const Segs &sg, int qg, const SLane &sl,
                              const f16x2_t (&xa)[16], float fx, const uint32_t *tab, float (&acc)[NQ])
     {
@@ -562,51 +602,73 @@ struct Gemv {
         const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
         const int lg = lg_gps(sl.lgroup);
         const int gl = (c >> (4 - lg)) & ((1 << lg) - 1);  // this lane's group within the slab
+        uint32_t l4s[NQ], sb[NQ];
+        bool qon[NQ];
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
             const int vq = vquad(sg, qg, i, wave);
-            const int slot = PAIRED ? (i >= RQ ? 1 : 0) : (vq < sg.qb ? seg_of(sg, vq, i) - sg.sfirst : 0);
-            const uint32_t l4s = lane4 | ((uint32_t)slot << 7);
-            // the 16 lookups of the chunk are issued back to back, then
-            // consumed (source order is kept where registers are tight)
-            uint32_t tv[16];
+            qon[i] = vq < sg.qb;
+            const int slot = PAIRED ? (i >= RQ ? 1 : 0) : (qon[i] ? seg_of(sg, vq, i) - sg.sfirst : 0);
+            l4s[i] = lane4 | ((uint32_t)slot << 7);
+            sb[i] = (uint32_t)__shfl((int)bk.s, (((i * 4 + rq) << lg) | gl), 64);
+        }
+        constexpr int NL = 16 * NQ;
+        auto lookup = [&](int m) {
+            const int i = m >> 4, k = m & 15;
+            return lds_read_u32(tab, __builtin_amdgcn_perm(bk.w[i][k >> 2], l4s[i], kSelByte[k & 3]));
+        };
+        uint32_t tv[NL];
 #pragma unroll
-            for (int wd = 0; wd < 4; ++wd)
+        for (int m = 0; m < kLookAhead && m < NL; ++m)
+            tv[m] = lookup(m);
+        f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    tv[wd * 4 + q] = lds_read_u32(tab, __builtin_amdgcn_perm(bk.w[i][wd], l4s, kSelByte[q]));
-            f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int n = 0; n < NL / 2; ++n) {
 #pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                const f16x2_t a0 = xa[2 * n], a1 = xa[2 * n + 1];
-                const f16x2_t b0 = as_f16x2(tv[2 * n]), b1 = as_f16x2(tv[2 * n + 1]);
-                const f16x4_t av = {a0[0], a0[1], a1[0], a1[1]};
-                const f16x4_t bv = {b0[0], b0[1], b1[0], b1[1]};
-                d = __builtin_amdgcn_mfma_f32_4x4x4f16(av, bv, d, 0, 0, 0);
+            for (int m = kLookAhead + 2 * n; m < kLookAhead + 2 * n + 2 && m < NL; ++m)
+                tv[m] = lookup(m);
+            __builtin_amdgcn_sched_barrier(0);
+            const int i = n >> 3, nn = n & 7;
+            const f16x2_t a0 = xa[2 * nn], a1 = xa[2 * nn + 1];
+            const f16x2_t b0 = as_f16x2(tv[2 * n]), b1 = as_f16x2(tv[2 * n + 1]);
+            const f16x4_t av = {a0[0], a0[1], a1[0], a1[1]};
+            const f16x4_t bv = {b0[0], b0[1], b1[0], b1[1]};
+            d = __builtin_amdgcn_mfma_f32_4x4x4f16(av, bv, nn == 0 ? (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f} : d,
+                                                   0, 0, 0);
+            if (nn == 7) {
+                const float sc = qon[i] ? (float)f16_from_bits((uint16_t)sb[i]) : 0.0f;
+                acc[i] = fmaf(d[0] + d[1], sc * fx, acc[i]);
             }
-            const uint32_t sb = (uint32_t)__shfl((int)bk.s, (((i * 4 + rq) << lg) | gl), 64);
-            const float sc = vq < sg.qb ? (float)f16_from_bits((uint16_t)sb) : 0.0f;
-            acc[i] = fmaf(d[0] + d[1], sc * fx, acc[i]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
     // Each row's sum over the 16 chunks (lanes r, r + 4, .., r + 60) of quad
-    // group qg into the LDS accumulator: DPP row_ror 4 and 8, then lanes
-    // l ^ 16 and l ^ 32.
+    // group qg into the LDS accumulator, the block's (up to) four quads
+    // reduced together: v_permlane32_swap pairs quads 0|1 and 2|3 (lanes l
+    // and l ^ 32 added, one quad per half), v_permlane16_swap pairs the two
+    // results (lanes l and l ^ 16 added, one quad per 16-lane row: rows 0..3
+    // hold quads 0, 2, 1, 3), then DPP row_ror 4 and 8 finish each row.
     static EP_DEV void reduce(const Segs &sg, int qg, const float (&acc)[NQ], float *red)
     {
         const int lane = tid_fresh() & 63, wave = wave_id();
-        const int rq = lane & 3;
+        float a[4];
 #pragma unroll
-        for (int i = 0; i < NQ; ++i) {
-            float v = acc[i];
-            v += dpp_mov<0x124>(v);
-            v += dpp_mov<0x128>(v);
-            v = xor32_sum(xor16_sum(v));
-            const int vq = vquad(sg, qg, i, wave);
-            if (lane < 4 && vq < sg.qb)
-                red[wave * RED_ROWS + (PAIRED && i >= RQ ? RED_ROWS / 2 : 0) + (vq - sg.qa) * 4 + rq] = v;
-        }
+        for (int i = 0; i < 4; ++i)
+            a[i] = i < NQ ? acc[i] : 0.0f;
+        const auto s01 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[0]), __float_as_uint(a[1]), false, false);
+        const auto s23 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a[2]), __float_as_uint(a[3]), false, false);
+        const float u = __uint_as_float(s01[0]) + __uint_as_float(s01[1]);
+        const float w = __uint_as_float(s23[0]) + __uint_as_float(s23[1]);
+        const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(u), __float_as_uint(w), false, false);
+        float v = __uint_as_float(t[0]) + __uint_as_float(t[1]);
+        v += dpp_mov<0x124>(v);
+        v += dpp_mov<0x128>(v);
+        const int row = lane >> 4;
+        const int i = row == 1 ? 2 : (row == 2 ? 1 : row);  // this row's quad
+        const int vq = vquad(sg, qg, i < NQ ? i : 0, wave);
+        if ((lane & 15) < 4 && i < NQ && vq < sg.qb)
+            red[wave * RED_ROWS + (PAIRED && i >= RQ ? RED_ROWS / 2 : 0) + (vq - sg.qa) * 4 + (lane & 3)] = v;
     }
 };
 
@@ -1240,6 +1302,10 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
     using PO = Gemv<M::SO, M::RQ_O, false, M::MQ_O, M::NB_O>;
     using PG = Gemv<M::SH, M::RQ_GU, true, M::MQ_GU, M::NB_GU>;
     using PD = Gemv<M::SI, M::RQ_D, false, M::MQ_D, M::NB_D>;
+    // gate|up blocks issued during the attention window; the rest go out
+    // during the o phase
+    constexpr int kGuEarly = M::GU_EARLY < PG::NBUF - 1 ? M::GU_EARLY : PG::NBUF - 1;
+    constexpr int kGuLate = PG::NBUF - 1 - kGuEarly;
 
     LayerC *layers = (LayerC *)a.layers;
     const int pos = ldg(a.state);
@@ -1305,7 +1371,8 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
                        : stage<XS_RMS, M::H>(h_prev, L.attn_norm, a.eps, tag_of(seq, l - 1, PH_DOWN),
                                              lh.xs, lh.xl, lh.xf, part8, err);
             PQ::template run<MODE_STORE>(qb, sq, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
-                                         rinv, nullptr, a.h0, false, nullptr, tag_of(seq, l, PH_QKV));
+                                         rinv, nullptr, a.h0, false, nullptr, tag_of(seq, l, PH_QKV),
+                                         [](int) {});
         }
         stamp(a, l, 1);
         // Attention workgroups issue their first item's K/V rows (cached by
@@ -1332,10 +1399,12 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
                                  [] {});
                 lds_sync();
             }
+            PG::prefetch_range(gb, segs_gu(L, sh), a.group, 0, kGuEarly);
             if (so.qb > so.qa)
                 build_tables(tab, cb16, cbv, so.ntab);
         } else {
             PO::prefetch(ob, so, a.group);
+            PG::prefetch_range(gb, segs_gu(L, sh), a.group, 0, kGuEarly);
             build_tables(tab, cb16, cbv, so.ntab);
             stamp(a, l, 9);
         }
@@ -1354,14 +1423,21 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
                                       part8, err);
                 const float hv = residual_take(hraw, so, a, h_prev, tag_of(seq, l - 1, PH_DOWN));
                 stamp(a, l, 3);
+                const Segs sgu = segs_gu(L, sh);
                 PO::template run<MODE_ACC>(ob, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
-                                           1.0f, h_o, a.h0, false, nullptr, tag_of(seq, l, PH_O));
+                                           1.0f, h_o, a.h0, false, nullptr, tag_of(seq, l, PH_O),
+                                           [&](int bi) {
+                                               PG::prefetch_range(gb, sgu, a.group,
+                                                                  kGuEarly + spread_lo<kGuLate, PO::MAXB>(bi),
+                                                                  kGuEarly + spread_lo<kGuLate, PO::MAXB>(bi + 1));
+                                           });
+            } else {
+                PG::prefetch_range(gb, segs_gu(L, sh), a.group, kGuEarly, PG::NBUF - 1);
             }
         }
         stamp(a, l, 4);
         {
             const Segs sg = segs_gu(L, sh);
-            PG::prefetch(gb, sg, a.group);
             stamp(a, l, 13);
             stamp(a, l, 14, 448);
             build_tables(tab, cb16, cbv, sg.ntab);
@@ -1375,13 +1451,18 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             const float rinv = stage<XS_RMS, M::H>(h_o, L.mlp_norm, a.eps, tag_of(seq, l, PH_O),
                                                    lh.xs, lh.xl, lh.xf, part8, err);
             stamp(a, l, 5);
+            const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
             PG::template run<MODE_SWIGLU>(gb, sg, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
-                                          rinv, nullptr, a.h0, false, actl, tag_of(seq, l, PH_ACT));
+                                          rinv, nullptr, a.h0, false, actl, tag_of(seq, l, PH_ACT),
+                                          [&](int bi) {
+                                              PD::prefetch_range(db, sd, a.group,
+                                                                 spread_lo<PD::NBUF - 1, PG::MAXB>(bi),
+                                                                 spread_lo<PD::NBUF - 1, PG::MAXB>(bi + 1));
+                                          });
         }
         stamp(a, l, 6);
         {
             const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
-            PD::prefetch(db, sd, a.group);
             build_tables(tab, cb16, cbv, sd.ntab);
             if (!last) {
                 const Segs sq = segs_qkv(layers[l + 1], a, sh);
@@ -1396,13 +1477,21 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
                                 err);
             const float hv = residual_take(hraw, sd, a, h_o, tag_of(seq, l, PH_O));
             stamp(a, l, 7);
+            // the next layer's q|k|v (an empty share after the last layer)
+            Segs sqn = segs_qkv(layers[last ? l : l + 1], a, sh);
+            if (last)
+                sqn.qb = sqn.qa;
             PD::template run<MODE_ACC>(db, sd, a.group, tab, li.xs, li.xl, li.xf, li.red, hrow, hv,
-                                       1.0f, h_d, a.h0, last, nullptr, tag_of(seq, l, PH_DOWN));
+                                       1.0f, h_d, a.h0, last, nullptr, tag_of(seq, l, PH_DOWN),
+                                       [&](int bi) {
+                                           PQ::prefetch_range(qb, sqn, a.group,
+                                                              spread_lo<PQ::NBUF - 1, PD::MAXB>(bi),
+                                                              spread_lo<PQ::NBUF - 1, PD::MAXB>(bi + 1));
+                                       });
         }
         stamp(a, l, 8);
         if (!last) {
             const Segs sq = segs_qkv(layers[l + 1], a, sh);
-            PQ::prefetch(qb, sq, a.group);
             build_tables(tab, cb16, cbv, sq.ntab);
             const Segs so = segs_one(layers[l + 1], 3, M::H, sh.ldsb_o, sh, xo);
             cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
