@@ -504,6 +504,7 @@ struct Gemv {
         if (wave_on(wv)) {
             const int ng = ngroups(sg);
             const SLane sl = slane(group);
+            const LaneC lc = lane_consts(sl);
             float acc[QB][NQ];
             f16x2_t xa[16];  // the slab's activations (MFMA A operand: hi, lo or 0)
             float fx = 0.0f;
@@ -520,9 +521,9 @@ struct Gemv {
                         acc[qg][i] = 0.0f;
                 }
                 if (qg < ng && slab_on(j, wv))
-                    block(bb[bi % NBUF], sg, qg, sl, xa, fx, tab, acc[qg]);
+                    block(bb[bi % NBUF], sg, qg, lc, xa, fx, tab, acc[qg]);
                 if (j == SPW - 1 && qg < ng)
-                    reduce(sg, qg, acc[qg], red);
+                    reduce(sg, qg, lc, acc[qg], red);
                 nx(bi);
             }
         } else {
@@ -581,6 +582,35 @@ struct Gemv {
         return xf[xo / 16];
     }
 
+    // Lane constants of a phase's block loop, computed once per phase (a
+    // per-block recomputation from the thread index is VALU work on the
+    // loop's critical resource): the lane's table copy, the ds_bpermute
+    // addresses of its quads' scales, and where reduce() puts its row sum.
+    struct LaneC {
+        uint32_t lane4;     // (lane & 31) * 4: the lane's table copy
+        uint32_t sidx[NQ];  // byte address of the lane holding quad i's scale
+        int rvq;            // reduce: the row's quad within a quad group (large: no write)
+        int raddr;          // reduce: accumulator slot of that row for quad group 0
+    };
+    static EP_DEV LaneC lane_consts(const SLane &sl)
+    {
+        LaneC lc;
+        const int lane = tid_fresh() & 63, wave = wave_id();
+        const int rq = lane & 3, c = lane >> 2;
+        lc.lane4 = ((uint32_t)lane & 31) << 2;
+        const int lg = lg_gps(sl.lgroup);
+        const int gl = (c >> (4 - lg)) & ((1 << lg) - 1);
+#pragma unroll
+        for (int i = 0; i < NQ; ++i)
+            lc.sidx[i] = (uint32_t)((((i * 4 + rq) << lg) | gl) << 2);
+        const int row = lane >> 4;
+        const int i = row == 1 ? 2 : (row == 2 ? 1 : row);  // rows 0..3 hold quads 0, 2, 1, 3
+        const int rv = (wave / WPR) * RQ + (PAIRED ? (i % RQ) : i);
+        lc.rvq = ((lane & 15) < 4 && i < NQ) ? rv : (1 << 20);
+        lc.raddr = wave * RED_ROWS + (PAIRED && i >= RQ ? RED_ROWS / 2 : 0) + rv * 4 + rq;
+        return lc;
+    }
+
     // Dot products of one block into the rows' partial sums on the matrix
     // cores: v_mfma_f32_4x4x4_16b_f16 with block b = the lane's chunk, A =
     // activations (rows hi, lo, 0, 0), B = the quad's dequantized weights
@@ -594,23 +624,19 @@ struct Gemv {
     // the LDS busy instead of draining it twice per quad.  Scheduling
     // fences hold that order.
     static constexpr int kLookAhead = 12;  // lgkmcnt counts at most 15
-    static EP_DEV void block(const Blk &bk, const Segs &sg, int qg, const SLane &sl,
+    static EP_DEV void block(const Blk &bk, const Segs &sg, int qg, const LaneC &lc,
                              const f16x2_t (&xa)[16], float fx, const uint32_t *tab, float (&acc)[NQ])
     {
-        const int lane = tid_fresh() & 63, wave = wave_id();
-        const int rq = lane & 3, c = lane >> 2;
-        const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
-        const int lg = lg_gps(sl.lgroup);
-        const int gl = (c >> (4 - lg)) & ((1 << lg) - 1);  // this lane's group within the slab
+        const int wave = wave_id();
         uint32_t l4s[NQ], sb[NQ];
         bool qon[NQ];
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
-            const int vq = vquad(sg, qg, i, wave);
+            const int vq = vquad(sg, qg, i, wave);  // wave-uniform
             qon[i] = vq < sg.qb;
             const int slot = PAIRED ? (i >= RQ ? 1 : 0) : (qon[i] ? seg_of(sg, vq, i) - sg.sfirst : 0);
-            l4s[i] = lane4 | ((uint32_t)slot << 7);
-            sb[i] = (uint32_t)__shfl((int)bk.s, (((i * 4 + rq) << lg) | gl), 64);
+            l4s[i] = lc.lane4 | ((uint32_t)slot << 7);
+            sb[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)lc.sidx[i], (int)bk.s);
         }
         constexpr int NL = 16 * NQ;
         auto lookup = [&](int m) {
@@ -649,9 +675,8 @@ struct Gemv {
     // and l ^ 32 added, one quad per half), v_permlane16_swap pairs the two
     // results (lanes l and l ^ 16 added, one quad per 16-lane row: rows 0..3
     // hold quads 0, 2, 1, 3), then DPP row_ror 4 and 8 finish each row.
-    static EP_DEV void reduce(const Segs &sg, int qg, const float (&acc)[NQ], float *red)
+    static EP_DEV void reduce(const Segs &sg, int qg, const LaneC &lc, const float (&acc)[NQ], float *red)
     {
-        const int lane = tid_fresh() & 63, wave = wave_id();
         float a[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -664,11 +689,9 @@ struct Gemv {
         float v = __uint_as_float(t[0]) + __uint_as_float(t[1]);
         v += dpp_mov<0x124>(v);
         v += dpp_mov<0x128>(v);
-        const int row = lane >> 4;
-        const int i = row == 1 ? 2 : (row == 2 ? 1 : row);  // this row's quad
-        const int vq = vquad(sg, qg, i < NQ ? i : 0, wave);
-        if ((lane & 15) < 4 && i < NQ && vq < sg.qb)
-            red[wave * RED_ROWS + (PAIRED && i >= RQ ? RED_ROWS / 2 : 0) + (vq - sg.qa) * 4 + (lane & 3)] = v;
+        // the row's quad is qa + qg QPB + rvq; rows past the share are not written
+        if (lc.rvq < sg.qb - sg.qa - qg * QPB)
+            red[lc.raddr + qg * QPB * 4] = v;
     }
 };
 
