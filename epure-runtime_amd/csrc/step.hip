@@ -235,6 +235,14 @@ EP_DEV int tid_fresh()
 // uniform).
 EP_DEV int wave_id() { return __builtin_amdgcn_readfirstlane(tid_fresh() >> 6); }
 
+// 64 zero bytes in LDS (written once at kernel entry): rows 2 and 3 of the
+// GEMV MFMAs' A operand.
+EP_DEV uint32_t *lds_zeros()
+{
+    __shared__ __align__(16) uint32_t z[16];
+    return z;
+}
+
 // ---------------------------------------------------------------- segments
 // The virtual row-quad space of one GEMV phase of a layer: up to three
 // weights stacked (q|k|v), or a gate/up pair sharing quad indices.
@@ -571,13 +579,14 @@ struct Gemv {
     {
         const int ai = tid_fresh() & 3;
         const uint32_t xo = chunk_byte(j, wv);  // pair index = byte index
-        const uint32_t *src = ai == 0 ? xs : xlo;
+        // lanes 4 b + 2 and 4 b + 3 read the 64 zero bytes (no per-value select)
+        const uint32_t *src = ai == 0 ? xs + xo : (ai == 1 ? xlo + xo : lds_zeros());
 #pragma unroll
         for (int p = 0; p < 16; p += 4) {
-            const u32x4_t q4 = *(const u32x4_t *)(src + xo + p);
+            const u32x4_t q4 = *(const u32x4_t *)(src + p);
 #pragma unroll
             for (int t = 0; t < 4; ++t)
-                xa[p + t] = as_f16x2(ai < 2 ? q4[t] : 0u);
+                xa[p + t] = as_f16x2(q4[t]);
         }
         return xf[xo / 16];
     }
@@ -1330,6 +1339,8 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
     constexpr int kGuEarly = M::GU_EARLY < PG::NBUF - 1 ? M::GU_EARLY : PG::NBUF - 1;
     constexpr int kGuLate = PG::NBUF - 1 - kGuEarly;
 
+    if (tid_fresh() < 16)
+        lds_zeros()[tid_fresh()] = 0u;  // read after the first table build's barrier
     LayerC *layers = (LayerC *)a.layers;
     const int pos = ldg(a.state);
     if (pos < 0 || pos >= a.max_pos)
