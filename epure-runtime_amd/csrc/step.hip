@@ -504,36 +504,14 @@ struct Gemv {
         }
         // Straight-line over the most blocks a share can hold, NBUF buffers
         // rotated (a register copy of a block would wait for its loads):
-        // block bi + NBUF - 1 is issued into the buffer block bi - 1 left,
-        // then block bi is computed.  Every block's loads are issued
-        // (zero-length where not live), only live blocks computed: with no
-        // loop and no conditional loads the compiler's wait before each
+        // block bi + NBUF - 1 is issued into the buffer block bi - 1 left.
+        // Every block's loads are issued (zero-length where not live): with
+        // no loop and no conditional loads the compiler's wait before each
         // block counts exactly the younger blocks still in flight.
         if (wave_on(wv)) {
-            const int ng = ngroups(sg);
             const SLane sl = slane(group);
             const LaneC lc = lane_consts(sl);
-            float acc[QB][NQ];
-            f16x2_t xa[16];  // the slab's activations (MFMA A operand: hi, lo or 0)
-            float fx = 0.0f;
-#pragma unroll
-            for (int bi = 0; bi < MAXB; ++bi) {
-                const int j = bi / QB, qg = bi % QB;
-                if (bi + NBUF - 1 < MAXB)
-                    issue(bb[(bi + NBUF - 1) % NBUF], sg, bi + NBUF - 1, sl);
-                if (qg == 0 && slab_on(j, wv))
-                    fx = load_x(j, wv, xs, xlo, xf, xa);
-                if (j == 0) {
-#pragma unroll
-                    for (int i = 0; i < NQ; ++i)
-                        acc[qg][i] = 0.0f;
-                }
-                if (qg < ng && slab_on(j, wv))
-                    block(bb[bi % NBUF], sg, qg, lc, xa, fx, tab, acc[qg]);
-                if (j == SPW - 1 && qg < ng)
-                    reduce(sg, qg, lc, acc[qg], red);
-                nx(bi);
-            }
+            stream(bb, sg, sl, lc, xs, xlo, xf, tab, red, nx);
         } else {
 #pragma unroll
             for (int bi = 0; bi < MAXB; ++bi)
@@ -620,61 +598,105 @@ struct Gemv {
         return lc;
     }
 
-    // Dot products of one block into the rows' partial sums on the matrix
-    // cores: v_mfma_f32_4x4x4_16b_f16 with block b = the lane's chunk, A =
-    // activations (rows hi, lo, 0, 0), B = the quad's dequantized weights
+    // Dot products of the share's blocks into the rows' partial sums on the
+    // matrix cores: v_mfma_f32_4x4x4_16b_f16 with block b = the lane's chunk,
+    // A = activations (rows hi, lo, 0, 0), B = a quad's dequantized weights
     // (columns = its 4 rows); eight MFMAs take the chunk's 32 weights.  Lane
     // 4 b + r then holds the chunk's hi and lo dot products of row r (D rows
     // 0 and 1), scaled by the row's group scale and the chunk's factor.
     //
-    // Schedule: the NQ scale shuffles go out first, then the block's 16 NQ
-    // table lookups run as one rolling window of kLookAhead reads in flight
-    // across quad boundaries (two new reads per MFMA), so every wave keeps
-    // the LDS busy instead of draining it twice per quad.  Scheduling
-    // fences hold that order.
+    // Schedule: the table lookups of all the phase's blocks form one stream
+    // with kLookAhead reads in flight (two new reads per MFMA), across quad
+    // and block boundaries: the next block's first lookups are already out
+    // while a block's last MFMAs, its reduction and the next phase's loads
+    // run, so the LDS never drains between blocks.  A block's set-up (the
+    // loads of block bi + NBUF - 1 into the buffer block bi - 1 left, its
+    // quads' table slots and scale shuffles) runs just before its first
+    // lookup.  Scheduling fences hold the order.  Blocks past the share or
+    // on an idle slab are streamed too (their loads are zero-length) and
+    // contribute nothing.
     static constexpr int kLookAhead = 12;  // lgkmcnt counts at most 15
-    static EP_DEV void block(const Blk &bk, const Segs &sg, int qg, const LaneC &lc,
-                             const f16x2_t (&xa)[16], float fx, const uint32_t *tab, float (&acc)[NQ])
+    template <class NX>
+    static EP_DEV void stream(Blk (&bb)[NBUF], const Segs &sg, const SLane &sl, const LaneC &lc,
+                              const uint32_t *xs, const uint32_t *xlo, const float *xf, const uint32_t *tab,
+                              float *red, NX &nx)
     {
-        const int wave = wave_id();
-        uint32_t l4s[NQ], sb[NQ];
-        bool qon[NQ];
+        const int wv = wave_id();
+        const int ng = ngroups(sg);
+        constexpr int NL = 16 * NQ;    // lookups per block
+        constexpr int T = MAXB * NL;   // lookups of the phase
+        uint32_t l4s[MAXB][NQ], sb[MAXB][NQ];
+        bool qon[MAXB][NQ];
+        auto start = [&](int bi) {
+            if (bi + NBUF - 1 < MAXB)
+                issue(bb[(bi + NBUF - 1) % NBUF], sg, bi + NBUF - 1, sl);
+            const int j = bi / QB, qg = bi % QB;
 #pragma unroll
-        for (int i = 0; i < NQ; ++i) {
-            const int vq = vquad(sg, qg, i, wave);  // wave-uniform
-            qon[i] = vq < sg.qb;
-            const int slot = PAIRED ? (i >= RQ ? 1 : 0) : (qon[i] ? seg_of(sg, vq, i) - sg.sfirst : 0);
-            l4s[i] = lc.lane4 | ((uint32_t)slot << 7);
-            sb[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)lc.sidx[i], (int)bk.s);
-        }
-        constexpr int NL = 16 * NQ;
-        auto lookup = [&](int m) {
-            const int i = m >> 4, k = m & 15;
-            return lds_read_u32(tab, __builtin_amdgcn_perm(bk.w[i][k >> 2], l4s[i], kSelByte[k & 3]));
+            for (int i = 0; i < NQ; ++i) {
+                const int vq = vquad(sg, qg, i, wv);  // wave-uniform
+                qon[bi][i] = vq < sg.qb && slab_on(j, wv);
+                const int slot = PAIRED ? (i >= RQ ? 1 : 0) : (vq < sg.qb ? seg_of(sg, vq, i) - sg.sfirst : 0);
+                l4s[bi][i] = lc.lane4 | ((uint32_t)slot << 7);
+                sb[bi][i] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)lc.sidx[i], (int)bb[bi % NBUF].s);
+            }
         };
-        uint32_t tv[NL];
+        auto lookup = [&](int g) {
+            const int bi = g / NL, m = g % NL, i = m >> 4, k = m & 15;
+            return lds_read_u32(tab, __builtin_amdgcn_perm(bb[bi % NBUF].w[i][k >> 2], l4s[bi][i], kSelByte[k & 3]));
+        };
+        float acc[QB][NQ];
+        f16x2_t xa[16];  // the slab's activations (MFMA A operand: hi, lo or 0)
+        float fx = 0.0f;
+        uint32_t tv[T];
+        static_assert(kLookAhead <= NL, "the first window lies in block 0");
+        start(0);
 #pragma unroll
-        for (int m = 0; m < kLookAhead && m < NL; ++m)
-            tv[m] = lookup(m);
+        for (int g = 0; g < kLookAhead; ++g)
+            tv[g] = lookup(g);
         f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int n = 0; n < NL / 2; ++n) {
+        for (int bi = 0; bi < MAXB; ++bi) {
+            const int j = bi / QB, qg = bi % QB;
 #pragma unroll
-            for (int m = kLookAhead + 2 * n; m < kLookAhead + 2 * n + 2 && m < NL; ++m)
-                tv[m] = lookup(m);
-            __builtin_amdgcn_sched_barrier(0);
-            const int i = n >> 3, nn = n & 7;
-            const f16x2_t a0 = xa[2 * nn], a1 = xa[2 * nn + 1];
-            const f16x2_t b0 = as_f16x2(tv[2 * n]), b1 = as_f16x2(tv[2 * n + 1]);
-            const f16x4_t av = {a0[0], a0[1], a1[0], a1[1]};
-            const f16x4_t bv = {b0[0], b0[1], b1[0], b1[1]};
-            d = __builtin_amdgcn_mfma_f32_4x4x4f16(av, bv, nn == 0 ? (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f} : d,
-                                                   0, 0, 0);
-            if (nn == 7) {
-                const float sc = qon[i] ? (float)f16_from_bits((uint16_t)sb[i]) : 0.0f;
-                acc[i] = fmaf(d[0] + d[1], sc * fx, acc[i]);
+            for (int n = 0; n < NL / 2; ++n) {
+                const int g0 = kLookAhead + 2 * (bi * (NL / 2) + n);  // this step's two new lookups
+                const int nb = (bi + 1) * NL;                         // the next block's first lookup
+                if (bi + 1 < MAXB && g0 <= nb && nb < g0 + 2)
+                    start(bi + 1);
+#pragma unroll
+                for (int g = g0; g < g0 + 2; ++g)
+                    if (g < T)
+                        tv[g] = lookup(g);
+                __builtin_amdgcn_sched_barrier(0);
+                if (n == 0) {
+                    if (qg == 0 && slab_on(j, wv))
+                        fx = load_x(j, wv, xs, xlo, xf, xa);
+                    if (j == 0) {
+#pragma unroll
+                        for (int i = 0; i < NQ; ++i)
+                            acc[qg][i] = 0.0f;
+                    }
+                }
+                const int i = n >> 3, nn = n & 7;
+                const int st = bi * (NL / 2) + n;
+                const f16x2_t a0 = xa[2 * nn], a1 = xa[2 * nn + 1];
+                const f16x2_t b0 = as_f16x2(tv[2 * st]), b1 = as_f16x2(tv[2 * st + 1]);
+                const f16x4_t av = {a0[0], a0[1], a1[0], a1[1]};
+                const f16x4_t bv = {b0[0], b0[1], b1[0], b1[1]};
+                d = __builtin_amdgcn_mfma_f32_4x4x4f16(av, bv, nn == 0 ? (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f} : d,
+                                                       0, 0, 0);
+                if (nn == 7) {
+                    // a quad past the share or an idle slab adds nothing (a
+                    // select: its A operand may never have been loaded)
+                    const float sc = (float)f16_from_bits((uint16_t)sb[bi][i]);
+                    const float upd = fmaf(d[0] + d[1], sc * fx, acc[qg][i]);
+                    acc[qg][i] = qon[bi][i] ? upd : acc[qg][i];
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
+            if (j == SPW - 1 && qg < ng)
+                reduce(sg, qg, lc, acc[qg], red);
+            nx(bi);
         }
     }
 
