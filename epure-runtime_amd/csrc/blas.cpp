@@ -11,9 +11,12 @@
 // the codebook reductions) in this library's own kernels.
 //
 // One handle per device, created on first use; plans (descriptors, layouts
-// and the heuristic's first algorithm) cached per shape.  Matrices are
-// column-major in hipBLASLt's terms; callers pass row-major buffers as
-// their transposes.
+// and an algorithm) cached per shape.  The algorithm: the heuristic's
+// candidates are each timed once on the call's own operands when the plan
+// is made (the first call for a shape, outside stream capture; a plan made
+// during capture takes the heuristic's first choice), the fastest kept.
+// Matrices are column-major in hipBLASLt's terms; callers pass row-major
+// buffers as their transposes.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
@@ -76,7 +79,32 @@ int handle_for(int dev, hipblasLtHandle_t *h)
     return EP_OK;
 }
 
-int make_plan(Plan &p, hipblasLtHandle_t h)
+// Mean time of `reps` runs of one algorithm (after one untimed run), or a
+// negative value when it does not run.
+float time_algo(hipblasLtHandle_t h, const Plan &p, const hipblasLtMatmulAlgo_t &algo, const float *alpha,
+                const void *A, const void *B, float *D, void *ws, size_t ws_bytes, hipStream_t stream,
+                hipEvent_t e0, hipEvent_t e1)
+{
+    const float beta = 0.0f;
+    constexpr int reps = 3;
+    if (hipblasLtMatmul(h, p.desc, alpha, A, p.la, B, p.lb, &beta, D, p.ld, D, p.ld, &algo, ws, ws_bytes,
+                        stream) != HIPBLAS_STATUS_SUCCESS)
+        return -1.0f;
+    if (hipEventRecord(e0, stream) != hipSuccess)
+        return -1.0f;
+    for (int r = 0; r < reps; ++r)
+        if (hipblasLtMatmul(h, p.desc, alpha, A, p.la, B, p.lb, &beta, D, p.ld, D, p.ld, &algo, ws, ws_bytes,
+                            stream) != HIPBLAS_STATUS_SUCCESS)
+            return -1.0f;
+    float ms = -1.0f;
+    if (hipEventRecord(e1, stream) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+        hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+        return -1.0f;
+    return ms / reps;
+}
+
+int make_plan(Plan &p, hipblasLtHandle_t h, const float *alpha, const void *A, const void *B, float *D,
+              void *ws, hipStream_t stream)
 {
     const hipDataType ab = p.ab_dtype == EP_F16 ? HIP_R_16F : HIP_R_16BF;
     EP_BLAS_CHECK(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
@@ -92,16 +120,36 @@ int make_plan(Plan &p, hipblasLtHandle_t h)
     uint64_t wsz = p.ws;
     hipblasStatus_t s = hipblasLtMatmulPreferenceSetAttribute(
         pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsz, sizeof(wsz));
-    hipblasLtMatmulHeuristicResult_t res[4];
+    constexpr int kCand = 8;
+    hipblasLtMatmulHeuristicResult_t res[kCand];
     int nres = 0;
     if (s == HIPBLAS_STATUS_SUCCESS)
-        s = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.ld, p.ld, pref, 4, res, &nres);
+        s = hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.ld, p.ld, pref, kCand, res, &nres);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (s != HIPBLAS_STATUS_SUCCESS)
         return set_error(EP_ERR_HIP, "hipblasLtMatmulAlgoGetHeuristic: %s", status_name(s));
     if (nres < 1)
         return set_error(EP_DECLINE_SHAPE, "hipBLASLt has no algorithm for this GEMM");
     p.algo = res[0].algo;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (nres < 2 || hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+        return EP_OK;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+        float best = -1.0f;
+        for (int i = 0; i < nres; ++i) {
+            const float t = time_algo(h, p, res[i].algo, alpha, A, B, D, ws, p.ws, stream, e0, e1);
+            if (t > 0.0f && (best < 0.0f || t < best)) {
+                best = t;
+                p.algo = res[i].algo;
+            }
+        }
+    }
+    if (e0)
+        hipEventDestroy(e0);
+    if (e1)
+        hipEventDestroy(e1);
+    (void)hipGetLastError();  // a candidate that failed leaves no error behind
     return EP_OK;
 }
 
@@ -141,7 +189,7 @@ int blas_gemm_f32out(int ta, int tb, int64_t m, int64_t n, int64_t k, int ab_dty
         p.ldb = ldb;
         p.ldd = ldd;
         p.ws = ws_bytes;
-        rc = make_plan(p, h);
+        rc = make_plan(p, h, &alpha, A, B, D, ws, stream);
         if (rc != EP_OK)
             return rc;
         g_plans.push_back(p);
