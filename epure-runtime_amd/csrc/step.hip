@@ -1063,6 +1063,10 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
 #pragma unroll
         for (int t = 0; t < 8; ++t)
             o[g][t] = 0.0f;
+    float osum[2 * GQ];  // the wave's P.V sums this lane stores (reduce-scattered)
+#pragma unroll
+    for (int m = 0; m < 2 * GQ; ++m)
+        osum[m] = 0.0f;
     float mwv[GQ], lwv[GQ];
     if (wave_live) {
         float qv[GQ][8];
@@ -1122,11 +1126,25 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
                     o[g][t] = fmaf(pe[g][k], vv, o[g][t]);
             }
         }
+        // the row sums (lanes l, l ^ 16, l ^ 32, l ^ 48) of the 8 GQ values,
+        // reduce-scattered: permlane32 pairs values 2m, 2m + 1 (one per lane
+        // half), permlane16 pairs those (one per 16-lane row); lane (row R,
+        // e16) then holds value 4 m + q(R), q = 0, 2, 1, 3 for R = 0..3
+        constexpr int NV = 8 * GQ;
+        float u[NV / 2];
 #pragma unroll
-        for (int g = 0; g < GQ; ++g)
+        for (int m = 0; m < NV / 2; ++m) {
+            const int i0 = 2 * m, i1 = 2 * m + 1;
+            const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(o[i0 / 8][i0 % 8]),
+                                                            __float_as_uint(o[i1 / 8][i1 % 8]), false, false);
+            u[m] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+        }
 #pragma unroll
-            for (int t = 0; t < 8; ++t)
-                o[g][t] = xor32_sum(xor16_sum(o[g][t]));
+        for (int m = 0; m < NV / 4; ++m) {
+            const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(u[2 * m]), __float_as_uint(u[2 * m + 1]),
+                                                            false, false);
+            osum[m] = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+        }
     } else {
 #pragma unroll
         for (int g = 0; g < GQ; ++g) {
@@ -1135,13 +1153,12 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
         }
     }
     stamp(a, l, 16);  // the wave's scores, softmax and P.V
-    if (rr == 0) {
+    {
+        const int q = 2 * (rr & 1) + (rr >> 1);  // the values this lane's row holds
 #pragma unroll
-        for (int g = 0; g < GQ; ++g) {
-            *(f32x4_t *)(ow + (wave * GQ + g) * kD + e16 * 8) =
-                (f32x4_t){o[g][0], o[g][1], o[g][2], o[g][3]};
-            *(f32x4_t *)(ow + (wave * GQ + g) * kD + e16 * 8 + 4) =
-                (f32x4_t){o[g][4], o[g][5], o[g][6], o[g][7]};
+        for (int m = 0; m < 2 * GQ; ++m) {
+            const int g = m >> 1, t = 4 * (m & 1) + q;
+            ow[(wave * GQ + g) * kD + e16 * 8 + t] = osum[m];
         }
     }
     if (lane == 0) {
