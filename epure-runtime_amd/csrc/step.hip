@@ -1293,6 +1293,11 @@ EP_DEV float residual_take(uint64_t v, const Segs &sg, const StepArgs &a, const 
 // layer descriptor; recomputed where needed).
 struct Shape {
     int Nq, Nkv, H, I, ldsb_h, ldsb_o, ldsb_i, b, G;
+    // this workgroup's shares of the four phases, fixed for the launch and
+    // computed once (a share is a 64-bit division by the grid size, ~50
+    // instructions per wave): q|k|v [qa, qb) with its first segment and
+    // table count, o (after the attention workgroups), gate|up, down
+    int q_qa, q_qb, q_sfirst, q_ntab, o_qa, o_qb, g_qa, g_qb, d_qa, d_qb;
 };
 
 EP_DEV Segs segs_qkv(LayerC &L, const StepArgs &a, const Shape &sh)
@@ -1314,13 +1319,16 @@ EP_DEV Segs segs_qkv(LayerC &L, const StepArgs &a, const Shape &sh)
     s.q2 = (sh.Nq + sh.Nkv) / 4;
     s.nq = (sh.Nq + 2 * sh.Nkv) / 4;
     s.ldsb = sh.ldsb_h;
-    share(s, sh.b, sh.G, false);
+    s.qa = sh.q_qa;
+    s.qb = sh.q_qb;
+    s.sfirst = sh.q_sfirst;
+    s.ntab = sh.q_ntab;
     return s;
 }
 
-// One weight's row quads over workgroups skip .. G - 1 (workgroups below
-// `skip` get an empty share).
-EP_DEV Segs segs_one(LayerC &L, int li, int N, int ldsb, const Shape &sh, int skip = 0)
+// One weight's rows: o (li 3; the workgroups below the attention ones hold
+// an empty share) or down (li 6), the shares computed once per launch.
+EP_DEV Segs segs_one(LayerC &L, int li, int N, int ldsb, const Shape &sh)
 {
     Segs s;
     s.pk0 = s.pk1 = s.pk2 = L.packed[li];
@@ -1330,13 +1338,10 @@ EP_DEV Segs segs_one(LayerC &L, int li, int N, int ldsb, const Shape &sh, int sk
     s.q1 = s.q2 = 0x7fffffff;
     s.nq = N / 4;
     s.ldsb = ldsb;
-    if (sh.b < skip) {
-        s.qa = s.qb = 0;
-        s.sfirst = 0;
-        s.ntab = 1;
-    } else {
-        share(s, sh.b - skip, sh.G - skip, false);
-    }
+    s.qa = li == 3 ? sh.o_qa : sh.d_qa;  // a single segment: table slot 0 only
+    s.qb = li == 3 ? sh.o_qb : sh.d_qb;
+    s.sfirst = 0;
+    s.ntab = 1;
     return s;
 }
 
@@ -1353,7 +1358,10 @@ EP_DEV Segs segs_gu(LayerC &L, const Shape &sh)
     s.q1 = s.q2 = 0x7fffffff;
     s.nq = sh.I / 4;
     s.ldsb = sh.ldsb_h;
-    share(s, sh.b, sh.G, true);
+    s.qa = sh.g_qa;
+    s.qb = sh.g_qb;
+    s.sfirst = 0;
+    s.ntab = 2;
     return s;
 }
 
@@ -1405,6 +1413,34 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
     // half the grid): the o phase then never waits for its slowest members,
     // the combining attention workgroups
     const int xo = nitems < G / 2 ? nitems : G / 2;
+    {
+        Segs t;
+        t.q1 = sh.Nq / 4;
+        t.q2 = (sh.Nq + sh.Nkv) / 4;
+        t.nq = (sh.Nq + 2 * sh.Nkv) / 4;
+        share(t, b, G, false);
+        sh.q_qa = t.qa;
+        sh.q_qb = t.qb;
+        sh.q_sfirst = t.sfirst;
+        sh.q_ntab = t.ntab;
+        t.q1 = t.q2 = 0x7fffffff;
+        t.nq = M::H / 4;  // o: rows H, over the workgroups from xo
+        if (b < xo) {
+            sh.o_qa = sh.o_qb = 0;
+        } else {
+            share(t, b - xo, G - xo, false);
+            sh.o_qa = t.qa;
+            sh.o_qb = t.qb;
+        }
+        t.nq = M::I / 4;  // gate|up
+        share(t, b, G, true);
+        sh.g_qa = t.qa;
+        sh.g_qb = t.qb;
+        t.nq = M::H / 4;  // down: rows H
+        share(t, b, G, false);
+        sh.d_qa = t.qa;
+        sh.d_qb = t.qb;
+    }
 
     typename PQ::Blk qb[PQ::NBUF];
     typename PO::Blk ob[PO::NBUF];
@@ -1420,7 +1456,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         __builtin_amdgcn_sched_barrier(0);
         PQ::prefetch(qb, sq, a.group);
         build_tables(tab, cb16, cbv, sq.ntab);
-        const Segs so = segs_one(layers[0], 3, M::H, sh.ldsb_o, sh, xo);
+        const Segs so = segs_one(layers[0], 3, M::H, sh.ldsb_o, sh);
         cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
     }
 
@@ -1454,7 +1490,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // would delay it: results return in order) and the o table is built
         // after the attention.  The other workgroups prefetch o and build
         // its table now.
-        const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh, xo);
+        const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
         if (b < nitems) {
             AttnRegs ar;
             attn_load(ar, L.kcache, L.vcache, b % a.Hkv, b / a.Hkv, pos, a.max_pos);
@@ -1489,7 +1525,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // ---- o (+= residual); attention workgroups below xo hold no o rows
         // and go straight on to gate|up (no wait for the attention output)
         {
-            const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh, xo);
+            const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
             if (so.qb > so.qa) {
                 const uint64_t hraw = residual_issue(so, a, h_prev);
                 stage<XS_F32, M::HQD>(at_l, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf,
@@ -1566,7 +1602,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         if (!last) {
             const Segs sq = segs_qkv(layers[l + 1], a, sh);
             build_tables(tab, cb16, cbv, sq.ntab);
-            const Segs so = segs_one(layers[l + 1], 3, M::H, sh.ldsb_o, sh, xo);
+            const Segs so = segs_one(layers[l + 1], 3, M::H, sh.ldsb_o, sh);
             cbv = load_cb(so, so.ntab, a.levels, a.cb_dtype);
         }
     }
