@@ -146,9 +146,9 @@ int make_plan(Plan &p, hipblasLtHandle_t h, const float *alpha, const void *A, c
         }
     }
     if (e0)
-        hipEventDestroy(e0);
+        (void)hipEventDestroy(e0);
     if (e1)
-        hipEventDestroy(e1);
+        (void)hipEventDestroy(e1);
     (void)hipGetLastError();  // a candidate that failed leaves no error behind
     return EP_OK;
 }

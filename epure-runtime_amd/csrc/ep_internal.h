@@ -46,6 +46,10 @@ int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc 
                 hipStream_t stream);
 int launch_gemv_generic(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,
                         hipStream_t stream);
+// One GEMV per token over a stack of E weights shaped as w (w.packed and
+// w.scale point at expert 0): y[t] = x[t] . W[ids[t]]^T, ids on the device.
+int launch_gemv_gather(const PackedDesc &w, const ActDesc &x, int64_t T, const int *ids, int E,
+                       const OutDesc &y, hipStream_t stream);
 bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M);
 
 // Decode-step GEMV: M = 1, up to three weights sharing K (fused q/k/v or

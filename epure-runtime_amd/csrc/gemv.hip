@@ -89,6 +89,13 @@ struct GemvArgs {
     int group;
     int nseg;
     Seg seg[kMaxSeg];
+    // Gathered rows (stacked experts): when gidx is set, grid row y serves
+    // token y -- x row y, y row y -- with the rows of expert gidx[y] of a
+    // stack of E weights, each estride_w packed bytes and estride_s scale
+    // bytes after the previous one (seg[0] points at expert 0).
+    const int *gidx;
+    int E, ntok;
+    int64_t estride_w, estride_s;
 };
 
 // Writes one chunk of 2 * PAIRS activations (already multiplied by the
@@ -159,6 +166,17 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     const int nwg = wg_end - wg_begin;
     const int nblk = (N + ROWS - 1) / ROWS;
     int blk = bid - wg_begin;
+    const char *xbase = (const char *)a.x;
+    if (a.gidx) {
+        // the token's expert (clamped into the stack: ids are checked on the
+        // host where the caller can be synchronized)
+        int e = __builtin_amdgcn_readfirstlane(a.gidx[blockIdx.y]);
+        e = e < 0 ? 0 : (e >= a.E ? a.E - 1 : e);
+        packed += (int64_t)e * a.estride_w;
+        scale = (const char *)scale + (int64_t)e * a.estride_s;
+        xbase += (int64_t)blockIdx.y * a.ldx * (XDT == EP_F32 ? 4 : 2);
+        yseg = (char *)yseg + (int64_t)blockIdx.y * a.ldy * (a.y_dtype == EP_F32 ? 4 : 2);
+    }
 
     // This lane's 16-byte chunk of each of its slabs (fixed for the kernel).
     uint32_t cbyte[SPW];
@@ -270,7 +288,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     if constexpr (FAST) {
         const int xc = tid < (int)(a.K / KPC) ? tid : 0;
         const auto *xp = (const __attribute__((address_space(1))) u32x4_t *)(
-            (const char *)a.x + (int64_t)xc * KPC * (XDT == EP_F32 ? 4 : 2));
+            xbase + (int64_t)xc * KPC * (XDT == EP_F32 ? 4 : 2));
 #pragma unroll
         for (int p = 0; p < XPC; ++p)
             xraw[p] = xp[p];
@@ -338,7 +356,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
             const int64_t k0 = (int64_t)cc * KPC;
             float v[KPC];
             if constexpr (XS == XS_RMSNORM) {
-                const float *hp = (const float *)a.x + k0;
+                const float *hp = (const float *)xbase + k0;
                 const uint16_t *wp = (const uint16_t *)a.x2 + k0;
 #pragma unroll
                 for (int p = 0; p < KPC; p += 8) {
@@ -357,7 +375,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                     }
                 }
             } else if constexpr (XS == XS_SWIGLU) {
-                const float *gp = (const float *)a.x + k0;
+                const float *gp = (const float *)xbase + k0;
                 const float *up = (const float *)a.x2 + k0;
 #pragma unroll
                 for (int p = 0; p < KPC; p += 4) {
@@ -368,7 +386,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                         v[p + t] = silu_mul(g[t], u[t]);
                 }
             } else if constexpr (XDT == EP_F32) {
-                const float *xp = (const float *)a.x + (int64_t)(live_m ? m : 0) * a.ldx + k0;
+                const float *xp = (const float *)xbase + (int64_t)(live_m ? m : 0) * a.ldx + k0;
 #pragma unroll
                 for (int p = 0; p < KPC; p += 4) {
                     const f32x4_t t4 = *(const f32x4_t *)(xp + p);
@@ -377,7 +395,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
                         v[p + t] = live_m ? t4[t] : 0.0f;
                 }
             } else {
-                const uint16_t *xp = (const uint16_t *)a.x + (int64_t)(live_m ? m : 0) * a.ldx + k0;
+                const uint16_t *xp = (const uint16_t *)xbase + (int64_t)(live_m ? m : 0) * a.ldx + k0;
 #pragma unroll
                 for (int p = 0; p < PAIRS; p += 4) {
                     const u32x4_t t4 = *(const u32x4_t *)(xp + 2 * p);
@@ -696,12 +714,13 @@ int launch_xcap(GemvArgs a, int waves, hipStream_t stream)
     bool multi = false;
     for (int i = 0; i < a.nseg; ++i)
         multi |= (a.seg[i].N + 4 * RQ - 1) / (4 * RQ) > a.seg[i].wg_end - a.seg[i].wg_begin;
+    const dim3 g3((unsigned)grid, a.gidx ? (unsigned)a.ntok : 1u);
     if (multi)
-        hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, true, XCAP>), dim3(grid),
+        hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, true, XCAP>), g3,
                            dim3(waves * 64), 0, stream, a);
     else
-        hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, false, XCAP>),
-                           dim3(grid), dim3(waves * 64), 0, stream, a);
+        hipLaunchKernelGGL((gemv_lut_kernel<BITS, MT, RQ, SPW, XDT, XS, false, XCAP>), g3,
+                           dim3(waves * 64), 0, stream, a);
     EP_HIP_CHECK(hipGetLastError());
     return EP_OK;
 }
@@ -859,6 +878,28 @@ int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc 
     if (mt == 2)
         return dispatch_spw<8, 2>(a, x.dtype, spw, waves, stream);
     return dispatch_spw<8, 4>(a, x.dtype, spw, waves, stream);
+}
+
+int launch_gemv_gather(const PackedDesc &w, const ActDesc &x, int64_t T, const int *ids, int E,
+                       const OutDesc &y, hipStream_t stream)
+{
+    if (!gemv_serves(w, x, 1) || y.accumulate)
+        return EP_DECLINE_SHAPE;
+    if (T > 65535)
+        return set_error(EP_DECLINE_SHAPE, "gathered GEMV: at most 65535 tokens per launch");
+    GemvArgs a = make_args(w, x, 1, y);
+    a.ldx = x.ld;
+    a.ldy = y.ld;
+    a.gidx = ids;
+    a.E = E;
+    a.ntok = (int)T;
+    a.estride_w = w.N * a.row_bytes;
+    a.estride_s = w.N * w.ld_scale * (w.scale_dtype == EP_F32 ? 4 : 2);
+    int spw, waves;
+    plan(a.row_bytes, spw, waves);
+    if (w.bits() == 4)
+        return dispatch_spw<4, 1>(a, x.dtype, spw, waves, stream);
+    return dispatch_spw<8, 1>(a, x.dtype, spw, waves, stream);
 }
 
 int launch_gemv_generic(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,

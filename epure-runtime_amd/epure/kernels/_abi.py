@@ -43,6 +43,12 @@ _SIGS = {
         _c_i64, _c_i64, _c_i64,                  # M, N, K
         _p, _c_int, _c_i64, _c_int,              # y, y_dtype, ldy, flags
         _p]),                                    # stream
+    "ep_expert_matmul": (_c_int, [
+        _p, _c_int, _c_i64, _p, _c_i64,         # x, x_dtype, ldx, expert_ids (int32), T
+        _p, _p, _c_int, _c_i64,                  # packed, scale, scale_dtype, ld_scale
+        _p, _c_int, _c_int, _c_int,              # cb, cb_dtype, levels, group
+        _c_i64, _c_i64, _c_i64,                  # E, N, K
+        _p, _c_int, _c_i64, _p]),                # y, y_dtype, ldy, stream
     "ep_dequant_matmul_bwd_workspace": (_sz, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "ep_dequant_matmul_bwd": (_c_int, [
         _p, _c_int, _c_i64,                      # gy, gy_dtype, ldgy

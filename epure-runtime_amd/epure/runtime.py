@@ -338,27 +338,43 @@ class PackedExperts(nn.Module):
     batch-1 GEMV, the small-M or the MFMA path by their count -- without
     expanding any expert (the reference's holder materializes the whole
     slab per call, runtime.py:163-186).  GPU tensors only.
+
+    Up to ``GATHER_MAX_TOKENS`` tokens (f16/bf16 ``x``) run one gathered
+    launch that reads the ids on the device: no host synchronization with
+    ``check_ids=False`` and capturable in a HIP graph (ids outside
+    ``[0, E)`` are then clamped on the device).  With ``check_ids`` (the
+    default) an eager call range-checks the ids on the host first and raises
+    ``IndexError``; more tokens group per expert on the host.
     """
 
-    def __init__(self, store):
+    def __init__(self, store, check_ids=True):
         super().__init__()
         if len(store.shape) != 3:
             raise ValueError(f"expert store must be (E, N, K), got {store.shape}")
         self.store = store
+        self.check_ids = bool(check_ids)
         self.num_experts, self.out_features, self.in_features = store.shape
+
+    # At most this many tokens run the gathered path (one launch, expert ids
+    # read on the device, no host synchronization, capturable in a HIP
+    # graph); it re-reads an expert's weights per token, so more tokens are
+    # grouped per expert.
+    GATHER_MAX_TOKENS = 8
 
     def forward(self, x, expert_ids):
         s = self.store
         K, N = self.in_features, self.out_features
         x2 = x.reshape(-1, K)
-        ids = expert_ids.reshape(-1).to(torch.int64)
-        if ids.numel() != x2.shape[0]:
+        if expert_ids.numel() != x2.shape[0]:
             raise ValueError("one expert id per row of x")
         if not (x2.is_cuda and cuda_kernel.available()):
             raise RuntimeError("PackedExperts runs on the gfx950 backend only")
         out = torch.empty((x2.shape[0], N), dtype=x2.dtype, device=x2.device)
-        if ids.numel() == 0:
+        if x2.shape[0] == 0:
             return out
+        if x2.shape[0] <= self.GATHER_MAX_TOKENS and self._gathered(x2, expert_ids, out):
+            return out
+        ids = expert_ids.reshape(-1).to(torch.int64)
         order = torch.argsort(ids, stable=True)
         experts, counts = torch.unique_consecutive(ids[order], return_counts=True)
         experts, counts = experts.tolist(), counts.tolist()
@@ -390,6 +406,35 @@ class PackedExperts(nn.Module):
                 raise RuntimeError(f"PackedExperts: shape declined: {_abi.last_error()}")
             out.index_copy_(0, rows, ye)
         return out
+
+    def _gathered(self, x2, expert_ids, out):
+        """One ``ep_expert_matmul`` launch for every token; False where the
+        kernel declines the shape.  With ``check_ids`` and outside stream
+        capture the ids are range checked first (IndexError, as the grouped
+        path); otherwise they are clamped on the device."""
+        s = self.store
+        K, N = self.in_features, self.out_features
+        if x2.dtype not in (torch.float16, torch.bfloat16) or x2.stride(1) != 1:
+            return False
+        h = cuda_kernel._hot(s)
+        if not h.usable():
+            return False
+        ids32 = expert_ids.reshape(-1).to(device=x2.device, dtype=torch.int32).contiguous()
+        if self.check_ids and not torch.cuda.is_current_stream_capturing():
+            lo, hi = int(ids32.min()), int(ids32.max())
+            if lo < 0 or hi >= self.num_experts:
+                raise IndexError(f"expert id out of range [0, {self.num_experts})")
+        rc = _abi.lib.ep_expert_matmul(
+            x2.data_ptr(), _abi.dtype_code(x2.dtype), x2.stride(0), ids32.data_ptr(), x2.shape[0],
+            h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+            h.cb.data_ptr(), h.cb_dt, h.levels, h.group,
+            self.num_experts, N, K, out.data_ptr(), _abi.dtype_code(out.dtype), out.stride(0),
+            _abi.stream_handle(x2.device))
+        if rc > 0:
+            return False
+        if not _abi.check(rc, "ep_expert_matmul"):
+            raise RuntimeError(f"PackedExperts: {_abi.last_error()}")
+        return True
 
 
 # ---------------------------------------------------------------- model surgery

@@ -94,6 +94,25 @@ int ep_dequant_matmul(const void *x, int x_dtype, int64_t ldx,
                       void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Expert-indexed packed linear for a few tokens: y[t, :] = x[t, :] . W[e_t]^T
+ * with e_t = expert_ids[t] (int32, device memory) and W[e] the rows
+ * e*N .. e*N + N - 1 of a stack of E weights folded as (E*N, K) with one
+ * codebook (`packed`, `scale` point at expert 0; ld_scale = K / group).
+ * Replaces the per-expert loop of the stacked-expert forward (the
+ * reference's expert holder materializes the whole slab per call,
+ * epure/runtime.py:163-186): one launch, the ids read on the device, so the
+ * call has no host synchronization and can be captured in a HIP graph.
+ * The batch-1 LUT GEMV runs once per token (weights re-read per token: meant
+ * for decode-sized T). Ids outside [0, E) are clamped on the device; callers
+ * that can synchronize check them first. Returns EP_DECLINE_SHAPE where the
+ * GEMV does not serve the shape (the caller then groups tokens per expert).
+ */
+int ep_expert_matmul(const void *x, int x_dtype, int64_t ldx, const int32_t *expert_ids, int64_t T,
+                     const uint8_t *packed, const void *scale, int scale_dtype, int64_t ld_scale,
+                     const void *cb, int cb_dtype, int levels, int group, int64_t E, int64_t N,
+                     int64_t K, void *y, int y_dtype, int64_t ldy, void *stream);
+
+/*
  * Compressed-state backward of y = x . W^T with frozen indices
  * (fine-tuning/README.md:62-68; autograd through runtime.py:84-88):
  *   grad_x[M, K]            = gy[M, N] . W                (gx_dtype; NULL = skip)

@@ -79,3 +79,67 @@ def test_expert_holder_attaches_only_during_forward():
     y = m(torch.randn(3, 128, device=DEV))
     assert m.weight is None and y.shape == (3, 4, 64)
     assert torch.equal(m.seen, s.materialize(torch.bfloat16))
+
+
+@pytest.mark.parametrize("E,n,k,levels,T,dt", [(4, 256, 512, 16, 1, torch.bfloat16),
+                                               (6, 512, 2048, 16, 8, torch.float16),
+                                               (8, 384, 1024, 16, 5, torch.bfloat16),
+                                               (3, 128, 256, 256, 4, torch.float16)])
+def test_gathered_experts_vs_oracle(E, n, k, levels, T, dt):
+    """T <= GATHER_MAX_TOKENS: one ep_expert_matmul launch, ids on the device
+    (repeated and out-of-order ids included)."""
+    group = 128
+    s, packed, scale, cb = experts(E, n, k, levels, group, seed=3 * E + T)
+    g = torch.Generator(device=DEV).manual_seed(100 + T)
+    x = torch.randn(T, k, generator=g, device=DEV).to(dt)
+    ids = torch.randint(0, E, (T,), generator=g, device=DEV)
+    if T > 2:
+        ids[1] = ids[0]                     # two tokens on one expert
+    y = PackedExperts(s)(x, ids)
+    assert y.shape == (T, n) and y.dtype == dt
+    want = want_rows(x.float().cpu().numpy(), ids.cpu().tolist(), packed, scale, cb, E, n, k,
+                     group, levels)
+    err = np.abs(y.float().cpu().numpy() - want).max() / np.abs(want).max()
+    assert err < 2e-3 + 2.0 ** -8, err
+
+
+def test_gathered_experts_match_grouped_path():
+    """The gathered launch and the per-expert grouped route agree bit for bit
+    on the same rows (both run the batch-1 GEMV per token row)."""
+    s, *_ = experts(5, 512, 1024, 16, 128, seed=7)
+    g = torch.Generator(device=DEV).manual_seed(9)
+    x = torch.randn(6, 1024, generator=g, device=DEV).to(torch.bfloat16)
+    ids = torch.tensor([4, 0, 2, 2, 1, 3], device=DEV)
+    m = PackedExperts(s)
+    y_g = m(x, ids)
+    m.GATHER_MAX_TOKENS = 0                 # this instance groups per expert
+    ys = [m(x[t:t + 1], ids[t:t + 1]) for t in range(6)]
+    assert torch.equal(y_g, torch.cat(ys))
+
+
+def test_gathered_experts_graph_replay_follows_ids():
+    """Captured once, the gathered call follows ids and x rewritten in place
+    between replays (no host synchronization inside the call)."""
+    E, n, k, T = 6, 256, 1024, 4
+    s, packed, scale, cb = experts(E, n, k, 16, 128, seed=11)
+    m = PackedExperts(s, check_ids=False)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    x = torch.randn(T, k, generator=g, device=DEV).to(torch.bfloat16)
+    ids = torch.tensor([0, 1, 2, 3], device=DEV, dtype=torch.int32)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        m(x, ids)                           # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = m(x, ids)
+    for r in range(4):
+        new_ids = torch.randint(0, E, (T,), generator=g, device=DEV, dtype=torch.int32)
+        ids.copy_(new_ids)
+        x.copy_(torch.randn(T, k, generator=g, device=DEV).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = PackedExperts(s)(x, ids)
+        assert torch.equal(y, eager), r
