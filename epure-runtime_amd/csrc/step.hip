@@ -1080,14 +1080,28 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
                 qv[g][4 + t] = a1[t];
             }
         }
+        // this step's k and v rows (the lane's 8 dims), read by every lane
+        // and selected per row below (a read under the per-lane condition
+        // would branch per value)
+        float knl[8], vnl[8];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const f32x4_t k4 = *(const f32x4_t *)(kn + e16 * 8 + 4 * h);
+            const f32x4_t v4 = *(const f32x4_t *)(vn + e16 * 8 + 4 * h);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                knl[4 * h + t] = k4[t];
+                vnl[4 * h + t] = v4[t];
+            }
+        }
         float sc[GQ][kLoadsPerWave];
 #pragma unroll
         for (int k = 0; k < kLoadsPerWave; ++k) {
             const int p = pw0 + 4 * k + rr;
             float kw[8];
 #pragma unroll
-            for (int t = 0; t < 8; ++t)  // row pos: this step's key, from LDS
-                kw[t] = p == pos ? kn[e16 * 8 + t] : r.k[k][t >> 2][t & 3];
+            for (int t = 0; t < 8; ++t)  // row pos: this step's key
+                kw[t] = p == pos ? knl[t] : r.k[k][t >> 2][t & 3];
 #pragma unroll
             for (int g = 0; g < GQ; ++g) {
                 float acc = 0.0f;
@@ -1120,7 +1134,7 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
             const int p = pw0 + 4 * k + rr;
 #pragma unroll
             for (int t = 0; t < 8; ++t) {
-                const float vv = p == pos ? vn[e16 * 8 + t] : (p < pos ? r.v[k][t >> 2][t & 3] : 0.0f);
+                const float vv = p == pos ? vnl[t] : (p < pos ? r.v[k][t >> 2][t & 3] : 0.0f);
 #pragma unroll
                 for (int g = 0; g < GQ; ++g)
                     o[g][t] = fmaf(pe[g][k], vv, o[g][t]);
@@ -1384,6 +1398,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
     // gate|up blocks issued during the attention window; the rest go out
     // during the o phase
     constexpr int kGuEarly = M::GU_EARLY < PG::NBUF - 1 ? M::GU_EARLY : PG::NBUF - 1;
+    constexpr int kGuPace = 40;  // s_sleep units (64 cycles) between paced blocks
     constexpr int kGuLate = PG::NBUF - 1 - kGuEarly;
 
     if (tid_fresh() < 16)
@@ -1513,8 +1528,19 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
                 build_tables(tab, cb16, cbv, so.ntab);
         } else {
             PO::prefetch(ob, so, a.group);
-            PG::prefetch_range(gb, segs_gu(L, sh), a.group, 0, kGuEarly);
             build_tables(tab, cb16, cbv, so.ntab);
+            // the early gate|up blocks paced (~1.1 us apart): a burst of
+            // every block at once fills the memory queues that the
+            // attention chain's hand-overs and K/V reads go through
+            {
+                const Segs sgu = segs_gu(L, sh);
+#pragma unroll
+                for (int k = 0; k < kGuEarly; ++k) {
+                    if (k > 0)
+                        __builtin_amdgcn_s_sleep(kGuPace);
+                    PG::prefetch_range(gb, sgu, a.group, k, k + 1);
+                }
+            }
             stamp(a, l, 9);
         }
         {
