@@ -222,6 +222,9 @@ struct Spin {
     }
 };
 
+// true when `p` holds on every active lane of the wave (a wave-uniform value)
+EP_DEV bool wave_all(bool p) { return __builtin_amdgcn_ballot_w64(!p) == 0; }
+
 // threadIdx.x through an opaque move: values derived from it are recomputed
 // per phase instead of being hoisted out of the layer loop and kept live
 // (registers) for the whole step.
@@ -1220,52 +1223,62 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
         return;
     }
     if (cth) {
-        // running combine in chunk order; the partials of up to kCombine
-        // chunks are requested at once, then re-read where not yet there
-        constexpr int kCombine = 8;
-        const uint64_t *pg = a.part + (int64_t)(hq0 + g) * maxch * (kD + 2);
-        auto ready = [&](const uint64_t (&e)[4]) {
-            return (uint32_t)(e[0] >> 32) == tpart && (uint32_t)(e[1] >> 32) == tpart &&
-                   (uint32_t)(e[2] >> 32) == tpart && (uint32_t)(e[3] >> 32) == tpart;
-        };
-        auto fetch = [&](uint64_t (&e)[4], int cc) {
-            const uint64_t *pc = pg + (int64_t)cc * (kD + 2);
-            e[0] = ld_tag(pc);
-            e[1] = ld_tag(pc + 1);
-            e[2] = ld_tag(pc + 2 + dd);
-            e[3] = ld_tag(pc + 3 + dd);
-        };
-        for (int c0 = 1; c0 < nchunk; c0 += kCombine) {
-            uint64_t e[kCombine][4];
+        // running combine in chunk order over the partials of up to kCombine
+        // chunks at once: per chunk two coherent 16-byte loads, (max, sum)
+        // and the thread's two values.  Two polls are in flight, the next
+        // one issued before the current one is checked, so a partial is
+        // seen about one round trip after it lands rather than up to two.
+        constexpr int kCombine = 6;
+        const auto rp = buffer_rsrc(a.part + (int64_t)(hq0 + g) * maxch * (kD + 2),
+                                    (uint32_t)maxch * (kD + 2) * 8u);
+        using Poll = u32x4_t[2 * kCombine];
+        auto fetch = [&](Poll &e, int c0) {
 #pragma unroll
-            for (int k = 0; k < kCombine; ++k)
-                fetch(e[k], c0 + k < nchunk ? c0 + k : c0);
-            // re-read every chunk not there yet in the same round (one round
-            // trip per round, not one per chunk)
-            Spin sp;
-            for (;;) {
-                bool all = true;
-#pragma unroll
-                for (int k = 0; k < kCombine; ++k)
-                    all = all && (c0 + k >= nchunk || ready(e[k]));
-                if (all || !sp.again(err))
-                    break;
-#pragma unroll
-                for (int k = 0; k < kCombine; ++k)
-                    if (c0 + k < nchunk && !ready(e[k]))
-                        fetch(e[k], c0 + k);
+            for (int k = 0; k < kCombine; ++k) {
+                const uint32_t off = (uint32_t)(c0 + k < nchunk ? c0 + k : c0) * (kD + 2) * 8u;
+                e[2 * k] = ldc16(rp, off);
+                e[2 * k + 1] = ldc16(rp, off + (uint32_t)(2 + dd) * 8u);
             }
+        };
+        auto ready = [&](const Poll &e, int c0) {
+            bool ok = true;
+#pragma unroll
+            for (int k = 0; k < 2 * kCombine; ++k)
+                ok = ok && (c0 + k / 2 >= nchunk || (e[k][1] == tpart && e[k][3] == tpart));
+            return wave_all(ok);
+        };
+        auto merge = [&](const Poll &e, int c0) {
 #pragma unroll
             for (int k = 0; k < kCombine; ++k) {
                 if (c0 + k >= nchunk)
                     break;
-                const float Mc = __uint_as_float((uint32_t)e[k][0]);
+                const float Mc = __uint_as_float(e[2 * k][0]);
                 const float Mn = fmaxf(M, Mc);
                 const float fa = __expf(M - Mn), fb = __expf(Mc - Mn);
-                Ls = Ls * fa + __uint_as_float((uint32_t)e[k][1]) * fb;
-                n0 = n0 * fa + __uint_as_float((uint32_t)e[k][2]) * fb;
-                n1 = n1 * fa + __uint_as_float((uint32_t)e[k][3]) * fb;
+                Ls = Ls * fa + __uint_as_float(e[2 * k][2]) * fb;
+                n0 = n0 * fa + __uint_as_float(e[2 * k + 1][0]) * fb;
+                n1 = n1 * fa + __uint_as_float(e[2 * k + 1][2]) * fb;
                 M = Mn;
+            }
+        };
+        for (int c0 = 1; c0 < nchunk; c0 += kCombine) {
+            Poll pa, pb;
+            fetch(pa, c0);
+            Spin sp;
+            for (;;) {
+                sp.again(err);
+                fetch(pb, c0);
+                if (ready(pa, c0)) {
+                    merge(pa, c0);
+                    break;
+                }
+                if (!sp.again(err))
+                    break;
+                fetch(pa, c0);
+                if (ready(pb, c0)) {
+                    merge(pb, c0);
+                    break;
+                }
             }
         }
         st_tag(outp, __float_as_uint(n0 / Ls), tatt);
