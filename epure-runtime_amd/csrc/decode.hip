@@ -276,6 +276,10 @@ struct HeadArgs {
 };
 
 constexpr int kHeadPerLane = 64;  // activations per lane: H <= 4096
+// two waves per SIMD: each wave keeps two rows' loads in flight while it
+// computes, so a CU holds 128 KB of requests (one wave per SIMD left the
+// stream latency-bound at ~5.8 TB/s)
+constexpr int kHeadWaves = 8;
 
 template <int CTRL>
 EP_DEV float dpp_f(float v)
@@ -299,18 +303,18 @@ EP_DEV float row16_sum_dpp(float v)
 // registers and streams whole bf16 rows with 16-byte loads, two rows in
 // flight, every product an exact f32 FMA of the widened bf16 weight; row
 // sums use DPP within 16-lane rows and readlane across them.
-__global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
+__global__ void __launch_bounds__(64 * kHeadWaves) lm_head_kernel(HeadArgs a)
 {
-    __shared__ float wv[4];
-    __shared__ int wi[4];
-    __shared__ float ssq_s[4];
+    __shared__ float wv[kHeadWaves];
+    __shared__ int wi[kHeadWaves];
+    __shared__ float ssq_s[kHeadWaves];
     __shared__ int s_last;
     __shared__ __align__(16) float xs[64 * kHeadPerLane];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = a.H;
     const int nld = H / 512;  // 16-byte loads per lane per row
 
-    const int gw = blockIdx.x * 4 + wave, nw = gridDim.x * 4;
+    const int gw = blockIdx.x * kHeadWaves + wave, nw = gridDim.x * kHeadWaves;
     // first rows' loads go out before the normalization
     u32x4_t w[2][kHeadPerLane / 8];
     auto load_rows = [&](int r0) {
@@ -329,7 +333,7 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
         load_rows(gw);
 
     float ss = 0.0f;
-    for (int k = threadIdx.x * 4; k < H; k += 1024) {
+    for (int k = threadIdx.x * 4; k < H; k += 4 * 64 * kHeadWaves) {
         const f32x4_t v = *(const f32x4_t *)(a.h + k);
         ss = fmaf(v[0], v[0], fmaf(v[1], v[1], fmaf(v[2], v[2], fmaf(v[3], v[3], ss))));
     }
@@ -337,8 +341,12 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
     if (lane == 0)
         ssq_s[wave] = ss;
     __syncthreads();
-    const float rinv = rsqrtf((ssq_s[0] + ssq_s[1] + ssq_s[2] + ssq_s[3]) / (float)H + a.eps);
-    for (int k = threadIdx.x; k < H; k += 256)
+    float sst = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kHeadWaves; ++w)
+        sst += ssq_s[w];
+    const float rinv = rsqrtf(sst / (float)H + a.eps);
+    for (int k = threadIdx.x; k < H; k += 64 * kHeadWaves)
         xs[k] = a.h[k] * rinv * bf16_to_f32(a.norm_w[k]);
     __syncthreads();
     // lane's values: dims (lane + 64 i) * 8 .. + 7 of load i
@@ -402,7 +410,7 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
     if (threadIdx.x == 0) {
         float b = wv[0];
         int bi = wi[0];
-        for (int w = 1; w < 4; ++w)
+        for (int w = 1; w < kHeadWaves; ++w)
             if (wv[w] > b || (wv[w] == b && wi[w] < bi)) {
                 b = wv[w];
                 bi = wi[w];
@@ -418,7 +426,7 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
     // last workgroup: global argmax, next token, next embedding
     float b = -INFINITY;
     int bi = 0x7fffffff;
-    for (int j = threadIdx.x; j < (int)gridDim.x; j += 256) {
+    for (int j = threadIdx.x; j < (int)gridDim.x; j += 64 * kHeadWaves) {
         const float v = ld_agent(a.part_val + j);
         const int i = ld_agent(a.part_idx + j);
         if (v > b || (v == b && i < bi)) {
@@ -444,7 +452,7 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
     if (threadIdx.x == 0) {
         float bb = wv[0];
         int bbi = wi[0];
-        for (int w = 1; w < 4; ++w)
+        for (int w = 1; w < kHeadWaves; ++w)
             if (wv[w] > bb || (wv[w] == bb && wi[w] < bbi)) {
                 bb = wv[w];
                 bbi = wi[w];
@@ -465,7 +473,7 @@ __global__ void __launch_bounds__(256) lm_head_kernel(HeadArgs a)
     }
     __syncthreads();
     const int next = s_next;
-    for (int k = threadIdx.x; k < H; k += 256)
+    for (int k = threadIdx.x; k < H; k += 64 * kHeadWaves)
         a.h[k] = bf16_to_f32(a.embed[(int64_t)next * H + k]);
 }
 
@@ -507,7 +515,7 @@ int launch_lm_head(const HeadDesc &d, hipStream_t stream)
     HeadArgs a{d.h, d.norm_w, d.eps, d.W, d.logits, d.V, d.H, d.part_val, d.part_idx,
                d.counter, d.state, d.prompt, d.n_prompt, d.tokens, d.argmax_out, d.embed,
                d.max_pos};
-    hipLaunchKernelGGL(lm_head_kernel, dim3(d.grid), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(lm_head_kernel, dim3(d.grid), dim3(64 * kHeadWaves), 0, stream, a);
     EP_HIP_CHECK(hipGetLastError());
     return EP_OK;
 }
