@@ -330,7 +330,7 @@ constexpr int MODE_SWIGLU = 2;  // act[row] = silu(gate * rinv) * (up * rinv)
 // their blocks independently: each row's 16-lane sum goes to an LDS
 // accumulator (one slot per wave and row), and the cross-wave sums and
 // outputs are formed once, after the last block.
-template <int S, int RQ, bool PAIRED, int MAXQ, int NBUF_SET = 0>
+template <int S, int RQ, bool PAIRED, int MAXQ, int NBUF_SET = 0, bool SEG3 = false>
 struct Gemv {
     static constexpr int WPR = geo_wpr(S), RG = geo_rg(S), SPW = geo_spw(S);
     static constexpr int NQ = PAIRED ? 2 * RQ : RQ;  // loads (row quads) per lane per block
@@ -438,7 +438,11 @@ struct Gemv {
         const int j = bi / QB, qg = bi % QB;
         const bool live = qg < ngroups(sg) && slab_on(j, wv);
         const int lane = tid_fresh() & 63;
-        const uint32_t rq = (uint32_t)lane & 3;
+        // the lane's row (lane & 3) and 16-byte chunk (lane >> 2) within a
+        // quad's slab: the vector offset; the quad and slab offsets are
+        // wave-uniform (scalar offset)
+        const uint32_t woff = (uint32_t)(lane & 3) * RB + (uint32_t)(lane >> 2) * 16u;
+        const int sbyte = slab(j, wv) * kSlabBytes;
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
             const int vq = vquad(sg, qg, i, wv);
@@ -446,20 +450,33 @@ struct Gemv {
             const int s = seg_of(sg, ok ? vq : sg.qa, i);
             const int quad = ok ? vq - first_quad(sg, s) : 0;
             const auto rp = buffer_rsrc(sel3(s, sg.pk0, sg.pk1, sg.pk2), live ? 0x7fffffffu : 0u);
-            bk.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)(rq * RB + chunk_byte(j, wv)),
-                                                            quad * 4 * RB, kAuxStream);
+            bk.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)woff, quad * 4 * RB + sbyte, kAuxStream);
         }
         const bool sok = sl.i < NQ;
-        const int vq = vquad(sg, qg, sok ? sl.i : 0, wv);
-        const bool ok = sok && live && vq < sg.qb;
-        const int s = seg_of(sg, ok ? vq : sg.qa, sok ? sl.i : 0);
-        const int row = ok ? (vq - first_quad(sg, s)) * 4 + sl.r : 0;
-        const int gi = ok ? slab_group(j, wv, sl.lgroup) + sl.g : 0;
-        // one scale row may belong to another segment than the lane's
-        // neighbours' (q|k|v): a per-lane address, row 0 of the segment
-        // where the entry is not used
-        const char *sc = sel3(s, sg.sc0, sg.sc1, sg.sc2) + (int64_t)row * sg.ldsb + gi * 2;
-        bk.s = ldg((const uint16_t *)sc);
+        if constexpr (!SEG3) {
+            // one segment (or gate|up by quad slot): the lane's scale row is
+            // the wave's first quad of the group (uniform) plus its own
+            // quad slot and row; a quad past the share reads row 0
+            const int li = PAIRED ? (sl.i >= RQ ? sl.i - RQ : sl.i) : sl.i;
+            const int q0 = sg.qa + qg * QPB + (wv / WPR) * RQ;
+            const bool ok = sok && live && li < sg.qb - q0;
+            const uint32_t off = ok ? (uint32_t)((q0 * 4 + li * 4 + sl.r) * sg.ldsb +
+                                                 (slab_group(j, wv, sl.lgroup) + sl.g) * 2)
+                                    : 0u;
+            const char *base = PAIRED && sok && sl.i >= RQ ? sg.sc1 : sg.sc0;
+            bk.s = ldg((const uint16_t *)(base + off));
+        } else {
+            const int vq = vquad(sg, qg, sok ? sl.i : 0, wv);
+            const bool ok = sok && live && vq < sg.qb;
+            const int s = seg_of(sg, ok ? vq : sg.qa, sok ? sl.i : 0);
+            const int row = ok ? (vq - first_quad(sg, s)) * 4 + sl.r : 0;
+            const int gi = ok ? slab_group(j, wv, sl.lgroup) + sl.g : 0;
+            // one scale row may belong to another segment than the lane's
+            // neighbours' (q|k|v): a per-lane address, row 0 of the segment
+            // where the entry is not used
+            const char *sc = sel3(s, sg.sc0, sg.sc1, sg.sc2) + (int64_t)row * sg.ldsb + gi * 2;
+            bk.s = ldg((const uint16_t *)sc);
+        }
     }
 
     // Blocks 0 .. NBUF - 2 of a phase, issued ahead of its hand-over wait.
@@ -615,7 +632,7 @@ struct Gemv {
     // run, so the LDS never drains between blocks.  A block's set-up (the
     // loads of block bi + NBUF - 1 into the buffer block bi - 1 left, its
     // quads' table slots and scale shuffles) runs just before its first
-    // lookup.  Scheduling fences hold the order.  Blocks past the share or
+    // lookup address is formed.  Scheduling fences hold the order.  Blocks past the share or
     // on an idle slab are streamed too (their loads are zero-length) and
     // contribute nothing.
     static constexpr int kLookAhead = 12;  // lgkmcnt counts at most 15
@@ -643,19 +660,26 @@ struct Gemv {
                 sb[bi][i] = (uint32_t)__builtin_amdgcn_ds_bpermute((int)lc.sidx[i], (int)bb[bi % NBUF].s);
             }
         };
-        auto lookup = [&](int g) {
+        // a lookup's table address (one v_perm of the weight byte), formed
+        // one step ahead of its read so the read never waits on it
+        auto addr = [&](int g) {
             const int bi = g / NL, m = g % NL, i = m >> 4, k = m & 15;
-            return lds_read_u32(tab, __builtin_amdgcn_perm(bb[bi % NBUF].w[i][k >> 2], l4s[bi][i], kSelByte[k & 3]));
+            return __builtin_amdgcn_perm(bb[bi % NBUF].w[i][k >> 2], l4s[bi][i], kSelByte[k & 3]);
         };
+        constexpr int AHL = 2;  // addresses this many lookups ahead of the reads
+        uint32_t ad[T + AHL];
         float acc[QB][NQ];
         f16x2_t xa[16];  // the slab's activations (MFMA A operand: hi, lo or 0)
         float fx = 0.0f;
         uint32_t tv[T];
-        static_assert(kLookAhead <= NL, "the first window lies in block 0");
+        static_assert(kLookAhead + AHL <= NL, "the first window lies in block 0");
         start(0);
 #pragma unroll
+        for (int g = 0; g < kLookAhead + AHL; ++g)
+            ad[g] = addr(g);
+#pragma unroll
         for (int g = 0; g < kLookAhead; ++g)
-            tv[g] = lookup(g);
+            tv[g] = lds_read_u32(tab, ad[g]);
         f32x4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int bi = 0; bi < MAXB; ++bi) {
@@ -664,12 +688,17 @@ struct Gemv {
             for (int n = 0; n < NL / 2; ++n) {
                 const int g0 = kLookAhead + 2 * (bi * (NL / 2) + n);  // this step's two new lookups
                 const int nb = (bi + 1) * NL;                         // the next block's first lookup
-                if (bi + 1 < MAXB && g0 <= nb && nb < g0 + 2)
+                const int ga = g0 + AHL;  // this step's two new addresses
+                if (bi + 1 < MAXB && ga <= nb && nb < ga + 2)
                     start(bi + 1);
+#pragma unroll
+                for (int g = ga; g < ga + 2; ++g)
+                    if (g < T)
+                        ad[g] = addr(g);
 #pragma unroll
                 for (int g = g0; g < g0 + 2; ++g)
                     if (g < T)
-                        tv[g] = lookup(g);
+                        tv[g] = lds_read_u32(tab, ad[g]);
                 __builtin_amdgcn_sched_barrier(0);
                 if (n == 0) {
                     if (qg == 0 && slab_on(j, wv))
@@ -1404,7 +1433,7 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
     const PhaseLds lh = phase_lds(region, M::H), lo = phase_lds(region, M::HQD),
                    li = phase_lds(region, M::I);
 
-    using PQ = Gemv<M::SH, M::RQ_QKV, false, M::MQ_QKV, M::NB_QKV>;
+    using PQ = Gemv<M::SH, M::RQ_QKV, false, M::MQ_QKV, M::NB_QKV, true>;
     using PO = Gemv<M::SO, M::RQ_O, false, M::MQ_O, M::NB_O>;
     using PG = Gemv<M::SH, M::RQ_GU, true, M::MQ_GU, M::NB_GU>;
     using PD = Gemv<M::SI, M::RQ_D, false, M::MQ_D, M::NB_D>;
