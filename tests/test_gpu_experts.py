@@ -143,3 +143,37 @@ def test_gathered_experts_graph_replay_follows_ids():
         torch.cuda.synchronize()
         eager = PackedExperts(s)(x, ids)
         assert torch.equal(y, eager), r
+
+
+def test_gathered_experts_f32_scales_and_bf16_codebook():
+    """The gathered launch with float32 group scales and a bfloat16 codebook
+    (per-expert scale stride in 4-byte units)."""
+    E, n, k, T, group = 5, 256, 1024, 6, 128
+    rng = np.random.Generator(np.random.PCG64(21))
+    idx = rng.integers(0, 16, E * n * k).astype(np.uint8)
+    packed = ref.pack4(idx, 16)
+    cb = torch.tensor(np.sort(rng.standard_normal(16)), dtype=torch.bfloat16)
+    scale = (np.abs(rng.normal(0, 0.02, (E * n, k // group))) + 1e-3).astype(np.float32)
+    s = PackedWeight((E, n, k), packed, scale, cb, group, 16).to(DEV)
+    assert s.scale.dtype == torch.float32 and s.cb.dtype == torch.bfloat16
+    g = torch.Generator(device=DEV).manual_seed(4)
+    x = torch.randn(T, k, generator=g, device=DEV).to(torch.bfloat16)
+    ids = torch.tensor([4, 0, 3, 3, 1, 2], device=DEV)
+    y = PackedExperts(s)(x, ids)
+    want = want_rows(x.float().cpu().numpy(), ids.cpu().tolist(), packed, scale,
+                     cb.float().numpy(), E, n, k, group, 16)
+    err = np.abs(y.float().cpu().numpy() - want).max() / np.abs(want).max()
+    assert err < 2e-3 + 2.0 ** -8, err
+
+
+def test_gathered_experts_clamp_ids_without_check():
+    """With check_ids=False ids outside [0, E) are clamped on the device
+    (-3 -> expert 0, E + 2 -> expert E - 1): the rows equal those of the
+    clamped ids."""
+    E, n, k = 4, 128, 512
+    s, *_ = experts(E, n, k, 16, 128, seed=13)
+    g = torch.Generator(device=DEV).manual_seed(6)
+    x = torch.randn(3, k, generator=g, device=DEV).to(torch.float16)
+    y = PackedExperts(s, check_ids=False)(x, torch.tensor([-3, 1, E + 2], device=DEV))
+    want = PackedExperts(s)(x, torch.tensor([0, 1, E - 1], device=DEV))
+    assert torch.equal(y, want)
