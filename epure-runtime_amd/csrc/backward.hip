@@ -23,6 +23,10 @@
 //     levels; histograms are reduced in a fixed order per workgroup and
 //     across workgroups by a final kernel.  No float atomics race, so the
 //     result is deterministic.  `packed` is only read.
+#include <array>
+#include <mutex>
+#include <vector>
+
 #include "ep_common.h"
 #include "ep_internal.h"
 
@@ -719,10 +723,10 @@ static bool blas_route(int64_t M, int64_t N, int64_t K)
 static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 
 // Library-route workspace: rexp [M] | gc partials [N / kEpiRows][16] | gy16
-// [M][N] | W16 [N][K] | f32 [max(M, N)][K] (grad_x's GEMM result, then G) |
-// hipBLASLt workspace.
+// [M][N] | W16 [N][K] | f32 [M][K] (grad_x's GEMM result) | f32 [N][K] (G) |
+// two hipBLASLt workspaces (the two chains may run at once).
 struct BlasWs {
-    size_t rexp, gc, gy16, w16, f32buf, blas, total;
+    size_t rexp, gc, gy16, w16, f32buf, gbuf, blas, blas2, total;
 };
 static BlasWs blas_ws(int64_t M, int64_t N, int64_t K)
 {
@@ -737,11 +741,68 @@ static BlasWs blas_ws(int64_t M, int64_t N, int64_t K)
     w.w16 = o;
     o += al256((size_t)N * K * 2);
     w.f32buf = o;
-    o += al256((size_t)(M > N ? M : N) * K * 4);
+    o += al256((size_t)M * K * 4);
+    w.gbuf = o;
+    o += al256((size_t)N * K * 4);
     w.blas = o;
+    o += blas_workspace_bytes();
+    w.blas2 = o;
     o += blas_workspace_bytes();
     w.total = o;
     return w;
+}
+
+// The library route's two chains -- grad_x (gy prescale, materialize, GEMM,
+// finish) and the scale/codebook gradients (GEMM G, epilogue, final sum) --
+// are independent: the second runs on a side stream forked from and joined
+// back into the caller's stream with events (both work under stream
+// capture), so the memory-bound kernels of one overlap the other's GEMM.
+// Per device: the side stream (default priority) and the two events,
+// created on the first call outside capture.  A shape's first call runs both chains
+// in order on the caller's stream (its library GEMM plans time their
+// candidate algorithms then, undisturbed).
+struct SideStream {
+    hipStream_t s = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
+};
+static std::mutex g_side_mu;
+static SideStream g_side[64];
+static std::vector<std::array<int64_t, 4>> g_bwd_seen;  // (device, M, N, K) run once
+
+// The side stream to fork to, or nullptr (run in order).
+static SideStream *side_for(hipStream_t stream, int64_t M, int64_t N, int64_t K)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+        return nullptr;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess)
+        return nullptr;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lk(g_side_mu);
+    SideStream &sd = g_side[dev];
+    if (!sd.s && !capturing) {
+        if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess) {
+            sd.s = nullptr;
+            (void)hipGetLastError();
+        } else if (hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
+                   hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) {
+            sd.join = nullptr;
+            (void)hipGetLastError();
+        }
+    }
+    const std::array<int64_t, 4> key{dev, M, N, K};
+    bool seen = false;
+    for (const auto &k : g_bwd_seen)
+        seen = seen || k == key;
+    if (!seen) {
+        if (!capturing)
+            g_bwd_seen.push_back(key);
+        return nullptr;
+    }
+    if (!sd.s)
+        return nullptr;
+    return sd.join ? &sd : nullptr;
 }
 
 size_t backward_workspace(int64_t M, int64_t N, int64_t K, int levels, int group)
@@ -808,52 +869,67 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         f16_t *gy16 = (f16_t *)(base + L.gy16);
         f16_t *w16 = (f16_t *)(base + L.w16);
         float *buf = (float *)(base + L.f32buf);
-        void *bws = base + L.blas;
-        if (gx.ptr) {
-            hipLaunchKernelGGL(gy_prep_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream,
-                               (const uint16_t *)gy.ptr, gy.ld, (int)M, (int)w.N, rexp, gy16);
-            EP_HIP_CHECK(hipGetLastError());
-            int rc = launch_dequant_tile(w, w16, EP_F16, w.K, stream);  // materialize(float16)
-            if (rc != EP_OK)
-                return rc;
-            // column-major: D (K x M) = W16 (K x N) . gy16 (N x M)
-            rc = blas_gemm_f32out(0, 0, w.K, M, w.N, EP_F16, w16, w.K, gy16, w.N, buf, w.K, 1.0f, bws,
-                                  blas_workspace_bytes(), stream);
-            if (rc != EP_OK)
-                return rc;
-            hipLaunchKernelGGL(dx_finish_kernel, dim3((unsigned)((w.K + 1023) / 1024), (unsigned)(M < 65535 ? M : 65535)), dim3(256),
-                               0, stream, buf, rexp, (int)M, (int)w.K, gx.ptr, gx.dtype, gx.ld);
-            EP_HIP_CHECK(hipGetLastError());
+        float *gbuf = (float *)(base + L.gbuf);
+        const bool want_g = grad_cb || grad_scale;
+        if (want_g && !grad_scale)
+            return set_error(EP_ERR_ARG, "grad_cb without grad_scale is not served");
+        SideStream *side = gx.ptr && want_g ? side_for(stream, M, w.N, w.K) : nullptr;
+        const hipStream_t gs = side ? side->s : stream;  // the G chain's stream
+        if (side) {
+            EP_HIP_CHECK(hipEventRecord(side->fork, stream));
+            EP_HIP_CHECK(hipStreamWaitEvent(side->s, side->fork, 0));
         }
-        if (grad_cb || grad_scale) {
-            if (!grad_scale)
-                return set_error(EP_ERR_ARG, "grad_cb without grad_scale is not served");
-            // column-major: G^T (K x N) = x (K x M) . gy^T (M x N): G row-major [N][K]
-            int rc = blas_gemm_f32out(0, 1, w.K, w.N, M, EP_BF16, x.ptr, x.ld, gy.ptr, gy.ld, buf, w.K, 1.0f,
-                                      bws, blas_workspace_bytes(), stream);
-            if (rc != EP_OK)
-                return rc;
-            const int nwg = (int)((w.N + kEpiRows - 1) / kEpiRows);
-            if (w.group == 32)
-                hipLaunchKernelGGL(gw_epilogue_kernel<8>, dim3((unsigned)nwg), dim3(256), 0, stream, buf,
-                                   w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
-                                   (int)w.N, (int)w.K, grad_scale, ld_gscale, gcp);
-            else if (w.group == 64)
-                hipLaunchKernelGGL(gw_epilogue_kernel<16>, dim3((unsigned)nwg), dim3(256), 0, stream, buf,
-                                   w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
-                                   (int)w.N, (int)w.K, grad_scale, ld_gscale, gcp);
-            else
-                hipLaunchKernelGGL(gw_epilogue_kernel<32>, dim3((unsigned)nwg), dim3(256), 0, stream, buf,
-                                   w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
-                                   (int)w.N, (int)w.K, grad_scale, ld_gscale, gcp);
-            EP_HIP_CHECK(hipGetLastError());
-            if (grad_cb) {
-                hipLaunchKernelGGL(gc_final_kernel, dim3(1), dim3(256), 0, stream, gcp, nwg, w.levels,
-                                   grad_cb);
+        // both chains; the side stream is joined back whatever they return
+        auto chains = [&]() -> int {
+            if (want_g) {
+                // column-major: G^T (K x N) = x (K x M) . gy^T (M x N): G row-major [N][K]
+                int rc = blas_gemm_f32out(0, 1, w.K, w.N, M, EP_BF16, x.ptr, x.ld, gy.ptr, gy.ld, gbuf, w.K, 1.0f,
+                                          base + L.blas2, blas_workspace_bytes(), gs);
+                if (rc != EP_OK)
+                    return rc;
+                const int nwg = (int)((w.N + kEpiRows - 1) / kEpiRows);
+                if (w.group == 32)
+                    hipLaunchKernelGGL(gw_epilogue_kernel<8>, dim3((unsigned)nwg), dim3(256), 0, gs, gbuf,
+                                       w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
+                                       (int)w.N, (int)w.K, grad_scale, ld_gscale, gcp);
+                else if (w.group == 64)
+                    hipLaunchKernelGGL(gw_epilogue_kernel<16>, dim3((unsigned)nwg), dim3(256), 0, gs, gbuf,
+                                       w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
+                                       (int)w.N, (int)w.K, grad_scale, ld_gscale, gcp);
+                else
+                    hipLaunchKernelGGL(gw_epilogue_kernel<32>, dim3((unsigned)nwg), dim3(256), 0, gs, gbuf,
+                                       w.packed, w.scale, w.scale_dtype, w.ld_scale, w.cb, w.cb_dtype, w.levels,
+                                       (int)w.N, (int)w.K, grad_scale, ld_gscale, gcp);
+                EP_HIP_CHECK(hipGetLastError());
+                if (grad_cb) {
+                    hipLaunchKernelGGL(gc_final_kernel, dim3(1), dim3(256), 0, gs, gcp, nwg, w.levels, grad_cb);
+                    EP_HIP_CHECK(hipGetLastError());
+                }
+            }
+            if (gx.ptr) {
+                hipLaunchKernelGGL(gy_prep_kernel, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, stream,
+                                   (const uint16_t *)gy.ptr, gy.ld, (int)M, (int)w.N, rexp, gy16);
+                EP_HIP_CHECK(hipGetLastError());
+                int rc = launch_dequant_tile(w, w16, EP_F16, w.K, stream);  // materialize(float16)
+                if (rc != EP_OK)
+                    return rc;
+                // column-major: D (K x M) = W16 (K x N) . gy16 (N x M)
+                rc = blas_gemm_f32out(0, 0, w.K, M, w.N, EP_F16, w16, w.K, gy16, w.N, buf, w.K, 1.0f, base + L.blas,
+                                      blas_workspace_bytes(), stream);
+                if (rc != EP_OK)
+                    return rc;
+                hipLaunchKernelGGL(dx_finish_kernel, dim3((unsigned)((w.K + 1023) / 1024), (unsigned)(M < 65535 ? M : 65535)), dim3(256),
+                                   0, stream, buf, rexp, (int)M, (int)w.K, gx.ptr, gx.dtype, gx.ld);
                 EP_HIP_CHECK(hipGetLastError());
             }
+            return EP_OK;
+        };
+        const int rc = chains();
+        if (side) {
+            EP_HIP_CHECK(hipEventRecord(side->join, side->s));
+            EP_HIP_CHECK(hipStreamWaitEvent(stream, side->join, 0));
         }
-        return EP_OK;
+        return rc;
     }
     BwdArgs a{};
     a.gy = gy.ptr;

@@ -180,3 +180,34 @@ def test_fp32_activations_take_the_exact_route():
     w = dense_tile(s.packed, s.scale, s.cb, 384, 1024, 128, 16).double()
     want = x.double() @ w.t()
     assert rel(y, want) < 1e-5
+
+
+def test_backward_library_route_graph_replays():
+    """The library route's two chains (grad_x on the caller's stream, the
+    scale/codebook gradients on a forked side stream joined back) captured
+    in a HIP graph: every replay, with x and gy rewritten in place between
+    them, equals the eager call bit for bit."""
+    n, k, m = 256, 384, 512
+    _, _, _, _, s = make(n, k, 128, seed=5)
+    h = cuda._hot(s)
+    x, gy = bf16((m, k), 21), bf16((m, n), 22, 1e-2)
+    for _ in range(2):                       # first call in order, then forked
+        run_bwd(s, gy, x)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        cuda.backward(gy, x, h, gx_dtype=torch.float32)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = cuda.backward(gy, x, h, gx_dtype=torch.float32)
+    assert out is not None
+    for r in range(3):
+        x.copy_(bf16((m, k), 30 + r))
+        gy.copy_(bf16((m, n), 40 + r, 1e-2))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = run_bwd(s, gy, x)
+        assert all(torch.equal(p, q) for p, q in zip(out, eager)), r
