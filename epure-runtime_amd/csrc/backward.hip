@@ -764,6 +764,7 @@ static BlasWs blas_ws(int64_t M, int64_t N, int64_t K)
 struct SideStream {
     hipStream_t s = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
+    std::mutex mu;  // an event's record and the wait on it stay one step (concurrent callers)
 };
 static std::mutex g_side_mu;
 static SideStream g_side[64];
@@ -876,6 +877,7 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         SideStream *side = gx.ptr && want_g ? side_for(stream, M, w.N, w.K) : nullptr;
         const hipStream_t gs = side ? side->s : stream;  // the G chain's stream
         if (side) {
+            std::lock_guard<std::mutex> lk(side->mu);
             EP_HIP_CHECK(hipEventRecord(side->fork, stream));
             EP_HIP_CHECK(hipStreamWaitEvent(side->s, side->fork, 0));
         }
@@ -926,6 +928,7 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         };
         const int rc = chains();
         if (side) {
+            std::lock_guard<std::mutex> lk(side->mu);
             EP_HIP_CHECK(hipEventRecord(side->join, side->s));
             EP_HIP_CHECK(hipStreamWaitEvent(stream, side->join, 0));
         }
