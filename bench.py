@@ -2,7 +2,7 @@
 4-bit codebook model (the reference's headline decode configuration) on one
 MI355X, plus the dequant-GEMV HBM bandwidth as a fraction of peak.
 
-    python bench.py [--steps K] [--warmup W] [--config llama3-8b|qwen3-1.7b]
+    python bench.py [--steps K] [--warmup W] [--config llama3-8b|qwen3-1.7b|qwen3-8b|llama3.2-3b|qwen3-4b]
 
 One "step" is one decode token: a replay of the captured HIP graph of the
 whole decode step -- the one-launch decode-step kernel (all 32 layers: fused
@@ -57,7 +57,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="llama3-8b",
-                    choices=["llama3-8b", "qwen3-1.7b", "qwen3-8b", "llama3.2-3b"])
+                    choices=["llama3-8b", "qwen3-1.7b", "qwen3-8b", "llama3.2-3b", "qwen3-4b"])
     ap.add_argument("--prompt", type=int, default=None)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")

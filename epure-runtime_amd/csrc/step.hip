@@ -121,7 +121,7 @@ struct Model {
     static_assert(H % 512 == 0 && HQD % 512 == 0 && I % 512 == 0, "rows of whole slabs");
 };
 
-// Llama-3-8B, Qwen3-1.7B, Qwen3-8B and Llama-3.2-3B shapes; shares at 256
+// Llama-3-8B, Qwen3-1.7B, Qwen3-8B and Llama-3.2-3B shapes (Qwen3-4B below); shares at 256
 // workgroups: q|k|v 6 / 4 / 6 / 5 quads, o 8 / 4 / 8 / 6 (on at least half
 // the grid), gate|up 14 / 6 / 12 / 8, down 4 / 2 / 4 / 3.
 // Llama-3-8B: q|k|v and o whole shares in flight, gate|up 5 of 7 blocks
@@ -130,6 +130,9 @@ using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 8, 14, 4, -1, -1, 6,
 using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 4, 6, 2>;
 using ModelQ8B = Model<4096, 4096, 12288, 4, 3, 2, 2, 4, 6, 8, 12, 4, -1, -1, 6, 4, 5>;
 using ModelL3B = Model<3072, 3072, 8192, 3, 2, 2, 2, 3, 5, 6, 8, 3>;
+// Qwen3-4B: hidden 2560 but 32 x 128 query columns; shares q|k|v 6, o 5,
+// gate|up 10 (9.5), down 3 (2.5) quads
+using ModelQ4B = Model<2560, 4096, 9728, 4, 3, 3, 2, 3, 6, 5, 10, 3>;
 
 // Where a phase of contraction length K keeps its activations, factors and
 // accumulator inside the region.
@@ -1744,6 +1747,8 @@ static int variant_of(const StepDesc &d)
         return 3;
     if (is(ModelL3B::H, ModelL3B::HQD, ModelL3B::I, ModelL3B::GQ))
         return 4;
+    if (is(ModelQ4B::H, ModelQ4B::HQD, ModelQ4B::I, ModelQ4B::GQ))
+        return 5;
     set_error(EP_DECLINE_SHAPE,
               "decode step: no persistent variant for hidden %d, heads %d/%d, intermediate %d",
               d.H, d.Hq, d.Hkv, d.I);
@@ -1824,8 +1829,10 @@ int launch_decode_step(const StepDesc &d, hipStream_t stream)
         return launch_model<ModelQ17>(a, stream);
     case 3:
         return launch_model<ModelQ8B>(a, stream);
-    default:
+    case 4:
         return launch_model<ModelL3B>(a, stream);
+    default:
+        return launch_model<ModelQ4B>(a, stream);
     }
 }
 

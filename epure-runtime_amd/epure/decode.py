@@ -68,8 +68,9 @@ class DecoderConfig:
 
 # Decoder shapes the one-launch step serves: the two BASELINE configurations
 # (Llama-3-8B, Qwen3-1.7B), Qwen3-8B (the shape of the reference's own
-# headline model, CHANGELOG.md:54-56: 36 layers, intermediate 12288) and
-# Llama-3.2-3B.  Other shapes run the per-layer launches.
+# headline model, CHANGELOG.md:54-56: 36 layers, intermediate 12288),
+# Llama-3.2-3B and Qwen3-4B (query width 4096 over hidden 2560).  Other
+# shapes run the per-layer launches.
 LLAMA3_8B = DecoderConfig(4096, 14336, 32, 32, 8, 128, 128256, 5e5, 1e-5, name="llama3-8b")
 QWEN3_1_7B = DecoderConfig(2048, 6144, 28, 16, 8, 128, 151936, 1e6, 1e-6, qk_norm=True,
                            tie_embeddings=True, name="qwen3-1.7b")
@@ -77,7 +78,9 @@ QWEN3_8B = DecoderConfig(4096, 12288, 36, 32, 8, 128, 151936, 1e6, 1e-6, qk_norm
                          name="qwen3-8b")
 LLAMA32_3B = DecoderConfig(3072, 8192, 28, 24, 8, 128, 128256, 5e5, 1e-5, tie_embeddings=True,
                            name="llama3.2-3b")
-CONFIGS = {c.name: c for c in (LLAMA3_8B, QWEN3_1_7B, QWEN3_8B, LLAMA32_3B)}
+QWEN3_4B = DecoderConfig(2560, 9728, 36, 32, 8, 128, 151936, 1e6, 1e-6, qk_norm=True,
+                         tie_embeddings=True, name="qwen3-4b")
+CONFIGS = {c.name: c for c in (LLAMA3_8B, QWEN3_1_7B, QWEN3_8B, LLAMA32_3B, QWEN3_4B)}
 
 
 def rope_tables(cfg, max_pos, device):

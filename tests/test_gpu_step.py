@@ -22,7 +22,7 @@ import numpy as np
 import pytest
 import torch
 
-from epure.decode import LLAMA3_8B, LLAMA32_3B, QWEN3_1_7B, QWEN3_8B, Decoder, random_weights
+from epure.decode import LLAMA3_8B, LLAMA32_3B, QWEN3_1_7B, QWEN3_4B, QWEN3_8B, Decoder, random_weights
 from oracle.decoder import RefDecoder
 
 pytestmark = pytest.mark.gpu
@@ -131,9 +131,10 @@ def test_persistent_eager_equals_graph(weights):
     assert not d.step_failed()
 
 
-@pytest.mark.parametrize("base", [QWEN3_8B, LLAMA32_3B], ids=["qwen3-8b", "llama3.2-3b"])
+@pytest.mark.parametrize("base", [QWEN3_8B, LLAMA32_3B, QWEN3_4B],
+                         ids=["qwen3-8b", "llama3.2-3b", "qwen3-4b"])
 def test_more_shapes_one_launch_against_oracle(base):
-    """The one-launch step at the Qwen3-8B and Llama-3.2-3B shapes (full
+    """The one-launch step at the Qwen3-8B, Llama-3.2-3B and Qwen3-4B shapes (full
     width, 3 layers: the layer count is a launch argument), teacher-forced
     over 140 random positions (three 64-position chunks) against the float32
     oracle, and 24 greedy tokens identical to the oracle's."""
