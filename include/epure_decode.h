@@ -102,7 +102,7 @@ int ep_lm_head_argmax(float *h, const uint16_t *norm_w, float eps, const uint16_
  * word 2 becomes nonzero if a hand-over wait timed out (the step's results
  * are then garbage).  `trace`, when not NULL, receives wall-clock stamps
  * [n_layers][24][grid] (debug).  Declines (> 0) shapes without a
- * persistent variant (ep_decode_step_serves: the Llama-3-8B, Qwen3-8B,
+ * persistent variant (ep_decode_step_serves: the Llama-3-8B, Qwen3-8B, Qwen3-4B,
  * Llama-3.2-3B and Qwen3-1.7B shapes, D = 128, groups a power of two >= 128,
  * fp16 scales, 4-bit indices).  Position = state[0].  Launches that share a workspace must be
  * stream-ordered (two in flight on one workspace race).
