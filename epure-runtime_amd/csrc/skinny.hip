@@ -10,10 +10,11 @@
 // At these M the contraction is HBM-bound: the packed bytes must stream at
 // full rate while the MFMA units and LDS are mostly idle.  So:
 //  * a workgroup (8 waves) owns one K split of KS values and up to TPW row
-//    tiles of 128 rows (16 per wave); every one of its weight loads (16
-//    bytes per lane, LD per tile, 16 in all) is issued at kernel entry, before the
+//    tiles of 128 rows (16 per wave); half of its weight loads (16 bytes
+//    per lane, LD per tile, 16 in all) go out at kernel entry, before the
 //    activation staging and the table build, so HBM streams from the first
-//    cycle;
+//    cycle, the other half right after the table build (all at once, they
+//    would hold the waves at the issue until most had landed);
 //  * weights are dequantized in registers straight into the B operand of
 //    v_mfma_f32_16x16x32_f16: lane (j = lane & 15, q = lane >> 4) loads 16
 //    bytes of row j -- 32 (4-bit) or 16 (8-bit) consecutive weights -- looks
@@ -134,25 +135,37 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
         const uint32_t off = ok ? (uint32_t)(((int64_t)xr * a.ldx + k) * XE) : kOut;
         xv[p] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
     }
+    // The weights in two halves: the first half goes out now, the second
+    // after the activation staging and the table build.  A workgroup's
+    // weights (up to 128 KB) are more than a CU keeps in flight, so issuing
+    // them all would hold the waves at the issue until most had landed and
+    // only then start the staging; this way the staging and the table build
+    // overlap the stream.
+    constexpr int LH = LD / 2;
     u32x4_t w[TPW][LD];
     uint32_t sraw[TPW][LD];  // fp16 scale bits; 0 where the chunk is masked
+    auto issue = [&](int l0, int l1) {
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-        const int tile = (int)blockIdx.x + t * a.gtiles;
-        const int n = tile * kSkRows + wave * 16 + j;
-        const bool live = tile < a.tiles && n < a.N;
+        for (int t = 0; t < TPW; ++t) {
+            const int tile = (int)blockIdx.x + t * a.gtiles;
+            const int n = tile * kSkRows + wave * 16 + j;
+            const bool live = tile < a.tiles && n < a.N;
 #pragma unroll
-        for (int l = 0; l < LD; ++l) {
-            const int kc = ka + KPL * (4 * l + q);  // first k of the lane's chunk
-            const bool ok = live && kc < a.K;
-            const uint32_t off = (uint32_t)n * a.row_bytes + kbyte + (uint32_t)(16 * (4 * l + q));
-            w[t][l] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (int)off : (int)kOut, 0, 2);
-            const uint32_t soff = (uint32_t)(((int64_t)n * a.lds + kc / a.group) * 2);
-            sraw[t][l] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (int)soff : (int)kOut, 0, 0);
+            for (int l = 0; l < LD; ++l) {
+                if (l < l0 || l >= l1)
+                    continue;
+                const int kc = ka + KPL * (4 * l + q);  // first k of the lane's chunk
+                const bool ok = live && kc < a.K;
+                const uint32_t off = (uint32_t)n * a.row_bytes + kbyte + (uint32_t)(16 * (4 * l + q));
+                w[t][l] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (int)off : (int)kOut, 0, 2);
+                const uint32_t soff = (uint32_t)(((int64_t)n * a.lds + kc / a.group) * 2);
+                sraw[t][l] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (int)soff : (int)kOut, 0, 0);
+            }
         }
-    }
+    };
+    issue(0, LH);
     // keep every load above ahead of the staging below (which waits for the
-    // activations, i.e. for every load issued before it)
+    // activations, i.e. for every load issued before them)
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- codebook -> fp16 bits; activations of the split -> LDS as fp16
@@ -208,6 +221,8 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
     }
     lds_barrier();
     build_table<BITS>(tab, s_cb);
+    issue(LH, LD);
+    __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
 
     const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
