@@ -265,6 +265,7 @@ def prefill_sweep(seed=0, replays=10):
     from epure.decode import _gen, random_packed_linear
     dev = torch.device("cuda:0")
     gen = _gen(seed, dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
     rows = []
     for n, k in [(4096, 4096), (14336, 4096), (4096, 14336)]:
         wb = _weight_bytes(n, k, 256)
@@ -284,6 +285,7 @@ def prefill_sweep(seed=0, replays=10):
                          "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
                          "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
                          "kernel": ("gemv_lut_kernel" if m == 1 else
+                                    "sk1_kernel" if m <= 16 and 12 * cus <= n <= 64 * cus else
                                     "sk_kernel + sk_reduce_kernel" if m <= 64 else
                                     "pf_prep_kernel + pf_kernel (+ sk_reduce_kernel when K is split)")})
             del lins, x

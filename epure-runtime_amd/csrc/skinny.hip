@@ -29,7 +29,11 @@
 //    exactly before they leave the workgroup;
 //  * with one split the results go straight to y; otherwise each split
 //    writes f32 partials [S][M][N] and sk_reduce_kernel sums them in split
-//    order (deterministic; no atomics, no counters).
+//    order (deterministic; no atomics, no counters);
+//  * at M <= 16 with 8-bit indices, 16-bit activations and enough 16-row
+//    tiles to fill the CUs, sk1_kernel instead: one workgroup per row tile
+//    over the whole of K, one launch, no partials (its comment has the
+//    layout).
 #include "ep_common.h"
 #include "ep_internal.h"
 #include "gemv_core.h"
@@ -63,6 +67,39 @@ constexpr int sk_ks()
 }
 
 constexpr uint32_t kOut = 0x7ffffff0u;  // a buffer offset past every buffer's end
+
+// The B operand of one lane's 16-byte chunk: its KPL weights dequantized
+// through the pair table and multiplied by the chunk's fp16 group scale (the
+// tile of materialize(float16), runtime.py:78-89), as KPL / 8 pieces of
+// eight (piece s = weights 8 s .. 8 s + 7 of the chunk).
+template <int BITS>
+EP_DEV void dequant_chunk(const uint32_t *tab, u32x4_t w, uint32_t sraw, uint32_t lane4, f16x8_t *bv)
+{
+    constexpr int KPL = sk_kpl<BITS>();
+    const f16_t s16 = f16_from_bits((uint16_t)sraw);
+    const f16x2_t s2 = (f16x2_t){s16, s16};
+    f16x2_t pr[KPL / 2];
+    if constexpr (BITS == 4) {
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                pr[wd * 4 + b] = as_f16x2(lds_read_u32(tab, __builtin_amdgcn_perm(w[wd], lane4, kSelByte[b]))) * s2;
+    } else {
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd)
+#pragma unroll
+            for (int b = 0; b < 4; b += 2) {
+                const uint32_t t0 = lds_read_u32(tab, __builtin_amdgcn_perm(w[wd], lane4, kSelByte[b]));
+                const uint32_t t1 = lds_read_u32(tab, __builtin_amdgcn_perm(w[wd], lane4, kSelByte[b + 1]));
+                pr[wd * 2 + b / 2] = as_f16x2(__builtin_amdgcn_perm(t1, t0, 0x05040100u)) * s2;
+            }
+    }
+#pragma unroll
+    for (int s = 0; s < KPL / 8; ++s)
+        bv[s] = (f16x8_t){pr[4 * s][0],     pr[4 * s][1],     pr[4 * s + 1][0], pr[4 * s + 1][1],
+                          pr[4 * s + 2][0], pr[4 * s + 2][1], pr[4 * s + 3][0], pr[4 * s + 3][1]};
+}
 
 struct SkArgs {
     uint32_t xbytes, wbytes, sbytes, cbbytes;  // extents of x, packed, scale, cb
@@ -237,36 +274,15 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
             acc[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int l = 0; l < LD; ++l) {
-            const f16_t s16 = f16_from_bits((uint16_t)sraw[t][l]);
-            const f16x2_t s2 = (f16x2_t){s16, s16};
-            f16x2_t pr[KPL / 2];
-            if constexpr (BITS == 4) {
-#pragma unroll
-                for (int wd = 0; wd < 4; ++wd)
-#pragma unroll
-                    for (int b = 0; b < 4; ++b)
-                        pr[wd * 4 + b] =
-                            as_f16x2(lds_read_u32(tab, __builtin_amdgcn_perm(w[t][l][wd], lane4, kSelByte[b]))) * s2;
-            } else {
-#pragma unroll
-                for (int wd = 0; wd < 4; ++wd)
-#pragma unroll
-                    for (int b = 0; b < 4; b += 2) {
-                        const uint32_t t0 = lds_read_u32(tab, __builtin_amdgcn_perm(w[t][l][wd], lane4, kSelByte[b]));
-                        const uint32_t t1 =
-                            lds_read_u32(tab, __builtin_amdgcn_perm(w[t][l][wd], lane4, kSelByte[b + 1]));
-                        pr[wd * 2 + b / 2] = as_f16x2(__builtin_amdgcn_perm(t1, t0, 0x05040100u)) * s2;
-                    }
-            }
+            f16x8_t bv[SUB];
+            dequant_chunk<BITS>(tab, w[t][l], sraw[t][l], lane4, bv);
 #pragma unroll
             for (int s = 0; s < SUB; ++s) {
-                const f16x8_t bv = {pr[4 * s][0], pr[4 * s][1], pr[4 * s + 1][0], pr[4 * s + 1][1],
-                                    pr[4 * s + 2][0], pr[4 * s + 2][1], pr[4 * s + 3][0], pr[4 * s + 3][1]};
                 const int kx = KPL * (4 * l + q) + 8 * s;
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt) {
                     const f16x8_t av = *(const f16x8_t *)(xs + (16 * mt + j) * XLD + kx);
-                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[mt], 0, 0, 0);
+                    acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[s], acc[mt], 0, 0, 0);
                 }
             }
         }
@@ -295,6 +311,258 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
                         }
                     }
                 }
+        }
+    }
+}
+
+// One launch for M <= 16 with fp16/bf16 activations and 8-bit indices.  A
+// workgroup owns T row tiles of 16 rows (tiles blockIdx.x + t * gridDim.x)
+// over the whole of K, so its sums are final: no partials, no second
+// launch.  Its 16 waves (four per SIMD, to hide the latency of the table
+// lookups) split K into contiguous runs of rounds; a round is RK = 4 KPL P
+// values of K.  In a round, lane (j, q) loads P 16-byte pieces of row j
+// (piece c at chunk 4 c + q of the round: each load instruction covers 64
+// bytes of 16 rows, the P of a round, issued back to back, 64 P contiguous
+// bytes of each) for each of the T tiles -- the B operand, dequantized
+// through the table -- and the KPL activations of row j at each piece's k
+// -- the A operand, straight from global memory: x is small and stays in
+// L2, and one load serves the T tiles.  fp16 activations are the operand
+// as they are; bf16 ones become fp16 after the power-of-two rescale of the
+// row's largest |x| in the piece (bf16_operand), and each piece's MFMA sums
+// are scaled back exactly before they join the running f32 sums.  Loads
+// run D rounds ahead of the MFMAs.  At the end the waves' sums meet in LDS
+// (over the table, which is no longer needed) and are added in wave order.
+constexpr int kSk1Threads = 1024;
+constexpr int kSk1Waves = kSk1Threads / 64;
+
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
+
+EP_DEV uint32_t max_over_row_lanes(uint32_t v)  // max over lanes l, l ^ 16, l ^ 32, l ^ 48
+{
+    const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max(a[0], a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max(b[0], b[1]);
+}
+
+// bf16 activations -> the fp16 A operand times 2^-e, e the row's exponent
+// over its four lanes' pieces (returned; the same in the four lanes).  On
+// the bit patterns, two values per instruction: |x| as a 15-bit integer
+// orders like |x|; e = (largest exponent field of the row) - 140 puts the
+// row's largest |x| * 2^-e in [2^13, 2^14); the exponent field drops by
+// 112 + e and the 7-bit mantissa moves up 3 bits, exactly (values below
+// 2^-14 after the rescale, 2^-27 of the row's largest, flush to 0).  With
+// inf, NaN or |x| >= 2^124 anywhere in the wave, in floats instead, where
+// fp16 overflows to inf as it would unscaled.
+template <int SUB>
+EP_DEV int bf16_operand(const u32x4_t *xv, f16x8_t *av)
+{
+    u16x2_t mx = {0, 0};
+#pragma unroll
+    for (int p = 0; p < SUB; ++p)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, xv[p][t] & 0x7fff7fffu));
+    const uint32_t em = max_over_row_lanes(max((uint32_t)mx[0], (uint32_t)mx[1]));
+    int e = em == 0 ? 0 : (int)(em >> 7) - 140;
+    e = e < -110 ? -110 : e;
+    if (__builtin_amdgcn_ballot_w64(e > 110) == 0) {
+        const uint16_t sub = (uint16_t)((112 + e) << 7);
+        const u16x2_t sub2 = {sub, sub};
+#pragma unroll
+        for (int p = 0; p < SUB; ++p) {
+            u32x4_t h;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t u = xv[p][t];
+                u16x2_t m = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2_t, u & 0x7fff7fffu), sub2);
+                m = m << (u16x2_t){3, 3};
+                h[t] = __builtin_bit_cast(uint32_t, m) | (u & 0x80008000u);
+            }
+            av[p] = __builtin_bit_cast(f16x8_t, h);
+        }
+        return e;
+    }
+    e = row_exponent(__uint_as_float(em << 16));  // em: the row's largest |x| as bf16 bits
+    const float pw = ldexpf(1.0f, -e);
+#pragma unroll
+    for (int p = 0; p < SUB; ++p)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            float lo, hi;
+            unpack_pair<EP_BF16>(xv[p][t], lo, hi);
+            av[p][2 * t] = (f16_t)(lo * pw);
+            av[p][2 * t + 1] = (f16_t)(hi * pw);
+        }
+    return e;
+}
+
+template <int BITS, int XDT, int T, int D, int P>
+__global__ void __launch_bounds__(kSk1Threads) sk1_kernel(SkArgs a)
+{
+    constexpr int KPL = sk_kpl<BITS>();
+    constexpr int RK = 4 * KPL * P;  // P pieces of 16 bytes per lane and tile: 64 P bytes of a row
+    constexpr int SUB = KPL / 8;     // MFMA sub-steps per piece = 16-byte x loads per lane and piece
+    static_assert(T * kSk1Waves * 256 <= kTabDwords, "wave sums fit over the table");
+    static_assert(XDT != EP_F32, "16-bit activations");
+
+    __shared__ __align__(16) uint32_t tab[kTabDwords];
+    __shared__ uint32_t s_cbraw[kSk1Threads];
+    __shared__ uint16_t s_cb[256];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, q = lane >> 4;
+    const int nr = (a.K + RK - 1) / RK;
+    const int rb = wave * nr / kSk1Waves, re = (wave + 1) * nr / kSk1Waves;
+    const auto rx = buffer_rsrc(a.x, a.xbytes), rw = buffer_rsrc(a.packed, a.wbytes);
+    const auto rs = buffer_rsrc(a.scale, a.sbytes), rcb = buffer_rsrc(a.cb, a.cbbytes);
+
+    const uint32_t cbraw = __builtin_amdgcn_raw_buffer_load_b32(rcb, tid < 256 ? tid * 4 : kOut, 0, 0);
+    // Loads of round r into slot d (masked lanes read 0 from past the
+    // buffer's end; rounds past the wave's run are all masked, so every
+    // slot sees the same number of loads).
+    // Piece c of a round is chunk 4 c + q: a load instruction covers 64
+    // bytes of each of 16 rows, and the P instructions of a round, issued
+    // back to back, 64 P contiguous bytes of each.
+    u32x4_t xv[D][P][SUB];
+    u32x4_t wv[D][P][T];
+    uint32_t sv[D][P][T];
+    auto issue = [&](int d, int r) {
+#pragma unroll
+        for (int c = 0; c < P; ++c) {
+            const int kc = r * RK + KPL * (4 * c + q);
+            const bool xok = r < re && kc < a.K && j < a.M;  // K % KPL == 0: chunks are whole
+#pragma unroll
+            for (int p = 0; p < SUB; ++p) {
+                const uint32_t off = xok ? (uint32_t)(((int64_t)j * a.ldx + kc + 8 * p) * 2) : kOut;
+                xv[d][c][p] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int tile = (int)blockIdx.x + t * (int)gridDim.x;
+            const int n = tile * 16 + j;
+#pragma unroll
+            for (int c = 0; c < P; ++c) {
+                const int kc = r * RK + KPL * (4 * c + q);
+                const bool ok = r < re && kc < a.K && tile < a.tiles && n < a.N;
+                const uint32_t woff = (uint32_t)n * a.row_bytes + (uint32_t)(BITS == 4 ? kc / 2 : kc);
+                wv[d][c][t] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (int)woff : (int)kOut, 0, 2);
+            }
+#pragma unroll
+            for (int c = 0; c < P; ++c) {
+                const int kc = r * RK + KPL * (4 * c + q);
+                const bool ok = r < re && kc < a.K && tile < a.tiles && n < a.N;
+                const uint32_t soff = (uint32_t)(((int64_t)n * a.lds + kc / a.group) * 2);
+                sv[d][c][t] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (int)soff : (int)kOut, 0, 0);
+            }
+        }
+    };
+    // Every wave's codebook load goes out before any weight load (returns
+    // come back in the order the CU issued the loads, so a codebook load
+    // behind other waves' weights would hold the table build until those
+    // arrived); then the first half of the prologue's rounds, the table
+    // build, and the rest after it, each wave on its own.
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    constexpr int DH = D / 2;
+#pragma unroll
+    for (int d = 0; d < DH; ++d)
+        issue(d, rb + d);
+    __builtin_amdgcn_sched_barrier(0);
+    s_cbraw[tid] = cbraw;
+    lds_barrier();
+    if (tid < 256) {
+        float c = 0.0f;
+        if (tid < a.levels) {
+            if (a.cb_dtype == EP_F32) {
+                c = __uint_as_float(s_cbraw[tid]);
+            } else {
+                const uint16_t h = (uint16_t)(s_cbraw[tid >> 1] >> (16 * (tid & 1)));
+                c = a.cb_dtype == EP_F16 ? (float)f16_from_bits(h) : bf16_to_f32(h);
+            }
+        }
+        s_cb[tid] = f16_bits((f16_t)c);
+    }
+    lds_barrier();
+    build_table<BITS>(tab, s_cb);
+    lds_barrier();
+#pragma unroll
+    for (int d = DH; d < D; ++d)
+        issue(d, rb + d);
+
+    const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
+    f32x4_t acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+        acc[t] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    for (int r0 = rb; r0 < re; r0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            if (r0 + d < re) {
+#pragma unroll
+                for (int c = 0; c < P; ++c) {
+                    f16x8_t av[SUB];
+                    float bk[4];  // the piece's power of two of accumulator rows 4 q + r
+                    if constexpr (XDT == EP_F16) {
+#pragma unroll
+                        for (int s = 0; s < SUB; ++s)
+                            av[s] = __builtin_bit_cast(f16x8_t, xv[d][c][s]);
+                    } else {
+                        // D[m][n] of a 16x16 tile: lane n + 16 (m / 4),
+                        // register m % 4; lane m holds row m's power of two
+                        const float back = ldexpf(1.0f, bf16_operand<SUB>(xv[d][c], av));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            bk[r] = __shfl(back, 4 * q + r, 64);
+                    }
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        f16x8_t bv[SUB];
+                        dequant_chunk<BITS>(tab, wv[d][c][t], sv[d][c][t], lane4, bv);
+                        if constexpr (XDT == EP_F16) {
+#pragma unroll
+                            for (int s = 0; s < SUB; ++s)
+                                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[s], bv[s], acc[t], 0, 0, 0);
+                        } else {
+                            f32x4_t cs = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                            for (int s = 0; s < SUB; ++s)
+                                cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[s], bv[s], cs, 0, 0, 0);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                acc[t][r] += cs[r] * bk[r];
+                        }
+                    }
+                }
+            }
+            issue(d, r0 + d + D);
+        }
+    }
+
+    // the waves' sums, added in wave order
+    __syncthreads();  // every table read of every wave is done
+    float *red = (float *)tab;
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            red[(t * kSk1Waves + wave) * 256 + (4 * q + r) * 16 + j] = acc[t][r];
+    __syncthreads();
+    for (int i = tid; i < T * 256; i += kSk1Threads) {
+        const int t = i >> 8, m = (i >> 4) & 15;
+        const int tile = (int)blockIdx.x + t * (int)gridDim.x;
+        const int n = tile * 16 + (i & 15);
+        if (tile < a.tiles && n < a.N && m < a.M) {
+            float s = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kSk1Waves; ++w)
+                s += red[(t * kSk1Waves + w) * 256 + (i & 255)];
+            const int64_t off = (int64_t)m * a.ldy + n;
+            if (a.accumulate)
+                s += load_as_f32(a.y, a.y_dtype, off);
+            store_from_f32(a.y, a.y_dtype, off, s);
         }
     }
 }
@@ -406,6 +674,44 @@ int sk_launch_bits(const SkArgs &a, int S, int ld, int xdt, hipStream_t s)
     return sk_launch_ld<BITS, 4>(a, S, ld, xdt, s);
 }
 
+// Row tiles per workgroup of the one-launch path: the fewest that keep the
+// grid within one workgroup per CU; 0 when the path does not serve (8-bit
+// indices, 16-bit activations, M <= 16, enough 16-row tiles to fill 3/4 of
+// the CUs and at most 4 per CU).  4-bit indices stay on the split-K kernel:
+// their B operands take twice the registers, and the 1024-thread
+// workgroups leave 128 per lane.
+int sk1_tiles_per_wg(int bits, const ActDesc &x, int64_t M, int64_t N)
+{
+    if (bits != 8 || M > 16 || x.dtype == EP_F32)
+        return 0;
+    const int64_t tiles = (N + 15) / 16, cus = device_cus();
+    if (tiles * 4 < cus * 3)
+        return 0;
+    for (int t = 1; t <= 4; t *= 2)
+        if (tiles <= t * cus)
+            return t;
+    return 0;
+}
+
+template <int BITS, int XDT, int T>
+void sk1_launch_t(const SkArgs &a, hipStream_t s)
+{
+    constexpr int P = T == 1 ? 2 : 1;  // (more would spill past 128 VGPRs)
+    constexpr int D = 2;
+    hipLaunchKernelGGL((sk1_kernel<BITS, XDT, T, D, P>), dim3((unsigned)a.gtiles), dim3(kSk1Threads), 0, s, a);
+}
+
+template <int XDT>
+void sk1_launch_x(const SkArgs &a, int tpw, hipStream_t s)
+{
+    if (tpw == 1)
+        sk1_launch_t<8, XDT, 1>(a, s);
+    else if (tpw == 2)
+        sk1_launch_t<8, XDT, 2>(a, s);
+    else
+        sk1_launch_t<8, XDT, 4>(a, s);
+}
+
 }  // namespace
 
 bool skinny_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
@@ -440,9 +746,10 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     if (!skinny_serves(w, x, M))
         return EP_DECLINE_SHAPE;
     const int bits = w.bits();
+    const int tpw1 = sk1_tiles_per_wg(bits, x, M, w.N);
     const int ld = sk_choose_ld(bits, M, w.N, w.K);
     const int S = sk_splits_ld(bits, ld, w.K);
-    const bool partials = S > 1 || y.accumulate;
+    const bool partials = tpw1 == 0 && (S > 1 || y.accumulate);
     const size_t need = partials ? skinny_workspace(M, w.N, w.K, w.levels) : 0;
     if (need > 0 && (!ws || ws_bytes < need))
         return set_error(EP_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws_bytes);
@@ -466,6 +773,20 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     a.N = (int)w.N;
     a.K = (int)w.K;
     a.group = w.group;
+    a.y = y.ptr;
+    a.y_dtype = y.dtype;
+    a.ldy = y.ld;
+    a.accumulate = y.accumulate;
+    if (tpw1 > 0) {
+        a.tiles = (int)((w.N + 15) / 16);
+        a.gtiles = (a.tiles + tpw1 - 1) / tpw1;
+        if (x.dtype == EP_F16)
+            sk1_launch_x<EP_F16>(a, tpw1, stream);
+        else
+            sk1_launch_x<EP_BF16>(a, tpw1, stream);
+        EP_HIP_CHECK(hipGetLastError());
+        return EP_OK;
+    }
     a.tiles = (int)((w.N + kSkRows - 1) / kSkRows);
     // one resident workgroup per CU: enough row-tile groups that S of them
     // fill the device, at most sk_tpw tiles per workgroup
@@ -478,10 +799,6 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     if (g > a.tiles)
         g = a.tiles;
     a.gtiles = g;
-    a.y = y.ptr;
-    a.y_dtype = y.dtype;
-    a.ldy = y.ld;
-    a.accumulate = y.accumulate;
     a.part = partials ? (float *)ws : nullptr;
     const int rc = bits == 4 ? sk_launch_bits<4>(a, S, ld, x.dtype, stream) : sk_launch_bits<8>(a, S, ld, x.dtype, stream);
     if (rc != EP_OK || !partials)

@@ -189,3 +189,62 @@ def test_skinny_workspace_covers_partials(m, levels, n, k):
     """The workspace query covers every split's partial sums."""
     need = _abi.lib.ep_dequant_matmul_workspace(m, n, k, levels, 128)
     assert need >= skinny_splits(m, n, k, levels) * m * n * 4
+
+
+# The one-launch path: M <= 16 with 8-bit indices, 16-bit activations and
+# enough 16-row tiles to fill 3/4 of the CUs (N >= 12 x CUs, at most 4 tiles
+# per CU); the 8-bit shapes below take it on a 256-CU device, the 4-bit ones
+# the split-K kernel.
+@pytest.mark.parametrize("levels", [16, 256])
+@pytest.mark.parametrize("m,n,k", [(2, 4096, 4096), (16, 4096, 4096 + 32), (9, 8200, 2048),
+                                   (4, 14336, 1024), (13, 4100, 1568)])
+def test_skinny_one_launch(levels, m, n, k):
+    """All of K in one workgroup per row tile: K past the last full round
+    of a wave (and a last group of 32 values), N past the last 16-row tile,
+    one, two and four row tiles per workgroup."""
+    _, packed, scale, cb, s = make(n, k, levels, seed=n + k + m)
+    x32, x = x_bf16(m, k, m + levels)
+    assert_close(run(s, x).cpu().numpy(), rust_ref(x32, packed, scale, cb, n, k, levels, 128))
+
+
+@pytest.mark.parametrize("levels", [16, 256])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_skinny_one_launch_accumulate_f16_x(out_dtype, levels):
+    """fp16 activations (the operand as they are); results written, then
+    added to y in the same launch."""
+    n, k, m = 4096, 2048, 11
+    _, packed, scale, cb, s = make(n, k, levels, seed=61)
+    x32 = rng(62).standard_normal((m, k)).astype(np.float32)
+    x = torch.from_numpy(x32).to(DEV).to(torch.float16)
+    want = rust_ref(x.float().cpu().numpy(), packed, scale, cb, n, k, levels, 128)
+    out_tol = TOL if out_dtype == torch.float32 else TOL + 2.0 ** -8
+    assert_close(run(s, x, out_dtype).float().cpu().numpy(), want, out_tol)
+    out = torch.from_numpy(rng(63).standard_normal((m, n)).astype(np.float32)).to(DEV).to(out_dtype)
+    start = out.float().cpu().numpy()
+    run(s, x, out_dtype, accumulate=True, out=out)
+    assert_close(out.float().cpu().numpy(), want + start, out_tol)
+
+
+def test_skinny_one_launch_rows_of_very_different_magnitude():
+    """A power of two per row and round: rows at 3e5, 1, 1e-12, 1e-30 and 0
+    stay exact relative to their own size."""
+    n, k = 4096, 2048
+    idx, packed, scale, cb, s = make(n, k, seed=71)
+    w64 = ref.dequant_tile_f32(idx, scale, cb, 128).astype(np.float64)
+    mags = np.array([3e5, 1.0, 1e-12, 1e-30, 0.0], np.float32)
+    x32 = ref.round_bf16((rng(72).standard_normal((5, k)) * mags[:, None]).astype(np.float32))
+    x = torch.from_numpy(x32).to(DEV).to(torch.bfloat16)
+    y = run(s, x).cpu().numpy()
+    want = ref.linear_f64(x32, w64)
+    for r in range(4):
+        assert_close(y[r:r + 1], want[r:r + 1])
+    assert np.all(y[4] == 0.0)
+
+
+def test_skinny_one_launch_deterministic():
+    n, k, m = 4096, 4096, 16
+    _, packed, scale, cb, s = make(n, k, 256, seed=81)
+    _, x = x_bf16(m, k, 82)
+    a = run(s, x).cpu().numpy()
+    b = run(s, x).cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
