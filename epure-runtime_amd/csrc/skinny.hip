@@ -328,7 +328,7 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
 // -- the A operand, straight from global memory: x is small and stays in
 // L2, and one load serves the T tiles.  fp16 activations are the operand
 // as they are; bf16 ones become fp16 after the power-of-two rescale of the
-// row's largest |x| in the piece (bf16_operand), and each piece's MFMA sums
+// row's largest |x| in the round (bf16_operand), and each round's MFMA sums
 // are scaled back exactly before they join the running f32 sums.  Loads
 // run D rounds ahead of the MFMAs.  At the end the waves' sums meet in LDS
 // (over the table, which is no longer needed) and are added in wave order.
@@ -501,39 +501,40 @@ __global__ void __launch_bounds__(kSk1Threads) sk1_kernel(SkArgs a)
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             if (r0 + d < re) {
+                f16x8_t av[P][SUB];
+                float bk[4];  // the round's power of two of accumulator rows 4 q + r
+                if constexpr (XDT == EP_F16) {
 #pragma unroll
-                for (int c = 0; c < P; ++c) {
-                    f16x8_t av[SUB];
-                    float bk[4];  // the piece's power of two of accumulator rows 4 q + r
-                    if constexpr (XDT == EP_F16) {
+                    for (int c = 0; c < P; ++c)
 #pragma unroll
                         for (int s = 0; s < SUB; ++s)
-                            av[s] = __builtin_bit_cast(f16x8_t, xv[d][c][s]);
-                    } else {
-                        // D[m][n] of a 16x16 tile: lane n + 16 (m / 4),
-                        // register m % 4; lane m holds row m's power of two
-                        const float back = ldexpf(1.0f, bf16_operand<SUB>(xv[d][c], av));
+                            av[c][s] = __builtin_bit_cast(f16x8_t, xv[d][c][s]);
+                } else {
+                    // one exponent per row over the round's P pieces.  D[m][n]
+                    // of a 16x16 tile: lane n + 16 (m / 4), register m % 4;
+                    // lane m holds row m's power of two
+                    const float back = ldexpf(1.0f, bf16_operand<P * SUB>(&xv[d][0][0], &av[0][0]));
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            bk[r] = __shfl(back, 4 * q + r, 64);
-                    }
+                    for (int r = 0; r < 4; ++r)
+                        bk[r] = __shfl(back, 4 * q + r, 64);
+                }
 #pragma unroll
-                    for (int t = 0; t < T; ++t) {
+                for (int t = 0; t < T; ++t) {
+                    f32x4_t cs = XDT == EP_F16 ? acc[t] : (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int c = 0; c < P; ++c) {
                         f16x8_t bv[SUB];
                         dequant_chunk<BITS>(tab, wv[d][c][t], sv[d][c][t], lane4, bv);
-                        if constexpr (XDT == EP_F16) {
 #pragma unroll
-                            for (int s = 0; s < SUB; ++s)
-                                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[s], bv[s], acc[t], 0, 0, 0);
-                        } else {
-                            f32x4_t cs = {0.0f, 0.0f, 0.0f, 0.0f};
+                        for (int s = 0; s < SUB; ++s)
+                            cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[c][s], bv[s], cs, 0, 0, 0);
+                    }
+                    if constexpr (XDT == EP_F16) {
+                        acc[t] = cs;
+                    } else {
 #pragma unroll
-                            for (int s = 0; s < SUB; ++s)
-                                cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[s], bv[s], cs, 0, 0, 0);
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                acc[t][r] += cs[r] * bk[r];
-                        }
+                        for (int r = 0; r < 4; ++r)
+                            acc[t][r] += cs[r] * bk[r];
                     }
                 }
             }
