@@ -332,9 +332,6 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
 // are scaled back exactly before they join the running f32 sums.  Loads
 // run D rounds ahead of the MFMAs.  At the end the waves' sums meet in LDS
 // (over the table, which is no longer needed) and are added in wave order.
-constexpr int kSk1Threads = 1024;
-constexpr int kSk1Waves = kSk1Threads / 64;
-
 typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
 
 EP_DEV uint32_t max_over_row_lanes(uint32_t v)  // max over lanes l, l ^ 16, l ^ 32, l ^ 48
@@ -397,48 +394,51 @@ EP_DEV int bf16_operand(const u32x4_t *xv, f16x8_t *av)
     return e;
 }
 
-template <int BITS, int XDT, int T, int D, int P>
-__global__ void __launch_bounds__(kSk1Threads) sk1_kernel(SkArgs a)
+template <int BITS, int XDT, int T, int D, int P, int MT, int NT>
+__global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
 {
+    constexpr int NW = NT / 64;      // waves
     constexpr int KPL = sk_kpl<BITS>();
     constexpr int RK = 4 * KPL * P;  // P pieces of 16 bytes per lane and tile: 64 P bytes of a row
     constexpr int SUB = KPL / 8;     // MFMA sub-steps per piece = 16-byte x loads per lane and piece
-    static_assert(T * kSk1Waves * 256 <= kTabDwords, "wave sums fit over the table");
+    static_assert(NW * MT * 256 <= kTabDwords, "one tile's wave sums fit over the table");
     static_assert(XDT != EP_F32, "16-bit activations");
 
     __shared__ __align__(16) uint32_t tab[kTabDwords];
-    __shared__ uint32_t s_cbraw[kSk1Threads];
+    __shared__ uint32_t s_cbraw[NT];
     __shared__ uint16_t s_cb[256];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, q = lane >> 4;
     const int nr = (a.K + RK - 1) / RK;
-    const int rb = wave * nr / kSk1Waves, re = (wave + 1) * nr / kSk1Waves;
+    const int rb = wave * nr / NW, re = (wave + 1) * nr / NW;
     const auto rx = buffer_rsrc(a.x, a.xbytes), rw = buffer_rsrc(a.packed, a.wbytes);
     const auto rs = buffer_rsrc(a.scale, a.sbytes), rcb = buffer_rsrc(a.cb, a.cbbytes);
 
     const uint32_t cbraw = __builtin_amdgcn_raw_buffer_load_b32(rcb, tid < 256 ? tid * 4 : kOut, 0, 0);
     // Loads of round r into slot d (masked lanes read 0 from past the
     // buffer's end; rounds past the wave's run are all masked, so every
-    // slot sees the same number of loads).
-    // Piece c of a round is chunk 4 c + q: a load instruction covers 64
-    // bytes of each of 16 rows, and the P instructions of a round, issued
-    // back to back, 64 P contiguous bytes of each.
-    u32x4_t xv[D][P][SUB];
+    // slot sees the same number of loads).  Piece c of a round is chunk
+    // 4 c + q: a load instruction covers 64 bytes of each of 16 rows, and
+    // the P instructions of a round, issued back to back, 64 P contiguous
+    // bytes of each.  Activation rows 16 mt + j, mt < MT.
+    u32x4_t xv[D][MT][P][SUB];
     u32x4_t wv[D][P][T];
     uint32_t sv[D][P][T];
     auto issue = [&](int d, int r) {
 #pragma unroll
-        for (int c = 0; c < P; ++c) {
-            const int kc = r * RK + KPL * (4 * c + q);
-            const bool xok = r < re && kc < a.K && j < a.M;  // K % KPL == 0: chunks are whole
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int p = 0; p < SUB; ++p) {
-                const uint32_t off = xok ? (uint32_t)(((int64_t)j * a.ldx + kc + 8 * p) * 2) : kOut;
-                xv[d][c][p] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+            for (int c = 0; c < P; ++c) {
+                const int kc = r * RK + KPL * (4 * c + q), m = 16 * mt + j;
+                const bool xok = r < re && kc < a.K && m < a.M;  // K % KPL == 0: chunks are whole
+#pragma unroll
+                for (int p = 0; p < SUB; ++p) {
+                    const uint32_t off = xok ? (uint32_t)(((int64_t)m * a.ldx + kc + 8 * p) * 2) : kOut;
+                    xv[d][mt][c][p] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+                }
             }
-        }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const int tile = (int)blockIdx.x + t * (int)gridDim.x;
@@ -493,48 +493,61 @@ __global__ void __launch_bounds__(kSk1Threads) sk1_kernel(SkArgs a)
         issue(d, rb + d);
 
     const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
-    f32x4_t acc[T];
+    f32x4_t acc[T][MT];
 #pragma unroll
     for (int t = 0; t < T; ++t)
-        acc[t] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            acc[t][mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
     for (int r0 = rb; r0 < re; r0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
             if (r0 + d < re) {
-                f16x8_t av[P][SUB];
-                float bk[4];  // the round's power of two of accumulator rows 4 q + r
-                if constexpr (XDT == EP_F16) {
+                f16x8_t av[MT][P][SUB];
+                float bk[MT][4];  // the round's power of two of accumulator rows 16 mt + 4 q + r
 #pragma unroll
-                    for (int c = 0; c < P; ++c)
+                for (int mt = 0; mt < MT; ++mt) {
+                    if constexpr (XDT == EP_F16) {
 #pragma unroll
-                        for (int s = 0; s < SUB; ++s)
-                            av[c][s] = __builtin_bit_cast(f16x8_t, xv[d][c][s]);
-                } else {
-                    // one exponent per row over the round's P pieces.  D[m][n]
-                    // of a 16x16 tile: lane n + 16 (m / 4), register m % 4;
-                    // lane m holds row m's power of two
-                    const float back = ldexpf(1.0f, bf16_operand<P * SUB>(&xv[d][0][0], &av[0][0]));
+                        for (int c = 0; c < P; ++c)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        bk[r] = __shfl(back, 4 * q + r, 64);
+                            for (int s = 0; s < SUB; ++s)
+                                av[mt][c][s] = __builtin_bit_cast(f16x8_t, xv[d][mt][c][s]);
+                    } else {
+                        // one exponent per row over the round's P pieces.
+                        // D[m][n] of a 16x16 tile: lane n + 16 (m / 4),
+                        // register m % 4; lane m holds row m's power of two
+                        const float back = ldexpf(1.0f, bf16_operand<P * SUB>(&xv[d][mt][0][0], &av[mt][0][0]));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            bk[mt][r] = __shfl(back, 4 * q + r, 64);
+                    }
                 }
 #pragma unroll
                 for (int t = 0; t < T; ++t) {
-                    f32x4_t cs = XDT == EP_F16 ? acc[t] : (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+                    f32x4_t cs[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        cs[mt] = XDT == EP_F16 ? acc[t][mt] : (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                     for (int c = 0; c < P; ++c) {
                         f16x8_t bv[SUB];
                         dequant_chunk<BITS>(tab, wv[d][c][t], sv[d][c][t], lane4, bv);
 #pragma unroll
                         for (int s = 0; s < SUB; ++s)
-                            cs = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[c][s], bv[s], cs, 0, 0, 0);
-                    }
-                    if constexpr (XDT == EP_F16) {
-                        acc[t] = cs;
-                    } else {
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            acc[t][r] += cs[r] * bk[r];
+                            for (int mt = 0; mt < MT; ++mt)
+                                cs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mt][c][s], bv[s], cs[mt], 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        if constexpr (XDT == EP_F16) {
+                            acc[t][mt] = cs[mt];
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                acc[t][mt][r] += cs[mt][r] * bk[mt][r];
+                        }
                     }
                 }
             }
@@ -542,28 +555,31 @@ __global__ void __launch_bounds__(kSk1Threads) sk1_kernel(SkArgs a)
         }
     }
 
-    // the waves' sums, added in wave order
-    __syncthreads();  // every table read of every wave is done
+    // the waves' sums, added in wave order, one tile at a time, in LDS over
+    // the table (no longer needed once every wave has passed the barrier)
     float *red = (float *)tab;
 #pragma unroll
-    for (int t = 0; t < T; ++t)
+    for (int t = 0; t < T; ++t) {
+        __syncthreads();
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            red[(t * kSk1Waves + wave) * 256 + (4 * q + r) * 16 + j] = acc[t][r];
-    __syncthreads();
-    for (int i = tid; i < T * 256; i += kSk1Threads) {
-        const int t = i >> 8, m = (i >> 4) & 15;
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                red[(wave * MT + mt) * 256 + (4 * q + r) * 16 + j] = acc[t][mt][r];
+        __syncthreads();
         const int tile = (int)blockIdx.x + t * (int)gridDim.x;
-        const int n = tile * 16 + (i & 15);
-        if (tile < a.tiles && n < a.N && m < a.M) {
-            float s = 0.0f;
+        for (int i = tid; i < MT * 256; i += NT) {
+            const int m = i >> 4, n = tile * 16 + (i & 15);  // i = (16 mt + row) * 16 + col
+            if (tile < a.tiles && n < a.N && m < a.M) {
+                float s = 0.0f;
 #pragma unroll
-            for (int w = 0; w < kSk1Waves; ++w)
-                s += red[(t * kSk1Waves + w) * 256 + (i & 255)];
-            const int64_t off = (int64_t)m * a.ldy + n;
-            if (a.accumulate)
-                s += load_as_f32(a.y, a.y_dtype, off);
-            store_from_f32(a.y, a.y_dtype, off, s);
+                for (int w = 0; w < NW; ++w)
+                    s += red[w * MT * 256 + i];
+                const int64_t off = (int64_t)m * a.ldy + n;
+                if (a.accumulate)
+                    s += load_as_f32(a.y, a.y_dtype, off);
+                store_from_f32(a.y, a.y_dtype, off, s);
+            }
         }
     }
 }
@@ -676,41 +692,59 @@ int sk_launch_bits(const SkArgs &a, int S, int ld, int xdt, hipStream_t s)
 }
 
 // Row tiles per workgroup of the one-launch path: the fewest that keep the
-// grid within one workgroup per CU; 0 when the path does not serve (8-bit
-// indices, 16-bit activations, M <= 16, enough 16-row tiles to fill 3/4 of
-// the CUs and at most 4 per CU).  4-bit indices stay on the split-K kernel:
-// their B operands take twice the registers, and the 1024-thread
-// workgroups leave 128 per lane.
+// grid within one workgroup per CU; 0 when the path does not serve.  It
+// serves 8-bit indices with 16-bit activations and enough 16-row tiles to
+// fill 3/4 of the CUs, at most 4 per CU: M <= 16 always, 17..32 only with
+// two or more tiles per workgroup.  Each tile reads all M x K activations
+// from L2, so at one tile per workgroup and M > 16 (and at any M > 32) the
+// split-K kernel, which stages them once per split, is faster.  4-bit
+// indices stay on the split-K kernel too: their B operands and activations
+// take twice the registers.
+int sk1_mt(int64_t M) { return M <= 16 ? 1 : 2; }
 int sk1_tiles_per_wg(int bits, const ActDesc &x, int64_t M, int64_t N)
 {
-    if (bits != 8 || M > 16 || x.dtype == EP_F32)
+    if (bits != 8 || M > 32 || x.dtype == EP_F32)
         return 0;
     const int64_t tiles = (N + 15) / 16, cus = device_cus();
     if (tiles * 4 < cus * 3)
         return 0;
     for (int t = 1; t <= 4; t *= 2)
         if (tiles <= t * cus)
-            return t;
+            return t == 1 && M > 16 ? 0 : t;
     return 0;
 }
 
-template <int BITS, int XDT, int T>
+// 16 waves with one 16-row activation block and up to two tiles (four per
+// SIMD hide the table lookups' latency), 8 otherwise (the second block's
+// activations or the four tiles' sums take the registers of two waves); two
+// pieces per round where one tile and one block leave the registers for
+// them.
+template <int XDT, int T, int MT>
 void sk1_launch_t(const SkArgs &a, hipStream_t s)
 {
-    constexpr int P = T == 1 ? 2 : 1;  // (more would spill past 128 VGPRs)
-    constexpr int D = 2;
-    hipLaunchKernelGGL((sk1_kernel<BITS, XDT, T, D, P>), dim3((unsigned)a.gtiles), dim3(kSk1Threads), 0, s, a);
+    constexpr int NT = MT == 1 && T < 4 ? 1024 : 512;
+    constexpr int P = MT == 1 && T == 1 ? 2 : 1;
+    hipLaunchKernelGGL((sk1_kernel<8, XDT, T, 2, P, MT, NT>), dim3((unsigned)a.gtiles), dim3(NT), 0, s, a);
+}
+
+template <int XDT, int MT>
+void sk1_launch_m(const SkArgs &a, int tpw, hipStream_t s)
+{
+    if (tpw == 1)
+        sk1_launch_t<XDT, 1, MT>(a, s);
+    else if (tpw == 2)
+        sk1_launch_t<XDT, 2, MT>(a, s);
+    else
+        sk1_launch_t<XDT, 4, MT>(a, s);
 }
 
 template <int XDT>
 void sk1_launch_x(const SkArgs &a, int tpw, hipStream_t s)
 {
-    if (tpw == 1)
-        sk1_launch_t<8, XDT, 1>(a, s);
-    else if (tpw == 2)
-        sk1_launch_t<8, XDT, 2>(a, s);
+    if (sk1_mt(a.M) == 1)
+        sk1_launch_m<XDT, 1>(a, tpw, s);
     else
-        sk1_launch_t<8, XDT, 4>(a, s);
+        sk1_launch_m<XDT, 2>(a, tpw, s);
 }
 
 }  // namespace

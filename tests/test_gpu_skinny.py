@@ -191,28 +191,34 @@ def test_skinny_workspace_covers_partials(m, levels, n, k):
     assert need >= skinny_splits(m, n, k, levels) * m * n * 4
 
 
-# The one-launch path: M <= 16 with 8-bit indices, 16-bit activations and
-# enough 16-row tiles to fill 3/4 of the CUs (N >= 12 x CUs, at most 4 tiles
-# per CU); the 8-bit shapes below take it on a 256-CU device, the 4-bit ones
+# The one-launch path: 8-bit indices, 16-bit activations and enough 16-row
+# tiles to fill 3/4 of the CUs (N >= 12 x CUs, at most 4 tiles per CU), at
+# M <= 16, and at M 17..32 with two or more tiles per workgroup (N > 16 x
+# CUs).  On a 256-CU device the 8-bit shapes with M <= 16, (32, 8200),
+# (24, 14336) and (20, 6144) take it; the others, and every 4-bit shape,
 # the split-K kernel.
 @pytest.mark.parametrize("levels", [16, 256])
 @pytest.mark.parametrize("m,n,k", [(2, 4096, 4096), (16, 4096, 4096 + 32), (9, 8200, 2048),
-                                   (4, 14336, 1024), (13, 4100, 1568)])
+                                   (4, 14336, 1024), (13, 4100, 1568), (17, 4096, 4096),
+                                   (32, 8200, 2048), (24, 14336, 1024), (20, 6144, 2048 + 32),
+                                   (33, 4100, 1568), (64, 4096, 4096 + 32)])
 def test_skinny_one_launch(levels, m, n, k):
     """All of K in one workgroup per row tile: K past the last full round
     of a wave (and a last group of 32 values), N past the last 16-row tile,
-    one, two and four row tiles per workgroup."""
+    one, two and four row tiles per workgroup, one, two and four 16-row
+    activation blocks."""
     _, packed, scale, cb, s = make(n, k, levels, seed=n + k + m)
     x32, x = x_bf16(m, k, m + levels)
     assert_close(run(s, x).cpu().numpy(), rust_ref(x32, packed, scale, cb, n, k, levels, 128))
 
 
+@pytest.mark.parametrize("m,n", [(11, 4096), (28, 8192)])
 @pytest.mark.parametrize("levels", [16, 256])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_skinny_one_launch_accumulate_f16_x(out_dtype, levels):
+def test_skinny_one_launch_accumulate_f16_x(out_dtype, levels, m, n):
     """fp16 activations (the operand as they are); results written, then
     added to y in the same launch."""
-    n, k, m = 4096, 2048, 11
+    k = 2048
     _, packed, scale, cb, s = make(n, k, levels, seed=61)
     x32 = rng(62).standard_normal((m, k)).astype(np.float32)
     x = torch.from_numpy(x32).to(DEV).to(torch.float16)
@@ -227,22 +233,25 @@ def test_skinny_one_launch_accumulate_f16_x(out_dtype, levels):
 
 def test_skinny_one_launch_rows_of_very_different_magnitude():
     """A power of two per row and round: rows at 3e5, 1, 1e-12, 1e-30 and 0
-    stay exact relative to their own size."""
-    n, k = 4096, 2048
-    idx, packed, scale, cb, s = make(n, k, seed=71)
+    stay exact relative to their own size (the same five again in the
+    second 16-row block)."""
+    n, k = 8192, 2048
+    idx, packed, scale, cb, s = make(n, k, levels=256, seed=71)
     w64 = ref.dequant_tile_f32(idx, scale, cb, 128).astype(np.float64)
-    mags = np.array([3e5, 1.0, 1e-12, 1e-30, 0.0], np.float32)
-    x32 = ref.round_bf16((rng(72).standard_normal((5, k)) * mags[:, None]).astype(np.float32))
+    mags = np.array([3e5, 1.0, 1e-12, 1e-30, 0.0] + [1.0] * 11 + [3e5, 1.0, 1e-12, 1e-30, 0.0],
+                    np.float32)
+    x32 = ref.round_bf16((rng(72).standard_normal((21, k)) * mags[:, None]).astype(np.float32))
     x = torch.from_numpy(x32).to(DEV).to(torch.bfloat16)
     y = run(s, x).cpu().numpy()
     want = ref.linear_f64(x32, w64)
-    for r in range(4):
+    for r in list(range(4)) + list(range(16, 20)):
         assert_close(y[r:r + 1], want[r:r + 1])
-    assert np.all(y[4] == 0.0)
+    assert np.all(y[4] == 0.0) and np.all(y[20] == 0.0)
 
 
-def test_skinny_one_launch_deterministic():
-    n, k, m = 4096, 4096, 16
+@pytest.mark.parametrize("m,n", [(16, 4096), (32, 8192)])
+def test_skinny_one_launch_deterministic(m, n):
+    k = 4096
     _, packed, scale, cb, s = make(n, k, 256, seed=81)
     _, x = x_bf16(m, k, 82)
     a = run(s, x).cpu().numpy()
