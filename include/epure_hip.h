@@ -83,8 +83,11 @@ size_t ep_dequant_matmul_workspace(int64_t M, int64_t N, int64_t K, int levels, 
  * the products as fp16(cb[idx]) (the dot-product path) or
  * fp16(cb[idx]*scale) (the MFMA path); x enters as fp16 after an exact
  * per-row power-of-two rescale, so it cannot overflow fp16.
- * The kernel is chosen from M (batch-1 GEMV for small M, dequant-to-LDS +
- * MFMA for large M); both read the packed bytes exactly once per launch.
+ * The kernel is chosen from M: the LUT GEMV at M = 1 (up to 4 where its
+ * activations fit), register-dequant MFMA kernels up to M = 64 (one launch
+ * per linear for 8-bit indices at M <= 16 and wide N, split-K with an
+ * ordered reduction otherwise), dequant-to-LDS + MFMA above.  Each reads
+ * the packed bytes exactly once per launch.
  */
 int ep_dequant_matmul(const void *x, int x_dtype, int64_t ldx,
                       const uint8_t *packed, const void *scale, int scale_dtype,
