@@ -257,3 +257,27 @@ def test_skinny_one_launch_deterministic(m, n):
     a = run(s, x).cpu().numpy()
     b = run(s, x).cpu().numpy()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k", [(3, 16), (5, 256), (16, 1040)])
+def test_skinny_one_launch_short_k(m, k):
+    """K of one 16-value chunk, of two rounds (most of the 16 waves own no
+    round and add zeros), and one chunk past a full round."""
+    n = 4096
+    _, packed, scale, cb, s = make(n, k, 256, group=16, seed=91 + k)
+    x32, x = x_bf16(m, k, 92 + k)
+    assert_close(run(s, x).cpu().numpy(), rust_ref(x32, packed, scale, cb, n, k, 256, 16))
+
+
+@pytest.mark.parametrize("m", [4, 24])
+def test_skinny_one_launch_strided_x(m):
+    """Activation rows further apart than K (a column slice of a wider
+    tensor): every row read at its own stride."""
+    n, k = 8192, 2048
+    _, packed, scale, cb, s = make(n, k, 256, seed=101)
+    x32 = ref.round_bf16(rng(102).standard_normal((m, k + 96)).astype(np.float32))
+    wide = torch.from_numpy(x32).to(DEV).to(torch.bfloat16)
+    x = wide[:, :k]
+    assert x.stride(0) == k + 96
+    assert_close(run(s, x).cpu().numpy(), rust_ref(np.ascontiguousarray(x32[:, :k]), packed, scale, cb, n,
+                                                    k, 256, 128))
