@@ -30,10 +30,10 @@
 //  * with one split the results go straight to y; otherwise each split
 //    writes f32 partials [S][M][N] and sk_reduce_kernel sums them in split
 //    order (deterministic; no atomics, no counters);
-//  * at M <= 16 with 8-bit indices, 16-bit activations and enough 16-row
-//    tiles to fill the CUs, sk1_kernel instead: one workgroup per row tile
-//    over the whole of K, one launch, no partials (its comment has the
-//    layout).
+//  * at M <= 16 with 8-bit indices (M <= 8 with 4-bit), 16-bit activations
+//    and enough 16-row tiles to fill the CUs, sk1_kernel instead: one
+//    workgroup per row tile over the whole of K, one launch, no partials
+//    (its comment has the layout).
 #include "ep_common.h"
 #include "ep_internal.h"
 #include "gemv_core.h"
@@ -315,7 +315,7 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
     }
 }
 
-// One launch for M <= 16 with fp16/bf16 activations and 8-bit indices.  A
+// One launch for small M with fp16/bf16 activations.  A
 // workgroup owns T row tiles of 16 rows (tiles blockIdx.x + t * gridDim.x)
 // over the whole of K, so its sums are final: no partials, no second
 // launch.  Its 16 waves (four per SIMD, to hide the latency of the table
@@ -693,17 +693,17 @@ int sk_launch_bits(const SkArgs &a, int S, int ld, int xdt, hipStream_t s)
 
 // Row tiles per workgroup of the one-launch path: the fewest that keep the
 // grid within one workgroup per CU; 0 when the path does not serve.  It
-// serves 8-bit indices with 16-bit activations and enough 16-row tiles to
-// fill 3/4 of the CUs, at most 4 per CU: M <= 16 always, 17..32 only with
-// two or more tiles per workgroup.  Each tile reads all M x K activations
-// from L2, so at one tile per workgroup and M > 16 (and at any M > 32) the
-// split-K kernel, which stages them once per split, is faster.  4-bit
-// indices stay on the split-K kernel too: their B operands and activations
-// take twice the registers.
+// serves 16-bit activations and enough 16-row tiles to fill 3/4 of the
+// CUs, at most 4 per CU: with 8-bit indices at M <= 16, and at M 17..32
+// with two or more tiles per workgroup; with 4-bit indices at M <= 8.
+// Each tile reads all M x K activations from L2, so at one tile per
+// workgroup and M > 16 (and at any M > 32; for 4-bit indices, whose tiles
+// hold half the bytes, from M > 8) the split-K kernel, which stages them
+// once per split, is as fast or faster.
 int sk1_mt(int64_t M) { return M <= 16 ? 1 : 2; }
 int sk1_tiles_per_wg(int bits, const ActDesc &x, int64_t M, int64_t N)
 {
-    if (bits != 8 || M > 32 || x.dtype == EP_F32)
+    if (M > (bits == 8 ? 32 : 8) || x.dtype == EP_F32)
         return 0;
     const int64_t tiles = (N + 15) / 16, cus = device_cus();
     if (tiles * 4 < cus * 3)
@@ -714,37 +714,37 @@ int sk1_tiles_per_wg(int bits, const ActDesc &x, int64_t M, int64_t N)
     return 0;
 }
 
-// 16 waves with one 16-row activation block and up to two tiles (four per
-// SIMD hide the table lookups' latency), 8 otherwise (the second block's
-// activations or the four tiles' sums take the registers of two waves); two
-// pieces per round where one tile and one block leave the registers for
-// them.
-template <int XDT, int T, int MT>
+// 16 waves with 8-bit indices, one 16-row activation block and up to two
+// tiles (four per SIMD hide the table lookups' latency), 8 otherwise (4-bit
+// B operands and activations, the second block's activations or the four
+// tiles' sums take the registers of two waves); two pieces per round where
+// one tile and one block of 8-bit indices leave the registers for them.
+template <int BITS, int XDT, int T, int MT>
 void sk1_launch_t(const SkArgs &a, hipStream_t s)
 {
-    constexpr int NT = MT == 1 && T < 4 ? 1024 : 512;
-    constexpr int P = MT == 1 && T == 1 ? 2 : 1;
-    hipLaunchKernelGGL((sk1_kernel<8, XDT, T, 2, P, MT, NT>), dim3((unsigned)a.gtiles), dim3(NT), 0, s, a);
+    constexpr int NT = BITS == 8 && MT == 1 && T < 4 ? 1024 : 512;
+    constexpr int P = BITS == 8 && MT == 1 && T == 1 ? 2 : 1;
+    hipLaunchKernelGGL((sk1_kernel<BITS, XDT, T, 2, P, MT, NT>), dim3((unsigned)a.gtiles), dim3(NT), 0, s, a);
 }
 
-template <int XDT, int MT>
+template <int BITS, int XDT, int MT>
 void sk1_launch_m(const SkArgs &a, int tpw, hipStream_t s)
 {
     if (tpw == 1)
-        sk1_launch_t<XDT, 1, MT>(a, s);
+        sk1_launch_t<BITS, XDT, 1, MT>(a, s);
     else if (tpw == 2)
-        sk1_launch_t<XDT, 2, MT>(a, s);
+        sk1_launch_t<BITS, XDT, 2, MT>(a, s);
     else
-        sk1_launch_t<XDT, 4, MT>(a, s);
+        sk1_launch_t<BITS, XDT, 4, MT>(a, s);
 }
 
-template <int XDT>
+template <int BITS, int XDT>
 void sk1_launch_x(const SkArgs &a, int tpw, hipStream_t s)
 {
-    if (sk1_mt(a.M) == 1)
-        sk1_launch_m<XDT, 1>(a, tpw, s);
+    if (BITS == 4 || sk1_mt(a.M) == 1)
+        sk1_launch_m<BITS, XDT, 1>(a, tpw, s);
     else
-        sk1_launch_m<XDT, 2>(a, tpw, s);
+        sk1_launch_m<BITS, XDT, BITS == 4 ? 1 : 2>(a, tpw, s);
 }
 
 }  // namespace
@@ -815,10 +815,10 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     if (tpw1 > 0) {
         a.tiles = (int)((w.N + 15) / 16);
         a.gtiles = (a.tiles + tpw1 - 1) / tpw1;
-        if (x.dtype == EP_F16)
-            sk1_launch_x<EP_F16>(a, tpw1, stream);
+        if (bits == 4)
+            x.dtype == EP_F16 ? sk1_launch_x<4, EP_F16>(a, tpw1, stream) : sk1_launch_x<4, EP_BF16>(a, tpw1, stream);
         else
-            sk1_launch_x<EP_BF16>(a, tpw1, stream);
+            x.dtype == EP_F16 ? sk1_launch_x<8, EP_F16>(a, tpw1, stream) : sk1_launch_x<8, EP_BF16>(a, tpw1, stream);
         EP_HIP_CHECK(hipGetLastError());
         return EP_OK;
     }

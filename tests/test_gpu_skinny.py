@@ -191,17 +191,19 @@ def test_skinny_workspace_covers_partials(m, levels, n, k):
     assert need >= skinny_splits(m, n, k, levels) * m * n * 4
 
 
-# The one-launch path: 8-bit indices, 16-bit activations and enough 16-row
-# tiles to fill 3/4 of the CUs (N >= 12 x CUs, at most 4 tiles per CU), at
+# The one-launch path: 16-bit activations and enough 16-row tiles to fill
+# 3/4 of the CUs (N >= 12 x CUs, at most 4 tiles per CU); 8-bit indices at
 # M <= 16, and at M 17..32 with two or more tiles per workgroup (N > 16 x
-# CUs).  On a 256-CU device the 8-bit shapes with M <= 16, (32, 8200),
-# (24, 14336) and (20, 6144) take it; the others, and every 4-bit shape,
+# CUs); 4-bit indices at M <= 8 (M <= 4 at K <= 4096 stays on the GEMV).
+# On a 256-CU device: 8-bit at M <= 16, (32, 8200), (24, 14336) and
+# (20, 6144); 4-bit at (5, 4128), (8, 8200), (7, 14336); the others take
 # the split-K kernel.
 @pytest.mark.parametrize("levels", [16, 256])
 @pytest.mark.parametrize("m,n,k", [(2, 4096, 4096), (16, 4096, 4096 + 32), (9, 8200, 2048),
                                    (4, 14336, 1024), (13, 4100, 1568), (17, 4096, 4096),
                                    (32, 8200, 2048), (24, 14336, 1024), (20, 6144, 2048 + 32),
-                                   (33, 4100, 1568), (64, 4096, 4096 + 32)])
+                                   (33, 4100, 1568), (64, 4096, 4096 + 32), (5, 4096, 4096 + 32),
+                                   (8, 8200, 2048), (7, 4096, 14336)])
 def test_skinny_one_launch(levels, m, n, k):
     """All of K in one workgroup per row tile: K past the last full round
     of a wave (and a last group of 32 values), N past the last 16-row tile,
