@@ -8,15 +8,17 @@ One "step" is one decode token: a replay of the captured HIP graph of the
 whole decode step -- the one-launch decode-step kernel (all 32 layers: fused
 q|k|v dequant-GEMV with RMSNorm, attention, o GEMV, gate|up GEMV with
 SwiGLU, down GEMV; phases hand over through tagged data, no grid barrier)
-and the lm_head/argmax launch.  The prompt (128 random ids) is consumed
-first, untimed; then W warm-up tokens, then K timed tokens, with the device
-synchronised on both sides.  Weights are random-init in the packed format (synthetic data; no
+and the lm_head/argmax launch.  The run is config 2's: the prompt (128
+random ids) is consumed first, untimed; then 256 tokens are decoded: W
+warm-up tokens, K timed tokens (the device synchronised on both sides), and
+the rest untimed (W + K > 256 decodes W + K).  The line reports the timed
+KV positions.  Weights are random-init in the packed format (synthetic data; no
 checkpoints offline).  --per-layer times the five-launches-per-layer path
 instead.
 
 The roofline entry is for the dominant kernel, the decode-step kernel: it is
-captured alone into a second graph (at the final position) and replayed K
-times between HIP events on the launch stream; achieved = its algorithmic
+captured alone into a second graph (at the position after the timed ones)
+and replayed K times between HIP events on the launch stream; achieved = its algorithmic
 bytes (packed indices + group scales + codebooks of the 224 linears, RMSNorm
 weights, and the KV rows attention reads at that position) / time per
 replay.  `traffic` is the HBM bytes per launch of the same replays from the
@@ -59,6 +61,10 @@ def parse():
     ap.add_argument("--config", default="llama3-8b",
                     choices=["llama3-8b", "qwen3-1.7b", "qwen3-8b", "llama3.2-3b", "qwen3-4b"])
     ap.add_argument("--prompt", type=int, default=None)
+    ap.add_argument("--decode", type=int, default=None,
+                    help="tokens decoded after the prompt (default: the configuration's, "
+                         "256 for the 8B shape, 128 for Qwen3-1.7B); the timed steps lie "
+                         "inside them, after the warm-up")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
@@ -561,10 +567,15 @@ def main():
 
     cfg = CONFIGS[args.config]
     n_prompt = args.prompt or (32 if args.config == "qwen3-1.7b" else 128)
+    # configs 1 and 2: the prompt, then 128 / 256 greedy tokens; W warm-up
+    # and K timed tokens are the first W + K of them, the rest decoded after
+    # (untimed), so the run is the configuration's whole decode
+    n_decode = args.decode or (128 if args.config == "qwen3-1.7b" else 256)
+    n_dec = max(n_decode, args.warmup + args.steps)
     dev = torch.device("cuda:0")
     print(f"# building {cfg.name} random weights (seed {args.seed})", file=sys.stderr, flush=True)
     w = random_weights(cfg, seed=args.seed, device=dev)
-    total_steps = n_prompt - 1 + args.warmup + args.steps
+    total_steps = n_prompt - 1 + n_dec
     dec = Decoder(w, total_steps + 2, persistent=False if args.per_layer else None)
     import numpy as np
     prompt = np.random.Generator(np.random.PCG64(args.seed + 1)).integers(
@@ -584,15 +595,14 @@ def main():
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     tok_s = args.steps / dt
-    toks = dec.tokens[:n_prompt + args.warmup + args.steps].cpu().tolist()
-
-    if dec.step_failed():
-        raise RuntimeError("a grid barrier of the decode-step kernel timed out")
 
     # dominant kernel alone: the layers of one step (one launch, or the 160
-    # per-layer launches), replayed at the final position between events on
-    # the launch stream
+    # per-layer launches), replayed at the next position between events on
+    # the launch stream.  The replays overwrite the residual input (the next
+    # token's embedding) and that position's KV rows: the input is saved and
+    # restored, and the next real step rewrites the rows.
     stream = torch.cuda.current_stream()
+    h_saved = dec.h.clone()
     g = torch.cuda.CUDAGraph()
     torch.cuda.synchronize()
     with torch.cuda.graph(g):
@@ -608,6 +618,16 @@ def main():
     e1.synchronize()
     kern_ms = e0.elapsed_time(e1) / args.steps
     pos = int(dec.state[0].item())
+    dec.h.copy_(h_saved)
+    torch.cuda.synchronize()
+    rest = n_dec - args.warmup - args.steps
+    print(f"# decoding the remaining {rest} tokens (untimed)", file=sys.stderr, flush=True)
+    for _ in range(rest):
+        dec.step()
+    torch.cuda.synchronize()
+    toks = dec.tokens[:n_prompt + n_dec].cpu().tolist()
+    if dec.step_failed():
+        raise RuntimeError("a hand-over wait of the decode-step kernel timed out")
     packed = w.packed_bytes()
     norm_bytes = sum(t.numel() * 2 for L in w.layers
                      for t in (L.attn_norm, L.mlp_norm, L.q_norm, L.k_norm) if t is not None)
@@ -640,7 +660,7 @@ def main():
                         f"linears (16-entry cb, group {cfg.group}), bf16 embed/lm_head, "
                         f"prompt {n_prompt}",
             "layers": cfg.layers, "hidden": cfg.hidden, "intermediate": cfg.intermediate,
-            "vocab": cfg.vocab, "prompt": n_prompt, "decoded": args.warmup + args.steps,
+            "vocab": cfg.vocab, "prompt": n_prompt, "decoded": n_dec,
             "packed_linear_bytes": packed, "model_bytes_per_token": model_bytes,
             "step_gbs_model": round(model_bytes / (step_ms * 1e-3) / 1e9, 1),
             "step_frac_model": round(model_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -651,6 +671,7 @@ def main():
             "layers_alg_bytes": alg,
             "layers_kv_position": pos,
             "first_tokens": toks[n_prompt:n_prompt + 8],
+            "last_tokens": toks[n_prompt + n_dec - 8:n_prompt + n_dec],
         },
         "roofline": {
             "bound": "hbm",

@@ -757,43 +757,47 @@ static BlasWs blas_ws(int64_t M, int64_t N, int64_t K)
 // are independent: the second runs on a side stream forked from and joined
 // back into the caller's stream with events (both work under stream
 // capture), so the memory-bound kernels of one overlap the other's GEMM.
-// Per device: the side stream (default priority) and the two events,
-// created on the first call outside capture.  A shape's first call runs both chains
-// in order on the caller's stream (its library GEMM plans time their
-// candidate algorithms then, undisturbed).
+// Each caller stream gets its own side stream (default priority) and two
+// events, created on its first forked call outside capture (at most
+// kMaxSides per process; further caller streams run the chains in order):
+// a capture on one caller stream then never joins a side stream that
+// another thread's eager calls use.  The first call of a shape bucket (the
+// one whose library GEMM plans time their candidate algorithms) runs both
+// chains in order on the caller's stream, undisturbed.
 struct SideStream {
-    hipStream_t s = nullptr;
+    int dev = -1;
+    hipStream_t caller = nullptr, s = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
-    std::mutex mu;  // an event's record and the wait on it stay one step (concurrent callers)
+    std::mutex mu;  // held across fork, G chain and join (callers sharing a caller stream)
 };
+constexpr int kMaxSides = 32;
+constexpr size_t kMaxSeen = 1024;
 static std::mutex g_side_mu;
-static SideStream g_side[64];
-static std::vector<std::array<int64_t, 4>> g_bwd_seen;  // (device, M, N, K) run once
+static SideStream g_side[kMaxSides];
+static int g_nside = 0;
+static std::vector<std::array<int64_t, 4>> g_bwd_seen;  // (device, shape bucket) run once
+
+static int64_t pow2_ceil(int64_t v)
+{
+    int64_t b = 1;
+    while (b < v)
+        b <<= 1;
+    return b;
+}
 
 // The side stream to fork to, or nullptr (run in order).
 static SideStream *side_for(hipStream_t stream, int64_t M, int64_t N, int64_t K)
 {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0)
         return nullptr;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &cs) != hipSuccess)
         return nullptr;
     const bool capturing = cs != hipStreamCaptureStatusNone;
     std::lock_guard<std::mutex> lk(g_side_mu);
-    SideStream &sd = g_side[dev];
-    if (!sd.s && !capturing) {
-        if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess) {
-            sd.s = nullptr;
-            (void)hipGetLastError();
-        } else if (hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
-                   hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) {
-            sd.join = nullptr;
-            (void)hipGetLastError();
-        }
-    }
-    const std::array<int64_t, 4> key{dev, M, N, K};
-    bool seen = false;
+    const std::array<int64_t, 4> key{dev, pow2_ceil(M), pow2_ceil(N), pow2_ceil(K)};
+    bool seen = g_bwd_seen.size() >= kMaxSeen;
     for (const auto &k : g_bwd_seen)
         seen = seen || k == key;
     if (!seen) {
@@ -801,9 +805,51 @@ static SideStream *side_for(hipStream_t stream, int64_t M, int64_t N, int64_t K)
             g_bwd_seen.push_back(key);
         return nullptr;
     }
-    if (!sd.s)
+    for (int i = 0; i < g_nside; ++i)
+        if (g_side[i].dev == dev && g_side[i].caller == stream)
+            return g_side[i].join ? &g_side[i] : nullptr;
+    if (capturing || g_nside >= kMaxSides)
         return nullptr;
-    return sd.join ? &sd : nullptr;
+    SideStream &sd = g_side[g_nside++];
+    sd.dev = dev;
+    sd.caller = stream;
+    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess) {
+        sd.s = nullptr;
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) {
+        sd.join = nullptr;
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return &sd;
+}
+
+// Whether the library route can run on `stream` now: always outside
+// capture; under capture only once the device has a hipBLASLt handle
+// (creating one allocates device memory), else the fused kernels serve.
+static bool blas_usable(hipStream_t stream)
+{
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess)
+        return false;
+    if (cs == hipStreamCaptureStatusNone)
+        return true;
+    int dev = 0;
+    return hipGetDevice(&dev) == hipSuccess && blas_ready(dev);
+}
+
+// Workspace of the fused kernels: rexp [M] | gc partials | gy16 [M][N] |
+// grad_x split partials.
+static size_t fused_ws(int64_t M, int64_t N, int64_t K)
+{
+    const int64_t nwg = ((K + T - 1) / T) * ((N + T - 1) / T);
+    const int S = dx_splits(M, N, K);
+    return (size_t)((M * 4 + 255) / 256 * 256) + (size_t)nwg * 16 * sizeof(float) +
+           (size_t)((M * N * 2 + 255) / 256 * 256) +
+           (S > 1 ? (size_t)S * (size_t)M * (size_t)K * sizeof(float) : 0);
 }
 
 size_t backward_workspace(int64_t M, int64_t N, int64_t K, int levels, int group)
@@ -812,13 +858,12 @@ size_t backward_workspace(int64_t M, int64_t N, int64_t K, int levels, int group
     (void)group;
     if (M <= 0 || N <= 0 || K <= 0)
         return 0;
-    if (blas_route(M, N, K))
-        return blas_ws(M, N, K).total;
-    const int64_t nwg = ((K + T - 1) / T) * ((N + T - 1) / T);
-    const int S = dx_splits(M, N, K);
-    return (size_t)((M * 4 + 255) / 256 * 256) + (size_t)nwg * 16 * sizeof(float) +
-           (size_t)((M * N * 2 + 255) / 256 * 256) +
-           (S > 1 ? (size_t)S * (size_t)M * (size_t)K * sizeof(float) : 0);
+    const size_t f = fused_ws(M, N, K);
+    if (blas_route(M, N, K)) {
+        const size_t b = blas_ws(M, N, K).total;
+        return b > f ? b : f;  // either route may run (the fused one under capture)
+    }
+    return f;
 }
 
 bool backward_serves(const PackedDesc &w, int gy_dtype, int x_dtype)
@@ -852,7 +897,8 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         EP_HIP_CHECK(hipGetLastError());
         return EP_OK;
     }
-    const size_t need = backward_workspace(M, w.N, w.K, w.levels, w.group);
+    const bool lib = blas_route(M, w.N, w.K) && blas_usable(stream);
+    const size_t need = lib ? blas_ws(M, w.N, w.K).total : fused_ws(M, w.N, w.K);
     if (!ws || ws_bytes < need)
         return set_error(EP_ERR_WORKSPACE, "backward workspace of %zu bytes needed, %zu given",
                          need, ws_bytes);
@@ -861,7 +907,7 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         return set_error(EP_DECLINE_SHAPE, "fused backward needs 16-byte aligned rows");
     if (64 * gy.ld * 2 >= kBwOut || 64 * x.ld * 2 >= kBwOut)
         return set_error(EP_DECLINE_SHAPE, "fused backward: row strides of gy and x below 16M elements");
-    if (blas_route(M, w.N, w.K)) {
+    if (lib) {
         // grad_x = (gy16 . W16) * 2^rexp per row; G = gy^T . x -> grad_scale, grad_cb
         const BlasWs L = blas_ws(M, w.N, w.K);
         char *base = (char *)ws;
@@ -876,8 +922,9 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
             return set_error(EP_ERR_ARG, "grad_cb without grad_scale is not served");
         SideStream *side = gx.ptr && want_g ? side_for(stream, M, w.N, w.K) : nullptr;
         const hipStream_t gs = side ? side->s : stream;  // the G chain's stream
+        std::unique_lock<std::mutex> side_lock;
         if (side) {
-            std::lock_guard<std::mutex> lk(side->mu);
+            side_lock = std::unique_lock<std::mutex>(side->mu);
             EP_HIP_CHECK(hipEventRecord(side->fork, stream));
             EP_HIP_CHECK(hipStreamWaitEvent(side->s, side->fork, 0));
         }
@@ -928,7 +975,6 @@ int launch_backward(const PackedDesc &w, const ActDesc &gy, const ActDesc &x, in
         };
         const int rc = chains();
         if (side) {
-            std::lock_guard<std::mutex> lk(side->mu);
             EP_HIP_CHECK(hipEventRecord(side->join, side->s));
             EP_HIP_CHECK(hipStreamWaitEvent(stream, side->join, 0));
         }

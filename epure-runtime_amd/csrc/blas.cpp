@@ -10,16 +10,24 @@
 // with every special step (the materialization, the exact gy prescale,
 // the codebook reductions) in this library's own kernels.
 //
-// One handle per device, created on first use; plans (descriptors, layouts
-// and an algorithm) cached per shape.  The algorithm: the heuristic's
-// candidates are each timed once on the call's own operands when the plan
-// is made (the first call for a shape, outside stream capture; a plan made
-// during capture takes the heuristic's first choice), the fastest kept.
+// One handle per device, created on first use outside stream capture
+// (blas_ready() tells a caller under capture whether one exists).  Plans
+// (descriptors, layouts and an algorithm) are cached per exact shape, at
+// most kMaxPlans of them (the least recently used is destroyed to make
+// room), so callers with a new token count on every call do not grow it
+// without bound.  The algorithm: the heuristic's candidates are timed once
+// per shape bucket (each dimension rounded up to a power of two) on the
+// first call of the bucket outside stream capture -- that call waits for
+// its timing runs on the host -- and the fastest is kept for the bucket;
+// later shapes of the bucket take it when the heuristic offers it for
+// them, else the heuristic's first choice, with no timing and no host
+// wait.  A plan made during capture takes the heuristic's first choice.
 // Matrices are column-major in hipBLASLt's terms; callers pass row-major
 // buffers as their transposes.
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstring>
 #include <mutex>
 #include <vector>
 
@@ -36,11 +44,47 @@ struct Plan {
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
     hipblasLtMatmulAlgo_t algo;
+    uint64_t used = 0;  // last use (g_clock)
 };
+
+// The timed choice of one shape bucket.
+struct Timed {
+    int dev, ta, tb, ab_dtype;
+    int64_t bm, bn, bk;
+    size_t ws;
+    hipblasLtMatmulAlgo_t algo;
+};
+
+constexpr size_t kMaxPlans = 64;
+constexpr size_t kMaxTimed = 256;
 
 std::mutex g_mu;
 hipblasLtHandle_t g_handle[64] = {};
 std::vector<Plan> g_plans;
+std::vector<Timed> g_timed;
+uint64_t g_clock = 0;
+
+int64_t bucket(int64_t v)
+{
+    int64_t b = 1;
+    while (b < v)
+        b <<= 1;
+    return b;
+}
+
+void destroy_plan(Plan &p)
+{
+    if (p.desc)
+        hipblasLtMatmulDescDestroy(p.desc);
+    if (p.la)
+        hipblasLtMatrixLayoutDestroy(p.la);
+    if (p.lb)
+        hipblasLtMatrixLayoutDestroy(p.lb);
+    if (p.ld)
+        hipblasLtMatrixLayoutDestroy(p.ld);
+    p.desc = nullptr;
+    p.la = p.lb = p.ld = nullptr;
+}
 
 const char *status_name(hipblasStatus_t s)
 {
@@ -69,12 +113,17 @@ const char *status_name(hipblasStatus_t s)
             return set_error(EP_ERR_HIP, "%s: %s", #expr, status_name(_s));                   \
     } while (0)
 
-int handle_for(int dev, hipblasLtHandle_t *h)
+int handle_for(int dev, hipStream_t stream, hipblasLtHandle_t *h)
 {
     if (dev < 0 || dev >= 64)
         return set_error(EP_ERR_ARG, "device %d", dev);
-    if (!g_handle[dev])
+    if (!g_handle[dev]) {
+        // creating the handle allocates device memory: never under capture
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+            return set_error(EP_DECLINE_SHAPE, "library GEMM: no hipBLASLt handle yet (first call under capture)");
         EP_BLAS_CHECK(hipblasLtCreate(&g_handle[dev]));
+    }
     *h = g_handle[dev];
     return EP_OK;
 }
@@ -131,6 +180,17 @@ int make_plan(Plan &p, hipblasLtHandle_t h, const float *alpha, const void *A, c
     if (nres < 1)
         return set_error(EP_DECLINE_SHAPE, "hipBLASLt has no algorithm for this GEMM");
     p.algo = res[0].algo;
+    // the bucket's timed choice, where the heuristic offers it for this shape
+    const int64_t bm = bucket(p.m), bn = bucket(p.n), bk = bucket(p.k);
+    for (const Timed &t : g_timed) {
+        if (t.dev != p.dev || t.ta != p.ta || t.tb != p.tb || t.ab_dtype != p.ab_dtype || t.bm != bm ||
+            t.bn != bn || t.bk != bk || t.ws != p.ws)
+            continue;
+        for (int i = 0; i < nres; ++i)
+            if (std::memcmp(res[i].algo.data, t.algo.data, sizeof(t.algo.data)) == 0)
+                p.algo = res[i].algo;
+        return EP_OK;
+    }
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (nres < 2 || hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
         return EP_OK;
@@ -144,6 +204,8 @@ int make_plan(Plan &p, hipblasLtHandle_t h, const float *alpha, const void *A, c
                 p.algo = res[i].algo;
             }
         }
+        if (best > 0.0f && g_timed.size() < kMaxTimed)
+            g_timed.push_back(Timed{p.dev, p.ta, p.tb, p.ab_dtype, bm, bn, bk, p.ws, p.algo});
     }
     if (e0)
         (void)hipEventDestroy(e0);
@@ -157,6 +219,12 @@ int make_plan(Plan &p, hipblasLtHandle_t h, const float *alpha, const void *A, c
 
 size_t blas_workspace_bytes() { return (size_t)32 << 20; }
 
+bool blas_ready(int dev)
+{
+    std::lock_guard<std::mutex> lock(g_mu);
+    return dev >= 0 && dev < 64 && g_handle[dev] != nullptr;
+}
+
 // D[m x n] (f32, column-major, ldd) = alpha * op(A) . op(B); op(A) is m x k.
 int blas_gemm_f32out(int ta, int tb, int64_t m, int64_t n, int64_t k, int ab_dtype, const void *A,
                      int64_t lda, const void *B, int64_t ldb, float *D, int64_t ldd, float alpha,
@@ -168,7 +236,7 @@ int blas_gemm_f32out(int ta, int tb, int64_t m, int64_t n, int64_t k, int ab_dty
     EP_HIP_CHECK(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_mu);
     hipblasLtHandle_t h;
-    int rc = handle_for(dev, &h);
+    int rc = handle_for(dev, stream, &h);
     if (rc != EP_OK)
         return rc;
     Plan *plan = nullptr;
@@ -177,6 +245,15 @@ int blas_gemm_f32out(int ta, int tb, int64_t m, int64_t n, int64_t k, int ab_dty
             p.k == k && p.lda == lda && p.ldb == ldb && p.ldd == ldd && p.ws == ws_bytes)
             plan = &p;
     if (!plan) {
+        if (g_plans.size() >= kMaxPlans) {
+            // room for the new plan: destroy the least recently used one
+            size_t lru = 0;
+            for (size_t i = 1; i < g_plans.size(); ++i)
+                if (g_plans[i].used < g_plans[lru].used)
+                    lru = i;
+            destroy_plan(g_plans[lru]);
+            g_plans.erase(g_plans.begin() + (std::ptrdiff_t)lru);
+        }
         Plan p;
         p.dev = dev;
         p.ta = ta;
@@ -190,11 +267,14 @@ int blas_gemm_f32out(int ta, int tb, int64_t m, int64_t n, int64_t k, int ab_dty
         p.ldd = ldd;
         p.ws = ws_bytes;
         rc = make_plan(p, h, &alpha, A, B, D, ws, stream);
-        if (rc != EP_OK)
+        if (rc != EP_OK) {
+            destroy_plan(p);
             return rc;
+        }
         g_plans.push_back(p);
         plan = &g_plans.back();
     }
+    plan->used = ++g_clock;
     const float beta = 0.0f;
     EP_BLAS_CHECK(hipblasLtMatmul(h, plan->desc, &alpha, A, plan->la, B, plan->lb, &beta, D, plan->ld,
                                   D, plan->ld, &plan->algo, ws, ws_bytes, stream));

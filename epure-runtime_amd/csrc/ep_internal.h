@@ -169,6 +169,9 @@ int launch_dequant_tile(const PackedDesc &w, void *out, int out_dtype, int64_t l
 // Library GEMM (blas.cpp, hipBLASLt): D[m x n] (f32, column-major) = alpha *
 // op(A) . op(B), fp16 or bf16 operands, f32 accumulation.
 size_t blas_workspace_bytes();
+// true once device `dev` has a hipBLASLt handle (created by a call outside
+// stream capture); a caller under capture without one takes another route
+bool blas_ready(int dev);
 int blas_gemm_f32out(int ta, int tb, int64_t m, int64_t n, int64_t k, int ab_dtype, const void *A,
                      int64_t lda, const void *B, int64_t ldb, float *D, int64_t ldd, float alpha,
                      void *ws, size_t ws_bytes, hipStream_t stream);

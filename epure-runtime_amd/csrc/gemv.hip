@@ -885,6 +885,10 @@ int launch_gemv_gather(const PackedDesc &w, const ActDesc &x, int64_t T, const i
 {
     if (!gemv_serves(w, x, 1) || y.accumulate)
         return EP_DECLINE_SHAPE;
+    // token y's activations are read with 16-byte loads at x + y * ldx
+    const int esz = x.dtype == EP_F32 ? 4 : 2;
+    if (T > 1 && (x.ld * esz) % 16 != 0)
+        return set_error(EP_DECLINE_SHAPE, "gathered GEMV: x row stride not a multiple of 16 bytes");
     if (T > 65535)
         return set_error(EP_DECLINE_SHAPE, "gathered GEMV: at most 65535 tokens per launch");
     GemvArgs a = make_args(w, x, 1, y);

@@ -31,13 +31,16 @@
 // a wait that outlasts ~0.1 s marks the step failed (sync[2]) and all
 // waits then give up, so the grid always drains.
 //
-// GEMV arithmetic is the LUT dequant-GEMV of gemv.hip (pair table per
-// codebook, v_dot2_f32_f16 with f32 accumulation, group scale per 32
-// weights, DPP row sums, fixed-order cross-wave sums: deterministic), with
-// the activations compensated: after an exact power-of-two factor per 32
-// values each activation is split into two fp16 terms, hi = fp16(x) and
-// lo = fp16(x - hi) (~22 significant bits together), and every table lookup
-// feeds two dot products.  The codebook entries are exact fp16 values, so
+// GEMV arithmetic is a LUT dequant-GEMV (pair table per codebook in LDS:
+// one lookup per packed byte gives two fp16 weights) whose dot products run
+// on the matrix cores: v_mfma_f32_4x4x4_16b_f16 with a quad of rows as B
+// and the activations as A, f32 accumulation, the group scale applied per
+// 32 weights, permlane/DPP row sums and fixed-order cross-wave sums
+// (deterministic).  The activations are compensated: after an exact
+// power-of-two factor per 32 values each activation is split into two fp16
+// terms, hi = fp16(x) and lo = fp16(x - hi) (~22 significant bits
+// together), the A operand's rows 0 and 1, so every table lookup feeds two
+// dot products.  The codebook entries are exact fp16 values, so
 // the GEMV then agrees with float32 arithmetic to f32 accumulation order,
 // which keeps bf16 storage roundings downstream (KV rows, attention output)
 // on the same side as a float32 reference's.

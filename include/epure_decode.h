@@ -7,8 +7,10 @@
  * :373-415) and calls the fused kernel once per linear per token
  * (epure/kernels/cuda.py:88-117).  These entry points are the MI355X form
  * of that step: the packed GEMVs with the RMSNorm / SwiGLU of the decoder
- * fused into their activation load, grouped-query attention over a bf16 KV
- * cache, and the bf16 lm_head with greedy selection.
+ * fused into their activation load, grouped-query attention over a float32
+ * KV cache (the decoder computes in float32 semantics: residual, attention
+ * and the lm_head input are f32), and the bf16 lm_head with greedy
+ * selection.
  *
  * All entry points follow include/epure_hip.h conventions (device pointers,
  * caller-owned buffers, return codes, no host synchronisation).  The token

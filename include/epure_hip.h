@@ -14,9 +14,18 @@
  *
  * Conventions (all entry points):
  *   - plain device pointers and sizes; the caller owns every buffer,
- *     including workspaces; nothing here allocates or frees device memory;
+ *     including workspaces; nothing here allocates or frees device memory,
+ *     with one exception: the backward's library route (512 tokens and
+ *     more) creates a hipBLASLt handle per device on its first call, and a
+ *     side stream with two events per caller stream on a later call, both
+ *     kept for the process (never under stream capture);
  *   - work is enqueued on `stream` (a hipStream_t; NULL = the null stream);
- *     no host synchronisation, so every call is capture-safe;
+ *     no host synchronisation, with one exception: the first library-route
+ *     backward call of a shape bucket (every dimension rounded up to a
+ *     power of two) outside capture times its GEMM candidates and waits for
+ *     them on the host.  Every call is capture-safe (under capture the
+ *     backward takes no timing and, before a handle exists, the fused
+ *     kernels instead of the library);
  *   - return 0 on success; > 0 = DECLINE (the caller falls back to
  *     materialize, the `None` of epure/kernels/__init__.py:5-11);
  *     < 0 = error, with a message from ep_last_error().
@@ -121,9 +130,19 @@ int ep_expert_matmul(const void *x, int x_dtype, int64_t ldx, const int32_t *exp
  *   grad_x[M, K]            = gy[M, N] . W                (gx_dtype; NULL = skip)
  *   grad_cb[levels]   (f32) = sum_{idx==l} (gy^T x)[n,k] * scale[n, k/group]
  *   grad_scale[N, G]  (f32) = sum_{k in g} (gy^T x)[n,k] * cb[idx[n,k]]
- * (grad_cb / grad_scale NULL = skip).  grad_W is never written to memory.
- * grad_cb and grad_scale are overwritten, not accumulated, and are
- * deterministic (fixed-order reductions).  `packed` is only read.
+ * (grad_cb / grad_scale NULL = skip).  grad_cb and grad_scale are
+ * overwritten, not accumulated, and are deterministic (fixed-order
+ * reductions).  `packed` is only read.
+ * Two routes, chosen by shape:
+ *   M < 512 (or N, K < 256): the fused kernels.  Each grad_W tile stays in
+ *     registers and is reduced against the codebook in place: neither W nor
+ *     grad_W is written to memory; the workspace holds per-row exponents,
+ *     an fp16 copy of gy and grad_x split partials.
+ *   M >= 512: library GEMMs.  The workspace receives W materialized as fp16
+ *     [N, K] and grad_W = gy^T . x as f32 [N, K] (written once, read once by
+ *     the epilogue that forms grad_scale and grad_cb), plus the fp16 gy, an
+ *     f32 [M, K] grad_x product and two 32 MiB hipBLASLt workspaces.
+ * ep_dequant_matmul_bwd_workspace() returns the larger of the two needs.
  */
 size_t ep_dequant_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int levels, int group);
 int ep_dequant_matmul_bwd(const void *gy, int gy_dtype, int64_t ldgy,

@@ -1,9 +1,15 @@
 """Fused compressed-state backward against the closed forms
 (fine-tuning/README.md:62-68), float64 references.
 
-grad_x = gy W; G = gy^T x (never stored); grad_scale[n, g] = sum_{k in g}
-G[n, k] cb[idx[n, k]]; grad_cb[l] = sum_{idx == l} G[n, k] scale[n, g(k)].
+grad_x = gy W; G = gy^T x; grad_scale[n, g] = sum_{k in g} G[n, k]
+cb[idx[n, k]]; grad_cb[l] = sum_{idx == l} G[n, k] scale[n, g(k)].
 Indices must be bit-identical before and after.
+
+Two routes serve it: below 512 tokens the fused kernels (dx_kernel,
+dw_kernel) keep each G tile in accumulators and never write G or W; from
+512 tokens (N, K >= 256) the library route materializes W as fp16 and
+writes G as f32 [N, K] into the caller's workspace.  Both are checked at
+token counts on either side of the switch and at the config-4 shapes.
 """
 import hashlib
 
@@ -73,6 +79,42 @@ def test_backward_small_vs_closed_forms(n, k, m, group):
     assert rel(gx.float().cpu(), torch.from_numpy(wgx)) < 2e-3
     assert rel(gsc.cpu(), torch.from_numpy(wgsc)) < 1e-4
     assert rel(gcb.cpu(), torch.from_numpy(wgcb)) < 1e-4
+
+
+@pytest.mark.parametrize("n,k,m,group", [(512, 1024, 131, 128), (384, 768, 257, 64),
+                                         (256, 2048, 384, 32), (1024, 512, 511, 128)])
+def test_backward_fused_route_mid_tokens(n, k, m, group):
+    """Token counts 131..511: the fused kernels (G kept in accumulators) with
+    several 128-token tiles, ragged last tiles and the grad_x K split."""
+    idx, packed, scale, cb, s = make(n, k, group, seed=n + 2 * k + m)
+    x, gy = bf16((m, k), 13), bf16((m, n), 14, 1e-2)
+    print(f"case: fused backward N={n} K={k} M={m} group={group}", flush=True)
+    gx, gcb, gsc = run_bwd(s, gy, x)
+    wgx, wgcb, wgsc = ref.backward_f64(gy.float().cpu().numpy(), x.float().cpu().numpy(), idx,
+                                       scale, cb, group)
+    assert rel(gx.float().cpu(), torch.from_numpy(wgx)) < 2e-3
+    assert rel(gsc.cpu(), torch.from_numpy(wgsc)) < 1e-4
+    assert rel(gcb.cpu(), torch.from_numpy(wgcb)) < 1e-4
+
+
+@pytest.mark.parametrize("m", [384, 511])
+@pytest.mark.parametrize("n,k", [(2048, 6144), (6144, 2048)])
+def test_backward_config4_shapes_fused_route(n, k, m):
+    """The config-4 weights below 512 tokens (the fused route) against the
+    float64 closed forms; deterministic; indices untouched."""
+    _, _, _, _, s = make(n, k, seed=17)
+    before = hashlib.blake2b(s.packed.cpu().numpy().tobytes(), digest_size=16).hexdigest()
+    x, gy = bf16((m, k), 23), bf16((m, n), 24, 1e-2)
+    print(f"case: fused backward config-4 N={n} K={k} M={m}", flush=True)
+    gx, gcb, gsc = run_bwd(s, gy, x)
+    wgx, wgcb, wgsc = closed_forms_t64(gy, x, s)
+    assert rel(gx.float(), wgx) < 2e-3
+    assert rel(gsc, wgsc) < 1e-4
+    assert rel(gcb, wgcb) < 1e-4
+    a = run_bwd(s, gy, x)
+    assert all(torch.equal(p, q) for p, q in zip((gx, gcb, gsc), a))   # deterministic
+    after = hashlib.blake2b(s.packed.cpu().numpy().tobytes(), digest_size=16).hexdigest()
+    assert before == after
 
 
 @pytest.mark.parametrize("n,k,m,group", [(384, 640, 600, 64), (256, 384, 512, 32),
@@ -211,3 +253,26 @@ def test_backward_library_route_graph_replays():
         torch.cuda.synchronize()
         eager = run_bwd(s, gy, x)
         assert all(torch.equal(p, q) for p, q in zip(out, eager)), r
+
+
+def test_backward_library_route_many_token_counts():
+    """A new token count on every call (70 counts from 512 up): each count
+    gets its own library GEMM plans -- the cache keeps at most 64 and drops
+    the least recently used -- and reuses its shape bucket's timed
+    algorithm.  Every call matches the closed forms, and the first count,
+    run again after its plans were dropped, gives the same bits."""
+    n, k = 256, 384
+    _, _, _, _, s = make(n, k, 128, seed=55)
+    first = None
+    for i, m in enumerate(range(512, 582)):
+        x, gy = bf16((m, k), 200 + i), bf16((m, n), 300 + i, 1e-2)
+        gx, gcb, gsc = run_bwd(s, gy, x)
+        wgx, wgcb, wgsc = closed_forms_t64(gy, x, s)
+        assert rel(gx.float(), wgx) < 2e-3, m
+        assert rel(gsc, wgsc) < 1e-4, m
+        assert rel(gcb, wgcb) < 1e-4, m
+        if first is None:
+            first = (x, gy, gx, gcb, gsc)
+    x, gy = first[0], first[1]
+    again = run_bwd(s, gy, x)
+    assert all(torch.equal(p, q) for p, q in zip(first[2:], again))

@@ -177,3 +177,36 @@ def test_gathered_experts_clamp_ids_without_check():
     y = PackedExperts(s, check_ids=False)(x, torch.tensor([-3, 1, E + 2], device=DEV))
     want = PackedExperts(s)(x, torch.tensor([0, 1, E - 1], device=DEV))
     assert torch.equal(y, want)
+
+
+@pytest.mark.parametrize("pad", [3, 8])
+def test_gathered_experts_strided_rows(pad):
+    """Activation rows at a stride of k + pad elements (a column slice of a
+    wider buffer).  The gathered launch reads each row with 16-byte loads,
+    so a stride that is not a multiple of 8 bf16 elements is declined
+    (the grouped path serves it); a multiple of 8 runs gathered.  Both
+    match the oracle."""
+    from epure.kernels import _abi
+    from epure.kernels import cuda as cuda_kernel
+
+    E, n, k, T = 4, 256, 512, 5
+    s, packed, scale, cb = experts(E, n, k, 16, 128, seed=40 + pad)
+    g = torch.Generator(device=DEV).manual_seed(41)
+    wide = torch.randn(T, k + pad, generator=g, device=DEV).to(torch.bfloat16)
+    x = wide[:, :k]
+    assert x.stride() == (k + pad, 1)
+    ids = torch.tensor([3, 0, 1, 1, 2], device=DEV)
+    h = cuda_kernel._hot(s)
+    y_try = torch.empty(T, n, device=DEV, dtype=torch.bfloat16)
+    rc = _abi.lib.ep_expert_matmul(
+        x.data_ptr(), _abi.dtype_code(x.dtype), x.stride(0),
+        ids.to(torch.int32).contiguous().data_ptr(), T, h.packed.data_ptr(), h.scale.data_ptr(),
+        h.scale_dt, h.ld_scale, h.cb.data_ptr(), h.cb_dt, h.levels, h.group, E, n, k,
+        y_try.data_ptr(), _abi.dtype_code(y_try.dtype), y_try.stride(0), _abi.stream_handle(DEV))
+    torch.cuda.synchronize()
+    assert (rc > 0) == (pad % 8 != 0), (rc, _abi.last_error())
+    y = PackedExperts(s)(x, ids)
+    want = want_rows(x.float().cpu().numpy(), ids.cpu().tolist(), packed, scale, cb, E, n, k,
+                     128, 16)
+    err = np.abs(y.float().cpu().numpy() - want).max() / np.abs(want).max()
+    assert err < 2e-3 + 2.0 ** -8, err

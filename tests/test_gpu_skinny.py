@@ -233,6 +233,23 @@ def test_skinny_one_launch_accumulate_f16_x(out_dtype, levels, m, n):
     assert_close(out.float().cpu().numpy(), want + start, out_tol)
 
 
+@pytest.mark.parametrize("m,n,k", [(5, 8200, 2048), (8, 4096, 14336)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_skinny_one_launch_4bit_accumulate_f16_x(out_dtype, m, n, k):
+    """The 4-bit one-launch kernel (M 5..8) with fp16 activations: results
+    written, then added to y in the same launch, for every output dtype."""
+    _, packed, scale, cb, s = make(n, k, 16, seed=64 + m)
+    x32 = rng(65 + m).standard_normal((m, k)).astype(np.float32)
+    x = torch.from_numpy(x32).to(DEV).to(torch.float16)
+    want = rust_ref(x.float().cpu().numpy(), packed, scale, cb, n, k, 16, 128)
+    out_tol = TOL if out_dtype == torch.float32 else TOL + 2.0 ** -8
+    assert_close(run(s, x, out_dtype).float().cpu().numpy(), want, out_tol)
+    out = torch.from_numpy(rng(66 + m).standard_normal((m, n)).astype(np.float32)).to(DEV).to(out_dtype)
+    start = out.float().cpu().numpy()
+    run(s, x, out_dtype, accumulate=True, out=out)
+    assert_close(out.float().cpu().numpy(), want + start, out_tol)
+
+
 def test_skinny_one_launch_rows_of_very_different_magnitude():
     """A power of two per row and round: rows at 3e5, 1, 1e-12, 1e-30 and 0
     stay exact relative to their own size (the same five again in the

@@ -70,6 +70,39 @@ def test_dequant_tile_reads_zero_beyond_levels():
     assert w.tolist() == [[1.0, 4.0, 10.0, 0.0]]
 
 
+@pytest.mark.parametrize("levels,n,k,group,f32_scale", [
+    (16, 7, 256, 128, False),     # 4-bit, two groups per row
+    (16, 5, 101, 32, False),      # odd K: rows straddle bytes of the flat stream
+    (16, 3, 77, 16, True),        # odd K, f32 scales (after make_trainable)
+    (10, 6, 96, 32, False),       # levels < 16: indices 10..15 read 0
+    (256, 4, 300, 128, False),    # 8-bit, partial last group
+    (256, 5, 129, 64, True),      # 8-bit, odd K, f32 scales
+    (200, 3, 64, 64, False),      # 8-bit with levels < 256
+])
+def test_dense_tile_matches_dequant_tile(levels, n, k, group, f32_scale):
+    """oracle/decoder.py dense_tile (the torch tile the large-shape GPU tests
+    and the decoder oracle use) equals dequant_tile_f32 (pinned above
+    against the pure-Python product) bit for bit."""
+    from oracle.decoder import dense_tile
+
+    r = rng(n * 1000 + k)
+    # indices over the whole nibble/byte range, so idx >= levels occurs
+    idx = r.integers(0, 16 if levels <= 16 else 256, (n, k), dtype=np.uint8)
+    packed = ref.pack4(idx, levels)
+    cb = np.sort(r.standard_normal(levels)).astype(np.float16)
+    g = (k + group - 1) // group
+    scale = (np.abs(r.normal(0.0, 0.02, (n, g))) + 1e-3).astype(np.float16)
+    if f32_scale:
+        scale = scale.astype(np.float32) * np.float32(1.0 + 2.0 ** -20)   # not fp16-valued
+    want = ref.dequant_tile_f32(ref.unpack4(packed, n * k, levels).reshape(n, k), scale, cb, group)
+    got = dense_tile(torch.from_numpy(packed), torch.from_numpy(scale), torch.from_numpy(cb),
+                     n, k, group, levels).numpy()
+    assert got.dtype == np.float32 and got.shape == (n, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if levels < (16 if levels <= 16 else 256):
+        assert (got[idx >= levels] == 0).all() and (idx >= levels).any()
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 def test_materialize_matches_torch_expression(dtype):
     tdt = {"f16": torch.float16, "bf16": torch.bfloat16}[dtype]

@@ -65,11 +65,14 @@ def test_noalloc_matches_workspace_entry_on_consecutive_calls():
 def test_noalloc_rejects_requests_beyond_the_scratch():
     need = _abi.lib.ep_dequant_matmul_workspace(2048, 14336, 14336, 16, 128)
     assert need > _abi.lib.ep_noalloc_scratch_bytes()
-    s, x, _ = _case(256, 512, 1, 16, seed=90)
-    h = cuda._hot(s)
-    # the size check runs before any pointer is used or kernel launched
+    # Null x, y and weight pointers: the size check rejects the request
+    # first; were it ever skipped, the null pointers are rejected with
+    # EP_ERR_ARG before any launch, so no kernel can run on them.
     rc = _abi.lib.ep_dequant_matmul_noalloc(
-        x.data_ptr(), _abi.BF16, 14336, h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt,
-        h.ld_scale, h.cb.data_ptr(), h.cb_dt, 16, 128, 2048, 14336, 14336, x.data_ptr(),
-        _abi.F32, 14336, 0, _abi.stream_handle(DEV))
+        None, _abi.BF16, 14336, None, None, _abi.F16, 112, None, _abi.F32, 16, 128, 2048,
+        14336, 14336, None, _abi.F32, 14336, 0, _abi.stream_handle(DEV))
     assert rc == -3 and "scratch" in _abi.last_error()
+    rc = _abi.lib.ep_dequant_matmul_noalloc(
+        None, _abi.BF16, 512, None, None, _abi.F16, 4, None, _abi.F32, 16, 128, 1, 256, 512,
+        None, _abi.F32, 256, 0, _abi.stream_handle(DEV))
+    assert rc == -1 and "null" in _abi.last_error()
