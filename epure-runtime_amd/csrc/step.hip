@@ -228,6 +228,25 @@ struct Spin {
     }
 };
 
+// f(std::integral_constant<int, 0>{}) .. f(..<N - 1>{}) in order, expanded at
+// compile time.
+template <int I, int N>
+struct StaticFor {
+    template <class F>
+    static EP_DEV void run(F &f)
+    {
+        if constexpr (I < N) {
+            f(std::integral_constant<int, I>{});
+            StaticFor<I + 1, N>::run(f);
+        }
+    }
+};
+template <int N, class F>
+EP_DEV void static_for(F &&f)
+{
+    StaticFor<0, N>::run(f);
+}
+
 // true when `p` holds on every active lane of the wave (a wave-uniform value)
 EP_DEV bool wave_all(bool p) { return __builtin_amdgcn_ballot_w64(!p) == 0; }
 
@@ -509,35 +528,60 @@ struct Gemv {
                 issue(bb[k], sg, k, sl);
     }
 
-    // Runs the share; outputs are tagged (`tag`).  MODE_ACC adds the share's
-    // residual rows (hv, one per thread, loaded with the staging) and writes
+    // Runs the share; outputs are tagged (`tag`).
+    //
+    // Each wave first stages its own slabs of the activation vector
+    // (`stage_fn()`, which waits only for the producers of those slabs and
+    // returns the lane's sum of squares of the source values) and starts its
+    // blocks right away: no workgroup barrier between staging and compute,
+    // so a wave whose slabs are ready computes while the others still wait.
+    // RMSNorm phases (MODE_STORE: q|k|v, MODE_SWIGLU: gate|up) put each
+    // wave's sum of squares in part8; the factor 1/rms multiplies the
+    // finished dot products.  MODE_ACC adds the share's residual rows
+    // (`hv()`, one per output thread, taken before the blocks) and writes
     // the sum to ht (and to h0 when `last`).
     //
     // `nx(bi)` runs after block bi (every wave, every bi < MAXB, in order;
     // bi is a constant of the unrolled loop): the next phase's loads go out
     // there, into the registers the computed blocks left.
-    template <int MODE, class NX>
+    template <int MODE, int K, class STG, class HV, class NX>
     static EP_DEV void run(Blk (&bb)[NBUF], const Segs &sg, int group, const uint32_t *tab,
-                           const uint32_t *xs, const uint32_t *xlo, const float *xf, float *red,
-                           float *hrow, float hv, float rinv, uint64_t *ht, float *h0, bool last,
-                           uint64_t *act, uint32_t tag, NX &&nx)
+                           const PhaseLds &pl, float *part8, float *hrow, float eps, STG &&stage_fn, HV &&hv,
+                           uint64_t *ht, float *h0, bool last, uint64_t *act, uint32_t tag, NX &&nx)
     {
+        constexpr bool RMS = MODE != MODE_ACC;
         const int wv = wave_id();
-        // residual rows of the share (loaded by the caller with the staging)
-        if constexpr (MODE == MODE_ACC) {
-            if (tid_fresh() < (sg.qb - sg.qa) * 4)
-                hrow[tid_fresh()] = hv;
-        }
         // Straight-line over the most blocks a share can hold, NBUF buffers
         // rotated (a register copy of a block would wait for its loads):
         // block bi + NBUF - 1 is issued into the buffer block bi - 1 left.
         // Every block's loads are issued (zero-length where not live): with
         // no loop and no conditional loads the compiler's wait before each
         // block counts exactly the younger blocks still in flight.
+        // (every wave stages: an idle wave's slabs read slab 0 and convert
+        // nothing; staging outside the branch below keeps the register
+        // allocation of its two sides alike)
+        const float ssq = stage_fn();
+        if constexpr (MODE == MODE_ACC) {
+            // the share's residual rows (threads below nrow: wave 0), loaded
+            // with the staging, into LDS for the output threads (a register
+            // held across the blocks would take one from the prefetch)
+            if (tid_fresh() < (sg.qb - sg.qa) * 4)
+                hrow[tid_fresh()] = hv();
+        }
+        if constexpr (RMS) {
+            // row groups past the first stage the same slabs again
+            const float sw = wave_sum(ssq);
+            if ((tid_fresh() & 63) == 0)
+                part8[wv] = wave_on(wv) && wv < WPR ? sw : 0.0f;
+        }
+        // the wave's own staging stores are ordered before its reads (LDS
+        // operations of one wave execute in order; this keeps the compiler
+        // from moving a read above them)
+        asm volatile("" ::: "memory");
         if (wave_on(wv)) {
             const SLane sl = slane(group);
             const LaneC lc = lane_consts(sl);
-            stream(bb, sg, sl, lc, xs, xlo, xf, tab, red, nx);
+            stream(bb, sg, sl, lc, pl.xs, pl.xl, pl.xf, tab, pl.red, nx);
         } else {
 #pragma unroll
             for (int bi = 0; bi < MAXB; ++bi)
@@ -548,14 +592,22 @@ struct Gemv {
         const int t = tid_fresh();
         const int nrow = (sg.qb - sg.qa) * 4;
         if (t < nrow) {
+            float rinv = 1.0f;
+            if constexpr (RMS) {
+                float q2 = 0.0f;
+#pragma unroll
+                for (int w2 = 0; w2 < kWaves; ++w2)
+                    q2 += part8[w2];
+                rinv = rsqrtf(q2 / (float)K + eps);
+            }
             const int q = t / 4;
             const int gg = (q % QPB) / RQ;  // row group that computed the row
             float v = 0.0f, u = 0.0f;
 #pragma unroll
             for (int wr = 0; wr < WPR; ++wr) {
-                v += red[(gg * WPR + wr) * RED_ROWS + t];
+                v += pl.red[(gg * WPR + wr) * RED_ROWS + t];
                 if constexpr (PAIRED)
-                    u += red[(gg * WPR + wr) * RED_ROWS + RED_ROWS / 2 + t];
+                    u += pl.red[(gg * WPR + wr) * RED_ROWS + RED_ROWS / 2 + t];
             }
             const int row = sg.qa * 4 + t;
             if constexpr (MODE == MODE_STORE) {
@@ -824,19 +876,22 @@ EP_DEV void build_tables(uint32_t *tab, uint16_t *cb16, float cbv, int ntab)
     // flight at once, then eight 16-byte writes.
     const int t = tid_fresh();
     const int slot = (t >> 3) & 1;
-    if (slot >= ntab)
-        return;
-    const uint16_t *cb = cb16 + slot * 16;
-    const uint32_t lo = cb[(t >> 4) & 15];
-    uint32_t hi[8];
+    if (slot < ntab) {
+        const uint16_t *cb = cb16 + slot * 16;
+        const uint32_t lo = cb[(t >> 4) & 15];
+        uint32_t hi[8];
 #pragma unroll
-    for (int it = 0; it < 8; ++it)
-        hi[it] = cb[(t >> 8) + 2 * it];
+        for (int it = 0; it < 8; ++it)
+            hi[it] = cb[(t >> 8) + 2 * it];
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-        const uint32_t v = lo | (hi[it] << 16);
-        ((u32x4_t *)tab)[t + kThreads * it] = (u32x4_t){v, v, v, v};
+        for (int it = 0; it < 8; ++it) {
+            const uint32_t v = lo | (hi[it] << 16);
+            ((u32x4_t *)tab)[t + kThreads * it] = (u32x4_t){v, v, v, v};
+        }
     }
+    // the tables are complete before any wave (which stages its own slabs
+    // and starts its blocks without a workgroup barrier) reads them
+    lds_sync();
 }
 
 // ---------------------------------------------------------------- activations
@@ -844,136 +899,138 @@ constexpr int XS_RMS_H0 = 0;  // h0 (f32, untagged: written by an earlier launch
 constexpr int XS_RMS = 1;     // tagged residual * norm weight (bf16); 1/rms returned
 constexpr int XS_F32 = 3;     // tagged f32 (attention output, SwiGLU output)
 
-// Converts the K-vector to fp16 pairs in LDS with one exact power-of-two
-// factor per 32 values (the 4 threads of a 32-value chunk agree on it
-// through a quad max), the same staging as gemv.hip's.  The loads of a
-// thread's groups (and of the norm weights) are issued together, up to 3
-// groups per batch; tagged groups whose tags are not all `tag` yet are then
-// re-read together, so a stale vector costs one round trip per re-read and
-// batch, not one per group.
-template <int XS, int K>
-EP_DEV float stage(const void *x, const uint16_t *w, float eps, uint32_t tag, uint32_t *xs,
-                   uint32_t *xl, float *xf, float *part8, int *err)
+// Stages this wave's slabs of a phase's K-vector into LDS as fp16 pairs
+// with one exact power-of-two factor per 32 values (the 4 lanes of a
+// 32-value chunk agree on it through a quad max), the same staging as
+// gemv.hip's, split into hi and lo terms.  Slab s holds values 512 s ..
+// 512 s + 511; lane l converts values 8 l .. 8 l + 7 of each of the wave's
+// slabs (P::slab(j, wave) for the slabs the wave computes).  The loads of
+// a batch of them (and of the norm weights) go out together; tagged groups
+// whose tags are not all `tag` yet are re-read together (coherently), so a
+// wave waits one round trip per re-read, and only for its own slabs'
+// producers.  Returns the lane's sum of squares of the source values (RMS
+// sources; the norm weight multiplies each value after it is squared).
+template <class P, int XS, int K, int J0, int NJ>
+EP_DEV float stage_batch(const void *x, const uint16_t *w, uint32_t tag, const PhaseLds &pl, int *err)
 {
-    constexpr int NE = K / 8;                            // groups of 8 values
-    constexpr int NIT = (NE + kThreads - 1) / kThreads;  // groups per thread
-    // groups in flight per batch (16 VGPRs each): all of them up to 3
-    constexpr int NB = NIT <= 3 ? NIT : 2;
     constexpr bool TAGGED = XS != XS_RMS_H0;
     constexpr bool RMS = XS == XS_RMS_H0 || XS == XS_RMS;
-    // exact extent: a group index past the vector reads zeros (never used)
+    const int wv = wave_id();
+    const int lane = tid_fresh() & 63;
+    // exact extent: every group lies inside the vector
     const auto rs = buffer_rsrc(x, TAGGED ? (uint32_t)K * 8u : (uint32_t)K * 4u);
-    const int t0 = tid_fresh();
+    u32x4_t q[NJ][4];
+    u32x4_t wr[NJ];
+#pragma unroll
+    for (int i = 0; i < NJ; ++i) {
+        // group of 8 values (an idle slab reads slab 0: never used)
+        const uint32_t e = (uint32_t)(P::slab(J0 + i, wv) * 64 + lane);
+        if constexpr (TAGGED) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h)  // a ring slot: first through the caches
+                q[i][h] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(e * 64 + 16 * h), 0, 0);
+        } else {
+            q[i][0] = ldc16(rs, e * 32);
+            q[i][1] = ldc16(rs, e * 32 + 16);
+        }
+        if constexpr (RMS)
+            wr[i] = ldg((const u32x4_t *)(w + e * 8));
+    }
+    if constexpr (TAGGED) {
+        auto ready = [&](const u32x4_t (&g)[4]) {
+            bool ok = true;
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                ok = ok && g[h][1] == tag && g[h][3] == tag;
+            return ok;
+        };
+        Spin sp;
+        for (;;) {
+            bool all = true;
+#pragma unroll
+            for (int i = 0; i < NJ; ++i)
+                all = all && (!P::slab_on(J0 + i, wv) || ready(q[i]));
+            if (all || !sp.again(err))
+                break;
+            // (a compile-time loop: the unroller declines this one inside
+            // the poll loop, and a rolled loop would index q dynamically)
+            static_for<NJ>([&](auto ic) {
+                constexpr int i = decltype(ic)::value;
+                if (P::slab_on(J0 + i, wv) && !ready(q[i])) {
+                    const uint32_t e = (uint32_t)(P::slab(J0 + i, wv) * 64 + lane);
+#pragma unroll
+                    for (int h = 0; h < 4; ++h)
+                        q[i][h] = ldc16(rs, e * 64 + 16 * h);
+                }
+            });
+        }
+    }
     float ssq = 0.0f;
 #pragma unroll
-    for (int b0 = 0; b0 < NIT; b0 += NB) {
-        u32x4_t q[NB][4];
-        u32x4_t wv[NB];
+    for (int i = 0; i < NJ; ++i) {
+        if (!P::slab_on(J0 + i, wv))  // wave-uniform
+            continue;
+        const uint32_t e = (uint32_t)(P::slab(J0 + i, wv) * 64 + lane);
+        float v[8];
 #pragma unroll
-        for (int k = 0; k < NB; ++k) {
-            const uint32_t e = (uint32_t)(t0 + (b0 + k) * kThreads);
+        for (int h = 0; h < 4; ++h) {
             if constexpr (TAGGED) {
-#pragma unroll
-                for (int h = 0; h < 4; ++h)  // a ring slot: first through the caches
-                    q[k][h] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(e * 64 + 16 * h), 0, 0);
+                v[2 * h] = __uint_as_float(q[i][h][0]);
+                v[2 * h + 1] = __uint_as_float(q[i][h][2]);
             } else {
-                q[k][0] = ldc16(rs, e * 32);
-                q[k][1] = ldc16(rs, e * 32 + 16);
-            }
-            if constexpr (RMS)
-                wv[k] = ldg((const u32x4_t *)(w + (e < (uint32_t)NE ? e : 0u) * 8));
-        }
-        if constexpr (TAGGED) {
-            auto ready = [&](const u32x4_t (&g)[4]) {
-                bool ok = true;
-#pragma unroll
-                for (int h = 0; h < 4; ++h)
-                    ok = ok && g[h][1] == tag && g[h][3] == tag;
-                return ok;
-            };
-            Spin sp;
-            for (;;) {
-                bool all = true;
-#pragma unroll
-                for (int k = 0; k < NB; ++k)
-                    all = all && (b0 + k >= NIT || t0 + (b0 + k) * kThreads >= NE || ready(q[k]));
-                if (all || !sp.again(err))
-                    break;
-#pragma unroll
-                for (int k = 0; k < NB; ++k) {
-                    const uint32_t e = (uint32_t)(t0 + (b0 + k) * kThreads);
-                    if (b0 + k < NIT && e < (uint32_t)NE && !ready(q[k])) {
-#pragma unroll
-                        for (int h = 0; h < 4; ++h)
-                            q[k][h] = ldc16(rs, e * 64 + 16 * h);
-                    }
-                }
+                v[h] = __uint_as_float(q[i][0][h]);
+                v[4 + h] = __uint_as_float(q[i][1][h]);
             }
         }
-#pragma unroll
-        for (int k = 0; k < NB; ++k) {
-            const int e = t0 + (b0 + k) * kThreads;
-            if (b0 + k >= NIT || e >= NE)
-                break;
-            float v[8];
+        if constexpr (RMS) {
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
-                if constexpr (TAGGED) {
-                    v[2 * h] = __uint_as_float(q[k][h][0]);
-                    v[2 * h + 1] = __uint_as_float(q[k][h][2]);
-                } else {
-                    v[h] = __uint_as_float(q[k][0][h]);
-                    v[4 + h] = __uint_as_float(q[k][1][h]);
-                }
+                float w0, w1;
+                unpack_pair<EP_BF16>(wr[i][h], w0, w1);
+                ssq = fmaf(v[2 * h], v[2 * h], fmaf(v[2 * h + 1], v[2 * h + 1], ssq));
+                v[2 * h] *= w0;
+                v[2 * h + 1] *= w1;
             }
-            if constexpr (RMS) {
-#pragma unroll
-                for (int h = 0; h < 4; ++h) {
-                    float w0, w1;
-                    unpack_pair<EP_BF16>(wv[k][h], w0, w1);
-                    ssq = fmaf(v[2 * h], v[2 * h], fmaf(v[2 * h + 1], v[2 * h + 1], ssq));
-                    v[2 * h] *= w0;
-                    v[2 * h + 1] *= w1;
-                }
-            }
-            float am = 0.0f;
-#pragma unroll
-            for (int h = 0; h < 8; ++h)
-                am = fmaxf(am, fabsf(v[h]));
-            am = fmaxf(am, dpp_mov<0xb1>(am));  // lanes ^ 1
-            am = fmaxf(am, dpp_mov<0x4e>(am));  // lanes ^ 2
-            const int ex = row_exponent(am);
-            const float pw = ldexpf(1.0f, -ex);
-            u32x4_t q4, l4;
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const float a0 = v[2 * p] * pw, a1 = v[2 * p + 1] * pw;
-                const f16_t h0 = (f16_t)a0, h1 = (f16_t)a1;
-                q4[p] = (uint32_t)f16_bits(h0) | ((uint32_t)f16_bits(h1) << 16);
-                l4[p] = (uint32_t)f16_bits((f16_t)(a0 - (float)h0)) |
-                        ((uint32_t)f16_bits((f16_t)(a1 - (float)h1)) << 16);
-            }
-            *(u32x4_t *)(xs + e * 4) = q4;
-            *(u32x4_t *)(xl + e * 4) = l4;
-            if ((e & 3) == 0)
-                xf[e >> 2] = ldexpf(1.0f, ex);
         }
-    }
-    float rinv = 1.0f;
-    if constexpr (RMS) {
-        const float s = wave_sum(ssq);
-        if ((tid_fresh() & 63) == 0)
-            part8[tid_fresh() >> 6] = s;
-    }
-    lds_sync();
-    if constexpr (RMS) {
-        float q2 = 0.0f;
+        float am = 0.0f;
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves; ++w2)
-            q2 += part8[w2];
-        rinv = rsqrtf(q2 / (float)K + eps);
+        for (int h = 0; h < 8; ++h)
+            am = fmaxf(am, fabsf(v[h]));
+        am = fmaxf(am, dpp_mov<0xb1>(am));  // lanes ^ 1
+        am = fmaxf(am, dpp_mov<0x4e>(am));  // lanes ^ 2
+        const int ex = row_exponent(am);
+        const float pw = ldexpf(1.0f, -ex);
+        u32x4_t q4, l4;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const float a0 = v[2 * p] * pw, a1 = v[2 * p + 1] * pw;
+            const f16_t h0 = (f16_t)a0, h1 = (f16_t)a1;
+            q4[p] = (uint32_t)f16_bits(h0) | ((uint32_t)f16_bits(h1) << 16);
+            l4[p] = (uint32_t)f16_bits((f16_t)(a0 - (float)h0)) |
+                    ((uint32_t)f16_bits((f16_t)(a1 - (float)h1)) << 16);
+        }
+        *(u32x4_t *)(pl.xs + e * 4) = q4;
+        *(u32x4_t *)(pl.xl + e * 4) = l4;
+        if ((e & 3) == 0)
+            pl.xf[e >> 2] = ldexpf(1.0f, ex);
     }
-    return rinv;
+    return ssq;
+}
+
+// The wave's slabs in batches of at most kStageBatch: one slab (16 VGPRs of
+// tagged values in flight) per batch.  Two per batch measured no faster
+// and cost the down phase a prefetched block (the registers do not allow
+// both).
+constexpr int kStageBatch = 1;
+template <class P, int XS, int K, int J0 = 0>
+EP_DEV float stage_wave(const void *x, const uint16_t *w, uint32_t tag, const PhaseLds &pl, int *err)
+{
+    constexpr int NJ = P::SPW - J0 < kStageBatch ? P::SPW - J0 : kStageBatch;
+    const float s = stage_batch<P, XS, K, J0, NJ>(x, w, tag, pl, err);
+    if constexpr (J0 + NJ < P::SPW)
+        return s + stage_wave<P, XS, K, J0 + NJ>(x, w, tag, pl, err);
+    else
+        return s;
 }
 
 // ---------------------------------------------------------------- attention
@@ -1324,9 +1381,10 @@ EP_DEV void attn_item(const StepArgs &a, LayerC &L, int l, uint32_t seq, int j, 
 }
 
 // ---------------------------------------------------------------- kernel
-// The residual rows an accumulating phase owns (one per thread): the load
-// is issued before the phase's activation staging (residual_issue) and
-// checked after it (residual_take), so both share one round trip.  Layer
+// The residual rows an accumulating phase owns (one per output thread):
+// the load is issued before the phase's activation staging
+// (residual_issue), so it shares the staging's round trip, and checked at
+// the phase's output (residual_take).  Layer
 // 0's o reads the untagged input h0, later phases the tagged residual.
 EP_DEV uint64_t residual_issue(const Segs &sg, const StepArgs &a, const uint64_t *hsrc)
 {
@@ -1538,13 +1596,14 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // ---- q|k|v (RMSNorm of the residual in the activation load)
         {
             const Segs sq = segs_qkv(L, a, sh);
-            const float rinv =
-                l == 0 ? stage<XS_RMS_H0, M::H>(a.h0, L.attn_norm, a.eps, 0, lh.xs, lh.xl, lh.xf, part8, err)
-                       : stage<XS_RMS, M::H>(h_prev, L.attn_norm, a.eps, tag_of(seq, l - 1, PH_DOWN),
-                                             lh.xs, lh.xl, lh.xf, part8, err);
-            PQ::template run<MODE_STORE>(qb, sq, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
-                                         rinv, nullptr, a.h0, false, nullptr, tag_of(seq, l, PH_QKV),
-                                         [](int) {});
+            const uint32_t tprev = tag_of(seq, l - 1, PH_DOWN);
+            PQ::template run<MODE_STORE, M::H>(
+                qb, sq, a.group, tab, lh, part8, hrow, a.eps,
+                [&] {
+                    return l == 0 ? stage_wave<PQ, XS_RMS_H0, M::H>(a.h0, L.attn_norm, 0, lh, err)
+                                  : stage_wave<PQ, XS_RMS, M::H>(h_prev, L.attn_norm, tprev, lh, err);
+                },
+                [] { return 0.0f; }, nullptr, a.h0, false, nullptr, tag_of(seq, l, PH_QKV), [](int) {});
         }
         stamp(a, l, 1);
         // Attention workgroups issue their first item's K/V rows (cached by
@@ -1602,18 +1661,20 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
             const Segs so = segs_one(L, 3, M::H, sh.ldsb_o, sh);
             if (so.qb > so.qa) {
                 const uint64_t hraw = residual_issue(so, a, h_prev);
-                stage<XS_F32, M::HQD>(at_l, nullptr, 0.0f, tag_of(seq, l, PH_ATT), lo.xs, lo.xl, lo.xf,
-                                      part8, err);
-                const float hv = residual_take(hraw, so, a, h_prev, tag_of(seq, l - 1, PH_DOWN));
-                stamp(a, l, 3);
-                const Segs sgu = segs_gu(L, sh);
-                PO::template run<MODE_ACC>(ob, so, a.group, tab, lo.xs, lo.xl, lo.xf, lo.red, hrow, hv,
-                                           1.0f, h_o, a.h0, false, nullptr, tag_of(seq, l, PH_O),
-                                           [&](int bi) {
-                                               PG::prefetch_range(gb, sgu, a.group,
-                                                                  kGuEarly + spread_lo<kGuLate, PO::MAXB>(bi),
-                                                                  kGuEarly + spread_lo<kGuLate, PO::MAXB>(bi + 1));
-                                           });
+                const uint32_t tatt = tag_of(seq, l, PH_ATT), tprev = tag_of(seq, l - 1, PH_DOWN);
+                PO::template run<MODE_ACC, M::HQD>(
+                    ob, so, a.group, tab, lo, part8, hrow, 0.0f,
+                    [&] {
+                        const float r = stage_wave<PO, XS_F32, M::HQD>(at_l, nullptr, tatt, lo, err);
+                        stamp(a, l, 3);
+                        return r;
+                    },
+                    [&] { return residual_take(hraw, so, a, h_prev, tprev); }, h_o, a.h0, false, nullptr,
+                    tag_of(seq, l, PH_O), [&](int bi) {
+                        const Segs sgu = segs_gu(L, sh);  // (formed where used: scalar registers)
+                        PG::prefetch_range(gb, sgu, a.group, kGuEarly + spread_lo<kGuLate, PO::MAXB>(bi),
+                                           kGuEarly + spread_lo<kGuLate, PO::MAXB>(bi + 1));
+                    });
             } else {
                 PG::prefetch_range(gb, segs_gu(L, sh), a.group, kGuEarly, PG::NBUF - 1);
             }
@@ -1631,17 +1692,19 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         // ---- gate|up -> silu(gate) * up
         {
             const Segs sg = segs_gu(L, sh);
-            const float rinv = stage<XS_RMS, M::H>(h_o, L.mlp_norm, a.eps, tag_of(seq, l, PH_O),
-                                                   lh.xs, lh.xl, lh.xf, part8, err);
-            stamp(a, l, 5);
-            const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
-            PG::template run<MODE_SWIGLU>(gb, sg, a.group, tab, lh.xs, lh.xl, lh.xf, lh.red, hrow, 0.0f,
-                                          rinv, nullptr, a.h0, false, actl, tag_of(seq, l, PH_ACT),
-                                          [&](int bi) {
-                                              PD::prefetch_range(db, sd, a.group,
-                                                                 spread_lo<PD::NBUF - 1, PG::MAXB>(bi),
-                                                                 spread_lo<PD::NBUF - 1, PG::MAXB>(bi + 1));
-                                          });
+            const uint32_t to = tag_of(seq, l, PH_O);
+            PG::template run<MODE_SWIGLU, M::H>(
+                gb, sg, a.group, tab, lh, part8, hrow, a.eps,
+                [&] {
+                    const float r = stage_wave<PG, XS_RMS, M::H>(h_o, L.mlp_norm, to, lh, err);
+                    stamp(a, l, 5);
+                    return r;
+                },
+                [] { return 0.0f; }, nullptr, a.h0, false, actl, tag_of(seq, l, PH_ACT), [&](int bi) {
+                    const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
+                    PD::prefetch_range(db, sd, a.group, spread_lo<PD::NBUF - 1, PG::MAXB>(bi),
+                                       spread_lo<PD::NBUF - 1, PG::MAXB>(bi + 1));
+                });
         }
         stamp(a, l, 6);
         {
@@ -1656,21 +1719,23 @@ __global__ void __launch_bounds__(kThreads) decode_step_kernel(StepArgs a)
         {
             const Segs sd = segs_one(L, 6, M::H, sh.ldsb_i, sh);
             const uint64_t hraw = residual_issue(sd, a, h_o);
-            stage<XS_F32, M::I>(actl, nullptr, 0.0f, tag_of(seq, l, PH_ACT), li.xs, li.xl, li.xf, part8,
-                                err);
-            const float hv = residual_take(hraw, sd, a, h_o, tag_of(seq, l, PH_O));
-            stamp(a, l, 7);
-            // the next layer's q|k|v (an empty share after the last layer)
-            Segs sqn = segs_qkv(layers[last ? l : l + 1], a, sh);
-            if (last)
-                sqn.qb = sqn.qa;
-            PD::template run<MODE_ACC>(db, sd, a.group, tab, li.xs, li.xl, li.xf, li.red, hrow, hv,
-                                       1.0f, h_d, a.h0, last, nullptr, tag_of(seq, l, PH_DOWN),
-                                       [&](int bi) {
-                                           PQ::prefetch_range(qb, sqn, a.group,
-                                                              spread_lo<PQ::NBUF - 1, PD::MAXB>(bi),
-                                                              spread_lo<PQ::NBUF - 1, PD::MAXB>(bi + 1));
-                                       });
+            const uint32_t tact = tag_of(seq, l, PH_ACT), to = tag_of(seq, l, PH_O);
+            PD::template run<MODE_ACC, M::I>(
+                db, sd, a.group, tab, li, part8, hrow, 0.0f,
+                [&] {
+                    const float r = stage_wave<PD, XS_F32, M::I>(actl, nullptr, tact, li, err);
+                    stamp(a, l, 7);
+                    return r;
+                },
+                [&] { return residual_take(hraw, sd, a, h_o, to); }, h_d, a.h0, last, nullptr,
+                tag_of(seq, l, PH_DOWN), [&](int bi) {
+                    // the next layer's q|k|v (an empty share after the last layer)
+                    Segs sqn = segs_qkv(layers[last ? l : l + 1], a, sh);
+                    if (last)
+                        sqn.qb = sqn.qa;
+                    PQ::prefetch_range(qb, sqn, a.group, spread_lo<PQ::NBUF - 1, PD::MAXB>(bi),
+                                       spread_lo<PQ::NBUF - 1, PD::MAXB>(bi + 1));
+                });
         }
         stamp(a, l, 8);
         if (!last) {
