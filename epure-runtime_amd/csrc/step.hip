@@ -127,11 +127,13 @@ struct Model {
 // Llama-3-8B, Qwen3-1.7B, Qwen3-8B and Llama-3.2-3B shapes (Qwen3-4B below); shares at 256
 // workgroups: q|k|v 6 / 4 / 6 / 5 quads, o 8 / 4 / 8 / 6 (on at least half
 // the grid), gate|up 14 / 6 / 12 / 8, down 4 / 2 / 4 / 3.
-// Llama-3-8B: q|k|v and o whole shares in flight, gate|up 5 of 7 blocks
-// (issued during the attention window), down 3 of 4 (issued during gate|up).
-using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 8, 14, 4, -1, -1, 6, 4, 5>;
+// Llama-3-8B: q|k|v and o whole shares in flight, gate|up 4 of 7 blocks
+// issued during the attention window (5: 1.167 ms per step, 4: 1.141, 3:
+// 1.163 with per-wave staging) and 1 during o, down 3 of 4 (issued during
+// gate|up); Qwen3-8B the same (4 early blocks: 1.217 -> 1.170 ms).
+using ModelL8B = Model<4096, 4096, 14336, 4, 3, 2, 2, 4, 6, 8, 14, 4, -1, -1, 6, 4, 4>;
 using ModelQ17 = Model<2048, 2048, 6144, 2, 1, 1, 1, 1, 4, 4, 6, 2>;
-using ModelQ8B = Model<4096, 4096, 12288, 4, 3, 2, 2, 4, 6, 8, 12, 4, -1, -1, 6, 4, 5>;
+using ModelQ8B = Model<4096, 4096, 12288, 4, 3, 2, 2, 4, 6, 8, 12, 4, -1, -1, 6, 4, 4>;
 using ModelL3B = Model<3072, 3072, 8192, 3, 2, 2, 2, 3, 5, 6, 8, 3>;
 // Qwen3-4B: hidden 2560 but 32 x 128 query columns; shares q|k|v 6, o 5,
 // gate|up 10 (9.5), down 3 (2.5) quads
