@@ -190,7 +190,7 @@ def gemv_sweep(seed=0, sets=64, replays=20):
     ms = _graph_time([L.fwd for L in lins], replays) / sets
     wb = _weight_bytes(n, k, 16)
     gbs = wb / (ms * 1e-3) / 1e9
-    return {"kernel": "gemv_lut_kernel", "shape": "4096x4096 4-bit, M=1, bf16 x/y",
+    return {"kernel": "gemv_row_kernel", "shape": "4096x4096 4-bit, M=1, bf16 x/y",
             "rotating_sets": sets, "us_per_launch": round(ms * 1e3, 3),
             "alg_bytes_per_launch": wb, "achieved_gbs": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
@@ -290,7 +290,9 @@ def prefill_sweep(seed=0, replays=10):
                          "hbm_frac": round(byt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
                          "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
-                         "kernel": ("gemv_lut_kernel" if m == 1 else
+                         # 8-bit rows of 4 or 8 slabs (K = 1024, 2048) take gemv_row_kernel
+                         "kernel": (("gemv_row_kernel" if k in (1024, 2048) else "gemv_lut_kernel")
+                                    if m == 1 else
                                     "sk1_kernel" if m <= 16 and 12 * cus <= n <= 64 * cus else
                                     "sk_kernel + sk_reduce_kernel" if m <= 64 else
                                     "pf_prep_kernel + pf_kernel (+ sk_reduce_kernel when K is split)")})

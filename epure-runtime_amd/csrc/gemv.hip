@@ -50,6 +50,9 @@ namespace {
 #ifndef EP_GEMV_PER_CU
 #define EP_GEMV_PER_CU 2        // workgroups per CU for one-slab variants
 #endif
+#ifndef EP_GEMV_ROW_WAVES
+#define EP_GEMV_ROW_WAVES 8     // waves per workgroup of gemv_row_kernel
+#endif
 
 constexpr int kMaxWaves = 8;   // 512 threads: up to 256 VGPRs per lane
 constexpr int kMaxSeg = 3;
@@ -602,6 +605,236 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     }
 }
 
+// Batch-1 GEMV over rows of S = 4 or 8 slabs (K = 2048 / 4096 with 4-bit
+// indices, 1024 / 2048 with 8-bit), one block of ROWS rows per workgroup:
+// wave w owns rows RW w .. RW w + RW - 1 across the whole row (each 16-byte
+// load of a lane covers 4 slabs of one row: lane (sl, c) reads chunk c of
+// slab 4 j + sl), so each row's dot product is summed inside one wave (DPP
+// and permlane) and stored by it -- no cross-wave reduction and no barrier
+// after the loads.  The one barrier orders the pair table and the staged
+// activations (one chunk per thread, as gemv_lut_kernel's) before their
+// reads.  All loads go out at entry: the thread's activation chunk and
+// codebook entries first (needed before the barrier), then the weights and
+// their scale halves; results return in order.
+template <int BITS, int XDT, int S>
+__global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvArgs a)
+{
+    constexpr int NW = EP_GEMV_ROW_WAVES;       // waves per workgroup
+    constexpr int NT = 64 * NW;
+    constexpr int PAIRS = BITS == 4 ? 16 : 8;  // weight pairs per 16-byte chunk
+    constexpr int KPC = 2 * PAIRS;              // k values per chunk
+    constexpr int LPR = S / 4;                  // 16-byte loads of a lane per row
+    constexpr int RW = 4 / LPR;                 // rows per wave (4 loads per lane)
+    constexpr int ROWS = NW * RW;
+    constexpr int NPC = 2048 / NT;              // table pieces per thread
+    constexpr int NCH = S * 16;                 // chunks per row
+    constexpr bool HL = XDT == EP_F32;          // f32 rows: hi and lo fp16 terms
+    constexpr int ESZ = XDT == EP_F32 ? 4 : 2;
+    constexpr int XPC = ESZ * KPC / 16;         // 16-byte pieces of x per chunk
+    static_assert(S == 4 || S == 8, "rows of 4 or 8 slabs");
+    __shared__ __align__(16) uint32_t tab[kTabDwords];
+    __shared__ __align__(16) uint32_t xs[NCH * PAIRS];
+    __shared__ __align__(16) uint32_t xl[HL ? NCH * PAIRS : 4];
+    __shared__ float xf[NCH];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int sl = lane >> 4, c = lane & 15;
+    const uint8_t *packed = a.seg[0].packed;
+    const void *scale = a.seg[0].scale;
+    const void *cbp = a.seg[0].cb;
+    void *yp = a.seg[0].y;
+    const int N = a.seg[0].N;
+    const char *xbase = (const char *)a.x;
+    if (a.gidx) {
+        // the token's expert (clamped into the stack, as gemv_lut_kernel)
+        int e = __builtin_amdgcn_readfirstlane(a.gidx[blockIdx.y]);
+        e = e < 0 ? 0 : (e >= a.E ? a.E - 1 : e);
+        packed += (int64_t)e * a.estride_w;
+        scale = (const char *)scale + (int64_t)e * a.estride_s;
+        xbase += (int64_t)blockIdx.y * a.ldx * ESZ;
+        yp = (char *)yp + (int64_t)blockIdx.y * a.ldy * (a.y_dtype == EP_F32 ? 4 : 2);
+    }
+    const int row0 = (int)blockIdx.x * ROWS + wave * RW;
+
+    // ---- loads, in the order they are needed
+    u32x4_t xraw[XPC];
+    {
+        const auto *xp = (const __attribute__((address_space(1))) u32x4_t *)(
+            xbase + (int64_t)(tid < NCH ? tid : 0) * KPC * ESZ);
+#pragma unroll
+        for (int p = 0; p < XPC; ++p)
+            xraw[p] = xp[p];
+    }
+    // codebook entries of this thread's NPC table stores (store i = tid +
+    // NT k writes a 16-byte piece of entry b = i >> 3): 4-bit: cb[b & 15]
+    // (the same for every k) and cb[b >> 4]; 8-bit: cb[b]
+    const bool cb32 = a.cb_dtype == EP_F32;
+    const auto *cp = (const __attribute__((address_space(1))) uint16_t *)cbp;
+    auto cb_at = [&](int i, uint32_t &lo, uint32_t &hi) {
+        const uint32_t ci = (uint32_t)(i < a.levels ? i : 0);
+        lo = cp[cb32 ? 2 * ci : ci];
+        hi = cp[cb32 ? 2 * ci + 1 : ci];
+    };
+    constexpr int NCB = BITS == 4 ? NPC + 1 : NPC;
+    uint32_t cbr[NCB][2];
+    int cbi[NCB];
+#pragma unroll
+    for (int k = 0; k < NCB; ++k) {
+        const int b = (tid + NT * k) >> 3;
+        if constexpr (BITS == 4)
+            cbi[k] = k == NPC ? b & 15 : b >> 4;
+        else
+            cbi[k] = b;
+        cb_at(cbi[k], cbr[k][0], cbr[k][1]);
+    }
+    // weights: load i covers row r = i / LPR, slabs 4 (i % LPR) .. + 3
+    u32x4_t wq[4];
+    uint32_t sraw[4][2];
+    const bool sc_f32 = a.scale_dtype == EP_F32;
+    {
+        const auto *sp = (const __attribute__((address_space(1))) uint16_t *)scale;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = row0 + i / LPR;
+            const uint32_t rs = row < N ? (uint32_t)row : 0u;
+            const uint32_t b0 = (uint32_t)((i % LPR) * 4 + sl) * kSlabBytes + (uint32_t)c * 16;
+            const auto *wp = (const __attribute__((address_space(1))) u32x4_t *)(
+                packed + (rs * (uint32_t)a.row_bytes + b0));
+#if EP_GEMV_NT_LOADS
+            wq[i] = __builtin_nontemporal_load(wp);
+#else
+            wq[i] = *wp;
+#endif
+            const uint32_t e = rs * (uint32_t)a.lds + (BITS == 4 ? 2 * b0 : b0) / (uint32_t)a.group;
+            sraw[i][0] = sp[sc_f32 ? 2 * e : e];
+            sraw[i][1] = sp[sc_f32 ? 2 * e + 1 : e];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load goes out before any use
+
+    // ---- stage the activation chunk and the pair table, one barrier
+    {
+        float v[KPC];
+        if constexpr (XDT == EP_F32) {
+#pragma unroll
+            for (int p = 0; p < XPC; ++p)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    v[4 * p + t] = __uint_as_float(xraw[p][t]);
+        } else {
+#pragma unroll
+            for (int p = 0; p < XPC; ++p)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    unpack_pair<XDT>(xraw[p][t], v[8 * p + 2 * t], v[8 * p + 2 * t + 1]);
+        }
+        float am = 0.0f;
+#pragma unroll
+        for (int t = 0; t < KPC; ++t)
+            am = fmaxf(am, fabsf(v[t]));
+        const int e = row_exponent(am);
+        if (tid < NCH) {
+            stage_chunk<HL, PAIRS>(v, ldexpf(1.0f, -e), xs + tid * PAIRS, xl + (HL ? tid * PAIRS : 0));
+            xf[tid] = ldexpf(1.0f, e);
+        }
+    }
+    {
+        auto cb16 = [&](int k) -> uint32_t {
+            const float f = cb32 ? __uint_as_float(cbr[k][0] | (cbr[k][1] << 16))
+                                 : (a.cb_dtype == EP_F16 ? (float)f16_from_bits((uint16_t)cbr[k][0])
+                                                         : bf16_to_f32((uint16_t)cbr[k][0]));
+            return cbi[k] < a.levels ? (uint32_t)f16_bits((f16_t)f) : 0u;
+        };
+#pragma unroll
+        for (int k = 0; k < NPC; ++k) {
+            uint32_t v;
+            if constexpr (BITS == 4)
+                v = cb16(NPC) | (cb16(k) << 16);
+            else
+                v = cb16(k) | (cb16(k) << 16);
+            // entry b = (tid + NT k) >> 3 at byte b << 8, its 16-byte piece tid & 7
+            // (the 32 copies fill the entry's first 128 bytes: gemv_core.h)
+            ((u32x4_t *)tab)[(((tid + NT * k) >> 3) << 4) + (tid & 7)] = (u32x4_t){v, v, v, v};
+        }
+    }
+    lds_barrier();
+
+    // ---- the lane's activation chunks (slab 4 j + sl, chunk c)
+    f16x2_t xh[LPR][PAIRS];
+    f16x2_t xlo[HL ? LPR : 1][HL ? PAIRS : 1];
+    float fexp[LPR];
+#pragma unroll
+    for (int j = 0; j < LPR; ++j) {
+        const int cc = (j * 4 + sl) * 16 + c;
+#pragma unroll
+        for (int p = 0; p < PAIRS; p += 4) {
+            const u32x4_t q4 = *(const u32x4_t *)(xs + cc * PAIRS + p);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                xh[j][p + t] = as_f16x2(q4[t]);
+            if constexpr (HL) {
+                const u32x4_t l4 = *(const u32x4_t *)(xl + cc * PAIRS + p);
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    xlo[j][p + t] = as_f16x2(l4[t]);
+            }
+        }
+        fexp[j] = xf[cc];
+    }
+
+    // ---- dot products: load i adds to row i / LPR
+    const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+        acc[r] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = i / LPR, j = i % LPR;
+        float part = 0.0f, plo = 0.0f;
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+            const uint32_t w = wq[i][wd];
+            if constexpr (BITS == 4) {
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const f16x2_t wv = as_f16x2(lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[b])));
+                    part = __builtin_amdgcn_fdot2(wv, xh[j][wd * 4 + b], part, false);
+                    if constexpr (HL)
+                        plo = __builtin_amdgcn_fdot2(wv, xlo[j][wd * 4 + b], plo, false);
+                }
+            } else {
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const uint32_t t0 = lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p]));
+                    const uint32_t t1 = lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p + 1]));
+                    const f16x2_t wv = as_f16x2(__builtin_amdgcn_perm(t1, t0, 0x07060100u));
+                    part = __builtin_amdgcn_fdot2(wv, xh[j][wd * 2 + p], part, false);
+                    if constexpr (HL)
+                        plo = __builtin_amdgcn_fdot2(wv, xlo[j][wd * 2 + p], plo, false);
+                }
+            }
+        }
+        const uint32_t raw = sraw[i][0] | (sraw[i][1] << 16);
+        const float sc = sc_f32 ? __uint_as_float(raw)
+                                : (a.scale_dtype == EP_F16 ? (float)f16_from_bits((uint16_t)raw)
+                                                           : bf16_to_f32((uint16_t)raw));
+        acc[r] = fmaf(HL ? part + plo : part, (row0 + r < N ? sc : 0.0f) * fexp[j], acc[r]);
+    }
+    // ---- each row's sum inside the wave; lane 0 stores it
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+        const float v = wave_sum(acc[r]);
+        const int row = row0 + r;
+        if (lane == 0 && row < N) {
+            float o = v;
+            if (a.accumulate)
+                o += load_as_f32(yp, a.y_dtype, row);
+            store_from_f32(yp, a.y_dtype, row, o);
+        }
+    }
+}
+
 // Any shape, any stride, any M: one wave per output row, fp32 arithmetic
 // (w = f32(cb[idx]) * f32(scale), fma into fp32).  Flat-stream indexing
 // (position n*K + k), so odd K with 4-bit packing is served too.
@@ -857,12 +1090,41 @@ bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
     return fits(bits, spw, mt, x.dtype == EP_F32);
 }
 
+// gemv_row_kernel serves a batch-1 row of exactly 4 or 8 slabs.
+static int row_kernel_slabs(const GemvArgs &a) { return a.row_bytes == 4 * kSlabBytes ? 4 : (a.row_bytes == 8 * kSlabBytes ? 8 : 0); }
+
+template <int BITS, int S>
+static int launch_row(const GemvArgs &a, int xdt, hipStream_t stream)
+{
+    const int rows = EP_GEMV_ROW_WAVES * (S == 8 ? 2 : 4);
+    const dim3 g((unsigned)((a.seg[0].N + rows - 1) / rows), a.gidx ? (unsigned)a.ntok : 1u);
+    const dim3 b(64 * EP_GEMV_ROW_WAVES);
+    if (xdt == EP_BF16)
+        hipLaunchKernelGGL((gemv_row_kernel<BITS, EP_BF16, S>), g, b, 0, stream, a);
+    else if (xdt == EP_F16)
+        hipLaunchKernelGGL((gemv_row_kernel<BITS, EP_F16, S>), g, b, 0, stream, a);
+    else
+        hipLaunchKernelGGL((gemv_row_kernel<BITS, EP_F32, S>), g, b, 0, stream, a);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+static int dispatch_row(const GemvArgs &a, int bits, int xdt, hipStream_t stream)
+{
+    const int S = row_kernel_slabs(a);
+    if (bits == 4)
+        return S == 8 ? launch_row<4, 8>(a, xdt, stream) : launch_row<4, 4>(a, xdt, stream);
+    return S == 8 ? launch_row<8, 8>(a, xdt, stream) : launch_row<8, 4>(a, xdt, stream);
+}
+
 int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,
                 hipStream_t stream)
 {
     if (!gemv_serves(w, x, M))
         return EP_DECLINE_SHAPE;
     const GemvArgs a = make_args(w, x, M, y);
+    if (M == 1 && row_kernel_slabs(a) != 0)
+        return dispatch_row(a, w.bits(), x.dtype, stream);
     int spw, waves;
     plan(a.row_bytes, spw, waves);
     const int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);
@@ -899,6 +1161,8 @@ int launch_gemv_gather(const PackedDesc &w, const ActDesc &x, int64_t T, const i
     a.ntok = (int)T;
     a.estride_w = w.N * a.row_bytes;
     a.estride_s = w.N * w.ld_scale * (w.scale_dtype == EP_F32 ? 4 : 2);
+    if (row_kernel_slabs(a) != 0)
+        return dispatch_row(a, w.bits(), x.dtype, stream);
     int spw, waves;
     plan(a.row_bytes, spw, waves);
     if (w.bits() == 4)
