@@ -2,7 +2,8 @@
 4-bit codebook model (the reference's headline decode configuration) on one
 MI355X, plus the dequant-GEMV HBM bandwidth as a fraction of peak.
 
-    python bench.py [--steps K] [--warmup W] [--config llama3-8b|qwen3-1.7b|qwen3-8b|llama3.2-3b|qwen3-4b]
+    python bench.py [--steps K] [--warmup W] [--config llama3-8b|qwen3-1.7b|qwen3-8b|llama3.2-3b|qwen3-4b|
+                                                       qwen3-0.6b|h2560-i6656]
 
 One "step" is one decode token: a replay of the captured HIP graph of the
 whole decode step -- the one-launch decode-step kernel (all 32 layers: fused
@@ -59,7 +60,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--config", default="llama3-8b",
-                    choices=["llama3-8b", "qwen3-1.7b", "qwen3-8b", "llama3.2-3b", "qwen3-4b"])
+                    choices=["llama3-8b", "qwen3-1.7b", "qwen3-8b", "llama3.2-3b", "qwen3-4b",
+                             "qwen3-0.6b", "h2560-i6656"])
     ap.add_argument("--prompt", type=int, default=None)
     ap.add_argument("--decode", type=int, default=None,
                     help="tokens decoded after the prompt (default: the configuration's, "

@@ -80,7 +80,15 @@ LLAMA32_3B = DecoderConfig(3072, 8192, 28, 24, 8, 128, 128256, 5e5, 1e-5, tie_em
                            name="llama3.2-3b")
 QWEN3_4B = DecoderConfig(2560, 9728, 36, 32, 8, 128, 151936, 1e6, 1e-6, qk_norm=True,
                          tie_embeddings=True, name="qwen3-4b")
-CONFIGS = {c.name: c for c in (LLAMA3_8B, QWEN3_1_7B, QWEN3_8B, LLAMA32_3B, QWEN3_4B)}
+# Shapes outside that list run the generic one-launch variants (hidden and
+# query width up to 4096, intermediate up to 16384, multiples of 512, up to
+# 8 query heads per kv head): e.g. the Qwen3-0.6B shape and a Llama-style
+# 2560 / 6656 decoder with 5 query heads per kv head.
+QWEN3_0_6B = DecoderConfig(1024, 3072, 28, 16, 8, 128, 151936, 1e6, 1e-6, qk_norm=True,
+                           tie_embeddings=True, name="qwen3-0.6b")
+H2560_I6656 = DecoderConfig(2560, 6656, 30, 20, 4, 128, 32000, 1e6, 1e-5, name="h2560-i6656")
+CONFIGS = {c.name: c for c in (LLAMA3_8B, QWEN3_1_7B, QWEN3_8B, LLAMA32_3B, QWEN3_4B, QWEN3_0_6B,
+                                H2560_I6656)}
 
 
 def rope_tables(cfg, max_pos, device):

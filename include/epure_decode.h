@@ -103,11 +103,15 @@ int ep_lm_head_argmax(float *h, const uint16_t *norm_w, float eps, const uint16_
  * zeroed before the first call and is left valid for the next; its int
  * word 2 becomes nonzero if a hand-over wait timed out (the step's results
  * are then garbage).  `trace`, when not NULL, receives wall-clock stamps
- * [n_layers][24][grid] (debug).  Declines (> 0) shapes without a
- * persistent variant (ep_decode_step_serves: the Llama-3-8B, Qwen3-8B, Qwen3-4B,
- * Llama-3.2-3B and Qwen3-1.7B shapes, D = 128, groups a power of two >= 128,
- * fp16 scales, 4-bit indices).  Position = state[0].  Launches that share a workspace must be
- * stream-ordered (two in flight on one workspace race).
+ * [n_layers][24][grid] (debug).  Served (ep_decode_step_serves): D = 128,
+ * 4-bit indices, groups a power of two >= 128, fp16 or f32 group scales,
+ * and either a tuned shape (Llama-3-8B, Qwen3-8B, Qwen3-4B, Llama-3.2-3B,
+ * Qwen3-1.7B, with fp16 scales) or the generic variants: H and Hq * D up
+ * to 4096, I up to 16384, each a multiple of 512, Hq / Hkv in 1..8 (the
+ * geometry of the largest such shape, blocks past a smaller shape's share
+ * skipped).  Other shapes decline (> 0).  Position = state[0].  Launches
+ * that share a workspace must be stream-ordered (two in flight on one
+ * workspace race).
  */
 size_t ep_decode_step_layer_bytes(void);
 size_t ep_decode_step_workspace(int H, int I, int Hq, int Hkv, int D, int max_pos);

@@ -145,9 +145,27 @@ def test_decode_step_serves_more_shapes(lib, shape):
 
 
 @pytest.mark.parametrize("change", [
-    dict(H=1024), dict(I=8192), dict(Hq=16), dict(D=64), dict(levels=256), dict(group=64),
-    dict(sdt=_abi.F32), dict(max_pos=100), dict(max_pos=32)])
+    dict(H=1024), dict(I=8192), dict(Hq=16), dict(sdt=_abi.F32), dict(H=2560, I=6656, Hq=20, Hkv=4),
+    dict(Hq=8, Hkv=8)])
+def test_decode_step_serves_generic_shapes(lib, change):
+    """Shapes outside the tuned list (and f32 group scales) take the generic
+    one-launch variants: hidden and query width <= 4096, intermediate
+    <= 16384, multiples of 512, up to 8 query heads per kv head."""
+    shape = dict(LLAMA8B)
+    kw = {k: v for k, v in change.items() if k in ("sdt",)}
+    shape.update({k: v for k, v in change.items() if k in shape})
+    assert _serves(lib, **shape, **kw) == 1
+
+
+@pytest.mark.parametrize("change", [
+    dict(D=64), dict(levels=256), dict(group=64), dict(max_pos=100), dict(max_pos=32),
+    dict(H=4352), dict(I=14592), dict(H=8192), dict(I=20480), dict(Hq=48), dict(Hkv=2),
+    dict(sdt=_abi.BF16)])
 def test_decode_step_declines_other_shapes(lib, change):
+    """Head dim other than 128, 8-bit indices, groups below 128, a cache not
+    of whole 64-position chunks, rows that are not whole 512-value slabs,
+    shapes past the generic maxima, more than 8 query heads per kv head,
+    bf16 scales."""
     shape = dict(LLAMA8B)
     kw = {k: v for k, v in change.items() if k in ("max_pos", "levels", "group", "sdt", "cdt")}
     shape.update({k: v for k, v in change.items() if k in shape})

@@ -22,7 +22,8 @@ import numpy as np
 import pytest
 import torch
 
-from epure.decode import LLAMA3_8B, LLAMA32_3B, QWEN3_1_7B, QWEN3_4B, QWEN3_8B, Decoder, random_weights
+from epure.decode import (H2560_I6656, LLAMA3_8B, LLAMA32_3B, QWEN3_0_6B, QWEN3_1_7B, QWEN3_4B, QWEN3_8B,
+                          Decoder, random_weights)
 from oracle.decoder import RefDecoder
 
 pytestmark = pytest.mark.gpu
@@ -159,3 +160,56 @@ def test_more_shapes_one_launch_against_oracle(base):
     got, _ = d.generate(prompt, 24)
     want, _, _ = ref.generate(prompt, 24)
     assert got == want
+
+
+def _teacher_forced_and_greedy(w, n_pos=140, seed=9):
+    """The one-launch step (it must serve the shape) teacher-forced over
+    n_pos random positions against the float32 oracle, then 24 greedy
+    tokens against the oracle's."""
+    cfg = w.cfg
+    toks = _ids(n_pos, cfg.vocab, seed)
+    d = Decoder(w, len(toks) + 1, persistent=True)
+    assert d.persistent
+    ref = RefDecoder.from_weights(w, d.max_pos)
+    d.reset(toks)
+    d.capture()
+    errs = []
+    for pos in range(len(toks) - 1):
+        d.step()
+        want = ref.step(toks[pos], pos)
+        errs.append(float((d.logits - want).abs().max() / want.abs().max()))
+    assert not d.step_failed()
+    errs = np.array(errs)
+    print(f"{cfg.name} x{cfg.layers} layers: normwise median {np.median(errs):.2e} max {errs.max():.2e}")
+    assert np.median(errs) < 1e-5 and errs.max() < 5e-5
+    prompt = _ids(12, cfg.vocab, seed + 1)
+    got, _ = d.generate(prompt, 24)
+    want, _, _ = ref.generate(prompt, 24)
+    assert got == want
+
+
+@pytest.mark.parametrize("base", [QWEN3_0_6B, H2560_I6656], ids=["qwen3-0.6b", "h2560-i6656"])
+def test_generic_shapes_one_launch_against_oracle(base):
+    """Shapes outside the tuned list run the generic one-launch variant:
+    the Qwen3-0.6B shape (hidden 1024, q/k norm, 2 query heads per kv head)
+    and a Llama-style hidden 2560 / intermediate 6656 decoder with 20 query
+    heads over 4 kv heads (GQ 5): 3 full-width layers, teacher-forced
+    against the float32 oracle over 140 positions, 24 greedy tokens
+    identical to the oracle's."""
+    w = random_weights(dataclasses.replace(base, layers=3), seed=11, device=DEV)
+    _teacher_forced_and_greedy(w)
+
+
+def test_one_launch_f32_scales_against_oracle():
+    """Group scales in f32 (as make_trainable leaves them, finetune.py:78),
+    perturbed off the fp16 grid, at the Qwen3-1.7B shape: the one-launch
+    step still serves it (the generic f32-scale variant) and matches the
+    float32 oracle built from the same f32 scales."""
+    w = random_weights(dataclasses.replace(QWEN3_1_7B, layers=3), seed=12, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(13)
+    for L in w.layers:
+        for s in L.lin.values():
+            noise = torch.rand(s.scale.shape, generator=g, device=DEV) * 2.0 ** -10
+            s.scale = (s.scale.float() * (1.0 + noise)).contiguous()
+            assert s.scale.dtype == torch.float32
+    _teacher_forced_and_greedy(w, seed=14)
