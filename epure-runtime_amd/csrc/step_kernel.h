@@ -330,9 +330,9 @@ struct StepArgs {
     const float *cos_t, *sin_t;  // [max_pos][D / 2]
     const int *state;            // [0] position
     int Hkv, max_pos, levels, group, cb_dtype;
-    int H, HQD, I;     // the shape (read by the generic variants)
     float eps, qk_eps, att_scale;
     long long *trace;  // optional [layers][kEvents][grid] wall-clock stamps
+    int H, HQD, I;     // the shape (read by the generic variants)
 };
 
 // ---------------------------------------------------------------- GEMV phase
@@ -377,9 +377,10 @@ struct Gemv {
     // NBUF_SET < 0: the whole share in flight (every block issued ahead)
     static constexpr int NBUF = NBUF_SET > 0 ? NBUF_SET : (NBUF_SET < 0 ? MAXB + 1 : NBUF_AUTO);
 
+    using SBits = typename std::conditional<SF32, uint32_t, uint16_t>::type;
     struct Blk {
         u32x4_t w[NQ];
-        uint32_t s;  // one group scale (fp16 or f32 bits) per lane, spread to
+        SBits s;     // one group scale (fp16 or f32 bits) per lane, spread to
                      // the lanes that use it at compute time; converted there
                      // (a conversion right after the load would wait for
                      // every load in flight)
@@ -387,13 +388,7 @@ struct Gemv {
 
     // group scales: fp16 (the container's) or f32 (after make_trainable)
     static constexpr int kSEsz = SF32 ? 4 : 2;
-    static EP_DEV uint32_t load_scale(const char *p)
-    {
-        if constexpr (SF32)
-            return ldg((const uint32_t *)p);
-        else
-            return ldg((const uint16_t *)p);
-    }
+    static EP_DEV SBits load_scale(const char *p) { return ldg((const SBits *)p); }
     static EP_DEV float scale_value(uint32_t bits)
     {
         if constexpr (SF32)
@@ -405,8 +400,16 @@ struct Gemv {
     // This lane's place in the phase (cheap; recomputed where needed so it
     // holds no registers across phases).
     static EP_DEV bool wave_on(int wv) { return wv / WPR < RG; }
-    // slabs of the phase's rows: ns (at most S; S sets the geometry)
-    static EP_DEV bool slab_on(int j, int wv, int ns) { return wave_on(wv) && (wv % WPR) + j * WPR < ns; }
+    // slabs and packed bytes of the phase's rows: S and S x 256 for the
+    // tuned variants (compile-time, so the slab tests fold away); the
+    // launch's own ns (at most S; S sets the geometry) for the generic ones
+    static constexpr int RB = S * kSlabBytes;
+    static EP_DEV int nslabs(int ns) { return GEN ? ns : S; }
+    static EP_DEV int row_bytes(const Segs &sg) { return GEN ? sg.rb : RB; }
+    static EP_DEV bool slab_on(int j, int wv, int ns)
+    {
+        return wave_on(wv) && (wv % WPR) + j * WPR < nslabs(ns);
+    }
     static EP_DEV int slab(int j, int wv, int ns) { return slab_on(j, wv, ns) ? (wv % WPR) + j * WPR : 0; }
     // byte offset of the lane's 16-byte chunk of slab j within a row: lane
     // l covers chunk l >> 2 of row l & 3 of a quad (the 4x4x4 MFMA layout)
@@ -482,7 +485,7 @@ struct Gemv {
         // the lane's row (lane & 3) and 16-byte chunk (lane >> 2) within a
         // quad's slab: the vector offset; the quad and slab offsets are
         // wave-uniform (scalar offset)
-        const uint32_t woff = (uint32_t)(lane & 3) * sg.rb + (uint32_t)(lane >> 2) * 16u;
+        const uint32_t woff = (uint32_t)(lane & 3) * row_bytes(sg) + (uint32_t)(lane >> 2) * 16u;
         const int sbyte = slab(j, wv, sg.ns) * kSlabBytes;
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
@@ -491,7 +494,7 @@ struct Gemv {
             const int s = seg_of(sg, ok ? vq : sg.qa, i);
             const int quad = ok ? vq - first_quad(sg, s) : 0;
             const auto rp = buffer_rsrc(sel3(s, sg.pk0, sg.pk1, sg.pk2), live ? 0x7fffffffu : 0u);
-            bk.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)woff, quad * 4 * sg.rb + sbyte, kAuxStream);
+            bk.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rp, (int)woff, quad * 4 * row_bytes(sg) + sbyte, kAuxStream);
         }
         const bool sok = sl.i < NQ;
         if constexpr (!SEG3) {
