@@ -264,6 +264,18 @@ def _dense_time(stores, x, replays):
     return _graph_time([one(h) for h in hs], replays) / len(hs)
 
 
+def _sk1_serves(m, n, cus):
+    """Whether the one-launch small-M kernel serves a config-3 linear (8-bit
+    indices, bf16 x, group 128): enough 16-row tiles for 3/4 of the CUs, at
+    most 4 per CU, and M <= 16 x the tiles per workgroup (skinny.hip
+    sk1_tiles_per_wg)."""
+    tiles = (n + 15) // 16
+    if tiles * 4 < cus * 3 or tiles > 4 * cus:
+        return False
+    t = next(t for t in (1, 2, 4) if tiles <= t * cus)
+    return m <= 16 * t
+
+
 def prefill_sweep(seed=0, replays=10):
     """Config 3: 8-bit indices (256-entry fp16-valued codebook, group-128 fp16
     scales), (N, K) in {4096x4096, 14336x4096, 4096x14336}, bf16 x with M in
@@ -295,7 +307,7 @@ def prefill_sweep(seed=0, replays=10):
                          # 8-bit rows of 4 or 8 slabs (K = 1024, 2048) take gemv_row_kernel
                          "kernel": (("gemv_row_kernel" if k in (1024, 2048) else "gemv_lut_kernel")
                                     if m == 1 else
-                                    "sk1_kernel" if m <= 16 and 12 * cus <= n <= 64 * cus else
+                                    "sk1_kernel" if _sk1_serves(m, n, cus) else
                                     "sk_kernel + sk_reduce_kernel" if m <= 64 else
                                     "pf_prep_kernel + pf_kernel (+ sk_reduce_kernel when K is split)")})
             del lins, x

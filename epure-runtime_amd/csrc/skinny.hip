@@ -30,10 +30,12 @@
 //  * with one split the results go straight to y; otherwise each split
 //    writes f32 partials [S][M][N] and sk_reduce_kernel sums them in split
 //    order (deterministic; no atomics, no counters);
-//  * at M <= 16 with 8-bit indices (M <= 8 with 4-bit), 16-bit activations
-//    and enough 16-row tiles to fill the CUs, sk1_kernel instead: one
-//    workgroup per row tile over the whole of K, one launch, no partials
-//    (its comment has the layout).
+//  * with 16-bit activations, enough 16-row tiles to fill the CUs and M at
+//    most 16 per tile of a workgroup (8-bit indices up to M = 64, 4-bit up
+//    to M = 8), sk1_kernel instead: a workgroup owns 1, 2 or 4 row tiles
+//    over the whole of K, one launch, no partials (its comment has the
+//    layout); bf16 activations with 8-bit indices take its bf16 path (raw
+//    bf16 operands, the codebook as exact bf16 hi + lo terms).
 #include "ep_common.h"
 #include "ep_internal.h"
 #include "gemv_core.h"
@@ -394,7 +396,52 @@ EP_DEV int bf16_operand(const u32x4_t *xv, f16x8_t *av)
     return e;
 }
 
-template <int BITS, int XDT, int T, int D, int P, int MT, int NT>
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// The 8-bit table of the bf16 path: entry b holds fp16(cb[b]) as two bf16
+// terms, hi = its top 8 significant bits (truncated) in the low half and
+// lo = fp16(cb[b]) - hi (at most 3 significant bits, so exact) in the high
+// half: hi + lo is the fp16 value exactly.  Same layout as build_table.
+EP_DEV void build_table_hl(uint32_t *tab, const uint16_t *cb16)
+{
+#pragma unroll 4
+    for (int i = threadIdx.x; i < 256 * kTabCopies / 4; i += blockDim.x) {
+        const int b = i >> 3;
+        const float f = (float)f16_from_bits(cb16[b]);
+        const uint32_t hi = __float_as_uint(f) & 0xffff0000u;
+        const float lo = f - __uint_as_float(hi);
+        const uint32_t v = (hi >> 16) | (__float_as_uint(lo) & 0xffff0000u);
+        ((u32x4_t *)tab)[b * 16 + (i & 7)] = (u32x4_t){v, v, v, v};
+    }
+}
+
+// The bf16 path's B operands of one lane's 16-byte chunk (8-bit indices):
+// the hi and the lo terms of weights 8 s .. 8 s + 7 as eight bf16 each (no
+// group scale: it multiplies the piece's sums).
+EP_DEV void dequant_chunk_hl(const uint32_t *tab, u32x4_t w, uint32_t lane4, u32x4_t *bh, u32x4_t *bl)
+{
+#pragma unroll
+    for (int wd = 0; wd < 4; ++wd)
+#pragma unroll
+        for (int b = 0; b < 4; b += 2) {
+            const uint32_t t0 = lds_read_u32(tab, __builtin_amdgcn_perm(w[wd], lane4, kSelByte[b]));
+            const uint32_t t1 = lds_read_u32(tab, __builtin_amdgcn_perm(w[wd], lane4, kSelByte[b + 1]));
+            const int p = wd * 2 + b / 2;  // weights 2 p, 2 p + 1: piece p / 4, dword p % 4
+            bh[p >> 2][p & 3] = __builtin_amdgcn_perm(t1, t0, 0x05040100u);
+            bl[p >> 2][p & 3] = __builtin_amdgcn_perm(t1, t0, 0x07060302u);
+        }
+}
+
+// HL (8-bit indices, bf16 activations, groups of a multiple of 64 values):
+// the bf16 path -- the raw bf16 x is the A operand of
+// v_mfma_f32_16x16x32_bf16 (no conversion, no rescale: bf16 has f32's
+// range), the codebook value the B operand as its exact hi + lo bf16 terms
+// (two MFMAs), and the group scale multiplies each piece's f32 sums (a
+// piece's 4 x 16 values lie in one group).  The products x * fp16(cb) are
+// exact in f32 and summed in f32; the f32 group scale then applies the
+// dequantized weight cb * scale without its rounding to fp16 (closer to
+// the f32 reference, not farther).
+template <int BITS, int XDT, int T, int D, int P, int MT, int NT, bool HL>
 __global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
 {
     constexpr int NW = NT / 64;      // waves
@@ -403,6 +450,7 @@ __global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
     constexpr int SUB = KPL / 8;     // MFMA sub-steps per piece = 16-byte x loads per lane and piece
     static_assert(NW * MT * 256 <= kTabDwords, "one tile's wave sums fit over the table");
     static_assert(XDT != EP_F32, "16-bit activations");
+    static_assert(!HL || (BITS == 8 && XDT == EP_BF16), "the bf16 path: 8-bit indices, bf16 x");
 
     __shared__ __align__(16) uint32_t tab[kTabDwords];
     __shared__ uint32_t s_cbraw[NT];
@@ -452,7 +500,9 @@ __global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
             }
 #pragma unroll
             for (int c = 0; c < P; ++c) {
-                const int kc = r * RK + KPL * (4 * c + q);
+                // HL: the piece's group (its first chunk's), the same in the
+                // four lanes of a row whose sums the scale multiplies
+                const int kc = r * RK + KPL * (HL ? 4 * c : 4 * c + q);
                 const bool ok = r < re && kc < a.K && tile < a.tiles && n < a.N;
                 const uint32_t soff = (uint32_t)(((int64_t)n * a.lds + kc / a.group) * 2);
                 sv[d][c][t] = __builtin_amdgcn_raw_buffer_load_b16(rs, ok ? (int)soff : (int)kOut, 0, 0);
@@ -486,7 +536,10 @@ __global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
         s_cb[tid] = f16_bits((f16_t)c);
     }
     lds_barrier();
-    build_table<BITS>(tab, s_cb);
+    if constexpr (HL)
+        build_table_hl(tab, s_cb);
+    else
+        build_table<BITS>(tab, s_cb);
     lds_barrier();
 #pragma unroll
     for (int d = DH; d < D; ++d)
@@ -502,7 +555,35 @@ __global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
     for (int r0 = rb; r0 < re; r0 += D) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
-            if (r0 + d < re) {
+            if (HL && r0 + d < re) {
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int c = 0; c < P; ++c) {
+                        u32x4_t bh[SUB], bl[SUB];
+                        dequant_chunk_hl(tab, wv[d][c][t], lane4, bh, bl);
+                        f32x4_t cs[MT];
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+                            cs[mt] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int s = 0; s < SUB; ++s)
+#pragma unroll
+                            for (int mt = 0; mt < MT; ++mt) {
+                                const bf16x8_t av = __builtin_bit_cast(bf16x8_t, xv[d][mt][c][s]);
+                                cs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    av, __builtin_bit_cast(bf16x8_t, bh[s]), cs[mt], 0, 0, 0);
+                                cs[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    av, __builtin_bit_cast(bf16x8_t, bl[s]), cs[mt], 0, 0, 0);
+                            }
+                        const float sc = (float)f16_from_bits((uint16_t)sv[d][c][t]);
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                acc[t][mt][r] = fmaf(cs[mt][r], sc, acc[t][mt][r]);
+                    }
+            } else if (r0 + d < re) {
                 f16x8_t av[MT][P][SUB];
                 float bk[MT][4];  // the round's power of two of accumulator rows 16 mt + 4 q + r
 #pragma unroll
@@ -694,57 +775,69 @@ int sk_launch_bits(const SkArgs &a, int S, int ld, int xdt, hipStream_t s)
 // Row tiles per workgroup of the one-launch path: the fewest that keep the
 // grid within one workgroup per CU; 0 when the path does not serve.  It
 // serves 16-bit activations and enough 16-row tiles to fill 3/4 of the
-// CUs, at most 4 per CU: with 8-bit indices at M <= 16, and at M 17..32
-// with two or more tiles per workgroup; with 4-bit indices at M <= 8.
-// Each tile reads all M x K activations from L2, so at one tile per
-// workgroup and M > 16 (and at any M > 32; for 4-bit indices, whose tiles
-// hold half the bytes, from M > 8) the split-K kernel, which stages them
-// once per split, is as fast or faster.
-int sk1_mt(int64_t M) { return M <= 16 ? 1 : 2; }
-int sk1_tiles_per_wg(int bits, const ActDesc &x, int64_t M, int64_t N)
+// CUs, at most 4 per CU, at M <= 16 x the tiles per workgroup: a workgroup
+// reads all M x K activations once from L2 (its waves split K) for all of
+// its tiles, so fewer tiles per workgroup mean more activation bytes per
+// weight byte, and past 16 M per tile the split-K kernel, which stages
+// them once per split, is faster (4096 x 4096 at M = 64: 19.5 against 22.2
+// us; 4096 x 14336: 53.6 against 67.7; 14336 x 4096 with four tiles per
+// workgroup: 40.0 against 52.7 for split-K).  8-bit indices up to M = 64
+// with fp16 activations or on the bf16 path (groups of a multiple of 64
+// values), else up to M = 32; 4-bit indices up to M = 8.
+int sk1_mt(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+bool sk1_hl(int bits, const ActDesc &x, int group) { return bits == 8 && x.dtype == EP_BF16 && group % 64 == 0; }
+int sk1_tiles_per_wg(int bits, const ActDesc &x, int64_t M, int64_t N, int group)
 {
-    if (M > (bits == 8 ? 32 : 8) || x.dtype == EP_F32)
+    if (x.dtype == EP_F32)
+        return 0;
+    const bool wide = bits == 8 && (x.dtype == EP_F16 || sk1_hl(bits, x, group));
+    if (M > (wide ? 64 : (bits == 8 ? 32 : 8)))
         return 0;
     const int64_t tiles = (N + 15) / 16, cus = device_cus();
     if (tiles * 4 < cus * 3)
         return 0;
     for (int t = 1; t <= 4; t *= 2)
         if (tiles <= t * cus)
-            return t == 1 && M > 16 ? 0 : t;
+            return M > 16 * t ? 0 : t;
     return 0;
 }
 
 // 16 waves with 8-bit indices, one 16-row activation block and up to two
 // tiles (four per SIMD hide the table lookups' latency), 8 otherwise (4-bit
-// B operands and activations, the second block's activations or the four
-// tiles' sums take the registers of two waves); two pieces per round where
-// one tile and one block of 8-bit indices leave the registers for them.
-template <int BITS, int XDT, int T, int MT>
+// B operands and activations, more activation blocks or the four tiles'
+// sums take the registers of two waves); two pieces per round where one
+// tile and one block of 8-bit indices leave the registers for them.
+template <int BITS, int XDT, int T, int MT, bool HL>
 void sk1_launch_t(const SkArgs &a, hipStream_t s)
 {
     constexpr int NT = BITS == 8 && MT == 1 && T < 4 ? 1024 : 512;
     constexpr int P = BITS == 8 && MT == 1 && T == 1 ? 2 : 1;
-    hipLaunchKernelGGL((sk1_kernel<BITS, XDT, T, 2, P, MT, NT>), dim3((unsigned)a.gtiles), dim3(NT), 0, s, a);
+    hipLaunchKernelGGL((sk1_kernel<BITS, XDT, T, 2, P, MT, NT, HL>), dim3((unsigned)a.gtiles), dim3(NT), 0, s, a);
 }
 
-template <int BITS, int XDT, int MT>
+template <int BITS, int XDT, int MT, bool HL>
 void sk1_launch_m(const SkArgs &a, int tpw, hipStream_t s)
 {
     if (tpw == 1)
-        sk1_launch_t<BITS, XDT, 1, MT>(a, s);
+        sk1_launch_t<BITS, XDT, 1, MT, HL>(a, s);
     else if (tpw == 2)
-        sk1_launch_t<BITS, XDT, 2, MT>(a, s);
+        sk1_launch_t<BITS, XDT, 2, MT, HL>(a, s);
     else
-        sk1_launch_t<BITS, XDT, 4, MT>(a, s);
+        sk1_launch_t<BITS, XDT, 4, MT, HL>(a, s);
 }
 
-template <int BITS, int XDT>
+template <int BITS, int XDT, bool HL>
 void sk1_launch_x(const SkArgs &a, int tpw, hipStream_t s)
 {
-    if (BITS == 4 || sk1_mt(a.M) == 1)
-        sk1_launch_m<BITS, XDT, 1>(a, tpw, s);
-    else
-        sk1_launch_m<BITS, XDT, BITS == 4 ? 1 : 2>(a, tpw, s);
+    const int mt = BITS == 4 ? 1 : sk1_mt(a.M);
+    if (mt == 1)
+        sk1_launch_m<BITS, XDT, 1, HL>(a, tpw, s);
+    else if constexpr (BITS == 8) {
+        if (mt == 2)
+            sk1_launch_m<BITS, XDT, 2, HL>(a, tpw, s);
+        else if constexpr (XDT == EP_F16 || HL)  // four blocks: fp16 or the bf16 path only
+            sk1_launch_m<BITS, XDT, 4, HL>(a, tpw, s);
+    }
 }
 
 }  // namespace
@@ -781,7 +874,7 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     if (!skinny_serves(w, x, M))
         return EP_DECLINE_SHAPE;
     const int bits = w.bits();
-    const int tpw1 = sk1_tiles_per_wg(bits, x, M, w.N);
+    const int tpw1 = sk1_tiles_per_wg(bits, x, M, w.N, w.group);
     const int ld = sk_choose_ld(bits, M, w.N, w.K);
     const int S = sk_splits_ld(bits, ld, w.K);
     const bool partials = tpw1 == 0 && (S > 1 || y.accumulate);
@@ -816,9 +909,14 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
         a.tiles = (int)((w.N + 15) / 16);
         a.gtiles = (a.tiles + tpw1 - 1) / tpw1;
         if (bits == 4)
-            x.dtype == EP_F16 ? sk1_launch_x<4, EP_F16>(a, tpw1, stream) : sk1_launch_x<4, EP_BF16>(a, tpw1, stream);
+            x.dtype == EP_F16 ? sk1_launch_x<4, EP_F16, false>(a, tpw1, stream)
+                              : sk1_launch_x<4, EP_BF16, false>(a, tpw1, stream);
+        else if (x.dtype == EP_F16)
+            sk1_launch_x<8, EP_F16, false>(a, tpw1, stream);
+        else if (sk1_hl(bits, x, w.group))
+            sk1_launch_x<8, EP_BF16, true>(a, tpw1, stream);
         else
-            x.dtype == EP_F16 ? sk1_launch_x<8, EP_F16>(a, tpw1, stream) : sk1_launch_x<8, EP_BF16>(a, tpw1, stream);
+            sk1_launch_x<8, EP_BF16, false>(a, tpw1, stream);
         EP_HIP_CHECK(hipGetLastError());
         return EP_OK;
     }

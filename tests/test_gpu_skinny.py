@@ -191,19 +191,22 @@ def test_skinny_workspace_covers_partials(m, levels, n, k):
     assert need >= skinny_splits(m, n, k, levels) * m * n * 4
 
 
-# The one-launch path: 16-bit activations and enough 16-row tiles to fill
-# 3/4 of the CUs (N >= 12 x CUs, at most 4 tiles per CU); 8-bit indices at
-# M <= 16, and at M 17..32 with two or more tiles per workgroup (N > 16 x
-# CUs); 4-bit indices at M <= 8 (M <= 4 at K <= 4096 stays on the GEMV).
-# On a 256-CU device: 8-bit at M <= 16, (32, 8200), (24, 14336) and
-# (20, 6144); 4-bit at (5, 4128), (8, 8200), (7, 14336); the others take
+# The one-launch path: 16-bit activations, enough 16-row tiles to fill 3/4
+# of the CUs (N >= 12 x CUs, at most 4 tiles per CU) and M <= 16 x the
+# tiles per workgroup (one tile up to N = 16 x CUs, two up to 32 x CUs,
+# four above); 8-bit indices up to M = 64 (bf16 x on the bf16 path, whose
+# groups are multiples of 64 values; else up to M = 32), 4-bit indices up
+# to M = 8 (M <= 4 at K <= 4096 stays on the GEMV).  On a 256-CU device:
+# 8-bit at M <= 16, (32, 8200), (24, 14336), (20, 6144), (64, 14336) and
+# (48, 12000); 4-bit at (5, 4096), (8, 8200), (7, 4096); the others take
 # the split-K kernel.
 @pytest.mark.parametrize("levels", [16, 256])
 @pytest.mark.parametrize("m,n,k", [(2, 4096, 4096), (16, 4096, 4096 + 32), (9, 8200, 2048),
                                    (4, 14336, 1024), (13, 4100, 1568), (17, 4096, 4096),
                                    (32, 8200, 2048), (24, 14336, 1024), (20, 6144, 2048 + 32),
                                    (33, 4100, 1568), (64, 4096, 4096 + 32), (5, 4096, 4096 + 32),
-                                   (8, 8200, 2048), (7, 4096, 14336)])
+                                   (8, 8200, 2048), (7, 4096, 14336), (64, 14336, 1024),
+                                   (48, 12000, 2048 + 64)])
 def test_skinny_one_launch(levels, m, n, k):
     """All of K in one workgroup per row tile: K past the last full round
     of a wave (and a last group of 32 values), N past the last 16-row tile,
@@ -214,7 +217,7 @@ def test_skinny_one_launch(levels, m, n, k):
     assert_close(run(s, x).cpu().numpy(), rust_ref(x32, packed, scale, cb, n, k, levels, 128))
 
 
-@pytest.mark.parametrize("m,n", [(11, 4096), (28, 8192)])
+@pytest.mark.parametrize("m,n", [(11, 4096), (28, 8192), (60, 14336)])
 @pytest.mark.parametrize("levels", [16, 256])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_skinny_one_launch_accumulate_f16_x(out_dtype, levels, m, n):
@@ -250,10 +253,22 @@ def test_skinny_one_launch_4bit_accumulate_f16_x(out_dtype, m, n, k):
     assert_close(out.float().cpu().numpy(), want + start, out_tol)
 
 
+@pytest.mark.parametrize("group,m", [(64, 24), (256, 24), (64, 40), (256, 64)])
+def test_skinny_one_launch_bf16_path_groups(group, m):
+    """The bf16 path (8-bit indices, bf16 x) scales each 64-value piece's
+    sums by its group's scale: groups of one piece and of four, two and
+    four activation blocks (four tiles per workgroup)."""
+    n, k = 8200, 2048
+    _, packed, scale, cb, s = make(n, k, 256, group=group, seed=111 + group + m)
+    x32, x = x_bf16(m, k, 112 + group + m)
+    assert_close(run(s, x).cpu().numpy(), rust_ref(x32, packed, scale, cb, n, k, 256, group))
+
+
 def test_skinny_one_launch_rows_of_very_different_magnitude():
-    """A power of two per row and round: rows at 3e5, 1, 1e-12, 1e-30 and 0
-    stay exact relative to their own size (the same five again in the
-    second 16-row block)."""
+    """Rows at 3e5, 1, 1e-12, 1e-30 and 0 stay exact relative to their own
+    size (the same five again in the second 16-row block): the bf16 path
+    keeps bf16's range, the fp16 one rescales each row by a power of two
+    per round."""
     n, k = 8192, 2048
     idx, packed, scale, cb, s = make(n, k, levels=256, seed=71)
     w64 = ref.dequant_tile_f32(idx, scale, cb, 128).astype(np.float64)
