@@ -1004,90 +1004,82 @@ constexpr int XS_F32 = 3;     // tagged f32 (attention output, SwiGLU output)
 // 32-value chunk agree on it through a quad max), the same staging as
 // gemv.hip's, split into hi and lo terms.  Slab s holds values 512 s ..
 // 512 s + 511; lane l converts values 8 l .. 8 l + 7 of each of the wave's
-// slabs (P::slab(j, wave) for the slabs the wave computes).  The loads of
-// a batch of them (and of the norm weights) go out together; tagged groups
-// whose tags are not all `tag` yet are re-read together (coherently), so a
-// wave waits one round trip per re-read, and only for its own slabs'
-// producers.  Returns the lane's sum of squares of the source values (RMS
-// sources; the norm weight multiplies each value after it is squared).
-template <class P, int XS, int J0, int NJ>
-EP_DEV float stage_batch(const void *x, const uint16_t *w, uint32_t tag, const PhaseLds &pl, int K, int ns,
-                         int *err)
+// slabs (P::slab(j, wave) for the slabs the wave computes), one slab at a
+// time, the next slab's first read (and its norm weights) issued before
+// the current one is polled, so its round trip overlaps the current slab's
+// wait and conversion (down phase of the 8B shapes, four slabs per wave:
+// 1.129 -> 1.100 ms per Llama-3-8B step; two slabs' values in registers).
+// Tagged groups whose tags are not all `tag` yet are re-read coherently,
+// so a wave waits for its own slabs' producers only.  Returns the lane's
+// sum of squares of the source values (RMS sources; the norm weight
+// multiplies each value after it is squared).
+template <class P, int XS>
+EP_DEV float stage_wave(const void *x, const uint16_t *w, uint32_t tag, const PhaseLds &pl, int K, int ns, int *err)
 {
     constexpr bool TAGGED = XS != XS_RMS_H0;
     constexpr bool RMS = XS == XS_RMS_H0 || XS == XS_RMS;
+    constexpr int SPW = P::SPW;
     const int wv = wave_id();
     const int lane = tid_fresh() & 63;
     // exact extent: every group lies inside the vector
     const auto rs = buffer_rsrc(x, TAGGED ? (uint32_t)K * 8u : (uint32_t)K * 4u);
-    u32x4_t q[NJ][4];
-    u32x4_t wr[NJ];
-#pragma unroll
-    for (int i = 0; i < NJ; ++i) {
+    u32x4_t q[2][4];
+    u32x4_t wr[2];
+    auto first = [&](int jj, u32x4_t (&qq)[4], u32x4_t &ww) {
         // group of 8 values (an idle slab reads slab 0: never used)
-        const uint32_t e = (uint32_t)(P::slab(J0 + i, wv, ns) * 64 + lane);
+        const uint32_t e = (uint32_t)(P::slab(jj, wv, ns) * 64 + lane);
         if constexpr (TAGGED) {
 #pragma unroll
             for (int h = 0; h < 4; ++h)  // a ring slot: first through the caches
-                q[i][h] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(e * 64 + 16 * h), 0, 0);
+                qq[h] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(e * 64 + 16 * h), 0, 0);
         } else {
-            q[i][0] = ldc16(rs, e * 32);
-            q[i][1] = ldc16(rs, e * 32 + 16);
+            qq[0] = ldc16(rs, e * 32);
+            qq[1] = ldc16(rs, e * 32 + 16);
         }
         if constexpr (RMS)
-            wr[i] = ldg((const u32x4_t *)(w + e * 8));
-    }
-    if constexpr (TAGGED) {
-        auto ready = [&](const u32x4_t (&g)[4]) {
-            bool ok = true;
+            ww = ldg((const u32x4_t *)(w + e * 8));
+    };
+    auto ready = [&](const u32x4_t (&g)[4]) {
+        bool ok = true;
 #pragma unroll
-            for (int h = 0; h < 4; ++h)
-                ok = ok && g[h][1] == tag && g[h][3] == tag;
-            return ok;
-        };
-        Spin sp;
-        for (;;) {
-            bool all = true;
-#pragma unroll
-            for (int i = 0; i < NJ; ++i)
-                all = all && (!P::slab_on(J0 + i, wv, ns) || ready(q[i]));
-            if (all || !sp.again(err))
-                break;
-            // (a compile-time loop: the unroller declines this one inside
-            // the poll loop, and a rolled loop would index q dynamically)
-            static_for<NJ>([&](auto ic) {
-                constexpr int i = decltype(ic)::value;
-                if (P::slab_on(J0 + i, wv, ns) && !ready(q[i])) {
-                    const uint32_t e = (uint32_t)(P::slab(J0 + i, wv, ns) * 64 + lane);
-#pragma unroll
-                    for (int h = 0; h < 4; ++h)
-                        q[i][h] = ldc16(rs, e * 64 + 16 * h);
-                }
-            });
-        }
-    }
+        for (int h = 0; h < 4; ++h)
+            ok = ok && g[h][1] == tag && g[h][3] == tag;
+        return ok;
+    };
+    first(0, q[0], wr[0]);
     float ssq = 0.0f;
+    static_for<SPW>([&](auto jc) {
+        constexpr int J = decltype(jc)::value;
+        constexpr int B = J & 1;
+        if constexpr (J + 1 < SPW)
+            first(J + 1, q[B ^ 1], wr[B ^ 1]);
+        if (!P::slab_on(J, wv, ns))  // wave-uniform
+            return;
+        const uint32_t e = (uint32_t)(P::slab(J, wv, ns) * 64 + lane);
+        if constexpr (TAGGED) {
+            Spin sp;
+            while (!ready(q[B]) && sp.again(err)) {
 #pragma unroll
-    for (int i = 0; i < NJ; ++i) {
-        if (!P::slab_on(J0 + i, wv, ns))  // wave-uniform
-            continue;
-        const uint32_t e = (uint32_t)(P::slab(J0 + i, wv, ns) * 64 + lane);
+                for (int h = 0; h < 4; ++h)
+                    q[B][h] = ldc16(rs, e * 64 + 16 * h);
+            }
+        }
         float v[8];
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
             if constexpr (TAGGED) {
-                v[2 * h] = __uint_as_float(q[i][h][0]);
-                v[2 * h + 1] = __uint_as_float(q[i][h][2]);
+                v[2 * h] = __uint_as_float(q[B][h][0]);
+                v[2 * h + 1] = __uint_as_float(q[B][h][2]);
             } else {
-                v[h] = __uint_as_float(q[i][0][h]);
-                v[4 + h] = __uint_as_float(q[i][1][h]);
+                v[h] = __uint_as_float(q[B][0][h]);
+                v[4 + h] = __uint_as_float(q[B][1][h]);
             }
         }
         if constexpr (RMS) {
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
                 float w0, w1;
-                unpack_pair<EP_BF16>(wr[i][h], w0, w1);
+                unpack_pair<EP_BF16>(wr[B][h], w0, w1);
                 ssq = fmaf(v[2 * h], v[2 * h], fmaf(v[2 * h + 1], v[2 * h + 1], ssq));
                 v[2 * h] *= w0;
                 v[2 * h + 1] *= w1;
@@ -1114,25 +1106,8 @@ EP_DEV float stage_batch(const void *x, const uint16_t *w, uint32_t tag, const P
         *(u32x4_t *)(pl.xl + e * 4) = l4;
         if ((e & 3) == 0)
             pl.xf[e >> 2] = ldexpf(1.0f, ex);
-    }
+    });
     return ssq;
-}
-
-// The wave's slabs in batches of at most kStageBatch: one slab (16 VGPRs of
-// tagged values in flight) per batch.  Two per batch measured no faster
-// and cost the down phase a prefetched block (the registers do not allow
-// both).
-constexpr int kStageBatch = 1;
-template <class P, int XS, int J0 = 0>
-EP_DEV float stage_wave(const void *x, const uint16_t *w, uint32_t tag, const PhaseLds &pl, int K, int ns,
-                        int *err)
-{
-    constexpr int NJ = P::SPW - J0 < kStageBatch ? P::SPW - J0 : kStageBatch;
-    const float s = stage_batch<P, XS, J0, NJ>(x, w, tag, pl, K, ns, err);
-    if constexpr (J0 + NJ < P::SPW)
-        return s + stage_wave<P, XS, J0 + NJ>(x, w, tag, pl, K, ns, err);
-    else
-        return s;
 }
 
 // ---------------------------------------------------------------- attention
