@@ -556,7 +556,11 @@ def side_workload(args):
                                      "T=2048, grad_x + grad_codebook + grad_scales",
                          "rows": rows,
                          "indices_frozen": all(r["indices_frozen"] for r in rows)}
-        out["roofline"] = {"bound": "mfma", "kernel": "dx_kernel + dw_kernel",
+        # T = 2048 takes the library route: two hipBLASLt GEMMs (grad_x, G = gy^T x)
+        # around this library's prescale, materialize, finish and codebook-epilogue
+        # kernels, the two chains on two streams
+        out["roofline"] = {"bound": "mfma",
+                           "kernel": "hipBLASLt GEMMs + gy_prep/dequant_tile4/dx_finish/gw_epilogue/gc_final",
                            "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS,
                            "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                            "traffic": None}

@@ -758,8 +758,8 @@ static BlasWs blas_ws(int64_t M, int64_t N, int64_t K)
 // back into the caller's stream with events (both work under stream
 // capture), so the memory-bound kernels of one overlap the other's GEMM.
 // Each caller stream gets its own side stream (default priority) and two
-// events, created on its first forked call outside capture (at most
-// kMaxSides per process; further caller streams run the chains in order):
+// events, created on its first call outside capture (at most kMaxSides
+// per process; further caller streams run the chains in order):
 // a capture on one caller stream then never joins a side stream that
 // another thread's eager calls use.  The first call of a shape bucket (the
 // one whose library GEMM plans time their candidate algorithms) runs both
@@ -796,6 +796,26 @@ static SideStream *side_for(hipStream_t stream, int64_t M, int64_t N, int64_t K)
         return nullptr;
     const bool capturing = cs != hipStreamCaptureStatusNone;
     std::lock_guard<std::mutex> lk(g_side_mu);
+    // the caller stream's side stream, created on its first call outside
+    // capture -- also when that call runs in order (a bucket's first call),
+    // so that a capture right after one eager call still forks
+    SideStream *sd = nullptr;
+    for (int i = 0; i < g_nside && !sd; ++i)
+        if (g_side[i].dev == dev && g_side[i].caller == stream)
+            sd = &g_side[i];
+    if (!sd && !capturing && g_nside < kMaxSides) {
+        sd = &g_side[g_nside++];
+        sd->dev = dev;
+        sd->caller = stream;
+        if (hipStreamCreateWithFlags(&sd->s, hipStreamNonBlocking) != hipSuccess) {
+            sd->s = nullptr;
+            (void)hipGetLastError();
+        } else if (hipEventCreateWithFlags(&sd->fork, hipEventDisableTiming) != hipSuccess ||
+                   hipEventCreateWithFlags(&sd->join, hipEventDisableTiming) != hipSuccess) {
+            sd->join = nullptr;
+            (void)hipGetLastError();
+        }
+    }
     const std::array<int64_t, 4> key{dev, pow2_ceil(M), pow2_ceil(N), pow2_ceil(K)};
     bool seen = g_bwd_seen.size() >= kMaxSeen;
     for (const auto &k : g_bwd_seen)
@@ -805,26 +825,7 @@ static SideStream *side_for(hipStream_t stream, int64_t M, int64_t N, int64_t K)
             g_bwd_seen.push_back(key);
         return nullptr;
     }
-    for (int i = 0; i < g_nside; ++i)
-        if (g_side[i].dev == dev && g_side[i].caller == stream)
-            return g_side[i].join ? &g_side[i] : nullptr;
-    if (capturing || g_nside >= kMaxSides)
-        return nullptr;
-    SideStream &sd = g_side[g_nside++];
-    sd.dev = dev;
-    sd.caller = stream;
-    if (hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking) != hipSuccess) {
-        sd.s = nullptr;
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    if (hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming) != hipSuccess ||
-        hipEventCreateWithFlags(&sd.join, hipEventDisableTiming) != hipSuccess) {
-        sd.join = nullptr;
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    return &sd;
+    return sd && sd->s && sd->join ? sd : nullptr;
 }
 
 // Whether the library route can run on `stream` now: always outside
