@@ -80,6 +80,9 @@ def parse():
                     help="decode: the headline (config 2); gemv: one 4096x4096 4-bit GEMV "
                          "over a rotating sweep (config 0); prefill: the 8-bit M sweep "
                          "(config 3); backward: the compressed-state backward (config 4)")
+    ap.add_argument("--fused-backward", action="store_true",
+                    help="backward: keep every token count on the fused kernels "
+                         "(EPURE_BWD_FUSED=1) instead of the library route from 512 tokens")
     ap.add_argument("--no-gemv", action="store_true",
                     help="decode: skip the config-0 GEMV sweep reported beside the step")
     ap.add_argument("--phases", action="store_true",
@@ -558,9 +561,12 @@ def side_workload(args):
                          "indices_frozen": all(r["indices_frozen"] for r in rows)}
         # T = 2048 takes the library route: two hipBLASLt GEMMs (grad_x, G = gy^T x)
         # around this library's prescale, materialize, finish and codebook-epilogue
-        # kernels, the two chains on two streams
+        # kernels, the two chains on two streams; --fused-backward the fused kernels
+        out["config"]["route"] = "fused" if args.fused_backward else "library"
         out["roofline"] = {"bound": "mfma",
-                           "kernel": "hipBLASLt GEMMs + gy_prep/dequant_tile4/dx_finish/gw_epilogue/gc_final",
+                           "kernel": ("gy_prep_kernel + dx_kernel + dw_kernel + gc_final_kernel"
+                                      if args.fused_backward else
+                                      "hipBLASLt GEMMs + gy_prep/dequant_tile4/dx_finish/gw_epilogue/gc_final"),
                            "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS,
                            "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                            "traffic": None}
@@ -570,6 +576,8 @@ def side_workload(args):
 
 def main():
     args = parse()
+    if args.fused_backward:
+        os.environ["EPURE_BWD_FUSED"] = "1"  # read by the library on its first backward call
     if args.copy_probe:
         copy_probe(args.copy_probe)
         return

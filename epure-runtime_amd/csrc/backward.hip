@@ -24,6 +24,7 @@
 //     across workgroups by a final kernel.  No float atomics race, so the
 //     result is deterministic.  `packed` is only read.
 #include <array>
+#include <cstdlib>
 #include <mutex>
 #include <vector>
 
@@ -715,10 +716,22 @@ static int dx_splits(int64_t M, int64_t N, int64_t K)
 // Token counts from which grad_x and G run as library GEMMs (hipBLASLt
 // reaches ~2x the fused kernels' MFMA rate on these plain products; below,
 // materializing W costs more than it saves).
+// EPURE_BWD_FUSED=1 in the environment (read on the first call) keeps every
+// token count on the fused kernels: no W or grad_W in memory, no hipBLASLt
+// handle, no host wait, at about half the library route's rate at 2048
+// tokens.
 constexpr int64_t kBlasMinM = 512;
+static bool fused_forced()
+{
+    static const bool forced = [] {
+        const char *v = std::getenv("EPURE_BWD_FUSED");
+        return v != nullptr && v[0] != '\0' && v[0] != '0';
+    }();
+    return forced;
+}
 static bool blas_route(int64_t M, int64_t N, int64_t K)
 {
-    return M >= kBlasMinM && N >= 256 && K >= 256;
+    return M >= kBlasMinM && N >= 256 && K >= 256 && !fused_forced();
 }
 static size_t al256(size_t b) { return (b + 255) / 256 * 256; }
 

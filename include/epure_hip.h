@@ -142,6 +142,8 @@ int ep_expert_matmul(const void *x, int x_dtype, int64_t ldx, const int32_t *exp
  *     [N, K] and grad_W = gy^T . x as f32 [N, K] (written once, read once by
  *     the epilogue that forms grad_scale and grad_cb), plus the fp16 gy, an
  *     f32 [M, K] grad_x product and two 32 MiB hipBLASLt workspaces.
+ *     EPURE_BWD_FUSED=1 in the environment (read on the first call) keeps
+ *     every M on the fused kernels instead.
  * ep_dequant_matmul_bwd_workspace() returns the larger of the two needs.
  */
 size_t ep_dequant_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int levels, int group);
