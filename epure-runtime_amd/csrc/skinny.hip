@@ -511,19 +511,19 @@ __global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
             }
         }
     };
-    // Every wave's codebook load goes out before any weight load (returns
-    // come back in the order the CU issued the loads, so a codebook load
-    // behind other waves' weights would hold the table build until those
-    // arrived); then the first half of the prologue's rounds, the table
+    // Each wave's codebook entry has landed before its first weight load
+    // goes out (issued together with the chip-wide weight burst, it would
+    // queue behind it and hold the table build: 4096^2 at M = 4, 11.1 ->
+    // 10.5 us); then the first half of the prologue's rounds, the table
     // build, and the rest after it, each wave on its own.
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
+    s_cbraw[tid] = cbraw;
+    __builtin_amdgcn_sched_barrier(0);
     constexpr int DH = D / 2;
 #pragma unroll
     for (int d = 0; d < DH; ++d)
         issue(d, rb + d);
     __builtin_amdgcn_sched_barrier(0);
-    s_cbraw[tid] = cbraw;
     lds_barrier();
     if (tid < 256) {
         float c = 0.0f;
