@@ -307,8 +307,8 @@ def prefill_sweep(seed=0, replays=10):
                          "hbm_frac": round(byt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
                          "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
-                         # 8-bit rows of 4 or 8 slabs (K = 1024, 2048) take gemv_row_kernel
-                         "kernel": (("gemv_row_kernel" if k in (1024, 2048) else "gemv_lut_kernel")
+                         # 8-bit rows of 4, 8 or 16 slabs (K = 1024, 2048, 4096) take gemv_row_kernel
+                         "kernel": (("gemv_row_kernel" if k in (1024, 2048, 4096) else "gemv_lut_kernel")
                                     if m == 1 else
                                     "sk1_kernel" if _sk1_serves(m, n, cus) else
                                     "sk_kernel + sk_reduce_kernel" if m <= 64 else

@@ -605,8 +605,9 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     }
 }
 
-// Batch-1 GEMV over rows of S = 4 or 8 slabs (K = 2048 / 4096 with 4-bit
-// indices, 1024 / 2048 with 8-bit), one block of ROWS rows per workgroup:
+// Batch-1 GEMV over rows of S = 4, 8 or 16 slabs (K = 2048 / 4096 / 8192
+// with 4-bit indices, 1024 / 2048 / 4096 with 8-bit), one block of ROWS rows
+// per workgroup (four 16-byte loads per lane: 4, 2 or 1 rows per wave):
 // wave w owns rows RW w .. RW w + RW - 1 across the whole row (each 16-byte
 // load of a lane covers 4 slabs of one row: lane (sl, c) reads chunk c of
 // slab 4 j + sl), so each row's dot product is summed inside one wave (DPP
@@ -636,7 +637,7 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
     constexpr bool HL = XDT == EP_F32;          // f32 rows: hi and lo fp16 terms
     constexpr int ESZ = XDT == EP_F32 ? 4 : 2;
     constexpr int XPC = ESZ * KPC / 16;         // 16-byte pieces of x per chunk
-    static_assert(S == 4 || S == 8, "rows of 4 or 8 slabs");
+    static_assert(S == 4 || S == 8 || S == 16, "rows of 4, 8 or 16 slabs");
     __shared__ __align__(16) uint32_t tab[kTabDwords];
     __shared__ __align__(16) uint32_t xs[NCH * PAIRS];
     __shared__ __align__(16) uint32_t xl[HL ? NCH * PAIRS : 4];
@@ -1098,8 +1099,13 @@ bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
     return fits(bits, spw, mt, x.dtype == EP_F32);
 }
 
-// gemv_row_kernel serves a batch-1 row of exactly 4 or 8 slabs.
-static int row_kernel_slabs(const GemvArgs &a) { return a.row_bytes == 4 * kSlabBytes ? 4 : (a.row_bytes == 8 * kSlabBytes ? 8 : 0); }
+// gemv_row_kernel serves a batch-1 row of exactly 4, 8 or 16 slabs (16:
+// config 3's 8-bit K = 4096 rows, 8.23 -> 5.84 us at 4096^2 and 21.6 ->
+// 17.6 us at 14336 x 4096 against gemv_lut_kernel).
+static int row_kernel_slabs(const GemvArgs &a)
+{
+    return a.row_bytes == 4 * kSlabBytes ? 4 : (a.row_bytes == 8 * kSlabBytes ? 8 : (a.row_bytes == 16 * kSlabBytes ? 16 : 0));
+}
 
 template <int BITS, int XDT, int S>
 static void launch_row_x(const GemvArgs &a, dim3 g, dim3 b, hipStream_t stream)
@@ -1113,7 +1119,7 @@ static void launch_row_x(const GemvArgs &a, dim3 g, dim3 b, hipStream_t stream)
 template <int BITS, int S>
 static int launch_row(const GemvArgs &a, int xdt, hipStream_t stream)
 {
-    const int rows = EP_GEMV_ROW_WAVES * (S == 8 ? 2 : 4);
+    const int rows = EP_GEMV_ROW_WAVES * (4 / (S / 4));
     const dim3 g((unsigned)((a.seg[0].N + rows - 1) / rows), a.gidx ? (unsigned)a.ntok : 1u);
     const dim3 b(64 * EP_GEMV_ROW_WAVES);
     if (xdt == EP_BF16)
@@ -1130,8 +1136,10 @@ static int dispatch_row(const GemvArgs &a, int bits, int xdt, hipStream_t stream
 {
     const int S = row_kernel_slabs(a);
     if (bits == 4)
-        return S == 8 ? launch_row<4, 8>(a, xdt, stream) : launch_row<4, 4>(a, xdt, stream);
-    return S == 8 ? launch_row<8, 8>(a, xdt, stream) : launch_row<8, 4>(a, xdt, stream);
+        return S == 16 ? launch_row<4, 16>(a, xdt, stream)
+                       : (S == 8 ? launch_row<4, 8>(a, xdt, stream) : launch_row<4, 4>(a, xdt, stream));
+    return S == 16 ? launch_row<8, 16>(a, xdt, stream)
+                   : (S == 8 ? launch_row<8, 8>(a, xdt, stream) : launch_row<8, 4>(a, xdt, stream));
 }
 
 int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,
