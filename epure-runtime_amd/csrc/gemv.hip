@@ -605,9 +605,10 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
     }
 }
 
-// Batch-1 GEMV over rows of S = 4, 8 or 16 slabs (K = 2048 / 4096 / 8192
-// with 4-bit indices, 1024 / 2048 / 4096 with 8-bit), one block of ROWS rows
-// per workgroup (four 16-byte loads per lane: 4, 2 or 1 rows per wave):
+// Batch-1 GEMV over rows of S = 4 .. 64 slabs, a multiple of 4 (served: 4,
+// 8, 12, 16, 24, 28, 32 and, with 8-bit indices, 56: K = 2048 .. 16384 with
+// 4-bit indices, 1024 .. 14336 with 8-bit), one block of ROWS rows per
+// workgroup (4, 2 or 1 rows per wave; S / 4 16-byte loads per lane and row):
 // wave w owns rows RW w .. RW w + RW - 1 across the whole row (each 16-byte
 // load of a lane covers 4 slabs of one row: lane (sl, c) reads chunk c of
 // slab 4 j + sl), so each row's dot product is summed inside one wave (DPP
@@ -630,14 +631,20 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
     constexpr int PAIRS = BITS == 4 ? 16 : 8;  // weight pairs per 16-byte chunk
     constexpr int KPC = 2 * PAIRS;              // k values per chunk
     constexpr int LPR = S / 4;                  // 16-byte loads of a lane per row
-    constexpr int RW = 4 / LPR;                 // rows per wave (4 loads per lane)
+    constexpr int RW = LPR < 4 && 4 % LPR == 0 ? 4 / LPR : 1;  // rows per wave
+    constexpr int NL = LPR * RW;                // 16-byte weight loads per lane
     constexpr int ROWS = NW * RW;
     constexpr int NPC = 2048 / NT;              // table pieces per thread
     constexpr int NCH = S * 16;                 // chunks per row
+    constexpr int CPT = (NCH + NT - 1) / NT;    // chunks staged per thread
     constexpr bool HL = XDT == EP_F32;          // f32 rows: hi and lo fp16 terms
     constexpr int ESZ = XDT == EP_F32 ? 4 : 2;
     constexpr int XPC = ESZ * KPC / 16;         // 16-byte pieces of x per chunk
-    static_assert(S == 4 || S == 8 || S == 16, "rows of 4, 8 or 16 slabs");
+    // rows of up to 4 loads per lane keep their activation chunks in
+    // registers for all their rows; longer rows read each chunk from LDS
+    // at its load (one use each)
+    constexpr bool XPRE = RW > 1 || LPR <= 4;
+    static_assert(S % 4 == 0 && S >= 4 && S <= 64, "rows of a multiple of 4 slabs, at most 64");
     __shared__ __align__(16) uint32_t tab[kTabDwords];
     __shared__ __align__(16) uint32_t xs[NCH * PAIRS];
     __shared__ __align__(16) uint32_t xl[HL ? NCH * PAIRS : 4];
@@ -664,13 +671,15 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
 
     // ---- the activation chunk and codebook loads (the weights follow the
     // table build)
-    u32x4_t xraw[XPC];
-    {
+    u32x4_t xraw[CPT][XPC];
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int ch = tid + NT * q;
         const auto *xp = (const __attribute__((address_space(1))) u32x4_t *)(
-            xbase + (int64_t)(tid < NCH ? tid : 0) * KPC * ESZ);
+            xbase + (int64_t)(ch < NCH ? ch : 0) * KPC * ESZ);
 #pragma unroll
         for (int p = 0; p < XPC; ++p)
-            xraw[p] = xp[p];
+            xraw[q][p] = xp[p];
     }
     // codebook entries of this thread's NPC table stores (store i = tid +
     // NT k writes a 16-byte piece of entry b = i >> 3): 4-bit: cb[b & 15]
@@ -695,30 +704,32 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
         cb_at(cbi[k], cbr[k][0], cbr[k][1]);
     }
 
-    // ---- stage the activation chunk and the pair table, one barrier
-    {
+    // ---- stage the activation chunks and the pair table, one barrier
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+        const int ch = tid + NT * q;
         float v[KPC];
         if constexpr (XDT == EP_F32) {
 #pragma unroll
             for (int p = 0; p < XPC; ++p)
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    v[4 * p + t] = __uint_as_float(xraw[p][t]);
+                    v[4 * p + t] = __uint_as_float(xraw[q][p][t]);
         } else {
 #pragma unroll
             for (int p = 0; p < XPC; ++p)
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    unpack_pair<XDT>(xraw[p][t], v[8 * p + 2 * t], v[8 * p + 2 * t + 1]);
+                    unpack_pair<XDT>(xraw[q][p][t], v[8 * p + 2 * t], v[8 * p + 2 * t + 1]);
         }
         float am = 0.0f;
 #pragma unroll
         for (int t = 0; t < KPC; ++t)
             am = fmaxf(am, fabsf(v[t]));
         const int e = row_exponent(am);
-        if (tid < NCH) {
-            stage_chunk<HL, PAIRS>(v, ldexpf(1.0f, -e), xs + tid * PAIRS, xl + (HL ? tid * PAIRS : 0));
-            xf[tid] = ldexpf(1.0f, e);
+        if (ch < NCH) {
+            stage_chunk<HL, PAIRS>(v, ldexpf(1.0f, -e), xs + ch * PAIRS, xl + (HL ? ch * PAIRS : 0));
+            xf[ch] = ldexpf(1.0f, e);
         }
     }
     {
@@ -742,12 +753,12 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
     }
     __builtin_amdgcn_sched_barrier(0);
     // weights: load i covers row r = i / LPR, slabs 4 (i % LPR) .. + 3
-    u32x4_t wq[4];
-    uint32_t sraw[4];  // the scale's bits: f32 (SC32) or fp16 / bf16
+    u32x4_t wq[NL];
+    uint32_t sraw[NL];  // the scale's bits: f32 (SC32) or fp16 / bf16
     {
         const auto *sp = (const __attribute__((address_space(1))) uint16_t *)scale;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NL; ++i) {
             const int row = row0 + i / LPR;
             const uint32_t rs = row < N ? (uint32_t)row : 0u;
             const uint32_t b0 = (uint32_t)((i % LPR) * 4 + sl) * kSlabBytes + (uint32_t)c * 16;
@@ -769,26 +780,31 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
     lds_barrier();
 
     // ---- the lane's activation chunks (slab 4 j + sl, chunk c)
-    f16x2_t xh[LPR][PAIRS];
-    f16x2_t xlo[HL ? LPR : 1][HL ? PAIRS : 1];
-    float fexp[LPR];
-#pragma unroll
-    for (int j = 0; j < LPR; ++j) {
+    constexpr int XR = XPRE ? LPR : 1;  // chunks held in registers
+    f16x2_t xh[XR][PAIRS];
+    f16x2_t xlo[HL ? XR : 1][HL ? PAIRS : 1];
+    float fexp[XR];
+    auto read_x = [&](int j, int slot) {
         const int cc = (j * 4 + sl) * 16 + c;
 #pragma unroll
         for (int p = 0; p < PAIRS; p += 4) {
             const u32x4_t q4 = *(const u32x4_t *)(xs + cc * PAIRS + p);
 #pragma unroll
             for (int t = 0; t < 4; ++t)
-                xh[j][p + t] = as_f16x2(q4[t]);
+                xh[slot][p + t] = as_f16x2(q4[t]);
             if constexpr (HL) {
                 const u32x4_t l4 = *(const u32x4_t *)(xl + cc * PAIRS + p);
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    xlo[j][p + t] = as_f16x2(l4[t]);
+                    xlo[slot][p + t] = as_f16x2(l4[t]);
             }
         }
-        fexp[j] = xf[cc];
+        fexp[slot] = xf[cc];
+    };
+    if constexpr (XPRE) {
+#pragma unroll
+        for (int j = 0; j < LPR; ++j)
+            read_x(j, j);
     }
 
     // ---- dot products: load i adds to row i / LPR
@@ -798,8 +814,11 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
     for (int r = 0; r < RW; ++r)
         acc[r] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NL; ++i) {
         const int r = i / LPR, j = i % LPR;
+        if constexpr (!XPRE)
+            read_x(j, 0);
+        const int xj = XPRE ? j : 0;  // the chunk's register slot
         float part = 0.0f, plo = 0.0f;
 #pragma unroll
         for (int wd = 0; wd < 4; ++wd) {
@@ -808,9 +827,9 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
                     const f16x2_t wv = as_f16x2(lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[b])));
-                    part = __builtin_amdgcn_fdot2(wv, xh[j][wd * 4 + b], part, false);
+                    part = __builtin_amdgcn_fdot2(wv, xh[xj][wd * 4 + b], part, false);
                     if constexpr (HL)
-                        plo = __builtin_amdgcn_fdot2(wv, xlo[j][wd * 4 + b], plo, false);
+                        plo = __builtin_amdgcn_fdot2(wv, xlo[xj][wd * 4 + b], plo, false);
                 }
             } else {
 #pragma unroll
@@ -818,9 +837,9 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
                     const uint32_t t0 = lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p]));
                     const uint32_t t1 = lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p + 1]));
                     const f16x2_t wv = as_f16x2(__builtin_amdgcn_perm(t1, t0, 0x07060100u));
-                    part = __builtin_amdgcn_fdot2(wv, xh[j][wd * 2 + p], part, false);
+                    part = __builtin_amdgcn_fdot2(wv, xh[xj][wd * 2 + p], part, false);
                     if constexpr (HL)
-                        plo = __builtin_amdgcn_fdot2(wv, xlo[j][wd * 2 + p], plo, false);
+                        plo = __builtin_amdgcn_fdot2(wv, xlo[xj][wd * 2 + p], plo, false);
                 }
             }
         }
@@ -828,7 +847,7 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
         const float sc = SC32 ? __uint_as_float(raw)
                               : (a.scale_dtype == EP_F16 ? (float)f16_from_bits((uint16_t)raw)
                                                          : bf16_to_f32((uint16_t)raw));
-        acc[r] = fmaf(HL ? part + plo : part, (row0 + r < N ? sc : 0.0f) * fexp[j], acc[r]);
+        acc[r] = fmaf(HL ? part + plo : part, (row0 + r < N ? sc : 0.0f) * fexp[xj], acc[r]);
     }
     // ---- each row's sum inside the wave; lane 0 stores it
 #pragma unroll
@@ -1099,12 +1118,16 @@ bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
     return fits(bits, spw, mt, x.dtype == EP_F32);
 }
 
-// gemv_row_kernel serves a batch-1 row of exactly 4, 8 or 16 slabs (16:
-// config 3's 8-bit K = 4096 rows, 8.23 -> 5.84 us at 4096^2 and 21.6 ->
-// 17.6 us at 14336 x 4096 against gemv_lut_kernel).
-static int row_kernel_slabs(const GemvArgs &a)
+// The row lengths gemv_row_kernel serves, in 256-byte slabs (against
+// gemv_lut_kernel at config 3's 8-bit M = 1: 4096^2 8.23 -> 5.84 us,
+// 14336 x 4096 21.6 -> 17.5 us, 4096 x 14336 22.6 -> 19.1 us).
+static int row_kernel_slabs(const GemvArgs &a, int bits)
 {
-    return a.row_bytes == 4 * kSlabBytes ? 4 : (a.row_bytes == 8 * kSlabBytes ? 8 : (a.row_bytes == 16 * kSlabBytes ? 16 : 0));
+    if (a.row_bytes % kSlabBytes != 0)
+        return 0;
+    const int s = (int)(a.row_bytes / kSlabBytes);
+    const bool ok = s == 4 || s == 8 || s == 12 || s == 16 || s == 24 || s == 28 || s == 32 || (s == 56 && bits == 8);
+    return ok ? s : 0;
 }
 
 template <int BITS, int XDT, int S>
@@ -1119,7 +1142,8 @@ static void launch_row_x(const GemvArgs &a, dim3 g, dim3 b, hipStream_t stream)
 template <int BITS, int S>
 static int launch_row(const GemvArgs &a, int xdt, hipStream_t stream)
 {
-    const int rows = EP_GEMV_ROW_WAVES * (4 / (S / 4));
+    constexpr int LPR = S / 4;
+    const int rows = EP_GEMV_ROW_WAVES * (LPR < 4 && 4 % LPR == 0 ? 4 / LPR : 1);
     const dim3 g((unsigned)((a.seg[0].N + rows - 1) / rows), a.gidx ? (unsigned)a.ntok : 1u);
     const dim3 b(64 * EP_GEMV_ROW_WAVES);
     if (xdt == EP_BF16)
@@ -1132,14 +1156,35 @@ static int launch_row(const GemvArgs &a, int xdt, hipStream_t stream)
     return EP_OK;
 }
 
+template <int BITS>
+static int dispatch_row_bits(const GemvArgs &a, int S, int xdt, hipStream_t stream)
+{
+    switch (S) {
+    case 4:
+        return launch_row<BITS, 4>(a, xdt, stream);
+    case 8:
+        return launch_row<BITS, 8>(a, xdt, stream);
+    case 12:
+        return launch_row<BITS, 12>(a, xdt, stream);
+    case 16:
+        return launch_row<BITS, 16>(a, xdt, stream);
+    case 24:
+        return launch_row<BITS, 24>(a, xdt, stream);
+    case 28:
+        return launch_row<BITS, 28>(a, xdt, stream);
+    case 32:
+        return launch_row<BITS, 32>(a, xdt, stream);
+    default:
+        if constexpr (BITS == 8)
+            return launch_row<BITS, 56>(a, xdt, stream);  // 8-bit K = 14336
+        return set_error(EP_DECLINE_SHAPE, "row GEMV: %d slabs", S);
+    }
+}
+
 static int dispatch_row(const GemvArgs &a, int bits, int xdt, hipStream_t stream)
 {
-    const int S = row_kernel_slabs(a);
-    if (bits == 4)
-        return S == 16 ? launch_row<4, 16>(a, xdt, stream)
-                       : (S == 8 ? launch_row<4, 8>(a, xdt, stream) : launch_row<4, 4>(a, xdt, stream));
-    return S == 16 ? launch_row<8, 16>(a, xdt, stream)
-                   : (S == 8 ? launch_row<8, 8>(a, xdt, stream) : launch_row<8, 4>(a, xdt, stream));
+    const int S = row_kernel_slabs(a, bits);
+    return bits == 4 ? dispatch_row_bits<4>(a, S, xdt, stream) : dispatch_row_bits<8>(a, S, xdt, stream);
 }
 
 int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y,
@@ -1148,7 +1193,7 @@ int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc 
     if (!gemv_serves(w, x, M))
         return EP_DECLINE_SHAPE;
     const GemvArgs a = make_args(w, x, M, y);
-    if (M == 1 && row_kernel_slabs(a) != 0)
+    if (M == 1 && row_kernel_slabs(a, w.bits()) != 0)
         return dispatch_row(a, w.bits(), x.dtype, stream);
     int spw, waves;
     plan(a.row_bytes, spw, waves);
@@ -1186,7 +1231,7 @@ int launch_gemv_gather(const PackedDesc &w, const ActDesc &x, int64_t T, const i
     a.ntok = (int)T;
     a.estride_w = w.N * a.row_bytes;
     a.estride_s = w.N * w.ld_scale * (w.scale_dtype == EP_F32 ? 4 : 2);
-    if (row_kernel_slabs(a) != 0)
+    if (row_kernel_slabs(a, w.bits()) != 0)
         return dispatch_row(a, w.bits(), x.dtype, stream);
     int spw, waves;
     plan(a.row_bytes, spw, waves);
