@@ -623,7 +623,7 @@ __global__ void __launch_bounds__(512) gemv_lut_kernel(GemvArgs a)
 // staging and the table build: 4.85).  SC32: f32 group scales; otherwise one
 // 16-bit load per scale (fp16 or bf16), not the two halves of a word
 // (4.61 -> 4.48 us).
-template <int BITS, int XDT, int S, bool SC32>
+template <int BITS, int XDT, int S, bool SC32, int MT>
 __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvArgs a)
 {
     constexpr int NW = EP_GEMV_ROW_WAVES;       // waves per workgroup
@@ -635,20 +635,21 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
     constexpr int NL = LPR * RW;                // 16-byte weight loads per lane
     constexpr int ROWS = NW * RW;
     constexpr int NPC = 2048 / NT;              // table pieces per thread
-    constexpr int NCH = S * 16;                 // chunks per row
-    constexpr int CPT = (NCH + NT - 1) / NT;    // chunks staged per thread
+    constexpr int NCH = S * 16;                 // chunks per activation row
+    constexpr int CPT = (NCH * MT + NT - 1) / NT;  // chunks staged per thread
     constexpr bool HL = XDT == EP_F32;          // f32 rows: hi and lo fp16 terms
     constexpr int ESZ = XDT == EP_F32 ? 4 : 2;
     constexpr int XPC = ESZ * KPC / 16;         // 16-byte pieces of x per chunk
-    // rows of up to 4 loads per lane keep their activation chunks in
-    // registers for all their rows; longer rows read each chunk from LDS
-    // at its load (one use each)
-    constexpr bool XPRE = RW > 1 || LPR <= 4;
+    // one activation row with up to 4 loads per lane keeps its chunks in
+    // registers for all its rows; otherwise each chunk is read from LDS at
+    // its load
+    constexpr bool XPRE = MT == 1 && (RW > 1 || LPR <= 4);
     static_assert(S % 4 == 0 && S >= 4 && S <= 64, "rows of a multiple of 4 slabs, at most 64");
+    static_assert(MT == 1 || MT == 2 || MT == 4, "1, 2 or 4 activation rows");
     __shared__ __align__(16) uint32_t tab[kTabDwords];
-    __shared__ __align__(16) uint32_t xs[NCH * PAIRS];
-    __shared__ __align__(16) uint32_t xl[HL ? NCH * PAIRS : 4];
-    __shared__ float xf[NCH];
+    __shared__ __align__(16) uint32_t xs[MT * NCH * PAIRS];
+    __shared__ __align__(16) uint32_t xl[HL ? MT * NCH * PAIRS : 4];
+    __shared__ float xf[MT * NCH];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sl = lane >> 4, c = lane & 15;
@@ -670,13 +671,15 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
     const int row0 = (int)blockIdx.x * ROWS + wave * RW;
 
     // ---- the activation chunk and codebook loads (the weights follow the
-    // table build)
+    // table build); chunk ch is chunk ch % NCH of activation row ch / NCH
     u32x4_t xraw[CPT][XPC];
 #pragma unroll
     for (int q = 0; q < CPT; ++q) {
         const int ch = tid + NT * q;
+        const int m = ch / NCH;
+        const bool ok = ch < NCH * MT && m < a.M;
         const auto *xp = (const __attribute__((address_space(1))) u32x4_t *)(
-            xbase + (int64_t)(ch < NCH ? ch : 0) * KPC * ESZ);
+            xbase + (ok ? ((int64_t)m * a.ldx + (int64_t)(ch % NCH) * KPC) * ESZ : 0));
 #pragma unroll
         for (int p = 0; p < XPC; ++p)
             xraw[q][p] = xp[p];
@@ -708,26 +711,27 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
 #pragma unroll
     for (int q = 0; q < CPT; ++q) {
         const int ch = tid + NT * q;
+        const bool live = ch / NCH < a.M;  // rows past M stage zeros (never stored)
         float v[KPC];
         if constexpr (XDT == EP_F32) {
 #pragma unroll
             for (int p = 0; p < XPC; ++p)
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    v[4 * p + t] = __uint_as_float(xraw[q][p][t]);
+                    v[4 * p + t] = live ? __uint_as_float(xraw[q][p][t]) : 0.0f;
         } else {
 #pragma unroll
             for (int p = 0; p < XPC; ++p)
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    unpack_pair<XDT>(xraw[q][p][t], v[8 * p + 2 * t], v[8 * p + 2 * t + 1]);
+                    unpack_pair<XDT>(live ? xraw[q][p][t] : 0u, v[8 * p + 2 * t], v[8 * p + 2 * t + 1]);
         }
         float am = 0.0f;
 #pragma unroll
         for (int t = 0; t < KPC; ++t)
             am = fmaxf(am, fabsf(v[t]));
         const int e = row_exponent(am);
-        if (ch < NCH) {
+        if (ch < NCH * MT) {
             stage_chunk<HL, PAIRS>(v, ldexpf(1.0f, -e), xs + ch * PAIRS, xl + (HL ? ch * PAIRS : 0));
             xf[ch] = ldexpf(1.0f, e);
         }
@@ -779,27 +783,31 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
     __builtin_amdgcn_sched_barrier(0);  // the weight loads go out before the barrier
     lds_barrier();
 
-    // ---- the lane's activation chunks (slab 4 j + sl, chunk c)
+    // ---- the lane's activation chunks (slab 4 j + sl, chunk c; row m)
     constexpr int XR = XPRE ? LPR : 1;  // chunks held in registers
-    f16x2_t xh[XR][PAIRS];
-    f16x2_t xlo[HL ? XR : 1][HL ? PAIRS : 1];
-    float fexp[XR];
+    f16x2_t xh[XR][MT][PAIRS];
+    f16x2_t xlo[HL ? XR : 1][HL ? MT : 1][HL ? PAIRS : 1];
+    float fexp[XR][MT];
     auto read_x = [&](int j, int slot) {
         const int cc = (j * 4 + sl) * 16 + c;
 #pragma unroll
-        for (int p = 0; p < PAIRS; p += 4) {
-            const u32x4_t q4 = *(const u32x4_t *)(xs + cc * PAIRS + p);
+        for (int m = 0; m < MT; ++m) {
+            const int ch = m * NCH + cc;
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-                xh[slot][p + t] = as_f16x2(q4[t]);
-            if constexpr (HL) {
-                const u32x4_t l4 = *(const u32x4_t *)(xl + cc * PAIRS + p);
+            for (int p = 0; p < PAIRS; p += 4) {
+                const u32x4_t q4 = *(const u32x4_t *)(xs + ch * PAIRS + p);
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    xlo[slot][p + t] = as_f16x2(l4[t]);
+                    xh[slot][m][p + t] = as_f16x2(q4[t]);
+                if constexpr (HL) {
+                    const u32x4_t l4 = *(const u32x4_t *)(xl + ch * PAIRS + p);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        xlo[slot][m][p + t] = as_f16x2(l4[t]);
+                }
             }
+            fexp[slot][m] = xf[ch];
         }
-        fexp[slot] = xf[cc];
     };
     if constexpr (XPRE) {
 #pragma unroll
@@ -807,19 +815,24 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
             read_x(j, j);
     }
 
-    // ---- dot products: load i adds to row i / LPR
+    // ---- dot products: load i adds to row i / LPR of every activation row
     const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
-    float acc[RW];
+    float acc[RW][MT];
 #pragma unroll
     for (int r = 0; r < RW; ++r)
-        acc[r] = 0.0f;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            acc[r][m] = 0.0f;
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
         const int r = i / LPR, j = i % LPR;
         if constexpr (!XPRE)
             read_x(j, 0);
         const int xj = XPRE ? j : 0;  // the chunk's register slot
-        float part = 0.0f, plo = 0.0f;
+        float part[MT], plo[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            part[m] = plo[m] = 0.0f;
 #pragma unroll
         for (int wd = 0; wd < 4; ++wd) {
             const uint32_t w = wq[i][wd];
@@ -827,9 +840,12 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
 #pragma unroll
                 for (int b = 0; b < 4; ++b) {
                     const f16x2_t wv = as_f16x2(lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[b])));
-                    part = __builtin_amdgcn_fdot2(wv, xh[xj][wd * 4 + b], part, false);
-                    if constexpr (HL)
-                        plo = __builtin_amdgcn_fdot2(wv, xlo[xj][wd * 4 + b], plo, false);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        part[m] = __builtin_amdgcn_fdot2(wv, xh[xj][m][wd * 4 + b], part[m], false);
+                        if constexpr (HL)
+                            plo[m] = __builtin_amdgcn_fdot2(wv, xlo[xj][m][wd * 4 + b], plo[m], false);
+                    }
                 }
             } else {
 #pragma unroll
@@ -837,9 +853,12 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
                     const uint32_t t0 = lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p]));
                     const uint32_t t1 = lds_read_u32(tab, __builtin_amdgcn_perm(w, lane4, kSelByte[2 * p + 1]));
                     const f16x2_t wv = as_f16x2(__builtin_amdgcn_perm(t1, t0, 0x07060100u));
-                    part = __builtin_amdgcn_fdot2(wv, xh[xj][wd * 2 + p], part, false);
-                    if constexpr (HL)
-                        plo = __builtin_amdgcn_fdot2(wv, xlo[xj][wd * 2 + p], plo, false);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        part[m] = __builtin_amdgcn_fdot2(wv, xh[xj][m][wd * 2 + p], part[m], false);
+                        if constexpr (HL)
+                            plo[m] = __builtin_amdgcn_fdot2(wv, xlo[xj][m][wd * 2 + p], plo[m], false);
+                    }
                 }
             }
         }
@@ -847,20 +866,26 @@ __global__ void __launch_bounds__(64 * EP_GEMV_ROW_WAVES) gemv_row_kernel(GemvAr
         const float sc = SC32 ? __uint_as_float(raw)
                               : (a.scale_dtype == EP_F16 ? (float)f16_from_bits((uint16_t)raw)
                                                          : bf16_to_f32((uint16_t)raw));
-        acc[r] = fmaf(HL ? part + plo : part, (row0 + r < N ? sc : 0.0f) * fexp[xj], acc[r]);
-    }
-    // ---- each row's sum inside the wave; lane 0 stores it
+        const float scr = row0 + r < N ? sc : 0.0f;
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-        const float v = wave_sum(acc[r]);
-        const int row = row0 + r;
-        if (lane == 0 && row < N) {
-            float o = v;
-            if (a.accumulate)
-                o += load_as_f32(yp, a.y_dtype, row);
-            store_from_f32(yp, a.y_dtype, row, o);
-        }
+        for (int m = 0; m < MT; ++m)
+            acc[r][m] = fmaf(HL ? part[m] + plo[m] : part[m], scr * fexp[xj][m], acc[r][m]);
     }
+    // ---- each row's sums inside the wave; lane 0 stores them
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float v = wave_sum(acc[r][m]);
+            const int row = row0 + r;
+            if (lane == 0 && row < N && m < a.M) {
+                const int64_t off = (int64_t)m * a.ldy + row;
+                float o = v;
+                if (a.accumulate)
+                    o += load_as_f32(yp, a.y_dtype, off);
+                store_from_f32(yp, a.y_dtype, off, o);
+            }
+        }
 }
 
 // Any shape, any stride, any M: one wave per output row, fp32 arithmetic
@@ -1100,6 +1125,36 @@ bool shape_ok(int bits, int64_t N, int64_t K, int group, int64_t ld_scale, bool 
 
 }  // namespace
 
+// The most activation rows the row kernel takes at once, with 16-bit
+// activations and rows of 4, 8 or 16 slabs: 4 with 4-bit indices (4096^2
+// at M = 2 / 3 / 4: 7.65 / 10.1 / 10.2 -> 5.8 / 7.9 / 8.3 us against
+// gemv_lut_kernel; 2 for rows of 16 slabs, whose four would spill), 2 with
+// 8-bit ones (10.1 -> 9.4 us at M = 2; at M = 3 and 4 the MFMA small-M
+// kernel is faster: 10.2 against 11.3 and 11.5); else 1
+constexpr int row_max_mt(int bits, int S, int xdt)
+{
+    return xdt == EP_F32 || (S != 4 && S != 8 && S != 16) ? 1 : (bits == 8 || S == 16 ? 2 : 4);
+}
+
+// The row lengths gemv_row_kernel serves, in 256-byte slabs (against
+// gemv_lut_kernel at config 3's 8-bit M = 1: 4096^2 8.23 -> 5.84 us,
+// 14336 x 4096 21.6 -> 17.5 us, 4096 x 14336 22.6 -> 19.1 us).
+static int row_slabs(int64_t row_bytes, int bits)
+{
+    if (row_bytes % kSlabBytes != 0)
+        return 0;
+    const int s = (int)(row_bytes / kSlabBytes);
+    const bool ok = s == 4 || s == 8 || s == 12 || s == 16 || s == 24 || s == 28 || s == 32 || (s == 56 && bits == 8);
+    return ok ? s : 0;
+}
+// M = 1 at every served length; M = 2..4 with 16-bit activations at rows of
+// 4, 8 or 16 slabs.
+static bool row_serves_shape(int bits, int64_t row_bytes, int xdt, int64_t M)
+{
+    const int s = row_slabs(row_bytes, bits);
+    return s != 0 && M <= row_max_mt(bits, s, xdt);
+}
+
 bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
 {
     const int bits = w.bits();
@@ -1110,6 +1165,8 @@ bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
     const int esz = x.dtype == EP_F32 ? 4 : 2;
     if (((uintptr_t)x.ptr & 15) != 0 || (M > 1 && (x.ld * esz) % 16 != 0))
         return false;
+    if (row_serves_shape(bits, bits == 4 ? w.K / 2 : w.K, x.dtype, M))
+        return true;
     int spw, waves;
     plan(bits == 4 ? w.K / 2 : w.K, spw, waves);
     const int mt = M == 1 ? 1 : (M == 2 ? 2 : 4);
@@ -1118,25 +1175,38 @@ bool gemv_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
     return fits(bits, spw, mt, x.dtype == EP_F32);
 }
 
-// The row lengths gemv_row_kernel serves, in 256-byte slabs (against
-// gemv_lut_kernel at config 3's 8-bit M = 1: 4096^2 8.23 -> 5.84 us,
-// 14336 x 4096 21.6 -> 17.5 us, 4096 x 14336 22.6 -> 19.1 us).
-static int row_kernel_slabs(const GemvArgs &a, int bits)
+static int row_kernel_slabs(const GemvArgs &a, int bits) { return row_slabs(a.row_bytes, bits); }
+static bool row_serves(const GemvArgs &a, int bits, int xdt, int64_t M)
 {
-    if (a.row_bytes % kSlabBytes != 0)
-        return 0;
-    const int s = (int)(a.row_bytes / kSlabBytes);
-    const bool ok = s == 4 || s == 8 || s == 12 || s == 16 || s == 24 || s == 28 || s == 32 || (s == 56 && bits == 8);
-    return ok ? s : 0;
+    return row_serves_shape(bits, a.row_bytes, xdt, M);
+}
+
+template <int BITS, int XDT, int S, int MT>
+static void launch_row_sc(const GemvArgs &a, dim3 g, dim3 b, hipStream_t stream)
+{
+    if (a.scale_dtype == EP_F32)
+        hipLaunchKernelGGL((gemv_row_kernel<BITS, XDT, S, true, MT>), g, b, 0, stream, a);
+    else
+        hipLaunchKernelGGL((gemv_row_kernel<BITS, XDT, S, false, MT>), g, b, 0, stream, a);
 }
 
 template <int BITS, int XDT, int S>
 static void launch_row_x(const GemvArgs &a, dim3 g, dim3 b, hipStream_t stream)
 {
-    if (a.scale_dtype == EP_F32)
-        hipLaunchKernelGGL((gemv_row_kernel<BITS, XDT, S, true>), g, b, 0, stream, a);
-    else
-        hipLaunchKernelGGL((gemv_row_kernel<BITS, XDT, S, false>), g, b, 0, stream, a);
+    constexpr int MX = row_max_mt(BITS, S, XDT);
+    if constexpr (MX >= 4) {
+        if (a.M > 2) {
+            launch_row_sc<BITS, XDT, S, 4>(a, g, b, stream);
+            return;
+        }
+    }
+    if constexpr (MX >= 2) {
+        if (a.M == 2) {
+            launch_row_sc<BITS, XDT, S, 2>(a, g, b, stream);
+            return;
+        }
+    }
+    launch_row_sc<BITS, XDT, S, 1>(a, g, b, stream);
 }
 
 template <int BITS, int S>
@@ -1193,7 +1263,7 @@ int launch_gemv(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc 
     if (!gemv_serves(w, x, M))
         return EP_DECLINE_SHAPE;
     const GemvArgs a = make_args(w, x, M, y);
-    if (M == 1 && row_kernel_slabs(a, w.bits()) != 0)
+    if (row_serves(a, w.bits(), x.dtype, M))
         return dispatch_row(a, w.bits(), x.dtype, stream);
     int spw, waves;
     plan(a.row_bytes, spw, waves);
