@@ -279,6 +279,17 @@ def _sk1_serves(m, n, cus):
     return m <= 16 * t
 
 
+def _row_serves(k, bits=8):
+    """Whether the batch-1 row GEMV takes a row of K indices (gemv.hip
+    row_kernel_slabs): rows of 4, 8, 12, 16, 24, 28 or 32 slabs of 256
+    bytes, and 56 with 8-bit indices."""
+    rb = k * bits // 8
+    if rb % 256:
+        return False
+    s = rb // 256
+    return s in (4, 8, 12, 16, 24, 28, 32) or (bits == 8 and s == 56)
+
+
 def prefill_sweep(seed=0, replays=10):
     """Config 3: 8-bit indices (256-entry fp16-valued codebook, group-128 fp16
     scales), (N, K) in {4096x4096, 14336x4096, 4096x14336}, bf16 x with M in
@@ -307,8 +318,7 @@ def prefill_sweep(seed=0, replays=10):
                          "hbm_frac": round(byt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                          "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
                          "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
-                         # 8-bit rows of 4, 8 or 16 slabs (K = 1024, 2048, 4096) take gemv_row_kernel
-                         "kernel": (("gemv_row_kernel" if k in (1024, 2048, 4096) else "gemv_lut_kernel")
+                         "kernel": (("gemv_row_kernel" if _row_serves(k) else "gemv_lut_kernel")
                                     if m == 1 else
                                     "sk1_kernel" if _sk1_serves(m, n, cus) else
                                     "sk_kernel + sk_reduce_kernel" if m <= 64 else

@@ -1147,8 +1147,9 @@ static int row_slabs(int64_t row_bytes, int bits)
     const bool ok = s == 4 || s == 8 || s == 12 || s == 16 || s == 24 || s == 28 || s == 32 || (s == 56 && bits == 8);
     return ok ? s : 0;
 }
-// M = 1 at every served length; M = 2..4 with 16-bit activations at rows of
-// 4, 8 or 16 slabs.
+// M = 1 at every served length; with 16-bit activations at rows of 4, 8 or
+// 16 slabs also M = 2 (and M = 3, 4 with 4-bit indices, but 2 at 16 slabs):
+// row_max_mt.
 static bool row_serves_shape(int bits, int64_t row_bytes, int xdt, int64_t M)
 {
     const int s = row_slabs(row_bytes, bits);
