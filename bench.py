@@ -31,7 +31,7 @@ kernel/src/lib.rs semantics) on one layer's 7 linears, scaled to the 224
 linears of a step.  The line also carries `gemv`: the config-0 dequant-GEMV
 (4096x4096 4-bit, batch 1) over 64 rotating weight sets, GB/s per launch.
 
-    python bench.py --workload gemv|prefill|backward
+    python bench.py --workload gemv|prefill|backward|experts
 
 prints one line for the other configurations instead: config 0 alone (GEMV
 GB/s, with the C port timed on the same linear), config 3 (the 8-bit M sweep;
@@ -76,10 +76,11 @@ def parse():
                     help="only copy a BYTES-long device buffer 10 times (the known-size "
                          "kernel that calibrates rocprofv3's FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--workload", default="decode",
-                    choices=["decode", "gemv", "prefill", "backward"],
+                    choices=["decode", "gemv", "prefill", "backward", "experts"],
                     help="decode: the headline (config 2); gemv: one 4096x4096 4-bit GEMV "
                          "over a rotating sweep (config 0); prefill: the 8-bit M sweep "
-                         "(config 3); backward: the compressed-state backward (config 4)")
+                         "(config 3); backward: the compressed-state backward (config 4); "
+                         "experts: a stacked-expert linear grouped on the device")
     ap.add_argument("--fused-backward", action="store_true",
                     help="backward: keep every token count on the fused kernels "
                          "(EPURE_BWD_FUSED=1) instead of the library route from 512 tokens")
@@ -329,6 +330,54 @@ def prefill_sweep(seed=0, replays=10):
     return rows
 
 
+def experts_sweep(seed=0, replays=10):
+    """A stacked-expert packed linear of the size of a Qwen3-30B-A3B layer's
+    expert gate (or up) projections: E = 128 experts of 768 x 2048, 4-bit
+    (16-entry codebook, group-128 fp16 scales, 100.7 MB), bf16 x, tokens
+    routed top-8 (T = 8 x tokens rows, ids uniform over the experts).  The
+    device-grouped call (ids sorted on the device, one grouped MFMA launch)
+    is timed inside a captured graph; the host-grouped route (a host
+    synchronization, one launch per expert) eagerly with events."""
+    import torch
+    from epure import PackedExperts, PackedWeight
+    from epure.decode import _gen, random_packed_linear
+    dev = torch.device("cuda:0")
+    gen = _gen(seed, dev)
+    E, n, k = 128, 768, 2048
+    flat = random_packed_linear(E * n, k, _spec(16), gen, dev)
+    store = PackedWeight((E, n, k), flat.packed, flat.scale, flat.cb, flat.group, flat.levels)
+    wbytes = _weight_bytes(E * n, k, 16)
+    rows = []
+    for tokens in (16, 128, 512, 2048):
+        T = 8 * tokens
+        x = torch.randn(T, k, generator=gen, device=dev).to(torch.bfloat16)
+        ids = torch.randint(0, E, (T,), generator=gen, device=dev, dtype=torch.int32)
+        m = PackedExperts(store, check_ids=False)
+        ms = _graph_time([lambda h: m(x, ids)], replays)
+        host = PackedExperts(store, check_ids=False)
+        host.GROUP_ON_DEVICE = False
+        host(x, ids)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            host(x, ids)
+        e1.record()
+        e1.synchronize()
+        host_ms = e0.elapsed_time(e1) / replays
+        used = int(torch.unique(ids).numel())
+        flop = 2.0 * T * n * k
+        byt = wbytes * used / E + T * k * 2 + T * n * 2
+        rows.append({"tokens": tokens, "rows": T, "experts_used": used, "us": round(ms * 1e3, 2),
+                     "host_grouped_us": round(host_ms * 1e3, 2),
+                     "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+                     "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                     "gbs": round(byt / (ms * 1e-3) / 1e9, 1),
+                     "hbm_frac": round(byt / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        del x, ids
+    return rows
+
+
 def backward_sweep(seed=0, replays=10):
     """Config 4: grad_x, grad_codebook and grad_scales of one 2048x6144 and one
     6144x2048 packed linear (4-bit, 16 levels, group 128), x bf16 [2048, K]
@@ -557,6 +606,20 @@ def side_workload(args):
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_gemv_baseline(4096, 4096, 256, [1, 4, 16],
                                                     args.cpu_threads)
+    elif args.workload == "experts":
+        rows = experts_sweep(args.seed, replays=min(args.steps, 20))
+        top = max(rows, key=lambda r: r["tflops"])
+        out = dict(metric="stacked-expert packed linear, device-grouped: TFLOP/s",
+                   value=top["tflops"], unit="TFLOP/s", ms_per_step=top["us"] / 1e3,
+                   dtype="f16", **base)
+        out["config"] = {"workload": "128 experts x 768 x 2048 4-bit (Qwen3-30B-A3B expert gate/up "
+                                     "size), bf16 x, top-8 routed rows, uniform ids",
+                         "kernel": "expert_sort_kernel + row_exp_kernel + mm_kernel (grouped)",
+                         "rows": rows}
+        out["roofline"] = {"bound": "mfma", "kernel": "mm_kernel (grouped)", "achieved": top["tflops"],
+                           "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": top["mfma_frac"],
+                           "traffic": None, "case": f"rows={top['rows']}"}
+        out["cpu_baseline"] = None  # the reference materializes the slab (no CPU expert kernel)
     else:
         rows = backward_sweep(args.seed, replays=min(args.steps, 20))
         flop = sum(4.0 * r["T"] * r["N"] * r["K"] for r in rows)

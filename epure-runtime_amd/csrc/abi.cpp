@@ -179,6 +179,41 @@ int ep_expert_matmul(const void *x, int x_dtype, int64_t ldx, const int32_t *exp
     return launch_gemv_gather(w, xa, T, expert_ids, (int)E, ya, (hipStream_t)stream);
 }
 
+size_t ep_expert_matmul_grouped_workspace(int64_t T, int64_t E, int64_t K)
+{
+    return expert_grouped_workspace(T, E, K);
+}
+
+int ep_expert_matmul_grouped(const void *x, int x_dtype, int64_t ldx, const int32_t *expert_ids, int64_t T,
+                             const uint8_t *packed, const void *scale, int scale_dtype, int64_t ld_scale,
+                             const void *cb, int cb_dtype, int levels, int group, int64_t E, int64_t N,
+                             int64_t K, void *y, int y_dtype, int64_t ldy, void *workspace,
+                             size_t workspace_bytes, void *stream)
+{
+    g_err[0] = 0;
+    PackedDesc w{packed, scale, scale_dtype, ld_scale, cb, cb_dtype, levels, group, N, K};
+    int rc = check_weight(w);
+    if (rc != EP_OK)
+        return rc;
+    if (!valid_dtype(x_dtype) || !valid_dtype(y_dtype))
+        return set_error(EP_DECLINE_DTYPE, "x/y dtype not served (x %d, y %d)", x_dtype, y_dtype);
+    if (T < 0 || E < 1 || E > INT32_MAX)
+        return set_error(EP_ERR_ARG, "T=%lld E=%lld", (long long)T, (long long)E);
+    if (T == 0 || N == 0)
+        return EP_OK;
+    if (!x || !y || !expert_ids)
+        return set_error(EP_ERR_ARG, "null x, y or expert_ids");
+    if ((T > 1 && ldx < K) || (T > 1 && ldy < N))
+        return set_error(EP_ERR_ARG, "ldx/ldy smaller than the row length");
+    const int64_t rb = levels <= 16 ? K / 2 : K;
+    if (E * N * rb >= ((int64_t)1 << 40))
+        return set_error(EP_DECLINE_SHAPE, "expert stack too large");
+    ActDesc xa{x, x_dtype, ldx};
+    OutDesc ya{y, y_dtype, ldy, 0};
+    return launch_expert_grouped(w, xa, T, expert_ids, (int)E, ya, workspace, workspace_bytes,
+                                 (hipStream_t)stream);
+}
+
 size_t ep_dequant_matmul_bwd_workspace(int64_t M, int64_t N, int64_t K, int levels, int group)
 {
     return backward_workspace(M, N, K, levels, group);

@@ -138,6 +138,18 @@ int launch_mfma(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc 
                 void *ws, size_t ws_bytes, hipStream_t stream);
 bool mfma_serves(const PackedDesc &w, const ActDesc &x, int64_t M);
 size_t mfma_workspace(int64_t M);
+// Stacked experts grouped on the device (mfma.hip): a stable sort of the
+// tokens by expert, then one MFMA launch over each expert's row tiles.
+size_t expert_grouped_workspace(int64_t T, int64_t E, int64_t K);
+bool expert_grouped_serves(const PackedDesc &w, const ActDesc &x, int64_t T, int64_t E);
+int launch_expert_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, const int *ids, int E,
+                          const OutDesc &y, void *ws, size_t ws_bytes, hipStream_t stream);
+// The prefill kernel over tiles of expert-sorted token rows (prefill.hip).
+bool prefill_grouped_serves(const PackedDesc &w, const ActDesc &x, int64_t T);
+size_t prefill_grouped_workspace(int64_t T, int64_t K);
+int launch_prefill_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, const int *perm,
+                           const int *tiles, const int *ntiles, int bm, unsigned tiles_y, const OutDesc &y,
+                           void *ws, hipStream_t stream);
 
 // Small-M (2..64 rows) split-K dequant-matmul on MFMA (skinny.hip).
 int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y, void *ws,

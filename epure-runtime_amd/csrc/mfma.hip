@@ -17,6 +17,7 @@
 // one.  The dense weight never reaches global memory.
 #include "ep_common.h"
 #include "ep_internal.h"
+#include "gemv_core.h"
 
 namespace ep {
 namespace {
@@ -44,6 +45,14 @@ struct MmArgs {
     int64_t K;
     int group;
     const int *rexp;
+    // grouped experts (mm_kernel<..., true>): row tile blockIdx.y is entry
+    // tiles[4 y ..] = (expert, first sorted row, rows, 0) while y < *ntiles;
+    // sorted row p is token perm[p] (its x row, y row and exponent); the
+    // expert's weight rows start estride_w bytes / estride_s scales further
+    const int *perm;
+    const int *tiles;
+    const int *ntiles;
+    int64_t estride_w, estride_s;
 };
 
 // One wave per activation row: exponent of the row's largest |x|.
@@ -62,7 +71,7 @@ __global__ void __launch_bounds__(256)
         rexp[row] = row_exponent(amax);
 }
 
-template <int BITS, int BM, int BN, int WM, int WN, int XDT>
+template <int BITS, int BM, int BN, int WM, int WN, int XDT, bool GR = false>
 __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
 {
     static_assert(WM * WN == 4, "four waves");
@@ -79,10 +88,23 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
     __shared__ uint32_t tab[256];
     __shared__ float s_pw[BM];
     __shared__ int s_e[BM];
+    __shared__ int s_row[GR ? BM : 1];  // grouped: token of each tile row (-1: none)
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    int gstart = 0, gcount = 0;
+    if constexpr (GR) {
+        // tiles past the sorted expert runs do nothing (uniform exit)
+        if ((int)blockIdx.y >= *a.ntiles)
+            return;
+        const int *tl = a.tiles + 4 * blockIdx.y;
+        const int e = tl[0];
+        gstart = tl[1];
+        gcount = tl[2];
+        a.packed += (int64_t)e * a.estride_w;
+        a.scale = (const char *)a.scale + e * a.estride_s * (a.scale_dtype == EP_F32 ? 4 : 2);
+    }
 
     {
         const int b = tid;  // 256 threads, 256 table entries
@@ -99,8 +121,15 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
         tab[b] = v;
     }
     for (int r = tid; r < BM; r += 256) {
-        const int m = m0 + r;
-        const int e = m < a.M ? a.rexp[m] : 0;
+        int e;
+        if constexpr (GR) {
+            const int t = r < gcount ? a.perm[gstart + r] : -1;
+            s_row[r] = t;
+            e = t >= 0 ? a.rexp[t] : 0;
+        } else {
+            const int m = m0 + r;
+            e = m < a.M ? a.rexp[m] : 0;
+        }
         s_e[r] = e;
         s_pw[r] = ldexpf(1.0f, -e);
     }
@@ -125,14 +154,15 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
         for (int i = 0; i < XCH; ++i) {
             const int c = tid + i * 256;
             const int r = c / (BK / 8), col = (c % (BK / 8)) * 8;
-            const int m = m0 + r;
+            const int m = GR ? s_row[r] : m0 + r;
+            const bool ok = GR ? m >= 0 : m < a.M;
             if constexpr (XDT == EP_F32) {
                 const float *p = (const float *)a.x + (int64_t)m * a.ldx + kbase + col;
-                xr[i][0] = m < a.M ? *(const u32x4_t *)p : (u32x4_t){0, 0, 0, 0};
-                xr[i][1] = m < a.M ? *(const u32x4_t *)(p + 4) : (u32x4_t){0, 0, 0, 0};
+                xr[i][0] = ok ? *(const u32x4_t *)p : (u32x4_t){0, 0, 0, 0};
+                xr[i][1] = ok ? *(const u32x4_t *)(p + 4) : (u32x4_t){0, 0, 0, 0};
             } else {
                 const uint16_t *p = (const uint16_t *)a.x + (int64_t)m * a.ldx + kbase + col;
-                xr[i][0] = m < a.M ? *(const u32x4_t *)p : (u32x4_t){0, 0, 0, 0};
+                xr[i][0] = ok ? *(const u32x4_t *)p : (u32x4_t){0, 0, 0, 0};
             }
         }
 #pragma unroll
@@ -264,8 +294,8 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
             for (int r = 0; r < 16; ++r) {
                 const int row = wm * TM * 32 + i * 32 + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
                 const int col = wn * TN * 32 + j * 32 + (lane & 31);
-                const int m = m0 + row, n = n0 + col;
-                if (m < a.M && n < a.N) {
+                const int m = GR ? s_row[row] : m0 + row, n = n0 + col;
+                if ((GR ? m >= 0 : m < a.M) && n < a.N) {
                     float v = ldexpf(acc[i][j][r], s_e[row]);
                     const int64_t off = (int64_t)m * a.ldy + n;
                     if (a.accumulate)
@@ -273,6 +303,140 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
                     store_from_f32(a.y, a.y_dtype, off, v);
                 }
             }
+}
+
+// Tokens grouped by expert on the device: a stable counting sort of the T
+// ids (clamped into [0, E)) into perm (sorted row p -> token) and the row
+// tiles of BM rows of each expert's run (tiles[4 i ..] = expert, first
+// sorted row, rows, 0; *ntiles of them).  One wave per expert in both
+// kernels: expert_count_kernel counts the expert's tokens (a ballot per 64
+// ids); expert_place_kernel sums the counts of the experts before it (its
+// run's start and first tile), writes its tiles, then walks the ids again
+// in token order and stores each of its tokens at start + its rank (the
+// popcount of the ballot below its lane), so equal ids keep their token
+// order.  Every id is read once per expert from L2; deterministic, no
+// atomics.
+constexpr int kSortWavesPerWg = 4;
+constexpr int kIdBatches = 16;  // batches of 64 ids read at once per wave
+constexpr int kMaxExperts = 1024;
+
+EP_DEV int clamp_expert(int e, int E) { return e < 0 ? 0 : (e >= E ? E - 1 : e); }
+
+__global__ void __launch_bounds__(64 * kSortWavesPerWg)
+    expert_count_kernel(const int *ids, int T, int E, int *counts)
+{
+    const int lane = threadIdx.x & 63;
+    const int e = (int)blockIdx.x * kSortWavesPerWg + (int)(threadIdx.x >> 6);
+    if (e >= E)
+        return;  // a whole wave
+    const auto rs = buffer_rsrc(ids, (uint32_t)T * 4u);  // ids past T read 0 (masked below)
+    int c = 0;
+    for (int b = 0; b < T; b += 64 * kIdBatches) {
+        int v[kIdBatches];  // 16 loads in flight per lane, no branch around them
+#pragma unroll
+        for (int u = 0; u < kIdBatches; ++u)
+            v[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs, (b + 64 * u + lane) * 4, 0, 0);
+#pragma unroll
+        for (int u = 0; u < kIdBatches; ++u) {
+            const int t = b + 64 * u + lane;
+            v[u] = t < T ? clamp_expert(v[u], E) : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kIdBatches; ++u)
+            c += __builtin_popcountll(__builtin_amdgcn_ballot_w64(v[u] == e));
+    }
+    if (lane == 0)
+        counts[e] = c;
+}
+
+__global__ void __launch_bounds__(64 * kSortWavesPerWg)
+    expert_place_kernel(const int *ids, int T, int E, int BM, const int *counts, int *perm, int *tiles,
+                        int *ntiles)
+{
+    const int lane = threadIdx.x & 63;
+    const int e = (int)blockIdx.x * kSortWavesPerWg + (int)(threadIdx.x >> 6);
+    if (e >= E)
+        return;  // a whole wave
+    // rows and tiles of the experts before e (lanes stride over them)
+    int rows = 0, tl = 0;
+    for (int f = lane; f < e; f += 64) {
+        const int c = counts[f];
+        rows += c;
+        tl += (c + BM - 1) / BM;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        rows += __shfl_xor(rows, o, 64);
+        tl += __shfl_xor(tl, o, 64);
+    }
+    const int cnt = counts[e];
+    const int nt = (cnt + BM - 1) / BM;
+    for (int j = lane; j < nt; j += 64) {
+        int *d = tiles + 4 * (tl + j);
+        d[0] = e;
+        d[1] = rows + j * BM;
+        d[2] = cnt - j * BM < BM ? cnt - j * BM : BM;
+        d[3] = 0;
+    }
+    if (e == E - 1 && lane == 0)
+        *ntiles = tl + nt;
+    int pos = rows;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));  // lanes under this one
+    const auto rs = buffer_rsrc(ids, (uint32_t)T * 4u);  // ids past T read 0 (masked below)
+    for (int b = 0; b < T && pos < rows + cnt; b += 64 * kIdBatches) {
+        int v[kIdBatches];  // 16 loads in flight per lane, then the batches in token order
+#pragma unroll
+        for (int u = 0; u < kIdBatches; ++u)
+            v[u] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs, (b + 64 * u + lane) * 4, 0, 0);
+#pragma unroll
+        for (int u = 0; u < kIdBatches; ++u) {
+            const int t = b + 64 * u + lane;
+            v[u] = t < T ? clamp_expert(v[u], E) : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < kIdBatches; ++u) {
+            const bool hit = v[u] == e;
+            const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
+            if (hit)
+                perm[pos + __builtin_popcountll(m & below)] = b + 64 * u + lane;
+            pos += __builtin_popcountll(m);
+        }
+    }
+}
+
+// Row exponents (row_exponent of the largest |x|) for 16-bit activation
+// rows with 16-byte aligned starts: one wave per row, 16-byte loads, four
+// in flight per lane.
+template <int XDT>
+__global__ void __launch_bounds__(256) row_exp16_kernel(const void *x, int64_t ldx, int M, int64_t K, int *rexp)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= M)
+        return;
+    const char *base = (const char *)x + row * ldx * 2;
+    const int64_t pieces = K / 8;  // 16-byte pieces (K % 8 == 0)
+    float amax = 0.0f;
+    for (int64_t p0 = lane; p0 < pieces; p0 += 256) {
+        u32x4_t v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t p = p0 + 64 * u;
+            v[u] = p < pieces ? *(const __attribute__((address_space(1))) u32x4_t *)(base + p * 16)
+                              : (u32x4_t){0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float lo, hi;
+                unpack_pair<XDT>(v[u][q], lo, hi);
+                amax = fmaxf(amax, fmaxf(fabsf(lo), fabsf(hi)));
+            }
+    }
+    amax = wave_max_bfly(amax);
+    if (lane == 0)
+        rexp[row] = row_exponent(amax);
 }
 
 template <int BITS, int BM, int BN, int WM, int WN>
@@ -304,7 +468,133 @@ int launch_bits(const MmArgs &a, int xdt, hipStream_t s)
     return launch_cfg<BITS, 128, 128, 2, 2>(a, xdt, s);
 }
 
+template <int BITS, int BM, int BN, int WM, int WN>
+int launch_grouped_cfg(const MmArgs &a, int xdt, unsigned tiles_y, hipStream_t s)
+{
+    dim3 grid((unsigned)((a.N + BN - 1) / BN), tiles_y);
+    switch (xdt) {
+    case EP_BF16:
+        hipLaunchKernelGGL((mm_kernel<BITS, BM, BN, WM, WN, EP_BF16, true>), grid, dim3(256), 0, s, a);
+        break;
+    case EP_F16:
+        hipLaunchKernelGGL((mm_kernel<BITS, BM, BN, WM, WN, EP_F16, true>), grid, dim3(256), 0, s, a);
+        break;
+    default:
+        hipLaunchKernelGGL((mm_kernel<BITS, BM, BN, WM, WN, EP_F32, true>), grid, dim3(256), 0, s, a);
+        break;
+    }
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
+// Row tile of the grouped launch from the mean rows per expert: 32 rows up
+// to 32 tokens per expert, 64 up to 64, else 128 (2 x 2 waves).
+int grouped_bm(int64_t T, int64_t E)
+{
+    const int64_t avg = (T + E - 1) / E;
+    return avg <= 32 ? 32 : (avg <= 64 ? 64 : 128);
+}
+int64_t grouped_max_tiles(int64_t T, int64_t E, int bm) { return (T + bm - 1) / bm + (E < T ? E : T); }
+
+template <int BITS>
+int launch_grouped_bits(const MmArgs &a, int xdt, int bm, unsigned tiles_y, hipStream_t s)
+{
+    if (bm == 32)
+        return launch_grouped_cfg<BITS, 32, 128, 1, 4>(a, xdt, tiles_y, s);
+    if (bm == 64)
+        return launch_grouped_cfg<BITS, 64, 128, 1, 4>(a, xdt, tiles_y, s);
+    return launch_grouped_cfg<BITS, 128, 128, 2, 2>(a, xdt, tiles_y, s);
+}
+
 }  // namespace
+
+// Workspace of the grouped expert launch: perm [T] | tiles [T / 32 + E][4]
+// | counts [E] | ntiles | the row exponents [T] and, for the prefill
+// kernel, the fp16 copy of the token rows [T][K] (every part 256-byte
+// aligned).
+static size_t al256(int64_t b) { return (size_t)((b + 255) / 256 * 256); }
+size_t expert_grouped_workspace(int64_t T, int64_t E, int64_t K)
+{
+    if (T <= 0 || E <= 0 || K <= 0)
+        return 0;
+    return al256(T * 4) + al256(grouped_max_tiles(T, E, 32) * 16) + al256(E * 4) + 256 +
+           prefill_grouped_workspace(T, K);
+}
+
+bool expert_grouped_serves(const PackedDesc &w, const ActDesc &x, int64_t T, int64_t E)
+{
+    return E >= 1 && E <= kMaxExperts && T >= 1 && T <= (int64_t)1 << 24 && mfma_serves(w, x, T);
+}
+
+// Experts averaging 64 tokens or more run the prefill kernel (the whole K
+// per workgroup, 64- or 128-row tiles); sparser ones the generic MFMA kernel
+// (32- or 64-row tiles).
+int launch_expert_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, const int *ids, int E,
+                          const OutDesc &y, void *ws, size_t ws_bytes, hipStream_t stream)
+{
+    if (!expert_grouped_serves(w, x, T, E))
+        return set_error(EP_DECLINE_SHAPE,
+                         "grouped experts: 1 <= E <= %d, T <= 2^24, K %% 64 == 0, 16-byte aligned rows", kMaxExperts);
+    const size_t need = expert_grouped_workspace(T, E, w.K);
+    if (!ws || ws_bytes < need)
+        return set_error(EP_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws_bytes);
+    char *base = (char *)ws;
+    int *perm = (int *)base;
+    base += al256(T * 4);
+    int *tiles = (int *)base;
+    base += al256(grouped_max_tiles(T, E, 32) * 16);
+    int *counts = (int *)base;
+    base += al256((int64_t)E * 4);
+    int *ntiles = (int *)base;
+    base += 256;
+    int *rexp = (int *)base;  // (the prefill kernel's exponents and fp16 rows start here too)
+    const int64_t avg = (T + E - 1) / E;
+    const bool pf = avg >= 64 && prefill_grouped_serves(w, x, T);
+    const int bm = pf ? (avg >= 128 ? 128 : 64) : grouped_bm(T, E);
+    const dim3 sg((unsigned)((E + kSortWavesPerWg - 1) / kSortWavesPerWg)), sb(64 * kSortWavesPerWg);
+    hipLaunchKernelGGL(expert_count_kernel, sg, sb, 0, stream, ids, (int)T, E, counts);
+    EP_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(expert_place_kernel, sg, sb, 0, stream, ids, (int)T, E, bm, counts, perm, tiles, ntiles);
+    EP_HIP_CHECK(hipGetLastError());
+    const unsigned ty = (unsigned)grouped_max_tiles(T, E, bm);
+    if (pf)
+        return launch_prefill_grouped(w, x, T, perm, tiles, ntiles, bm, ty, y, rexp, stream);
+    const dim3 rg((unsigned)((T + 3) / 4));
+    if (x.dtype == EP_BF16)
+        hipLaunchKernelGGL(row_exp16_kernel<EP_BF16>, rg, dim3(256), 0, stream, x.ptr, x.ld, (int)T, w.K, rexp);
+    else if (x.dtype == EP_F16)
+        hipLaunchKernelGGL(row_exp16_kernel<EP_F16>, rg, dim3(256), 0, stream, x.ptr, x.ld, (int)T, w.K, rexp);
+    else
+        hipLaunchKernelGGL(row_exp_kernel, rg, dim3(256), 0, stream, x.ptr, x.dtype, x.ld, (int)T, w.K, rexp);
+    EP_HIP_CHECK(hipGetLastError());
+    MmArgs a{};
+    a.x = x.ptr;
+    a.ldx = x.ld;
+    a.M = (int)T;
+    a.packed = w.packed;
+    a.row_bytes = w.bits() == 4 ? w.K / 2 : w.K;
+    a.scale = w.scale;
+    a.scale_dtype = w.scale_dtype;
+    a.lds = w.ld_scale;
+    a.cb = w.cb;
+    a.cb_dtype = w.cb_dtype;
+    a.levels = w.levels;
+    a.y = y.ptr;
+    a.y_dtype = y.dtype;
+    a.ldy = y.ld;
+    a.accumulate = 0;
+    a.N = (int)w.N;
+    a.K = w.K;
+    a.group = w.group;
+    a.rexp = rexp;
+    a.perm = perm;
+    a.tiles = tiles;
+    a.ntiles = ntiles;
+    a.estride_w = w.N * a.row_bytes;
+    a.estride_s = w.N * w.ld_scale;
+    return w.bits() == 4 ? launch_grouped_bits<4>(a, x.dtype, bm, ty, stream)
+                         : launch_grouped_bits<8>(a, x.dtype, bm, ty, stream);
+}
 
 size_t mfma_workspace(int64_t M) { return (size_t)((M * 4 + 255) / 256 * 256); }
 

@@ -76,6 +76,14 @@ struct PfArgs {
     int64_t ldy;
     int accumulate;  // with one split: y += result (read in the epilogue)
     float *part;     // [S][M][N] partials (null: results go straight to y)
+    // grouped experts (pf_kernel<..., true>): row tile blockIdx.y is entry
+    // tiles[4 y ..] = (expert, first sorted row, rows, 0) while y < *ntiles;
+    // sorted row p is token perm[p]; expert e's weight rows start
+    // e * estride_w bytes and its scales e * estride_s elements further
+    const int *perm;
+    const int *tiles;
+    const int *ntiles;
+    int64_t estride_w, estride_s;
 };
 
 // Per-row exponent of the largest |x| (row_exponent), then the row rescaled
@@ -154,7 +162,7 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-template <int BITS, int BM, int PD, int NT, int WAVES>
+template <int BITS, int BM, int PD, int NT, int WAVES, bool GR = false>
 __global__ void __launch_bounds__(WAVES * 64, 8 / WAVES) pf_kernel(PfArgs a)
 {
     constexpr int MT = BM / 32;                  // 32-row M tiles per wave
@@ -179,6 +187,7 @@ __global__ void __launch_bounds__(WAVES * 64, 8 / WAVES) pf_kernel(PfArgs a)
     __shared__ uint32_t s_cbraw[256];
     __shared__ uint16_t s_cb16[256];
     __shared__ int s_e[BM];
+    __shared__ int s_row[GR ? BM : 1];  // grouped: token of each tile row (-1: none)
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -187,21 +196,37 @@ __global__ void __launch_bounds__(WAVES * 64, 8 / WAVES) pf_kernel(PfArgs a)
     const int m0 = blockIdx.y * BM;
     const int kt0 = blockIdx.z * a.ksteps;
     const int nk = a.K / kPfBK;
+    int gstart = 0, gcount = 0;
+    if constexpr (GR) {
+        // tiles past the sorted expert runs do nothing (uniform exit)
+        if ((int)blockIdx.y >= *a.ntiles)
+            return;
+        const int *tl = a.tiles + 4 * blockIdx.y;
+        const int e = tl[0];
+        gstart = tl[1];
+        gcount = tl[2];
+        a.packed += (int64_t)e * a.estride_w;
+        a.scale = (const char *)a.scale + e * a.estride_s * 2;
+    }
     const auto rx = buffer_rsrc(a.x, a.xbytes), rw = buffer_rsrc(a.packed, a.wbytes);
     const auto rs = buffer_rsrc(a.scale, a.sbytes), rcb = buffer_rsrc(a.cb, a.cbbytes);
 
     // ---- first loads: codebook, row exponents, step 0's activations
     const uint32_t cbraw = __builtin_amdgcn_raw_buffer_load_b32(rcb, tid * 4, 0, 0);
     const int xr = tid / TPR, xq = tid % TPR;
-    const int xm = m0 + xr;
-    const int ex = *(const __attribute__((address_space(1))) int *)(a.rexp + (xm < a.M ? xm : 0));
+    int xm;
+    if constexpr (GR)
+        xm = xr < gcount ? a.perm[gstart + xr] : -1;
+    else
+        xm = m0 + xr < a.M ? m0 + xr : -1;
+    const int ex = *(const __attribute__((address_space(1))) int *)(a.rexp + (xm >= 0 ? xm : 0));
 
     // Load offsets = a per-lane part fixed for the whole loop (kPfOut for a
     // row past M or N) + a per-step part that is uniform (kPfOut for a step
     // past K or the split): one add per load.  Both parts stay below 2^31,
     // so a sum with either at kPfOut is past the buffer and reads zeros
     // (the bounds check covers the per-lane offset, which holds the sum).
-    const uint32_t xlo = xm < a.M ? (uint32_t)(((int64_t)xm * a.ldx + xq * VPT) * XE) : kPfOut;
+    const uint32_t xlo = xm >= 0 ? (uint32_t)(((int64_t)xm * a.ldx + xq * VPT) * XE) : kPfOut;
     uint32_t wlo[NT][WL], slo[NT][WL];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -287,8 +312,12 @@ __global__ void __launch_bounds__(WAVES * 64, 8 / WAVES) pf_kernel(PfArgs a)
                 row[i] = (u32x4_t){v, v, v, v};
         }
     }
-    if (tid % TPR == 0 && xm < a.M)
-        s_e[xr] = ex;
+    if (tid % TPR == 0) {
+        if (xm >= 0)
+            s_e[xr] = ex;
+        if constexpr (GR)
+            s_row[xr] = xm;
+    }
     store_x(xv[0], 0);
     lds_barrier();
 
@@ -388,8 +417,8 @@ __global__ void __launch_bounds__(WAVES * 64, 8 / WAVES) pf_kernel(PfArgs a)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = mt * 32 + (r % 4) + 4 * h + 8 * (r / 4);
-                const int m = m0 + row;
-                if (m >= a.M)
+                const int m = GR ? s_row[row] : m0 + row;
+                if (GR ? m < 0 : m >= a.M)
                     continue;
                 const float v = ldexpf(acc[mt][nt][r], s_e[row]);
                 if (a.part) {
@@ -464,7 +493,96 @@ int pf_launch(const PfArgs &a, const PfPlan &p, hipStream_t s)
     return EP_OK;
 }
 
+template <int BITS, int BM, int PD, int NT, int WAVES>
+int pf_launch_grouped(const PfArgs &a, unsigned tiles_y, hipStream_t s)
+{
+    constexpr int BN = WAVES * 32 * NT;
+    const dim3 grid((unsigned)((a.N + BN - 1) / BN), tiles_y, 1u);
+    hipLaunchKernelGGL((pf_kernel<BITS, BM, PD, NT, WAVES, true>), grid, dim3(WAVES * 64), 0, s, a);
+    EP_HIP_CHECK(hipGetLastError());
+    return EP_OK;
+}
+
 }  // namespace
+
+bool prefill_grouped_serves(const PackedDesc &w, const ActDesc &x, int64_t T)
+{
+    // one expert's rows and scales, and the T token rows of x, in buffer range
+    return prefill_serves(w, x, T);
+}
+
+size_t prefill_grouped_workspace(int64_t T, int64_t K)
+{
+    return (size_t)((T * 4 + 255) / 256 * 256) + (size_t)((T * K * 2 + 255) / 256 * 256);
+}
+
+// Stacked experts grouped by expert (tiles from the device sort): the fp16
+// copy of every token row, then pf_kernel over each expert's row tiles (bm
+// 64 or 128 rows, the whole K per workgroup), results at the tokens' rows.
+int launch_prefill_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, const int *perm,
+                           const int *tiles, const int *ntiles, int bm, unsigned tiles_y, const OutDesc &y,
+                           void *ws, hipStream_t stream)
+{
+    const int bits = w.bits();
+    int *rexp = (int *)ws;
+    f16_t *xh = (f16_t *)((char *)ws + (T * 4 + 255) / 256 * 256);
+    hipLaunchKernelGGL(pf_prep_kernel, dim3((unsigned)((T + 3) / 4)), dim3(256), 0, stream, x.ptr, x.dtype,
+                       x.ld, (int)T, (int)w.K, rexp, xh);
+    EP_HIP_CHECK(hipGetLastError());
+    PfArgs a{};
+    a.xbytes = (uint32_t)(T * w.K * 2);
+    a.wbytes = (uint32_t)(w.N * (bits == 4 ? w.K / 2 : w.K));
+    a.sbytes = (uint32_t)(((w.N - 1) * w.ld_scale + (w.K + w.group - 1) / w.group) * 2);
+    a.cbbytes = (uint32_t)(w.levels * (w.cb_dtype == EP_F32 ? 4 : 2));
+    a.x = xh;
+    a.ldx = w.K;
+    a.M = (int)T;
+    a.packed = w.packed;
+    a.row_bytes = (uint32_t)(bits == 4 ? w.K / 2 : w.K);
+    a.scale = w.scale;
+    a.lds = w.ld_scale;
+    a.cb = w.cb;
+    a.cb_dtype = w.cb_dtype;
+    a.levels = w.levels;
+    a.N = (int)w.N;
+    a.K = (int)w.K;
+    a.group = w.group;
+    a.gk_mul = w.group <= kPfBK ? kPfBK / w.group : 1;
+    a.gk_shift = 0;
+    while (w.group > kPfBK && (kPfBK << a.gk_shift) < w.group)
+        ++a.gk_shift;
+    const int nk = (int)(w.K / kPfBK);
+    a.rexp = rexp;
+    a.y = y.ptr;
+    a.y_dtype = y.dtype;
+    a.ldy = y.ld;
+    a.accumulate = 0;
+    a.part = nullptr;
+    a.perm = perm;
+    a.tiles = tiles;
+    a.ntiles = ntiles;
+    a.estride_w = w.N * (int64_t)a.row_bytes;
+    a.estride_s = w.N * w.ld_scale;
+    // the whole K per workgroup: steps rounded up to the register-set count
+    auto ks = [&](int pd) {
+        const int nb = (pd > 2 ? pd : 2) + 1;
+        return (nk + nb - 1) / nb * nb;
+    };
+    if (bits == 4) {
+        if (bm == 128) {
+            a.ksteps = ks(4);
+            return pf_launch_grouped<4, 128, 4, 1, 8>(a, tiles_y, stream);
+        }
+        a.ksteps = ks(4);
+        return pf_launch_grouped<4, 64, 4, 2, 4>(a, tiles_y, stream);
+    }
+    if (bm == 128) {
+        a.ksteps = ks(EP_PF_PD8);
+        return pf_launch_grouped<8, 128, EP_PF_PD8, 1, 8>(a, tiles_y, stream);
+    }
+    a.ksteps = ks(3);
+    return pf_launch_grouped<8, 64, 3, 2, 4>(a, tiles_y, stream);
+}
 
 bool prefill_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
 {

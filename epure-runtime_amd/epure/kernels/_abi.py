@@ -49,6 +49,14 @@ _SIGS = {
         _p, _c_int, _c_int, _c_int,              # cb, cb_dtype, levels, group
         _c_i64, _c_i64, _c_i64,                  # E, N, K
         _p, _c_int, _c_i64, _p]),                # y, y_dtype, ldy, stream
+    "ep_expert_matmul_grouped_workspace": (_sz, [_c_i64, _c_i64, _c_i64]),
+    "ep_expert_matmul_grouped": (_c_int, [
+        _p, _c_int, _c_i64, _p, _c_i64,         # x, x_dtype, ldx, expert_ids (int32), T
+        _p, _p, _c_int, _c_i64,                  # packed, scale, scale_dtype, ld_scale
+        _p, _c_int, _c_int, _c_int,              # cb, cb_dtype, levels, group
+        _c_i64, _c_i64, _c_i64,                  # E, N, K
+        _p, _c_int, _c_i64,                      # y, y_dtype, ldy
+        _p, _sz, _p]),                           # workspace, bytes, stream
     "ep_dequant_matmul_bwd_workspace": (_sz, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "ep_dequant_matmul_bwd": (_c_int, [
         _p, _c_int, _c_i64,                      # gy, gy_dtype, ldgy

@@ -340,11 +340,15 @@ class PackedExperts(nn.Module):
     slab per call, runtime.py:163-186).  GPU tensors only.
 
     Up to ``GATHER_MAX_TOKENS`` tokens (f16/bf16 ``x``) run one gathered
-    launch that reads the ids on the device: no host synchronization with
-    ``check_ids=False`` and capturable in a HIP graph (ids outside
-    ``[0, E)`` are then clamped on the device).  With ``check_ids`` (the
-    default) an eager call range-checks the ids on the host first and raises
-    ``IndexError``; more tokens group per expert on the host.
+    launch that reads the ids on the device; more tokens are sorted by
+    expert on the device and run one grouped MFMA launch over each expert's
+    row tiles (``ep_expert_matmul_grouped``).  Neither synchronizes with the
+    host when ``check_ids=False`` and both can be captured in a HIP graph
+    (ids outside ``[0, E)`` are then clamped on the device).  With
+    ``check_ids`` (the default) an eager call range-checks the ids on the
+    host first and raises ``IndexError``.  Shapes the grouped kernel
+    declines (K not a multiple of 64, more than 1024 experts) group per
+    expert on the host.
     """
 
     def __init__(self, store, check_ids=True):
@@ -360,6 +364,10 @@ class PackedExperts(nn.Module):
     # graph); it re-reads an expert's weights per token, so more tokens are
     # grouped per expert.
     GATHER_MAX_TOKENS = 8
+    # Group larger token counts on the device (one sort and one grouped
+    # launch); False groups them per expert on the host instead (one
+    # ep_dequant_matmul per expert after a host synchronization).
+    GROUP_ON_DEVICE = True
 
     def forward(self, x, expert_ids):
         s = self.store
@@ -373,6 +381,8 @@ class PackedExperts(nn.Module):
         if x2.shape[0] == 0:
             return out
         if x2.shape[0] <= self.GATHER_MAX_TOKENS and self._gathered(x2, expert_ids, out):
+            return out
+        if self.GROUP_ON_DEVICE and self._grouped(x2, expert_ids, out):
             return out
         ids = expert_ids.reshape(-1).to(torch.int64)
         order = torch.argsort(ids, stable=True)
@@ -407,6 +417,41 @@ class PackedExperts(nn.Module):
             out.index_copy_(0, rows, ye)
         return out
 
+    def _check_ids(self, ids32):
+        """Host range check of the ids (eager calls with ``check_ids``)."""
+        if self.check_ids and not torch.cuda.is_current_stream_capturing():
+            lo, hi = int(ids32.min()), int(ids32.max())
+            if lo < 0 or hi >= self.num_experts:
+                raise IndexError(f"expert id out of range [0, {self.num_experts})")
+
+    def _grouped(self, x2, expert_ids, out):
+        """One device sort of the tokens by expert and one grouped MFMA
+        launch (``ep_expert_matmul_grouped``); False where it declines the
+        shape."""
+        s = self.store
+        K, N = self.in_features, self.out_features
+        if x2.stride(1) != 1:
+            return False
+        h = cuda_kernel._hot(s)
+        if not h.usable():
+            return False
+        T = x2.shape[0]
+        ids32 = expert_ids.reshape(-1).to(device=x2.device, dtype=torch.int32).contiguous()
+        self._check_ids(ids32)
+        ws_bytes = _abi.lib.ep_expert_matmul_grouped_workspace(T, self.num_experts, K)
+        ws = torch.empty(ws_bytes, device=x2.device, dtype=torch.uint8)
+        rc = _abi.lib.ep_expert_matmul_grouped(
+            x2.data_ptr(), _abi.dtype_code(x2.dtype), x2.stride(0), ids32.data_ptr(), T,
+            h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,
+            h.cb.data_ptr(), h.cb_dt, h.levels, h.group,
+            self.num_experts, N, K, out.data_ptr(), _abi.dtype_code(out.dtype), out.stride(0),
+            ws.data_ptr(), ws_bytes, _abi.stream_handle(x2.device))
+        if rc > 0:
+            return False
+        if not _abi.check(rc, "ep_expert_matmul_grouped"):
+            raise RuntimeError(f"PackedExperts: {_abi.last_error()}")
+        return True
+
     def _gathered(self, x2, expert_ids, out):
         """One ``ep_expert_matmul`` launch for every token; False where the
         kernel declines the shape.  With ``check_ids`` and outside stream
@@ -420,10 +465,7 @@ class PackedExperts(nn.Module):
         if not h.usable():
             return False
         ids32 = expert_ids.reshape(-1).to(device=x2.device, dtype=torch.int32).contiguous()
-        if self.check_ids and not torch.cuda.is_current_stream_capturing():
-            lo, hi = int(ids32.min()), int(ids32.max())
-            if lo < 0 or hi >= self.num_experts:
-                raise IndexError(f"expert id out of range [0, {self.num_experts})")
+        self._check_ids(ids32)
         rc = _abi.lib.ep_expert_matmul(
             x2.data_ptr(), _abi.dtype_code(x2.dtype), x2.stride(0), ids32.data_ptr(), x2.shape[0],
             h.packed.data_ptr(), h.scale.data_ptr(), h.scale_dt, h.ld_scale,

@@ -125,6 +125,28 @@ int ep_expert_matmul(const void *x, int x_dtype, int64_t ldx, const int32_t *exp
                      int64_t K, void *y, int y_dtype, int64_t ldy, void *stream);
 
 /*
+ * The same product for any token count, grouped by expert on the device:
+ * a stable sort of the tokens by id (clamped into [0, E)), then one MFMA
+ * launch whose workgroups take row tiles of one expert's tokens, each
+ * reading that expert's weight rows once per tile and storing at the
+ * tokens' own rows of y: the prefill MFMA kernel (64- or 128-row tiles)
+ * where the experts average 64 tokens or more and its shape rules hold
+ * (fp16 scales), else the generic MFMA kernel (32- or 64-row tiles).
+ * Replaces the reference's per-call slab materialization
+ * (epure/runtime.py:163-186) and the caller's host-side grouping of tokens
+ * per expert: no host synchronization, capturable in a HIP graph,
+ * deterministic (no atomics in the product).  E <= 1024,
+ * T <= 2^24, K % 64 == 0, 16-byte aligned rows (else EP_DECLINE_SHAPE).
+ * Workspace: ep_expert_matmul_grouped_workspace(T, E, K) bytes.
+ */
+size_t ep_expert_matmul_grouped_workspace(int64_t T, int64_t E, int64_t K);
+int ep_expert_matmul_grouped(const void *x, int x_dtype, int64_t ldx, const int32_t *expert_ids, int64_t T,
+                             const uint8_t *packed, const void *scale, int scale_dtype, int64_t ld_scale,
+                             const void *cb, int cb_dtype, int levels, int group, int64_t E, int64_t N,
+                             int64_t K, void *y, int y_dtype, int64_t ldy, void *workspace,
+                             size_t workspace_bytes, void *stream);
+
+/*
  * Compressed-state backward of y = x . W^T with frozen indices
  * (fine-tuning/README.md:62-68; autograd through runtime.py:84-88):
  *   grad_x[M, K]            = gy[M, N] . W                (gx_dtype; NULL = skip)

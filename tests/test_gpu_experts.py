@@ -104,15 +104,16 @@ def test_gathered_experts_vs_oracle(E, n, k, levels, T, dt):
 
 
 def test_gathered_experts_match_grouped_path():
-    """The gathered launch and the per-expert grouped route agree bit for bit
-    on the same rows (both run the batch-1 GEMV per token row)."""
+    """The gathered launch and the per-expert host-grouped route agree bit
+    for bit on the same rows (both run the batch-1 GEMV per token row)."""
     s, *_ = experts(5, 512, 1024, 16, 128, seed=7)
     g = torch.Generator(device=DEV).manual_seed(9)
     x = torch.randn(6, 1024, generator=g, device=DEV).to(torch.bfloat16)
     ids = torch.tensor([4, 0, 2, 2, 1, 3], device=DEV)
     m = PackedExperts(s)
     y_g = m(x, ids)
-    m.GATHER_MAX_TOKENS = 0                 # this instance groups per expert
+    m.GATHER_MAX_TOKENS = 0                 # this instance groups per expert on the host
+    m.GROUP_ON_DEVICE = False
     ys = [m(x[t:t + 1], ids[t:t + 1]) for t in range(6)]
     assert torch.equal(y_g, torch.cat(ys))
 
@@ -210,3 +211,101 @@ def test_gathered_experts_strided_rows(pad):
                      128, 16)
     err = np.abs(y.float().cpu().numpy() - want).max() / np.abs(want).max()
     assert err < 2e-3 + 2.0 ** -8, err
+
+
+def skewed_ids(T, E, g, kind):
+    if kind == "uniform":
+        return torch.randint(0, E, (T,), generator=g, device=DEV)
+    if kind == "skewed":                    # most tokens on one expert, the rest spread
+        ids = torch.randint(0, E, (T,), generator=g, device=DEV)
+        hot = torch.rand(T, generator=g, device=DEV) < 0.8
+        return torch.where(hot, torch.full_like(ids, E // 2), ids)
+    if kind == "sparse":                    # every other expert empty
+        return 2 * torch.randint(0, (E + 1) // 2, (T,), generator=g, device=DEV)
+    return torch.full((T,), E - 1, device=DEV, dtype=torch.int64)   # one expert takes all
+
+
+@pytest.mark.parametrize("E,n,k,levels,T,dt,kind", [
+    (8, 256, 512, 16, 100, torch.bfloat16, "uniform"),     # 32-row tiles
+    (4, 384, 1024, 16, 300, torch.float16, "skewed"),      # 128-row tiles, one long run
+    (16, 128, 256, 256, 37, torch.bfloat16, "sparse"),     # 8-bit, empty experts
+    (64, 128, 512, 16, 2048, torch.bfloat16, "uniform"),   # many experts
+    (2, 256, 512, 256, 700, torch.float16, "one"),         # all tokens on the last expert
+    (6, 192, 512, 16, 90, torch.float32, "uniform"),       # f32 activations
+    # experts averaging >= 64 tokens: the prefill kernel over the sorted runs
+    (3, 512, 1024, 16, 400, torch.bfloat16, "uniform"),    # 4-bit, 128-row tiles
+    (4, 256, 2048, 256, 260, torch.bfloat16, "skewed"),    # 8-bit, 64-row tiles
+    (4, 320, 1024, 16, 300, torch.float16, "sparse"),      # 4-bit, 64-row tiles, empty experts
+    (2, 128, 512, 16, 300, torch.float32, "uniform"),      # f32 activations, 128-row tiles
+])
+def test_grouped_experts_vs_oracle(E, n, k, levels, T, dt, kind):
+    """T > GATHER_MAX_TOKENS: tokens sorted by expert on the device, one
+    grouped MFMA launch over each expert's row tiles (ep_expert_matmul_grouped),
+    results at the tokens' own rows."""
+    group = 128
+    s, packed, scale, cb = experts(E, n, k, levels, group, seed=5 * E + T)
+    g = torch.Generator(device=DEV).manual_seed(200 + T)
+    x = torch.randn(T, k, generator=g, device=DEV).to(dt)
+    ids = skewed_ids(T, E, g, kind)
+    print(f"case: grouped experts E={E} n={n} k={k} levels={levels} T={T} x={dt} ids={kind}", flush=True)
+    y = PackedExperts(s)(x, ids)
+    assert y.shape == (T, n) and y.dtype == dt
+    want = want_rows(x.float().cpu().numpy(), ids.cpu().tolist(), packed, scale, cb, E, n, k,
+                     group, levels)
+    got = y.float().cpu().numpy()
+    tol = 2e-3 + (0.0 if dt == torch.float32 else 2.0 ** -8)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err < tol, err
+    floor = np.sqrt(np.mean(want ** 2))
+    rel = (np.abs(got - want) / np.maximum(np.abs(want), floor)).max()
+    assert rel < 2 * tol, rel
+
+
+@pytest.mark.parametrize("E,T", [(12, 64), (4, 512)])
+def test_grouped_experts_graph_replay_follows_ids(E, T):
+    """Captured once, the grouped call (device sort + grouped launch: the
+    generic MFMA kernel at 12 experts x 64 tokens, the prefill kernel at 4 x
+    512) follows ids and x rewritten in place between replays; every replay
+    equals an eager call bit for bit."""
+    n, k = 256, 1024
+    s, *_ = experts(E, n, k, 16, 128, seed=17)
+    m = PackedExperts(s, check_ids=False)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    x = torch.randn(T, k, generator=g, device=DEV).to(torch.bfloat16)
+    ids = torch.randint(0, E, (T,), generator=g, device=DEV, dtype=torch.int32)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        m(x, ids)                           # warm-up outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = m(x, ids)
+    for r in range(4):
+        ids.copy_(skewed_ids(T, E, g, ["uniform", "skewed", "sparse", "one"][r]).to(torch.int32))
+        x.copy_(torch.randn(T, k, generator=g, device=DEV).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = PackedExperts(s)(x, ids)
+        assert torch.equal(y, eager), r
+
+
+def test_grouped_experts_clamp_ids_and_strided_rows():
+    """check_ids=False clamps ids outside [0, E) on the device; activation
+    rows at a stride of k + 8 elements; two calls give the same bits."""
+    E, n, k, T = 5, 128, 512, 40
+    s, *_ = experts(E, n, k, 16, 128, seed=19)
+    g = torch.Generator(device=DEV).manual_seed(12)
+    wide = torch.randn(T, k + 8, generator=g, device=DEV).to(torch.bfloat16)
+    x = wide[:, :k]
+    ids = torch.randint(0, E, (T,), generator=g, device=DEV)
+    bad = ids.clone()
+    bad[0], bad[1] = -3, E + 2
+    ids[0], ids[1] = 0, E - 1
+    y = PackedExperts(s, check_ids=False)(x, bad)
+    want = PackedExperts(s)(x.contiguous(), ids)
+    assert torch.equal(y, want)
+    assert torch.equal(PackedExperts(s)(x, ids), want)
+    with pytest.raises(IndexError):
+        PackedExperts(s)(x, bad)
