@@ -237,6 +237,11 @@ def skewed_ids(T, E, g, kind):
     (4, 256, 2048, 256, 260, torch.bfloat16, "skewed"),    # 8-bit, 64-row tiles
     (4, 320, 1024, 16, 300, torch.float16, "sparse"),      # 4-bit, 64-row tiles, empty experts
     (2, 128, 512, 16, 300, torch.float32, "uniform"),      # f32 activations, 128-row tiles
+    # longer rows on the generic kernel's 32-row tiles
+    (16, 256, 2048, 16, 40, torch.bfloat16, "uniform"),
+    (8, 384, 4096, 16, 50, torch.float16, "skewed"),       # one expert's run over two tiles
+    (12, 128, 2048, 256, 30, torch.bfloat16, "sparse"),
+    (6, 256, 8192, 16, 20, torch.bfloat16, "uniform"),
 ])
 def test_grouped_experts_vs_oracle(E, n, k, levels, T, dt, kind):
     """T > GATHER_MAX_TOKENS: tokens sorted by expert on the device, one
@@ -261,13 +266,13 @@ def test_grouped_experts_vs_oracle(E, n, k, levels, T, dt, kind):
     assert rel < 2 * tol, rel
 
 
-@pytest.mark.parametrize("E,T", [(12, 64), (4, 512)])
-def test_grouped_experts_graph_replay_follows_ids(E, T):
+@pytest.mark.parametrize("E,T,k", [(12, 64, 1024), (4, 512, 1024), (32, 64, 2048)])
+def test_grouped_experts_graph_replay_follows_ids(E, T, k):
     """Captured once, the grouped call (device sort + grouped launch: the
-    generic MFMA kernel at 12 experts x 64 tokens, the prefill kernel at 4 x
-    512) follows ids and x rewritten in place between replays; every replay
-    equals an eager call bit for bit."""
-    n, k = 256, 1024
+    generic MFMA kernel at 12 and 32 experts x 64 tokens, the prefill kernel
+    at 4 x 512) follows ids and x rewritten in place between replays; every
+    replay equals an eager call bit for bit."""
+    n = 256
     s, *_ = experts(E, n, k, 16, 128, seed=17)
     m = PackedExperts(s, check_ids=False)
     g = torch.Generator(device=DEV).manual_seed(8)
