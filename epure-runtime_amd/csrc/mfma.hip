@@ -19,6 +19,8 @@
 #include "ep_internal.h"
 #include "gemv_core.h"
 
+#include <type_traits>
+
 namespace ep {
 namespace {
 
@@ -143,47 +145,81 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
             for (int r = 0; r < 16; ++r)
                 acc[i][j][r] = 0.0f;
 
-    // register staging of one K-step
-    u32x4_t xr[XCH][XDT == EP_F32 ? 2 : 1];
-    u32x4_t wr[WCH];
-    float wsc[WCH];
+    // register staging, PD K-steps of loads in flight: every load goes out
+    // unconditionally (a row past M or N reads row 0 of its buffer and is
+    // zeroed at the store), and the scale's raw bits are converted at the
+    // store, so no wait for a load sits before the MFMAs of the steps ahead
+    constexpr int PD = 3;
+    constexpr int XW = XDT == EP_F32 ? 2 : 1;
+    u32x4_t xr[PD][XCH][XW];
+    u32x4_t wr[PD][WCH];
+    uint32_t wsr[PD][WCH];
+    const int KT = (int)(a.K / BK);
 
-    auto load_step = [&](int kt) {
-        const int64_t kbase = (int64_t)kt * BK;
+    auto load_step = [&](int kt, auto dc) {
+        constexpr int d = decltype(dc)::value;
+        const int64_t kbase = (int64_t)(kt < KT ? kt : KT - 1) * BK;
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
             const int c = tid + i * 256;
             const int r = c / (BK / 8), col = (c % (BK / 8)) * 8;
             const int m = GR ? s_row[r] : m0 + r;
             const bool ok = GR ? m >= 0 : m < a.M;
+            const int64_t mm = ok ? m : 0;
             if constexpr (XDT == EP_F32) {
-                const float *p = (const float *)a.x + (int64_t)m * a.ldx + kbase + col;
-                xr[i][0] = ok ? *(const u32x4_t *)p : (u32x4_t){0, 0, 0, 0};
-                xr[i][1] = ok ? *(const u32x4_t *)(p + 4) : (u32x4_t){0, 0, 0, 0};
+                const float *p = (const float *)a.x + mm * a.ldx + kbase + col;
+                xr[d][i][0] = *(const u32x4_t *)p;
+                xr[d][i][1] = *(const u32x4_t *)(p + 4);
             } else {
-                const uint16_t *p = (const uint16_t *)a.x + (int64_t)m * a.ldx + kbase + col;
-                xr[i][0] = ok ? *(const u32x4_t *)p : (u32x4_t){0, 0, 0, 0};
+                const uint16_t *p = (const uint16_t *)a.x + mm * a.ldx + kbase + col;
+                xr[d][i][0] = *(const u32x4_t *)p;
             }
         }
 #pragma unroll
         for (int i = 0; i < WCH; ++i) {
             const int c = tid + i * 256;
             const int r = c / WPR, part = c % WPR;
-            const int n = n0 + r;
+            const int n = n0 + r < a.N ? n0 + r : 0;
             const int64_t k0 = kbase + part * KPC;
             const int64_t byte0 = BITS == 4 ? k0 / 2 : k0;
-            if (n < a.N) {
-                wr[i] = __builtin_nontemporal_load(
-                    (const u32x4_t *)(a.packed + (int64_t)n * a.row_bytes + byte0));
-                wsc[i] = load_as_f32(a.scale, a.scale_dtype, (int64_t)n * a.lds + k0 / a.group);
-            } else {
-                wr[i] = (u32x4_t){0, 0, 0, 0};
-                wsc[i] = 0.0f;
-            }
+            wr[d][i] = __builtin_nontemporal_load((const u32x4_t *)(a.packed + (int64_t)n * a.row_bytes + byte0));
+            const int64_t e = (int64_t)n * a.lds + k0 / a.group;
+            wsr[d][i] = a.scale_dtype == EP_F32 ? ((const uint32_t *)a.scale)[e]
+                                                : (uint32_t)((const uint16_t *)a.scale)[e];
         }
     };
 
-    auto store_step = [&]() {
+    auto store_step = [&](auto dc) {
+        constexpr int d = decltype(dc)::value;
+        u32x4_t (&xrd)[XCH][XW] = xr[d];
+        u32x4_t (&wrd)[WCH] = wr[d];
+#pragma unroll
+        for (int i = 0; i < XCH; ++i) {
+            const int c = tid + i * 256;
+            const int r = c / (BK / 8);
+            const int m = GR ? s_row[r] : m0 + r;
+            if (!(GR ? m >= 0 : m < a.M)) {
+#pragma unroll
+                for (int w = 0; w < XW; ++w)
+                    xrd[i][w] = (u32x4_t){0u, 0u, 0u, 0u};
+            }
+        }
+        float wsc[WCH];
+#pragma unroll
+        for (int i = 0; i < WCH; ++i) {
+            const int c = tid + i * 256;
+            const int r = c / WPR;
+            const uint32_t raw = wsr[d][i];
+            const float sv = a.scale_dtype == EP_F32 ? __uint_as_float(raw)
+                             : (a.scale_dtype == EP_BF16 ? bf16_to_f32((uint16_t)raw)
+                                                         : (float)f16_from_bits((uint16_t)raw));
+            const bool nok = n0 + r < a.N;
+            wsc[i] = nok ? sv : 0.0f;
+            if (!nok)
+                wrd[i] = (u32x4_t){0u, 0u, 0u, 0u};
+        }
+        u32x4_t (&xr)[XCH][XW] = xrd;
+        u32x4_t (&wr)[WCH] = wrd;
 #pragma unroll
         for (int i = 0; i < XCH; ++i) {
             const int c = tid + i * 256;
@@ -255,14 +291,16 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
         }
     };
 
-    const int KT = (int)(a.K / BK);
     __syncthreads();  // table and row scales ready
-    load_step(0);
-    for (int kt = 0; kt < KT; ++kt) {
-        store_step();
+    load_step(0, std::integral_constant<int, 0>{});
+    load_step(1, std::integral_constant<int, 1>{});
+    // one K-step on register set D: step kt + PD - 1's loads into the set
+    // the previous step left, then this step's tiles into LDS and its MFMAs
+    auto kstep = [&](int kt, auto dc) {
+        constexpr int D = decltype(dc)::value;
+        load_step(kt + PD - 1, std::integral_constant<int, (D + PD - 1) % PD>{});
+        store_step(dc);
         __syncthreads();
-        if (kt + 1 < KT)
-            load_step(kt + 1);
 #pragma unroll
         for (int kk = 0; kk < BK / 16; ++kk) {
             f16x8_t af[TM], bfr[TN];
@@ -282,6 +320,13 @@ __global__ void __launch_bounds__(256) mm_kernel(MmArgs a)
                                                                        0, 0);
         }
         __syncthreads();
+    };
+    for (int kt = 0; kt < KT; kt += PD) {
+        kstep(kt, std::integral_constant<int, 0>{});
+        if (kt + 1 < KT)
+            kstep(kt + 1, std::integral_constant<int, 1>{});
+        if (kt + 2 < KT)
+            kstep(kt + 2, std::integral_constant<int, 2>{});
     }
 
     // epilogue: D[row][col] lives in lane col + 32 * ((row / 4) % 2),
@@ -526,9 +571,11 @@ bool expert_grouped_serves(const PackedDesc &w, const ActDesc &x, int64_t T, int
     return E >= 1 && E <= kMaxExperts && T >= 1 && T <= (int64_t)1 << 24 && mfma_serves(w, x, T);
 }
 
-// Experts averaging 64 tokens or more run the prefill kernel (the whole K
-// per workgroup, 64- or 128-row tiles); sparser ones the generic MFMA kernel
-// (32- or 64-row tiles).
+// The prefill kernel (the whole K per workgroup, 128-row tiles where the
+// experts average 128 tokens or more, else 64) wherever its shape rules
+// hold (fp16 scales; at 16 / 512 / 2048 tokens of a 128 x 768 x 2048 stack,
+// top-8: 52 / 87 / 213 us against 58 / 134 / 216 on the generic kernel);
+// the generic MFMA kernel (32- or 64-row tiles) for the rest.
 int launch_expert_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, const int *ids, int E,
                           const OutDesc &y, void *ws, size_t ws_bytes, hipStream_t stream)
 {
@@ -549,7 +596,7 @@ int launch_expert_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, cons
     base += 256;
     int *rexp = (int *)base;  // (the prefill kernel's exponents and fp16 rows start here too)
     const int64_t avg = (T + E - 1) / E;
-    const bool pf = avg >= 64 && prefill_grouped_serves(w, x, T);
+    const bool pf = prefill_grouped_serves(w, x, T);
     const int bm = pf ? (avg >= 128 ? 128 : 64) : grouped_bm(T, E);
     const dim3 sg((unsigned)((E + kSortWavesPerWg - 1) / kSortWavesPerWg)), sb(64 * kSortWavesPerWg);
     hipLaunchKernelGGL(expert_count_kernel, sg, sb, 0, stream, ids, (int)T, E, counts);

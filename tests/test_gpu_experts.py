@@ -226,18 +226,18 @@ def skewed_ids(T, E, g, kind):
 
 
 @pytest.mark.parametrize("E,n,k,levels,T,dt,kind", [
-    (8, 256, 512, 16, 100, torch.bfloat16, "uniform"),     # 32-row tiles
-    (4, 384, 1024, 16, 300, torch.float16, "skewed"),      # 128-row tiles, one long run
+    # the prefill kernel over the sorted runs (fp16 scales): 64-row tiles
+    # below 128 tokens per expert, 128-row tiles from there
+    (8, 256, 512, 16, 100, torch.bfloat16, "uniform"),
+    (4, 384, 1024, 16, 300, torch.float16, "skewed"),      # one long run
     (16, 128, 256, 256, 37, torch.bfloat16, "sparse"),     # 8-bit, empty experts
     (64, 128, 512, 16, 2048, torch.bfloat16, "uniform"),   # many experts
-    (2, 256, 512, 256, 700, torch.float16, "one"),         # all tokens on the last expert
+    (2, 256, 512, 256, 700, torch.float16, "one"),         # all tokens on the last expert, 128 rows
     (6, 192, 512, 16, 90, torch.float32, "uniform"),       # f32 activations
-    # experts averaging >= 64 tokens: the prefill kernel over the sorted runs
     (3, 512, 1024, 16, 400, torch.bfloat16, "uniform"),    # 4-bit, 128-row tiles
-    (4, 256, 2048, 256, 260, torch.bfloat16, "skewed"),    # 8-bit, 64-row tiles
-    (4, 320, 1024, 16, 300, torch.float16, "sparse"),      # 4-bit, 64-row tiles, empty experts
+    (4, 256, 2048, 256, 260, torch.bfloat16, "skewed"),    # 8-bit
+    (4, 320, 1024, 16, 300, torch.float16, "sparse"),      # empty experts
     (2, 128, 512, 16, 300, torch.float32, "uniform"),      # f32 activations, 128-row tiles
-    # longer rows on the generic kernel's 32-row tiles
     (16, 256, 2048, 16, 40, torch.bfloat16, "uniform"),
     (8, 384, 4096, 16, 50, torch.float16, "skewed"),       # one expert's run over two tiles
     (12, 128, 2048, 256, 30, torch.bfloat16, "sparse"),
@@ -268,10 +268,10 @@ def test_grouped_experts_vs_oracle(E, n, k, levels, T, dt, kind):
 
 @pytest.mark.parametrize("E,T,k", [(12, 64, 1024), (4, 512, 1024), (32, 64, 2048)])
 def test_grouped_experts_graph_replay_follows_ids(E, T, k):
-    """Captured once, the grouped call (device sort + grouped launch: the
-    generic MFMA kernel at 12 and 32 experts x 64 tokens, the prefill kernel
-    at 4 x 512) follows ids and x rewritten in place between replays; every
-    replay equals an eager call bit for bit."""
+    """Captured once, the grouped call (device sort + the prefill kernel over
+    the sorted runs: 64-row tiles at 12 and 32 experts x 64 tokens, 128-row
+    tiles at 4 x 512) follows ids and x rewritten in place between replays;
+    every replay equals an eager call bit for bit."""
     n = 256
     s, *_ = experts(E, n, k, 16, 128, seed=17)
     m = PackedExperts(s, check_ids=False)
@@ -294,6 +294,28 @@ def test_grouped_experts_graph_replay_follows_ids(E, T, k):
         torch.cuda.synchronize()
         eager = PackedExperts(s)(x, ids)
         assert torch.equal(y, eager), r
+
+
+@pytest.mark.parametrize("E,T", [(6, 40), (3, 200)])
+def test_grouped_experts_f32_scales_generic_kernel(E, T):
+    """float32 group scales and a bfloat16 codebook (after make_trainable)
+    take the generic MFMA kernel over the sorted runs (32- / 64-row tiles;
+    per-expert scale stride in 4-byte units)."""
+    n, k, group = 256, 1024, 128
+    rng = np.random.Generator(np.random.PCG64(31 + T))
+    idx = rng.integers(0, 16, E * n * k).astype(np.uint8)
+    packed = ref.pack4(idx, 16)
+    cb = torch.tensor(np.sort(rng.standard_normal(16)), dtype=torch.bfloat16)
+    scale = (np.abs(rng.normal(0, 0.02, (E * n, k // group))) + 1e-3).astype(np.float32)
+    s = PackedWeight((E, n, k), packed, scale, cb, group, 16).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(T)
+    x = torch.randn(T, k, generator=g, device=DEV).to(torch.bfloat16)
+    ids = skewed_ids(T, E, g, "skewed")
+    y = PackedExperts(s)(x, ids)
+    want = want_rows(x.float().cpu().numpy(), ids.cpu().tolist(), packed, scale,
+                     cb.float().numpy(), E, n, k, group, 16)
+    err = np.abs(y.float().cpu().numpy() - want).max() / np.abs(want).max()
+    assert err < 2e-3 + 2.0 ** -8, err
 
 
 def test_grouped_experts_clamp_ids_and_strided_rows():
