@@ -280,6 +280,14 @@ def _sk1_serves(m, n, cus):
     return m <= 16 * t
 
 
+def _sk2_serves(m, n, k):
+    """Whether the register-resident split-K kernel serves a config-3 linear
+    (8-bit indices, bf16 x, group 128): 17 <= M <= 64 on layers of at least
+    2^25 weights (skinny.hip sk2_serves); it takes the rows before the
+    one-launch kernel does."""
+    return 17 <= m <= 64 and n * k >= 2 ** 25
+
+
 def _row_serves(k, bits=8):
     """Whether the batch-1 row GEMV takes a row of K indices (gemv.hip
     row_kernel_slabs): rows of 4, 8, 12, 16, 24, 28 or 32 slabs of 256
@@ -321,6 +329,8 @@ def prefill_sweep(seed=0, replays=10):
                          "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS, 4),
                          "kernel": (("gemv_row_kernel" if _row_serves(k) else "gemv_lut_kernel")
                                     if m == 1 else
+                                    "sk2_kernel (+ sk_reduce_kernel when K is split)"
+                                    if _sk2_serves(m, n, k) else
                                     "sk1_kernel" if _sk1_serves(m, n, cus) else
                                     "sk_kernel + sk_reduce_kernel" if m <= 64 else
                                     "pf_prep_kernel + pf_kernel (+ sk_reduce_kernel when K is split)")})

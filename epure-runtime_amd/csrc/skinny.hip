@@ -36,7 +36,13 @@
 //    to M = 8), sk1_kernel instead: a workgroup owns 1, 2 or 4 row tiles
 //    over the whole of K, one launch, no partials (its comment has the
 //    layout); bf16 activations with 8-bit indices take its bf16 path (raw
-//    bf16 operands, the codebook as exact bf16 hi + lo terms).
+//    bf16 operands, the codebook as exact bf16 hi + lo terms);
+//  * with 8-bit indices at 17 <= M <= 64 on layers of at least 2^25
+//    weights, sk2_kernel instead: K slices of 2048 or 4096 values, each
+//    wave's activation columns held in registers for all of its
+//    workgroup's row tiles (its comment has the layout).
+#include <algorithm>
+
 #include "ep_common.h"
 #include "ep_internal.h"
 #include "gemv_core.h"
@@ -667,6 +673,192 @@ __global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
     }
 }
 
+// Split-K with the activations held in registers: 8-bit indices, 17 <= M
+// <= 64, fp16 activations, or bf16 ones with groups of a multiple of 64
+// values (the bf16 path).  A workgroup's 8 waves split its K slice of 8 R
+// values (R = 64 NC per wave).  Each wave loads its R columns of the MB
+// 16-row activation blocks once, as MFMA A operands, then streams its
+// workgroup's row tiles (16 rows each: tiles blockIdx.x + it * gtiles)
+// over those columns: lane (i, kq) loads 16 bytes of row i at k0 + 64 c +
+// 16 kq, c < NC (a row's R bytes, contiguous, over the wave's NC loads), D
+// tiles ahead of the MFMAs.  The MFMA k index 8 kq + j of sub-step (c, e)
+// is the value k0 + 64 c + 16 kq + 8 e + j in both operands.  After each
+// tile the waves' sums meet in LDS (two buffers, one barrier per tile) and
+// are added in wave order: with one split into y, else into the f32
+// partials [S][M][N] that sk_reduce_kernel adds in split order.  The
+// activations are never converted: fp16 x is the B operand as it is,
+// against fp16 weights (the tile of materialize(float16),
+// runtime.py:78-89); bf16 x is the A operand of the bf16 MFMA against the
+// codebook's exact bf16 hi + lo terms, each 64-value piece's f32 sums
+// times its group scale (as sk1_kernel's bf16 path).  Against sk_kernel (K
+// slices of 512 staged in LDS, the activations converted by every
+// workgroup) the slices are 4-8x longer, so 4-8x fewer partials.  Measured
+// and not kept: bf16 x converted once per wave to fp16 (exact power-of-two
+// row rescale) for single fp16 MFMAs -- no faster (4096 x 14336 at M = 64:
+// 42.1 against 40.3 us): the loop is bound by the lookups, the per-tile
+// barrier and the wave sums at two waves per SIMD, not by the MFMAs.
+template <int MB, int NC, int D, bool HL>
+__global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
+{
+    constexpr int R = 64 * NC;          // K values of a wave
+    constexpr int KW = kSkWaves * R;    // K values of a split
+    __shared__ __align__(16) uint32_t tab[kTabDwords];
+    __shared__ __align__(16) f32x4_t red[2][kSkWaves][MB][64];
+    __shared__ uint32_t s_cbraw[kSkThreads];
+    __shared__ uint16_t s_cb[256];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 15, kq = lane >> 4;
+    const int split = blockIdx.y;
+    const int k0 = split * KW + wave * R;
+    const int nit = (a.tiles - (int)blockIdx.x + a.gtiles - 1) / a.gtiles;  // this workgroup's row tiles
+    const auto rx = buffer_rsrc(a.x, a.xbytes), rw = buffer_rsrc(a.packed, a.wbytes);
+    const auto rs = buffer_rsrc(a.scale, a.sbytes), rcb = buffer_rsrc(a.cb, a.cbbytes);
+
+    // ---- loads in the order they are needed (results return in order):
+    // codebook, the wave's activation columns, the first D tiles' weights
+    const uint32_t cbraw = __builtin_amdgcn_raw_buffer_load_b32(rcb, tid < 256 ? tid * 4 : kOut, 0, 0);
+    u32x4_t xv[MB][NC][2];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int m = 16 * mb + i, k = k0 + 64 * c + 16 * kq + 8 * e;
+                const bool ok = m < a.M && k < a.K;  // K % 16 == 0: pieces of 8 are whole
+                const uint32_t off = ok ? (uint32_t)(((int64_t)m * a.ldx + k) * 2) : kOut;
+                xv[mb][c][e] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
+            }
+    u32x4_t wv[D][NC];
+    uint32_t sv[D][NC];  // fp16 scale bits; 0 where masked
+    auto issue = [&](int d, int it) {
+        const int n = ((int)blockIdx.x + it * a.gtiles) * 16 + i;
+        const bool live = it < nit && n < a.N;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int k = k0 + 64 * c + 16 * kq;
+            const bool ok = live && k < a.K;
+            const uint32_t woff = (uint32_t)n * a.row_bytes + (uint32_t)k;
+            wv[d][c] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (int)woff : (int)kOut, 0, 2);
+            // the bf16 path scales the sums of the 64-value piece: its
+            // group (its first value's), the same in the piece's four lanes
+            const int ks = HL ? k0 + 64 * c : k;
+            const bool sok = live && ks < a.K;
+            const uint32_t soff = (uint32_t)(((int64_t)n * a.lds + ks / a.group) * 2);
+            sv[d][c] = __builtin_amdgcn_raw_buffer_load_b16(rs, sok ? (int)soff : (int)kOut, 0, 0);
+        }
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        issue(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+    s_cbraw[tid] = cbraw;
+    lds_barrier();
+    if (tid < 256) {
+        float c = 0.0f;
+        if (tid < a.levels) {
+            if (a.cb_dtype == EP_F32) {
+                c = __uint_as_float(s_cbraw[tid]);
+            } else {
+                const uint16_t h = (uint16_t)(s_cbraw[tid >> 1] >> (16 * (tid & 1)));
+                c = a.cb_dtype == EP_F16 ? (float)f16_from_bits(h) : bf16_to_f32(h);
+            }
+        }
+        s_cb[tid] = f16_bits((f16_t)c);
+    }
+    lds_barrier();
+    if constexpr (HL)
+        build_table_hl(tab, s_cb);
+    else
+        build_table<8>(tab, s_cb);
+    lds_barrier();
+
+    const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
+    for (int it0 = 0; it0 < nit; it0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int it = it0 + d;
+            if (it >= nit)
+                break;
+            f32x4_t acc[MB];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                acc[mb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                if constexpr (HL) {
+                    u32x4_t bh[2], bl[2];
+                    dequant_chunk_hl(tab, wv[d][c], lane4, bh, bl);
+                    f32x4_t cs[MB];
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb)
+                        cs[mb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+                    // MB independent sums between two MFMAs on one sum
+#pragma unroll
+                    for (int e = 0; e < 2; ++e)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int mb = 0; mb < MB; ++mb)
+                                cs[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                    __builtin_bit_cast(bf16x8_t, xv[mb][c][e]),
+                                    __builtin_bit_cast(bf16x8_t, h ? bl[e] : bh[e]), cs[mb], 0, 0, 0);
+                    const float sc = (float)f16_from_bits((uint16_t)sv[d][c]);
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            acc[mb][r] = fmaf(cs[mb][r], sc, acc[mb][r]);
+                } else {
+                    // the weights are the A operand here: D[n][m]
+                    f16x8_t bv[2];
+                    dequant_chunk<8>(tab, wv[d][c], sv[d][c], lane4, bv);
+#pragma unroll
+                    for (int e = 0; e < 2; ++e)
+#pragma unroll
+                        for (int mb = 0; mb < MB; ++mb)
+                            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                bv[e], __builtin_bit_cast(f16x8_t, xv[mb][c][e]), acc[mb], 0, 0, 0);
+                }
+            }
+            issue(d, it + D);
+            // D[r][c] of a 16x16 block: lane c + 16 (r / 4), register r % 4
+            // (rows m, columns n on the bf16 path; rows n, columns m else)
+            const int buf = it & 1;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                red[buf][wave][mb][lane] = acc[mb];
+            lds_barrier();
+            if (tid < MB * 64) {
+                const int mb = tid >> 6, l = tid & 63;
+                f32x4_t s = red[buf][0][mb][l];
+#pragma unroll
+                for (int w = 1; w < kSkWaves; ++w)
+                    s += red[buf][w][mb][l];
+                const int n0 = ((int)blockIdx.x + it * a.gtiles) * 16;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = 16 * mb + (HL ? 4 * (l >> 4) + r : (l & 15));
+                    const int n = n0 + (HL ? (l & 15) : 4 * (l >> 4) + r);
+                    if (m < a.M && n < a.N) {
+                            if (a.part) {
+                                a.part[((int64_t)split * a.M + m) * a.N + n] = s[r];
+                            } else {
+                                const int64_t off = (int64_t)m * a.ldy + n;
+                                float v = s[r];
+                                if (a.accumulate)
+                                    v += load_as_f32(a.y, a.y_dtype, off);
+                            store_from_f32(a.y, a.y_dtype, off, v);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
 // y[m, n] (=|+=) sum over splits s = 0 .. S-1 of part[s][m][n], in that
 // order.  Four consecutive outputs per thread (N % 4 == 0: 16-byte loads),
 // the loads of eight splits in flight at a time.
@@ -842,6 +1034,48 @@ void sk1_launch_x(const SkArgs &a, int tpw, hipStream_t s)
     }
 }
 
+// The register-resident split-K kernel: MB = ceil(M / 16) activation
+// blocks, NC 64-value pieces per wave (the activations take 8 MB NC
+// registers: 128 at most), loads D tiles ahead (one where the pieces are
+// eight).  It serves 8-bit indices at 17 <= M <= 64 with fp16 activations,
+// or bf16 ones with groups of a multiple of 64 values, on layers of at
+// least 2^25 weights: each workgroup reads its 64 x 8 R activations once
+// from L2 (~9 us for the 256 KiB of 8 R = 2048) and then costs ~2.9 us per
+// tile on the bf16 path, so it pays where a workgroup streams several
+// tiles (bf16 x, 4096 x 14336 at M = 64 / 48 / 32 / 17: 52.9 / 48.6 / 40.2
+// / 38.7 -> 41.2 / 34.7 / 34.4 / 32.7 us; 14336 x 4096: 42.5 / 40.3 / 34.0
+// / 32.0 -> 38.7 / 33.2 / 31.9 / 31.0) and not at 4096 x 4096 (M = 64:
+// 18.9 against 20.2 us).
+int sk2_mb(int64_t M) { return (int)((M + 15) / 16); }
+int sk2_split_k(int64_t M) { return kSkWaves * 64 * (sk2_mb(M) <= 2 ? 8 : 4); }
+int sk2_splits(int64_t M, int64_t K) { return (int)((K + sk2_split_k(M) - 1) / sk2_split_k(M)); }
+bool sk2_serves(int bits, const ActDesc &x, int64_t M, int64_t N, int64_t K, int group)
+{
+    return bits == 8 && M > 16 && M <= 64 && N * K >= ((int64_t)1 << 25) &&
+           (x.dtype == EP_F16 || (x.dtype == EP_BF16 && group % 64 == 0));
+}
+
+template <int MB, bool HL>
+void sk2_launch_m(const SkArgs &a, int S, hipStream_t s)
+{
+    constexpr int NC = MB <= 2 ? 8 : 4;
+    constexpr int D = NC == 8 ? 1 : 2;
+    hipLaunchKernelGGL((sk2_kernel<MB, NC, D, HL>), dim3((unsigned)a.gtiles, (unsigned)S), dim3(kSkThreads), 0, s,
+                       a);
+}
+
+template <bool HL>
+void sk2_launch(const SkArgs &a, int S, hipStream_t s)
+{
+    const int mb = sk2_mb(a.M);
+    if (mb == 2)
+        sk2_launch_m<2, HL>(a, S, s);
+    else if (mb == 3)
+        sk2_launch_m<3, HL>(a, S, s);
+    else
+        sk2_launch_m<4, HL>(a, S, s);
+}
+
 }  // namespace
 
 bool skinny_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
@@ -866,8 +1100,11 @@ bool skinny_serves(const PackedDesc &w, const ActDesc &x, int64_t M)
 
 size_t skinny_workspace(int64_t M, int64_t N, int64_t K, int levels)
 {
-    // partial sums of every split (also with one split when accumulating)
-    return (size_t)sk_splits(levels <= 16 ? 4 : 8, M, N, K) * (size_t)M * (size_t)N * sizeof(float);
+    // partial sums of every split (also with one split when accumulating);
+    // the register-resident kernel's longer splits need no more
+    const int bits = levels <= 16 ? 4 : 8;
+    const int S = std::max(sk_splits(bits, M, N, K), M > 16 && M <= 64 ? sk2_splits(M, K) : 1);
+    return (size_t)S * (size_t)M * (size_t)N * sizeof(float);
 }
 
 int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDesc &y, void *ws,
@@ -876,10 +1113,11 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
     if (!skinny_serves(w, x, M))
         return EP_DECLINE_SHAPE;
     const int bits = w.bits();
-    const int tpw1 = sk1_tiles_per_wg(bits, x, M, w.N, w.group);
+    const bool reg = sk2_serves(bits, x, M, w.N, w.K, w.group);
+    const int tpw1 = reg ? 0 : sk1_tiles_per_wg(bits, x, M, w.N, w.group);
     const int ld = sk_choose_ld(bits, M, w.N, w.K);
-    const int S = sk_splits_ld(bits, ld, w.K);
-    const bool partials = tpw1 == 0 && (S > 1 || y.accumulate);
+    const int S = reg ? sk2_splits(M, w.K) : sk_splits_ld(bits, ld, w.K);
+    const bool partials = reg ? S > 1 : tpw1 == 0 && (S > 1 || y.accumulate);
     const size_t need = partials ? skinny_workspace(M, w.N, w.K, w.levels) : 0;
     if (need > 0 && (!ws || ws_bytes < need))
         return set_error(EP_ERR_WORKSPACE, "workspace of %zu bytes needed, %zu given", need, ws_bytes);
@@ -921,6 +1159,16 @@ int launch_skinny(const PackedDesc &w, const ActDesc &x, int64_t M, const OutDes
             sk1_launch_x<8, EP_BF16, false>(a, tpw1, stream);
         EP_HIP_CHECK(hipGetLastError());
         return EP_OK;
+    }
+    if (reg) {
+        // one resident workgroup per CU (its LDS): S splits of gtiles
+        // workgroups, each streaming every gtiles-th 16-row tile
+        a.tiles = (int)((w.N + 15) / 16);
+        a.gtiles = std::max(1, std::min(a.tiles, device_cus() / S));
+        a.part = partials ? (float *)ws : nullptr;
+        x.dtype == EP_F16 ? sk2_launch<false>(a, S, stream) : sk2_launch<true>(a, S, stream);
+        EP_HIP_CHECK(hipGetLastError());
+        return partials ? launch_split_reduce((const float *)ws, S, M, w.N, y, stream) : EP_OK;
     }
     a.tiles = (int)((w.N + kSkRows - 1) / kSkRows);
     // one resident workgroup per CU: enough row-tile groups that S of them

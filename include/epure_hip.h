@@ -94,9 +94,12 @@ size_t ep_dequant_matmul_workspace(int64_t M, int64_t N, int64_t K, int levels, 
  * per-row power-of-two rescale, so it cannot overflow fp16.
  * The kernel is chosen from M: the LUT GEMV at M = 1 (up to 4 where its
  * activations fit), register-dequant MFMA kernels up to M = 64 (one launch
- * per linear for 8-bit indices at M <= 16 and wide N, split-K with an
- * ordered reduction otherwise), dequant-to-LDS + MFMA above.  Each reads
- * the packed bytes exactly once per launch.
+ * per linear for 8-bit indices at M <= 16 and wide N; for 8-bit indices at
+ * 17 <= M <= 64 on layers of at least 2^25 weights, split-K over slices of
+ * 2048 or 4096 values with each wave's activations held in registers;
+ * split-K over slices of at most 1024 otherwise; the splits' f32 partials
+ * summed in split order), dequant-to-LDS + MFMA above.  Each reads the
+ * packed bytes exactly once per launch.
  */
 int ep_dequant_matmul(const void *x, int x_dtype, int64_t ldx,
                       const uint8_t *packed, const void *scale, int scale_dtype,

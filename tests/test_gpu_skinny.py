@@ -315,3 +315,67 @@ def test_skinny_one_launch_strided_x(m):
     assert x.stride(0) == k + 96
     assert_close(run(s, x).cpu().numpy(), rust_ref(np.ascontiguousarray(x32[:, :k]), packed, scale, cb, n,
                                                     k, 256, 128))
+
+
+# The register-resident split-K kernel: 8-bit indices, 17 <= M <= 64, fp16
+# x or bf16 x with groups of a multiple of 64 values (the bf16 path), layers
+# of at least 2^25 weights.  A split is 4096 values of K (M <= 32) or 2048;
+# a workgroup streams every gtiles-th 16-row tile of its split.
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,n,k,group,levels", [
+    (17, 8200, 4096 + 64, 128, 256),   # two splits, the second of 64 values; N past the last tile
+    (33, 8200, 4096 + 64, 64, 200),    # three activation blocks; levels below 256
+    (48, 2056, 16384 + 64, 256, 256),  # nine splits (the last of 64 values), 129 tiles
+    (64, 16400, 2048, 128, 256),       # one split: straight into y, several tiles per workgroup
+    (32, 4104, 8192 + 128, 128, 256),  # two blocks, three splits (the last of 128 values)
+    (20, 4104, 8192 + 32, 64, 256),    # K past the last whole 64-value piece
+])
+def test_skinny_register_resident(xdt, m, n, k, group, levels):
+    _, packed, scale, cb, s = make(n, k, levels, group, seed=n + k + m)
+    x32, x = x_bf16(m, k, m + levels)
+    x = x.to(xdt)
+    want = rust_ref(x.float().cpu().numpy(), packed, scale, cb, n, k, levels, group)
+    assert_close(run(s, x).cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("m,n,k", [(24, 16400, 2048), (64, 8200, 4096 + 64)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_skinny_register_resident_accumulate(out_dtype, m, n, k):
+    """Results written, then added to y: in the kernel with one split,
+    through the split reduction with three."""
+    _, packed, scale, cb, s = make(n, k, 256, seed=71 + m)
+    x32, x = x_bf16(m, k, 72 + m)
+    want = rust_ref(x32, packed, scale, cb, n, k, 256, 128)
+    out_tol = TOL if out_dtype == torch.float32 else TOL + 2.0 ** -8
+    assert_close(run(s, x, out_dtype).float().cpu().numpy(), want, out_tol)
+    out = torch.from_numpy(rng(73 + m).standard_normal((m, n)).astype(np.float32)).to(DEV).to(out_dtype)
+    start = out.float().cpu().numpy()
+    run(s, x, out_dtype, accumulate=True, out=out)
+    assert_close(out.float().cpu().numpy(), want + start, out_tol)
+
+
+def test_skinny_register_resident_rows_of_very_different_magnitude():
+    """bf16 rows from 1e30 down to 1e-30 and 0 are exact MFMA operands on
+    the bf16 path: each row stays exact relative to its own size."""
+    n, k = 8200, 4096 + 64
+    idx, packed, scale, cb, s = make(n, k, 256, seed=81)
+    w64 = ref.dequant_tile_f32(idx, scale, cb, 128).astype(np.float64)
+    mags = np.array([1e30, 3e5, 1.0, 1e-12, 1e-30, 0.0] * 3, np.float32)
+    x32 = ref.round_bf16((rng(82).standard_normal((len(mags), k)) * mags[:, None]).astype(np.float32))
+    x = torch.from_numpy(x32).to(DEV).to(torch.bfloat16)
+    y = run(s, x).cpu().numpy()
+    want = ref.linear_f64(x32, w64)
+    for r in range(len(mags)):
+        if mags[r] == 0.0:
+            assert np.all(y[r] == 0.0)
+        else:
+            assert_close(y[r:r + 1], want[r:r + 1])
+
+
+def test_skinny_register_resident_deterministic():
+    n, k, m = 8200, 4096 + 64, 40
+    _, packed, scale, cb, s = make(n, k, 256, seed=91)
+    _, x = x_bf16(m, k, 92)
+    a = run(s, x).cpu().numpy()
+    b = run(s, x).cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
