@@ -692,20 +692,35 @@ __global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
 // codebook's exact bf16 hi + lo terms, each 64-value piece's f32 sums
 // times its group scale (as sk1_kernel's bf16 path).  Against sk_kernel (K
 // slices of 512 staged in LDS, the activations converted by every
-// workgroup) the slices are 4-8x longer, so 4-8x fewer partials.  Measured
-// and not kept: bf16 x converted once per wave to fp16 (exact power-of-two
-// row rescale) for single fp16 MFMAs -- no faster (4096 x 14336 at M = 64:
-// 42.1 against 40.3 us): the loop is bound by the lookups, the per-tile
-// barrier and the wave sums at two waves per SIMD, not by the MFMAs.
-template <int MB, int NC, int D, bool HL>
+// workgroup) the slices are 4-8x longer, so 4-8x fewer partials.  Where a
+// time goes (14336 x 4096 at M = 64, seven tiles per workgroup): the table
+// is built ~10 us after entry (the codebook and the 256 KiB of activations
+// per CU arrive at ~28 GB/s per CU), then each tile takes ~2.7 us (~1.7 of
+// lookups, MFMAs and VALU at two waves per SIMD, ~0.9 of barrier and wave
+// sums).  Measured and not kept: bf16 x converted once per wave to fp16
+// (exact power-of-two row rescale) for single fp16 MFMAs (4096 x 14336 at
+// M = 64: 42.1 against 40.3 us); three tiles of loads in flight instead of
+// two (no change).
+template <int MB, int NC, int D, bool HL, bool G2>
 __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
 {
     constexpr int R = 64 * NC;          // K values of a wave
     constexpr int KW = kSkWaves * R;    // K values of a split
-    __shared__ __align__(16) uint32_t tab[kTabDwords];
-    __shared__ __align__(16) f32x4_t red[2][kSkWaves][MB][64];
-    __shared__ uint32_t s_cbraw[kSkThreads];
-    __shared__ uint16_t s_cb[256];
+    static_assert(!G2 || (HL && NC % 2 == 0), "pairs of pieces per scale: the bf16 path");
+    // one LDS block with the table first: at LDS address 0 a lookup's
+    // address is the v_perm result itself (at 64 KiB it would take one
+    // more add per lookup: the instruction's offset field is 16 bits)
+    struct Lds {
+        uint32_t tab[kTabDwords];
+        f32x4_t red[2][kSkWaves][MB][64];
+        uint32_t cbraw[kSkThreads];
+        uint16_t cb[256];
+    };
+    __shared__ __align__(16) Lds sm;
+    uint32_t *const tab = sm.tab;
+    auto &red = sm.red;
+    uint32_t *const s_cbraw = sm.cbraw;
+    uint16_t *const s_cb = sm.cb;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -731,23 +746,34 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
                 const uint32_t off = ok ? (uint32_t)(((int64_t)m * a.ldx + k) * 2) : kOut;
                 xv[mb][c][e] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
             }
+    // per piece, the same for every tile: whether it lies inside K and its
+    // scale's group (the bf16 path scales the sums of the 64-value piece --
+    // G2: of the pair of pieces c, c + 1 at a multiple of 128 -- by the
+    // group of its first value, the same in the piece's four lanes)
+    bool kin[NC], sin[NC];
+    uint32_t sgrp[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        const int k = k0 + 64 * c + 16 * kq, ks = HL ? k0 + 64 * c : k;
+        kin[c] = k < a.K;
+        sin[c] = ks < a.K;
+        sgrp[c] = (uint32_t)(ks / a.group);
+    }
     u32x4_t wv[D][NC];
     uint32_t sv[D][NC];  // fp16 scale bits; 0 where masked
     auto issue = [&](int d, int it) {
         const int n = ((int)blockIdx.x + it * a.gtiles) * 16 + i;
         const bool live = it < nit && n < a.N;
+        const uint32_t wrow = (uint32_t)n * a.row_bytes + (uint32_t)(k0 + 16 * kq);
+        const uint32_t srow = (uint32_t)n * (uint32_t)a.lds;  // in range: sbytes fits 32 bits
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-            const int k = k0 + 64 * c + 16 * kq;
-            const bool ok = live && k < a.K;
-            const uint32_t woff = (uint32_t)n * a.row_bytes + (uint32_t)k;
-            wv[d][c] = __builtin_amdgcn_raw_buffer_load_b128(rw, ok ? (int)woff : (int)kOut, 0, 2);
-            // the bf16 path scales the sums of the 64-value piece: its
-            // group (its first value's), the same in the piece's four lanes
-            const int ks = HL ? k0 + 64 * c : k;
-            const bool sok = live && ks < a.K;
-            const uint32_t soff = (uint32_t)(((int64_t)n * a.lds + ks / a.group) * 2);
-            sv[d][c] = __builtin_amdgcn_raw_buffer_load_b16(rs, sok ? (int)soff : (int)kOut, 0, 0);
+            wv[d][c] = __builtin_amdgcn_raw_buffer_load_b128(rw, live && kin[c] ? (int)(wrow + 64 * c) : (int)kOut,
+                                                             0, 2);
+            if (G2 && c % 2 == 1)
+                continue;
+            sv[d][c] = __builtin_amdgcn_raw_buffer_load_b16(
+                rs, live && sin[c] ? (int)((srow + sgrp[c]) * 2) : (int)kOut, 0, 0);
         }
     };
 #pragma unroll
@@ -782,7 +808,7 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
             const int it = it0 + d;
             if (it >= nit)
                 break;
-            f32x4_t acc[MB];
+            f32x4_t acc[MB], cs[MB];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
                 acc[mb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
@@ -791,10 +817,10 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
                 if constexpr (HL) {
                     u32x4_t bh[2], bl[2];
                     dequant_chunk_hl(tab, wv[d][c], lane4, bh, bl);
-                    f32x4_t cs[MB];
+                    if (!G2 || c % 2 == 0)
 #pragma unroll
-                    for (int mb = 0; mb < MB; ++mb)
-                        cs[mb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
+                        for (int mb = 0; mb < MB; ++mb)
+                            cs[mb] = (f32x4_t){0.0f, 0.0f, 0.0f, 0.0f};
                     // MB independent sums between two MFMAs on one sum
 #pragma unroll
                     for (int e = 0; e < 2; ++e)
@@ -805,12 +831,14 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
                                 cs[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                                     __builtin_bit_cast(bf16x8_t, xv[mb][c][e]),
                                     __builtin_bit_cast(bf16x8_t, h ? bl[e] : bh[e]), cs[mb], 0, 0, 0);
-                    const float sc = (float)f16_from_bits((uint16_t)sv[d][c]);
+                    if (!G2 || c % 2 == 1) {
+                        const float sc = (float)f16_from_bits((uint16_t)sv[d][G2 ? c - 1 : c]);
 #pragma unroll
-                    for (int mb = 0; mb < MB; ++mb)
+                        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            acc[mb][r] = fmaf(cs[mb][r], sc, acc[mb][r]);
+                            for (int r = 0; r < 4; ++r)
+                                acc[mb][r] = fmaf(cs[mb][r], sc, acc[mb][r]);
+                    }
                 } else {
                     // the weights are the A operand here: D[n][m]
                     f16x8_t bv[2];
@@ -837,22 +865,40 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
 #pragma unroll
                 for (int w = 1; w < kSkWaves; ++w)
                     s += red[buf][w][mb][l];
-                const int n0 = ((int)blockIdx.x + it * a.gtiles) * 16;
+                // element r: row m0 + r dm, column n0 + r dn
+                const int nt = ((int)blockIdx.x + it * a.gtiles) * 16;
+                const int m0 = 16 * mb + (HL ? 4 * (l >> 4) : (l & 15)), dm = HL ? 1 : 0;
+                const int n0 = nt + (HL ? (l & 15) : 4 * (l >> 4)), dn = HL ? 0 : 1;
+                bool ok[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int m = 16 * mb + (HL ? 4 * (l >> 4) + r : (l & 15));
-                    const int n = n0 + (HL ? (l & 15) : 4 * (l >> 4) + r);
-                    if (m < a.M && n < a.N) {
-                            if (a.part) {
-                                a.part[((int64_t)split * a.M + m) * a.N + n] = s[r];
-                            } else {
-                                const int64_t off = (int64_t)m * a.ldy + n;
-                                float v = s[r];
-                                if (a.accumulate)
-                                    v += load_as_f32(a.y, a.y_dtype, off);
-                            store_from_f32(a.y, a.y_dtype, off, v);
+                for (int r = 0; r < 4; ++r)
+                    ok[r] = m0 + r * dm < a.M && n0 + r * dn < a.N;
+                if (a.part) {
+                    float *dst = a.part + ((int64_t)split * a.M + m0) * a.N + n0;
+                    const int64_t step = (int64_t)dm * a.N + dn;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (ok[r])
+                            dst[r * step] = s[r];
+                } else if (a.y_dtype == EP_F32) {
+                    float *y = (float *)a.y + (int64_t)m0 * a.ldy + n0;
+                    const int64_t step = (int64_t)dm * a.ldy + dn;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (ok[r])
+                            y[r * step] = a.accumulate ? y[r * step] + s[r] : s[r];
+                } else {
+                    uint16_t *y = (uint16_t *)a.y + (int64_t)m0 * a.ldy + n0;
+                    const int64_t step = (int64_t)dm * a.ldy + dn;
+                    const bool h = a.y_dtype == EP_F16;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (ok[r]) {
+                            float t = s[r];
+                            if (a.accumulate)
+                                t += h ? (float)f16_from_bits(y[r * step]) : bf16_to_f32(y[r * step]);
+                            y[r * step] = h ? f16_bits((f16_t)t) : f32_to_bf16(t);
                         }
-                    }
                 }
             }
         }
@@ -1060,8 +1106,11 @@ void sk2_launch_m(const SkArgs &a, int S, hipStream_t s)
 {
     constexpr int NC = MB <= 2 ? 8 : 4;
     constexpr int D = NC == 8 ? 1 : 2;
-    hipLaunchKernelGGL((sk2_kernel<MB, NC, D, HL>), dim3((unsigned)a.gtiles, (unsigned)S), dim3(kSkThreads), 0, s,
-                       a);
+    const dim3 grid((unsigned)a.gtiles, (unsigned)S);
+    if (HL && a.group % 128 == 0)  // one scale per pair of 64-value pieces
+        hipLaunchKernelGGL((sk2_kernel<MB, NC, D, HL, HL>), grid, dim3(kSkThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((sk2_kernel<MB, NC, D, HL, false>), grid, dim3(kSkThreads), 0, s, a);
 }
 
 template <bool HL>
