@@ -282,10 +282,10 @@ def _sk1_serves(m, n, cus):
 
 def _sk2_serves(m, n, k):
     """Whether the register-resident split-K kernel serves a config-3 linear
-    (8-bit indices, bf16 x, group 128): 17 <= M <= 64 on layers of at least
-    2^25 weights (skinny.hip sk2_serves); it takes the rows before the
-    one-launch kernel does."""
-    return 17 <= m <= 64 and n * k >= 2 ** 25
+    (8-bit indices, bf16 x, group 128): 17 <= M <= 64, at M > 32 or on layers
+    of at least 2^25 weights (skinny.hip sk2_serves); it takes the rows
+    before the one-launch kernel does."""
+    return 17 <= m <= 64 and (m > 32 or n * k >= 2 ** 25)
 
 
 def _row_serves(k, bits=8):

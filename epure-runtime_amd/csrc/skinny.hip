@@ -37,8 +37,9 @@
 //    over the whole of K, one launch, no partials (its comment has the
 //    layout); bf16 activations with 8-bit indices take its bf16 path (raw
 //    bf16 operands, the codebook as exact bf16 hi + lo terms);
-//  * with 8-bit indices at 17 <= M <= 64 on layers of at least 2^25
-//    weights, sk2_kernel instead: K slices of 2048 or 4096 values, each
+//  * with 8-bit indices at 33 <= M <= 64, and at 17 <= M <= 32 on layers
+//    of at least 2^25 weights, sk2_kernel instead: K slices of 2048 or
+//    4096 values, each
 //    wave's activation columns held in registers for all of its
 //    workgroup's row tiles (its comment has the layout).
 #include <algorithm>
@@ -676,8 +677,9 @@ __global__ void __launch_bounds__(NT) sk1_kernel(SkArgs a)
 // Split-K with the activations held in registers: 8-bit indices, 17 <= M
 // <= 64, fp16 activations, or bf16 ones with groups of a multiple of 64
 // values (the bf16 path).  A workgroup's 8 waves split its K slice of 8 R
-// values (R = 64 NC per wave).  Each wave loads its R columns of the MB
-// 16-row activation blocks once, as MFMA A operands, then streams its
+// values (R = 64 NC per wave).  Each wave takes its R columns of the MB
+// 16-row activation blocks once (staged through LDS in rounds of whole
+// rows), as MFMA operands, then streams its
 // workgroup's row tiles (16 rows each: tiles blockIdx.x + it * gtiles)
 // over those columns: lane (i, kq) loads 16 bytes of row i at k0 + 64 c +
 // 16 kq, c < NC (a row's R bytes, contiguous, over the wave's NC loads), D
@@ -710,15 +712,21 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
     // one LDS block with the table first: at LDS address 0 a lookup's
     // address is the v_perm result itself (at 64 KiB it would take one
     // more add per lookup: the instruction's offset field is 16 bits)
+    // activation staging: XR rows of the split's KW values per round (32 KiB)
+    constexpr int XR = 16384 / KW, NR = MB * 16 / XR, WPR = kSkWaves / XR;
+    constexpr int XS = KW * 2 + 16;  // staged row stride (bytes): conflict-free 16-byte reads
     struct Lds {
         uint32_t tab[kTabDwords];
-        f32x4_t red[2][kSkWaves][MB][64];
+        union {
+            f32x4_t red[2][kSkWaves][MB][64];
+            uint8_t xs[XR * XS];
+        } u;
         uint32_t cbraw[kSkThreads];
         uint16_t cb[256];
     };
     __shared__ __align__(16) Lds sm;
     uint32_t *const tab = sm.tab;
-    auto &red = sm.red;
+    auto &red = sm.u.red;
     uint32_t *const s_cbraw = sm.cbraw;
     uint16_t *const s_cb = sm.cb;
 
@@ -732,20 +740,29 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
     const auto rs = buffer_rsrc(a.scale, a.sbytes), rcb = buffer_rsrc(a.cb, a.cbbytes);
 
     // ---- loads in the order they are needed (results return in order):
-    // codebook, the wave's activation columns, the first D tiles' weights
+    // codebook, the activations, the first D tiles' weights
     const uint32_t cbraw = __builtin_amdgcn_raw_buffer_load_b32(rcb, tid < 256 ? tid * 4 : kOut, 0, 0);
+    // activations: round r stages rows r XR .. r XR + XR - 1 of the split as
+    // whole contiguous rows (wave w loads 4 KiB of row w / WPR, 1 KiB per
+    // instruction), then each lane reads its operand pieces of those rows.
+    // Loaded straight into operand registers, every load instruction would
+    // take 64 bytes from each of 16 rows a power-of-two stride apart (8 KiB
+    // at K = 4096), and the 256 KiB per workgroup arrived at ~28 GB/s per CU
+    // (4096 x 4096 at M = 64: 18.9 -> 17.2 us staged).
+    u32x4_t xraw[2][4];
+    auto xload = [&](int slot, int r) {
+        const int m = r * XR + wave / WPR;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int k = split * KW + ((wave % WPR) * 4096 + p * 1024 + lane * 16) / 2;
+            const bool ok = r < NR && m < a.M && k < a.K;
+            xraw[slot][p] = __builtin_amdgcn_raw_buffer_load_b128(
+                rx, ok ? (int)(((int64_t)m * a.ldx + k) * 2) : (int)kOut, 0, 0);
+        }
+    };
+    xload(0, 0);
+    xload(1, 1);
     u32x4_t xv[MB][NC][2];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int m = 16 * mb + i, k = k0 + 64 * c + 16 * kq + 8 * e;
-                const bool ok = m < a.M && k < a.K;  // K % 16 == 0: pieces of 8 are whole
-                const uint32_t off = ok ? (uint32_t)(((int64_t)m * a.ldx + k) * 2) : kOut;
-                xv[mb][c][e] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)off, 0, 0);
-            }
     // per piece, the same for every tile: whether it lies inside K and its
     // scale's group (the bf16 path scales the sums of the 64-value piece --
     // G2: of the pair of pieces c, c + 1 at a multiple of 128 -- by the
@@ -776,9 +793,6 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
                 rs, live && sin[c] ? (int)((srow + sgrp[c]) * 2) : (int)kOut, 0, 0);
         }
     };
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-        issue(d, d);
     __builtin_amdgcn_sched_barrier(0);
     s_cbraw[tid] = cbraw;
     lds_barrier();
@@ -799,7 +813,29 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
         build_table_hl(tab, s_cb);
     else
         build_table<8>(tab, s_cb);
-    lds_barrier();
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        {
+            const int row = wave / WPR;
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                *(u32x4_t *)(sm.u.xs + row * XS + (wave % WPR) * 4096 + p * 1024 + lane * 16) = xraw[r & 1][p];
+        }
+        lds_barrier();
+        const int mb = r * XR / 16, i0 = (r * XR) % 16;
+        if (i >= i0 && i < i0 + XR) {
+#pragma unroll
+            for (int c = 0; c < NC; ++c)
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    xv[mb][c][e] = *(const u32x4_t *)(sm.u.xs + (i - i0) * XS + (wave * R + 64 * c + 16 * kq + 8 * e) * 2);
+        }
+        lds_barrier();
+        xload(r & 1, r + 2);
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+        issue(d, d);
 
     const uint32_t lane4 = ((uint32_t)lane & 31) << 2;  // the lane's table copy
     for (int it0 = 0; it0 < nit; it0 += D) {
@@ -1084,20 +1120,20 @@ void sk1_launch_x(const SkArgs &a, int tpw, hipStream_t s)
 // blocks, NC 64-value pieces per wave (the activations take 8 MB NC
 // registers: 128 at most), loads D tiles ahead (one where the pieces are
 // eight).  It serves 8-bit indices at 17 <= M <= 64 with fp16 activations,
-// or bf16 ones with groups of a multiple of 64 values, on layers of at
-// least 2^25 weights: each workgroup reads its 64 x 8 R activations once
-// from L2 (~9 us for the 256 KiB of 8 R = 2048) and then costs ~2.9 us per
-// tile on the bf16 path, so it pays where a workgroup streams several
-// tiles (bf16 x, 4096 x 14336 at M = 64 / 48 / 32 / 17: 52.9 / 48.6 / 40.2
-// / 38.7 -> 41.2 / 34.7 / 34.4 / 32.7 us; 14336 x 4096: 42.5 / 40.3 / 34.0
-// / 32.0 -> 38.7 / 33.2 / 31.9 / 31.0) and not at 4096 x 4096 (M = 64:
-// 18.9 against 20.2 us).
+// or bf16 ones with groups of a multiple of 64 values, at M > 32 and on
+// layers of at least 2^25 weights: each workgroup takes its 64 x 8 R
+// activations once and then costs ~2.7 us per tile on the bf16 path, so it
+// pays where a workgroup streams several tiles or M is large (bf16 x,
+// 4096 x 14336 at M = 64 / 48 / 32 / 17: 52.9 / 48.6 / 40.2 / 38.7 -> 36.2 /
+// 31.3 / 29.5 / 30.8 us; 14336 x 4096: 42.5 / 40.3 / 34.0 / 32.0 -> 35.3 /
+// 29.5 / 27.6 / 27.5; 4096 x 4096 at M = 64 / 48: 18.9 / 17.7 -> 17.2 /
+// 16.0) and not at 4096 x 4096 below M = 33 (M = 17: 13.2 against 13.9).
 int sk2_mb(int64_t M) { return (int)((M + 15) / 16); }
 int sk2_split_k(int64_t M) { return kSkWaves * 64 * (sk2_mb(M) <= 2 ? 8 : 4); }
 int sk2_splits(int64_t M, int64_t K) { return (int)((K + sk2_split_k(M) - 1) / sk2_split_k(M)); }
 bool sk2_serves(int bits, const ActDesc &x, int64_t M, int64_t N, int64_t K, int group)
 {
-    return bits == 8 && M > 16 && M <= 64 && N * K >= ((int64_t)1 << 25) &&
+    return bits == 8 && M > 16 && M <= 64 && (M > 32 || N * K >= ((int64_t)1 << 25)) &&
            (x.dtype == EP_F16 || (x.dtype == EP_BF16 && group % 64 == 0));
 }
 

@@ -95,8 +95,9 @@ size_t ep_dequant_matmul_workspace(int64_t M, int64_t N, int64_t K, int levels, 
  * The kernel is chosen from M: the LUT GEMV at M = 1 (up to 4 where its
  * activations fit), register-dequant MFMA kernels up to M = 64 (one launch
  * per linear for 8-bit indices at M <= 16 and wide N; for 8-bit indices at
- * 17 <= M <= 64 on layers of at least 2^25 weights, split-K over slices of
- * 2048 or 4096 values with each wave's activations held in registers;
+ * 33 <= M <= 64, and at 17 <= M <= 32 on layers of at least 2^25 weights,
+ * split-K over slices of 2048 or 4096 values with each wave's activations
+ * held in registers;
  * split-K over slices of at most 1024 otherwise; the splits' f32 partials
  * summed in split order), dequant-to-LDS + MFMA above.  Each reads the
  * packed bytes exactly once per launch.

@@ -317,9 +317,9 @@ def test_skinny_one_launch_strided_x(m):
                                                     k, 256, 128))
 
 
-# The register-resident split-K kernel: 8-bit indices, 17 <= M <= 64, fp16
-# x or bf16 x with groups of a multiple of 64 values (the bf16 path), layers
-# of at least 2^25 weights.  A split is 4096 values of K (M <= 32) or 2048;
+# The register-resident split-K kernel: 8-bit indices, 33 <= M <= 64 (17 <=
+# M on layers of at least 2^25 weights), fp16 x or bf16 x with groups of a
+# multiple of 64 values (the bf16 path).  A split is 4096 values of K (M <= 32) or 2048;
 # a workgroup streams every gtiles-th 16-row tile of its split.
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,n,k,group,levels", [
