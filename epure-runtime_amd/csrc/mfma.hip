@@ -571,11 +571,13 @@ bool expert_grouped_serves(const PackedDesc &w, const ActDesc &x, int64_t T, int
     return E >= 1 && E <= kMaxExperts && T >= 1 && T <= (int64_t)1 << 24 && mfma_serves(w, x, T);
 }
 
-// The prefill kernel (the whole K per workgroup, 128-row tiles where the
-// experts average 128 tokens or more, else 64) wherever its shape rules
-// hold (fp16 scales; at 16 / 512 / 2048 tokens of a 128 x 768 x 2048 stack,
-// top-8: 52 / 87 / 213 us against 58 / 134 / 216 on the generic kernel);
-// the generic MFMA kernel (32- or 64-row tiles) for the rest.
+// The prefill kernel (the whole K per workgroup; 128-row tiles where the
+// experts average 128 tokens or more, 64 from 32, else 32: a tile's MFMAs
+// cover all of its rows, live or not) wherever its shape rules hold (fp16
+// scales; at 16 / 128 / 512 / 2048 tokens of a 128 x 768 x 2048 stack,
+// top-8: 46 / 67 / 87 / 215 us against 58 / 76 / 134 / 216 on the generic
+// kernel; 32-row tiles against 64 at 16 / 128 tokens: 46 / 67 against 52 /
+// 74 us); the generic MFMA kernel (32- or 64-row tiles) for the rest.
 int launch_expert_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, const int *ids, int E,
                           const OutDesc &y, void *ws, size_t ws_bytes, hipStream_t stream)
 {
@@ -597,7 +599,7 @@ int launch_expert_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, cons
     int *rexp = (int *)base;  // (the prefill kernel's exponents and fp16 rows start here too)
     const int64_t avg = (T + E - 1) / E;
     const bool pf = prefill_grouped_serves(w, x, T);
-    const int bm = pf ? (avg >= 128 ? 128 : 64) : grouped_bm(T, E);
+    const int bm = pf ? (avg >= 128 ? 128 : avg >= 32 ? 64 : 32) : grouped_bm(T, E);
     const dim3 sg((unsigned)((E + kSortWavesPerWg - 1) / kSortWavesPerWg)), sb(64 * kSortWavesPerWg);
     hipLaunchKernelGGL(expert_count_kernel, sg, sb, 0, stream, ids, (int)T, E, counts);
     EP_HIP_CHECK(hipGetLastError());

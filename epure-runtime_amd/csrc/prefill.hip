@@ -578,6 +578,8 @@ int launch_prefill_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, con
             return pf_launch_grouped<4, 128, 4, 1, 8>(a, tiles_y, stream);
         }
         a.ksteps = ks(4);
+        if (bm == 32)
+            return pf_launch_grouped<4, 32, 4, 2, 4>(a, tiles_y, stream);
         return pf_launch_grouped<4, 64, 4, 2, 4>(a, tiles_y, stream);
     }
     if (bm == 128) {
@@ -585,6 +587,8 @@ int launch_prefill_grouped(const PackedDesc &w, const ActDesc &x, int64_t T, con
         return pf_launch_grouped<8, 128, EP_PF_PD8, 1, 8>(a, tiles_y, stream);
     }
     a.ksteps = ks(3);
+    if (bm == 32)
+        return pf_launch_grouped<8, 32, 3, 2, 4>(a, tiles_y, stream);
     return pf_launch_grouped<8, 64, 3, 2, 4>(a, tiles_y, stream);
 }
 

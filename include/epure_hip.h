@@ -133,9 +133,9 @@ int ep_expert_matmul(const void *x, int x_dtype, int64_t ldx, const int32_t *exp
  * a stable sort of the tokens by id (clamped into [0, E)), then one MFMA
  * launch whose workgroups take row tiles of one expert's tokens, each
  * reading that expert's weight rows once per tile and storing at the
- * tokens' own rows of y: the prefill MFMA kernel (64- or 128-row tiles)
- * where its shape rules hold (fp16 scales), else the generic MFMA kernel
- * (32- or 64-row tiles).
+ * tokens' own rows of y: the prefill MFMA kernel (32-, 64- or 128-row
+ * tiles) where its shape rules hold (fp16 scales), else the generic MFMA
+ * kernel (32- or 64-row tiles).
  * Replaces the reference's per-call slab materialization
  * (epure/runtime.py:163-186) and the caller's host-side grouping of tokens
  * per expert: no host synchronization, capturable in a HIP graph,
