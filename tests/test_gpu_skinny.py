@@ -379,3 +379,28 @@ def test_skinny_register_resident_deterministic():
     a = run(s, x).cpu().numpy()
     b = run(s, x).cpu().numpy()
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,n,k", [(16, 4096, 2048), (48, 2056, 4096 + 64), (24, 8200, 4096 + 64)])
+def test_skinny_graph_replays_match_eager(m, n, k):
+    """Captured once, replayed with new activations copied in: every replay
+    equals the eager call bit for bit (the one-launch kernel; the
+    register-resident kernel with three and with two splits and their
+    reduction launch)."""
+    _, packed, scale, cb, s = make(n, k, 256, seed=95 + m)
+    h = cuda._hot(s)
+    xs = torch.zeros((m, k), device=DEV, dtype=torch.bfloat16)
+    ys = torch.zeros((m, n), device=DEV, dtype=torch.float32)
+    cuda.forward(xs, h, out=ys)  # warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cuda.forward(xs, h, out=ys)
+    for i in range(3):
+        x32, x = x_bf16(m, k, 200 + i)
+        xs.copy_(x)
+        g.replay()
+        torch.cuda.synchronize()
+        eager = run(s, x).cpu().numpy()
+        assert np.array_equal(ys.cpu().numpy(), eager)
+        assert_close(eager, rust_ref(x32, packed, scale, cb, n, k, 256, 128))
