@@ -66,8 +66,8 @@ class DecoderConfig:
                 ("o", h, self.n_heads * d), ("gate", i, h), ("up", i, h), ("down", h, i)]
 
 
-# Decoder shapes the one-launch step serves: the two BASELINE configurations
-# (Llama-3-8B, Qwen3-1.7B), Qwen3-8B (the shape of the reference's own
+# Decoder shapes the one-launch step serves: the two benchmark
+# configurations (Llama-3-8B, Qwen3-1.7B), Qwen3-8B (the shape of the reference's own
 # headline model, CHANGELOG.md:54-56: 36 layers, intermediate 12288),
 # Llama-3.2-3B and Qwen3-4B (query width 4096 over hidden 2560).  Other
 # shapes run the per-layer launches.
