@@ -66,11 +66,11 @@ class DecoderConfig:
                 ("o", h, self.n_heads * d), ("gate", i, h), ("up", i, h), ("down", h, i)]
 
 
-# Decoder shapes the one-launch step serves: the two benchmark
-# configurations (Llama-3-8B, Qwen3-1.7B), Qwen3-8B (the shape of the reference's own
-# headline model, CHANGELOG.md:54-56: 36 layers, intermediate 12288),
-# Llama-3.2-3B and Qwen3-4B (query width 4096 over hidden 2560).  Other
-# shapes run the per-layer launches.
+# Decoder shapes with tuned one-launch variants: the two benchmark
+# configurations (Llama-3-8B, Qwen3-1.7B), Qwen3-8B (the shape of the
+# reference's own headline model, CHANGELOG.md:54-56: 36 layers,
+# intermediate 12288), Llama-3.2-3B and Qwen3-4B (query width 4096 over
+# hidden 2560).
 LLAMA3_8B = DecoderConfig(4096, 14336, 32, 32, 8, 128, 128256, 5e5, 1e-5, name="llama3-8b")
 QWEN3_1_7B = DecoderConfig(2048, 6144, 28, 16, 8, 128, 151936, 1e6, 1e-6, qk_norm=True,
                            tie_embeddings=True, name="qwen3-1.7b")
