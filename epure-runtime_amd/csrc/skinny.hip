@@ -746,9 +746,9 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
     // whole contiguous rows (wave w loads 4 KiB of row w / WPR, 1 KiB per
     // instruction), then each lane reads its operand pieces of those rows.
     // Loaded straight into operand registers, every load instruction would
-    // take 64 bytes from each of 16 rows a power-of-two stride apart (8 KiB
-    // at K = 4096), and the 256 KiB per workgroup arrived at ~28 GB/s per CU
-    // (4096 x 4096 at M = 64: 18.9 -> 17.2 us staged).
+    // take 64 bytes from each of 16 rows (runs of 64 bytes), and the 256 KiB
+    // per workgroup arrived at ~28 GB/s per CU (4096 x 4096 at M = 64: 18.9
+    // -> 17.2 us staged).
     u32x4_t xraw[2][4];
     auto xload = [&](int slot, int r) {
         const int m = r * XR + wave / WPR;
