@@ -404,3 +404,47 @@ def test_skinny_graph_replays_match_eager(m, n, k):
         eager = run(s, x).cpu().numpy()
         assert np.array_equal(ys.cpu().numpy(), eager)
         assert_close(eager, rust_ref(x32, packed, scale, cb, n, k, 256, 128))
+
+
+def _random_register_resident_cases(count=8, seed=2024):
+    """Seeded shapes the register-resident kernel serves: M 33..64 at any
+    size (and 17..32 at >= 2^25 weights), N and K ragged (K a multiple of
+    16; of 64 for groups of 64), groups of 64, 128 or 256, levels 17..256."""
+    g = rng(seed)
+    cases = []
+    while len(cases) < count:
+        m = int(g.integers(17, 65))
+        group = int(g.choice([64, 128, 256]))
+        k = int(g.integers(2, 80)) * 64
+        n = int(g.integers(1, 600)) * 8 + int(g.integers(0, 8))
+        if m <= 32 and n * k < 2 ** 25:
+            n = 2 ** 25 // k + 1 + int(g.integers(0, 64))
+        if n * k > 40_000_000:
+            continue
+        cases.append((m, n, k, group, int(g.integers(17, 257))))
+    return cases
+
+
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,n,k,group,levels", _random_register_resident_cases())
+def test_skinny_register_resident_random_shapes(xdt, m, n, k, group, levels):
+    """Seeded random shapes.  bf16 x: the products take the f32 weights (a
+    hi/lo bf16 pair of the codebook), held to the Rust-order result.  fp16 x:
+    the products take fp16(cb[idx] * scale), the operands of the reference's
+    Triton kernel (_triton.py:95-103), so the result is held to 1e-4 of the
+    fp64 product of those operands, and normwise to the Rust order.  Against
+    the Rust order per element, fp16 weight rounding (2^-11 of each weight)
+    reaches 2.5e-3 of max(|y|, rms y) at 28 x 58274 outputs, K = 576."""
+    _, packed, scale, cb, s = make(n, k, levels, group, seed=n + k + m + group)
+    x32, x = x_bf16(m, k, 3 * m + levels)
+    x = x.to(xdt)
+    xr = x.float().cpu().numpy()
+    want = rust_ref(xr, packed, scale, cb, n, k, levels, group)
+    y = run(s, x).cpu().numpy()
+    if xdt == torch.bfloat16:
+        assert_close(y, want)
+        return
+    w16 = ref.materialize(packed, scale, cb, n, k, group, levels, "f16")
+    assert_close(y, ref.linear_f64(xr, w16), 1e-4)
+    err = np.abs(y.astype(np.float64) - want).max()
+    assert err <= TOL * np.abs(want).max(), f"normwise {err / np.abs(want).max():.3e}"
