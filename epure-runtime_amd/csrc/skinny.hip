@@ -733,9 +733,18 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane & 15, kq = lane >> 4;
-    const int split = blockIdx.y;
+    // workgroup L runs on XCD L % 8 (round-robin dispatch).  One split: XCD
+    // x takes the consecutive tile groups x G / 8 .. (as near as G allows)
+    // -- 14336 x 4096 at M = 17: 28.3 -> 27.0 us.  Several: the pair (split
+    // L / gtiles, tile group L % gtiles), which puts the splits of a tile
+    // group on one XCD when gtiles % 8 == 0; the per-XCD order there (an
+    // XCD's L2 fetching one or two splits' activations, not every split's)
+    // measured 33.8 -> 35.0 us at 14336 x 4096, M = 64.
+    const int G = (int)gridDim.x, L = (int)blockIdx.x, xcd = L & 7;
+    const int q = G == a.gtiles ? xcd * (G >> 3) + min(xcd, G & 7) + (L >> 3) : L;
+    const int split = q / a.gtiles, tg = q - split * a.gtiles;
     const int k0 = split * KW + wave * R;
-    const int nit = (a.tiles - (int)blockIdx.x + a.gtiles - 1) / a.gtiles;  // this workgroup's row tiles
+    const int nit = (a.tiles - tg + a.gtiles - 1) / a.gtiles;  // this workgroup's row tiles
     const auto rx = buffer_rsrc(a.x, a.xbytes), rw = buffer_rsrc(a.packed, a.wbytes);
     const auto rs = buffer_rsrc(a.scale, a.sbytes), rcb = buffer_rsrc(a.cb, a.cbbytes);
 
@@ -779,7 +788,7 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
     u32x4_t wv[D][NC];
     uint32_t sv[D][NC];  // fp16 scale bits; 0 where masked
     auto issue = [&](int d, int it) {
-        const int n = ((int)blockIdx.x + it * a.gtiles) * 16 + i;
+        const int n = (tg + it * a.gtiles) * 16 + i;
         const bool live = it < nit && n < a.N;
         const uint32_t wrow = (uint32_t)n * a.row_bytes + (uint32_t)(k0 + 16 * kq);
         const uint32_t srow = (uint32_t)n * (uint32_t)a.lds;  // in range: sbytes fits 32 bits
@@ -902,7 +911,7 @@ __global__ void __launch_bounds__(kSkThreads) sk2_kernel(SkArgs a)
                 for (int w = 1; w < kSkWaves; ++w)
                     s += red[buf][w][mb][l];
                 // element r: row m0 + r dm, column n0 + r dn
-                const int nt = ((int)blockIdx.x + it * a.gtiles) * 16;
+                const int nt = (tg + it * a.gtiles) * 16;
                 const int m0 = 16 * mb + (HL ? 4 * (l >> 4) : (l & 15)), dm = HL ? 1 : 0;
                 const int n0 = nt + (HL ? (l & 15) : 4 * (l >> 4)), dn = HL ? 0 : 1;
                 bool ok[4];
@@ -1081,13 +1090,16 @@ int sk1_tiles_per_wg(int bits, const ActDesc &x, int64_t M, int64_t N, int group
 // 16 waves with 8-bit indices, one 16-row activation block and up to two
 // tiles (four per SIMD hide the table lookups' latency), 8 otherwise (4-bit
 // B operands and activations, more activation blocks or the four tiles'
-// sums take the registers of two waves); two pieces per round where one
-// tile and one block of 8-bit indices leave the registers for them.
+// sums take the registers of two waves); two pieces per round (128
+// contiguous bytes of each row, whole 128-byte lines) for 8-bit indices
+// and one activation block, except at two tiles, whose 16 waves have no
+// registers left for them (14336 x 4096 at M = 4, four tiles: 28.2 -> 27.2
+// us with two pieces).
 template <int BITS, int XDT, int T, int MT, bool HL>
 void sk1_launch_t(const SkArgs &a, hipStream_t s)
 {
     constexpr int NT = BITS == 8 && MT == 1 && T < 4 ? 1024 : 512;
-    constexpr int P = BITS == 8 && MT == 1 && T == 1 ? 2 : 1;
+    constexpr int P = BITS == 8 && MT == 1 && T != 2 ? 2 : 1;
     hipLaunchKernelGGL((sk1_kernel<BITS, XDT, T, 2, P, MT, NT, HL>), dim3((unsigned)a.gtiles), dim3(NT), 0, s, a);
 }
 
@@ -1142,7 +1154,7 @@ void sk2_launch_m(const SkArgs &a, int S, hipStream_t s)
 {
     constexpr int NC = MB <= 2 ? 8 : 4;
     constexpr int D = NC == 8 ? 1 : 2;
-    const dim3 grid((unsigned)a.gtiles, (unsigned)S);
+    const dim3 grid((unsigned)(a.gtiles * S));  // (split, tile group) pairs
     if (HL && a.group % 128 == 0)  // one scale per pair of 64-value pieces
         hipLaunchKernelGGL((sk2_kernel<MB, NC, D, HL, HL>), grid, dim3(kSkThreads), 0, s, a);
     else
