@@ -1087,19 +1087,20 @@ int sk1_tiles_per_wg(int bits, const ActDesc &x, int64_t M, int64_t N, int group
     return 0;
 }
 
-// 16 waves with 8-bit indices, one 16-row activation block and up to two
-// tiles (four per SIMD hide the table lookups' latency), 8 otherwise (4-bit
-// B operands and activations, more activation blocks or the four tiles'
-// sums take the registers of two waves); two pieces per round (128
-// contiguous bytes of each row, whole 128-byte lines) for 8-bit indices
-// and one activation block, except at two tiles, whose 16 waves have no
-// registers left for them (14336 x 4096 at M = 4, four tiles: 28.2 -> 27.2
-// us with two pieces).
+// 16 waves with 8-bit indices, one 16-row activation block and one tile
+// (four per SIMD hide the table lookups' latency), 8 otherwise (4-bit B
+// operands and activations, more activation blocks, or the two or four
+// tiles' weights at two pieces per round take the registers of two
+// waves); two pieces per round (128 contiguous bytes of each row, whole
+// 128-byte lines) for 8-bit indices and one activation block.  With one
+// piece (64 bytes of a row per round) each line is read by two rounds:
+// 8192 x 4096 at M = 4, two tiles on 16 waves, 17.3 -> 15.4 us on 8 waves
+// with two pieces; 14336 x 4096 at M = 4, four tiles, 28.2 -> 27.2 us.
 template <int BITS, int XDT, int T, int MT, bool HL>
 void sk1_launch_t(const SkArgs &a, hipStream_t s)
 {
-    constexpr int NT = BITS == 8 && MT == 1 && T < 4 ? 1024 : 512;
-    constexpr int P = BITS == 8 && MT == 1 && T != 2 ? 2 : 1;
+    constexpr int NT = BITS == 8 && MT == 1 && T < 2 ? 1024 : 512;
+    constexpr int P = BITS == 8 && MT == 1 ? 2 : 1;
     hipLaunchKernelGGL((sk1_kernel<BITS, XDT, T, 2, P, MT, NT, HL>), dim3((unsigned)a.gtiles), dim3(NT), 0, s, a);
 }
 
