@@ -253,6 +253,26 @@ def test_skinny_one_launch_4bit_accumulate_f16_x(out_dtype, m, n, k):
     assert_close(out.float().cpu().numpy(), want + start, out_tol)
 
 
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,n,k", [(6, 8184, 1104), (16, 8184, 2112), (5, 12300, 1104), (16, 12300, 2112)])
+def test_skinny_one_launch_whole_line_rounds(xdt, m, n, k):
+    """The one-launch kernel at two (N = 8184) and four (N = 12300) tiles
+    per workgroup on 256 CUs, 8-bit indices, M >= 5 (the GEMV takes M <= 4):
+    rounds of 128 values (two 16-byte pieces per row) over a K that ends
+    inside a round's second piece (1104 = 8 x 128 + 80) or first (2112 = 16
+    x 128 + 64)."""
+    _, packed, scale, cb, s = make(n, k, 256, 64, seed=n + k + m)
+    x32, x = x_bf16(m, k, 7 * m + k)
+    x = x.to(xdt)
+    xr = x.float().cpu().numpy()
+    y = run(s, x).cpu().numpy()
+    want = rust_ref(xr, packed, scale, cb, n, k, 256, 64)
+    if xdt == torch.bfloat16:
+        assert_close(y, want)
+    else:  # fp16 x: the products take fp16(cb[idx] * scale) (_triton.py:95-103)
+        assert_close(y, ref.linear_f64(xr, ref.materialize(packed, scale, cb, n, k, 64, 256, "f16")), 1e-4)
+
+
 @pytest.mark.parametrize("group,m", [(64, 24), (256, 24), (64, 40), (256, 64)])
 def test_skinny_one_launch_bf16_path_groups(group, m):
     """The bf16 path (8-bit indices, bf16 x) scales each 64-value piece's
