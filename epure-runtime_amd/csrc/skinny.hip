@@ -329,8 +329,9 @@ __global__ void __launch_bounds__(kSkThreads) sk_kernel(SkArgs a)
 // One launch for small M with fp16/bf16 activations.  A
 // workgroup owns T row tiles of 16 rows (tiles blockIdx.x + t * gridDim.x)
 // over the whole of K, so its sums are final: no partials, no second
-// launch.  Its 16 waves (four per SIMD, to hide the latency of the table
-// lookups) split K into contiguous runs of rounds; a round is RK = 4 KPL P
+// launch.  Its 16 waves at one tile (four per SIMD, to hide the latency of
+// the table lookups; 8 where the tiles' weights or more activation blocks
+// need the registers) split K into contiguous runs of rounds; a round is RK = 4 KPL P
 // values of K.  In a round, lane (j, q) loads P 16-byte pieces of row j
 // (piece c at chunk 4 c + q of the round: each load instruction covers 64
 // bytes of 16 rows, the P of a round, issued back to back, 64 P contiguous
